@@ -1,0 +1,151 @@
+/*
+ * ulspec.h -- C ABI of the MI355X (gfx950) speculative-decoding verification
+ * path.  Plain C: opaque context, status codes, device pointers and sizes.
+ *
+ * The reference exposes this path through the C++ class py::InferenceAPI
+ * (src/api/inference_api.h:52-123, pybind module `vulkangguf`,
+ * src/api/inference_api.cpp:389-427) over inference::InferenceEngine and
+ * inference::SpeculativeDecoder (src/inference/speculative_decoder.h:24-60).
+ * Those classes are mirrored in C++ on top of this ABI
+ * (universal-loader_amd/csrc/host/); each entry point below names the
+ * reference interface whose work it takes over.
+ *
+ * Conventions
+ *   - Every function returns ULSPEC_OK or an error code; no C++ exception
+ *     crosses the ABI.  ulspec_last_error() gives the message of the last
+ *     failure on a context.
+ *   - Arguments are validated on the host before any launch, so invalid
+ *     calls fail without touching the GPU.
+ *   - A context owns one HIP stream (default priority) on one device; compute
+ *     calls are asynchronous on that stream; ulspec_sync / ulspec_memcpy are
+ *     the host fences.  A context is not thread-safe (one per host thread, as
+ *     py::InferenceAPI serialises every call behind api_mutex_,
+ *     src/api/inference_api.h:115).
+ *   - Weights, KV caches and workspaces belong to the context; host buffers
+ *     belong to the caller.  There is no CPU fallback: without a usable
+ *     gfx950 device, ulspec_create fails with ULSPEC_EDEVICE.
+ */
+#ifndef ULSPEC_H
+#define ULSPEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ulspec_ctx ulspec_ctx;
+
+typedef enum {
+    ULSPEC_OK = 0,
+    ULSPEC_EINVAL = 1,       /* bad argument (checked before any launch) */
+    ULSPEC_ENOMEM = 2,       /* device or host allocation failed */
+    ULSPEC_EDEVICE = 3,      /* HIP runtime error / no gfx950 device */
+    ULSPEC_EUNSUPPORTED = 4  /* valid request this build does not implement */
+} ulspec_status;
+
+/* GGUF type ids (src/core/gguf_types.h:6-33). */
+enum { ULSPEC_GGML_Q4_0 = 2, ULSPEC_GGML_Q4_K = 12 };
+
+/* ---- library / context ---------------------------------------------------
+ * Replaces the Vulkan bring-up of InferenceEngine::initialize
+ * (src/inference/inference_engine.cpp:48-148). */
+const char*   ulspec_version(void);
+/* Block sizes of the GGUF types: elements per block (32 / 256) and bytes per
+ * block (18 / 144).  Replaces ggml_blck_size / ggml_type_size
+ * (src/core/gguf_types.h:35-81, whose Q4 byte sizes 6 / 12 are wrong). */
+int           ulspec_ggml_blck_size(uint32_t ggml_type);
+int           ulspec_ggml_type_size(uint32_t ggml_type);
+ulspec_status ulspec_create(int hip_device, ulspec_ctx** out);
+void          ulspec_destroy(ulspec_ctx* ctx);
+const char*   ulspec_last_error(const ulspec_ctx* ctx); /* valid until the next call on ctx */
+const char*   ulspec_status_str(ulspec_status s);
+
+/* ---- memory (device buffers owned by the caller through the context) ----- */
+ulspec_status ulspec_alloc(ulspec_ctx* ctx, size_t bytes, void** dev_ptr);
+ulspec_status ulspec_free(ulspec_ctx* ctx, void* dev_ptr);
+/* kind: 0 host->device, 1 device->host, 2 device->device; ordered on the
+ * context stream and synchronous for the host. */
+ulspec_status ulspec_memcpy(ulspec_ctx* ctx, void* dst, const void* src, size_t bytes, int kind);
+ulspec_status ulspec_sync(ulspec_ctx* ctx);
+
+/* ---- stream capture and timing ---------------------------------------------
+ * Record a sequence of compute calls on the context stream into a HIP graph
+ * and replay it; mark HIP events on the stream and read the time between two
+ * marks.  This is the launch-free replay of a fixed step (the reference
+ * submits one command buffer and waits on a fence per dispatch,
+ * src/vulkan_backend/compute.cpp:82-121) and the device-side timing behind
+ * InferenceAPI::enable_profiling / get_performance_report
+ * (src/api/inference_api.h:93-94).  Calls that allocate (weight uploads,
+ * workspace growth) must not run while capturing. */
+ulspec_status ulspec_capture_begin(ulspec_ctx* ctx);
+ulspec_status ulspec_capture_end(ulspec_ctx* ctx, uint32_t* graph_id);
+ulspec_status ulspec_graph_replay(ulspec_ctx* ctx, uint32_t graph_id, uint32_t times);
+ulspec_status ulspec_graph_destroy(ulspec_ctx* ctx, uint32_t graph_id);
+ulspec_status ulspec_timer_mark(ulspec_ctx* ctx, uint32_t slot /* < 16 */);
+ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t slot_b, float* ms);
+
+/* ---- K1: verify dequant-GEMM ------------------------------------------------
+ * Upload one linear weight given as GGUF blocks (host memory, rows of K
+ * elements, ne[0] = K contiguous; src/core/tensor.h:17-65).  The context keeps
+ * a device copy re-tiled for the kernel (same 18 / 144 bytes per block).
+ * Replaces the first-use repack + upload of run_linear_q4k
+ * (src/inference/inference_engine.cpp:536-548, repack_q4k_tensor :891-927). */
+ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t ggml_type, const void* gguf_blocks,
+                                   size_t nbytes, uint32_t n_rows /* N */, uint32_t k /* K */,
+                                   uint32_t* out_weight_id);
+ulspec_status ulspec_weight_info(ulspec_ctx* ctx, uint32_t weight_id, uint32_t* ggml_type,
+                                 uint32_t* n_rows, uint32_t* k, size_t* device_bytes);
+/* Y[M][N] (fp32, row-major) = X[M][K] (fp16, row-major) . W[N][K]^T.
+ * M >= 1 (any size; rows are processed in groups of up to 64).
+ * Replaces the dequantize + gemm_transposed_b_v2 pair of run_linear_q4k
+ * (src/inference/inference_engine.cpp:550-566). */
+ulspec_status ulspec_verify_gemm(ulspec_ctx* ctx, uint32_t weight_id, const uint16_t* x_f16,
+                                 uint32_t M, float* y_f32);
+
+/* ---- K2: verify attention ---------------------------------------------------
+ * q: fp16 [nq][H][D]; k_cache, v_cache: fp16 [L][Hkv][D] with L = n_prefix + nq
+ * (the nq new rows already written); out: fp32 [nq][H][D] (device memory).
+ * parent: NULL for a causal chain, else HOST int32 [nq] with parent[i] < i or
+ * -1 (child of the prefix).  1 <= nq <= 16, D == 128 or 64, H % Hkv == 0.
+ * Replaces the single-token attention dispatch of forward_layer_gpu
+ * (src/inference/inference_engine.cpp:627-630; semantics of
+ * src/shaders/attention/flash_attention_v2_fused.glsl:153-166). */
+ulspec_status ulspec_verify_attention(ulspec_ctx* ctx, const uint16_t* q, const uint16_t* k_cache,
+                                      const uint16_t* v_cache, uint32_t n_prefix, uint32_t nq,
+                                      const int32_t* parent, uint32_t H, uint32_t Hkv, uint32_t D,
+                                      float scale, float* out);
+
+/* ---- K3: acceptance sampling ------------------------------------------------ */
+typedef struct {
+    float    temperature; /* > 0 (ignored when greedy) */
+    uint32_t top_k;       /* 0 = off */
+    float    top_p;       /* >= 1 = off */
+    int32_t  greedy;      /* != 0: argmax-match rule */
+} ulspec_sampling;
+
+/* Per sequence b: p_i = warp(target[b][i]), q_i = warp(draft[b][i]); accept
+ * draft token x_i while u[b][i] * q_i(x_i) < p_i(x_i); on the first rejection
+ * draw from max(0, p_i - q_i) (renormalised) with u[b][k]; if all k pass, draw
+ * the bonus token from p_k with u[b][k].  Greedy: accept while argmax p_i ==
+ * x_i and emit the argmax.  out_tokens [B][k+1] holds n_accepted + 1 tokens
+ * then -1.  All arrays are device memory.  1 <= k <= 16, top_k <= 256.
+ * Replaces SpeculativeDecoder::verify_speculation and the sampling of
+ * InferenceEngine::sample_token (src/inference/speculative_decoder.cpp:89-110,
+ * src/inference/inference_engine.cpp:340-367). */
+ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
+                            uint32_t V, const float* target_logits, const float* draft_logits,
+                            const int32_t* draft_tokens, const float* uniforms,
+                            int32_t* out_tokens, int32_t* out_n_accepted);
+/* One token per row from warp(logits[r]) with uniforms[r] (greedy: argmax).
+ * Replaces InferenceEngine::sample_token (src/inference/inference_engine.cpp:340-367). */
+ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
+                            const float* logits, const float* uniforms, int32_t* out_tokens);
+/* uniforms[i] = top 24 bits of splitmix64(seed + (idx0 + i + 1) * golden) * 2^-24 */
+ulspec_status ulspec_uniforms(ulspec_ctx* ctx, uint64_t seed, uint64_t idx0, uint32_t n, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,242 @@
+"""ctypes binding of the CPU oracle (oracle/_build/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py.  The product never imports this module.
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+
+Q4_0 = 2
+Q4_K = 12
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE, "-B"], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-s", "-C", _HERE], check=True)
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("greedy", C.c_int32)]
+
+
+class LlamaCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("ffn", C.c_int32), ("vocab", C.c_int32), ("wtype", C.c_int32), ("max_ctx", C.c_int32),
+                ("rms_eps", C.c_float), ("rope_base", C.c_float)]
+
+
+P = C.c_void_p
+I64 = C.c_int64
+
+
+def _declare(L):
+    def d(name, res, *args):
+        f = getattr(L, name, None)
+        if f is None:
+            return
+        f.restype = res
+        f.argtypes = list(args)
+
+    d("ora_h2f", C.c_float, C.c_uint16)
+    d("ora_f2h", C.c_uint16, C.c_float)
+    d("ora_mix64", C.c_uint64, C.c_uint64)
+    d("ora_uniform", C.c_float, C.c_uint64, C.c_uint64)
+    d("ora_uniforms", None, C.c_uint64, C.c_uint64, C.c_size_t, P)
+    d("ora_normals", None, C.c_uint64, C.c_uint64, C.c_size_t, C.c_double, C.c_double, P, C.c_int)
+    d("ora_expf", C.c_float, C.c_float)
+    d("ora_blck_size", C.c_int, C.c_int)
+    d("ora_type_size", C.c_int, C.c_int)
+    d("ora_row_bytes", C.c_size_t, C.c_int, I64)
+    d("ora_quantize", C.c_int, C.c_int, P, I64, P)
+    d("ora_dequantize", C.c_int, C.c_int, P, I64, P)
+    d("ora_synth_q4", C.c_int, C.c_int, C.c_uint64, C.c_uint64, I64, I64, C.c_double, P, C.c_int)
+    d("ora_q4_gemm_f64", C.c_int, C.c_int, P, I64, I64, P, I64, P)
+    d("ora_q4_gemm_f32", C.c_int, C.c_int, P, I64, I64, P, I64, P, C.c_int)
+    d("ora_attention_f64", C.c_int, P, P, P, I64, I64, P, I64, I64, I64, C.c_float, P)
+    d("ora_attention_f32", C.c_int, P, P, P, I64, I64, P, I64, I64, I64, C.c_float, P, C.c_int)
+    d("ora_warp_row", I64, P, P, I64, P, P)
+    d("ora_warp_shift", C.c_int, I64)
+    d("ora_cdf_pick", I64, P, I64, C.c_uint64, C.c_float)
+    d("ora_sample", C.c_int, P, I64, I64, P, P, P)
+    d("ora_accept", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, C.c_int)
+    d("ora_llama_create", P, P, C.c_int)
+    d("ora_llama_free", None, P)
+    d("ora_llama_set_tensor", C.c_int, P, C.c_int, C.c_int, P, C.c_size_t)
+    d("ora_llama_reset", None, P)
+    d("ora_llama_kv_len", I64, P)
+    d("ora_llama_set_kv_len", C.c_int, P, I64)
+    d("ora_llama_forward", C.c_int, P, P, I64, P)
+    d("ora_llama_kv_io", C.c_int, P, C.c_int, C.c_int, I64, P, C.c_int)
+    d("ora_spec_generate", I64, P, P, P, C.c_int32, P, I64, I64, C.c_uint64, P, P, I64, I64)
+
+
+def _p(a):
+    return a.ctypes.data_as(C.c_void_p) if a is not None else None
+
+
+def nthreads_default():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# ---- thin numpy wrappers -----------------------------------------------------
+
+def f2h_fast(x):
+    """fp32 -> fp16 bits, round to nearest even (numpy; equal to ora_f2h, tested)."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def h2f_fast(h):
+    return np.asarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def f2h(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return np.array([lib().ora_f2h(float(v)) for v in x.ravel()], dtype=np.uint16).reshape(x.shape)
+
+
+def h2f(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    return np.array([lib().ora_h2f(int(v)) for v in h.ravel()], dtype=np.float32).reshape(h.shape)
+
+
+def expf(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    f = lib().ora_expf
+    return np.array([f(float(v)) for v in x.ravel()], dtype=np.float32).reshape(x.shape)
+
+
+def uniforms(seed, idx0, n):
+    out = np.empty(n, dtype=np.float32)
+    lib().ora_uniforms(seed, idx0, n, _p(out))
+    return out
+
+
+def normals(seed, stream, n, mean=0.0, std=1.0, nthreads=None):
+    out = np.empty(n, dtype=np.float32)
+    lib().ora_normals(seed, stream, n, mean, std, _p(out), nthreads or nthreads_default())
+    return out
+
+
+def row_bytes(wtype, k):
+    return lib().ora_row_bytes(wtype, k)
+
+
+def quantize(wtype, x):
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(row_bytes(wtype, x.size), dtype=np.uint8)
+    assert lib().ora_quantize(wtype, _p(x), x.size, _p(out)) == 0
+    return out
+
+
+def dequantize(wtype, b, n):
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    assert lib().ora_dequantize(wtype, _p(b), n, _p(out)) == 0
+    return out
+
+
+def synth_q4(wtype, seed, stream, N, K, std=0.02, nthreads=None):
+    out = np.empty(N * row_bytes(wtype, K), dtype=np.uint8)
+    assert lib().ora_synth_q4(wtype, seed, stream, N, K, std, _p(out), nthreads or nthreads_default()) == 0
+    return out
+
+
+def q4_gemm_f64(wtype, W, N, K, X):
+    X = np.ascontiguousarray(X, dtype=np.uint16)
+    M = X.shape[0]
+    Y = np.empty((M, N), dtype=np.float64)
+    assert lib().ora_q4_gemm_f64(wtype, _p(np.ascontiguousarray(W)), N, K, _p(X), M, _p(Y)) == 0
+    return Y
+
+
+def q4_gemm_f32(wtype, W, N, K, X, nthreads=None):
+    X = np.ascontiguousarray(X, dtype=np.uint16)
+    M = X.shape[0]
+    Y = np.empty((M, N), dtype=np.float32)
+    assert lib().ora_q4_gemm_f32(wtype, _p(np.ascontiguousarray(W)), N, K, _p(X), M, _p(Y),
+                                 nthreads or nthreads_default()) == 0
+    return Y
+
+
+def attention_f64(q, k, v, n_prefix, parent, H, Hkv, D, scale):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    nq = q.size // (H * D)
+    out = np.empty((nq, H, D), dtype=np.float64)
+    par = None if parent is None else np.ascontiguousarray(parent, dtype=np.int32)
+    rc = lib().ora_attention_f64(_p(q), _p(np.ascontiguousarray(k, dtype=np.uint16)),
+                                 _p(np.ascontiguousarray(v, dtype=np.uint16)), n_prefix, nq, _p(par),
+                                 H, Hkv, D, scale, _p(out))
+    assert rc == 0
+    return out
+
+
+def attention_f32(q, k, v, n_prefix, parent, H, Hkv, D, scale, nthreads=None):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    nq = q.size // (H * D)
+    out = np.empty((nq, H, D), dtype=np.float32)
+    par = None if parent is None else np.ascontiguousarray(parent, dtype=np.int32)
+    rc = lib().ora_attention_f32(_p(q), _p(np.ascontiguousarray(k, dtype=np.uint16)),
+                                 _p(np.ascontiguousarray(v, dtype=np.uint16)), n_prefix, nq, _p(par),
+                                 H, Hkv, D, scale, _p(out), nthreads or nthreads_default())
+    assert rc == 0
+    return out
+
+
+def sampling(temperature=1.0, top_k=0, top_p=1.0, greedy=False):
+    return Sampling(temperature, top_k, top_p, 1 if greedy else 0)
+
+
+def warp_row(s, logits):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    V = logits.size
+    E = np.empty(V, dtype=np.uint64)
+    Z = C.c_uint64(0)
+    nk = lib().ora_warp_row(C.byref(s), _p(logits), V, _p(E), C.byref(Z))
+    return E, int(Z.value), int(nk)
+
+
+def cdf_pick(W, Z, u):
+    W = np.ascontiguousarray(W, dtype=np.uint64)
+    return int(lib().ora_cdf_pick(_p(W), W.size, Z, u))
+
+
+def sample(s, logits, u):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    R, V = logits.shape
+    out = np.empty(R, dtype=np.int32)
+    uu = None if u is None else np.ascontiguousarray(u, dtype=np.float32)
+    assert lib().ora_sample(C.byref(s), R, V, _p(logits), _p(uu), _p(out)) == 0
+    return out
+
+
+def accept(s, target, draft, draft_tokens, u, nthreads=None):
+    target = np.ascontiguousarray(target, dtype=np.float32)
+    B, k1, V = target.shape
+    k = k1 - 1
+    out = np.empty((B, k + 1), dtype=np.int32)
+    nacc = np.empty(B, dtype=np.int32)
+    dr = None if draft is None else np.ascontiguousarray(draft, dtype=np.float32)
+    uu = None if u is None else np.ascontiguousarray(u, dtype=np.float32)
+    rc = lib().ora_accept(C.byref(s), B, k, V, _p(target), _p(dr),
+                          _p(np.ascontiguousarray(draft_tokens, dtype=np.int32)), _p(uu),
+                          _p(out), _p(nacc), nthreads or nthreads_default())
+    assert rc == 0
+    return out, nacc

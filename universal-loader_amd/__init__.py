@@ -1,0 +1,247 @@
+"""Python binding (ctypes) of libulspec, the gfx950 speculative-decoding
+verification path.
+
+Every call goes through the C ABI declared in include/ulspec.h and runs the
+HIP kernels built into lib/libulspec.so.  There is no CPU fallback: if the
+library is missing or no gfx950 device is present, the calls raise.
+
+Import this directory as a package with load_package() (its name contains a
+hyphen), e.g. from a test:
+
+    import importlib.util, sys
+    spec = importlib.util.spec_from_file_location(
+        "universal_loader_amd", "<repo>/universal-loader_amd/__init__.py",
+        submodule_search_locations=["<repo>/universal-loader_amd"])
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libulspec.so")
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+
+Q4_0 = 2
+Q4_K = 12
+
+OK, EINVAL, ENOMEM, EDEVICE, EUNSUPPORTED = 0, 1, 2, 3, 4
+
+
+class UlspecError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"ulspec status {status}: {msg}")
+        self.status = status
+
+
+def build(jobs=8, force=True):
+    """Compile libulspec.so for gfx950 (hipcc cross-compiles without a GPU)."""
+    args = ["make", "-s", "-C", CSRC_DIR, f"-j{jobs}"]
+    if force:
+        args.append("-B")
+    subprocess.run(args, check=True)
+
+
+class Sampling(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("greedy", C.c_int32)]
+
+
+def sampling(temperature=1.0, top_k=0, top_p=1.0, greedy=False):
+    return Sampling(temperature, top_k, top_p, 1 if greedy else 0)
+
+
+_lib = None
+P = C.c_void_p
+U32 = C.c_uint32
+
+
+def lib():
+    """Load libulspec.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise UlspecError(EDEVICE, f"{LIB_PATH} not built; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+# (name, restype, argtypes): every symbol include/ulspec.h declares
+ABI = [
+    ("ulspec_version", C.c_char_p, []),
+    ("ulspec_ggml_blck_size", C.c_int, [U32]),
+    ("ulspec_ggml_type_size", C.c_int, [U32]),
+    ("ulspec_create", C.c_int, [C.c_int, C.POINTER(P)]),
+    ("ulspec_destroy", None, [P]),
+    ("ulspec_last_error", C.c_char_p, [P]),
+    ("ulspec_status_str", C.c_char_p, [C.c_int]),
+    ("ulspec_alloc", C.c_int, [P, C.c_size_t, C.POINTER(P)]),
+    ("ulspec_free", C.c_int, [P, P]),
+    ("ulspec_memcpy", C.c_int, [P, P, P, C.c_size_t, C.c_int]),
+    ("ulspec_sync", C.c_int, [P]),
+    ("ulspec_capture_begin", C.c_int, [P]),
+    ("ulspec_capture_end", C.c_int, [P, C.POINTER(U32)]),
+    ("ulspec_graph_replay", C.c_int, [P, U32, U32]),
+    ("ulspec_graph_destroy", C.c_int, [P, U32]),
+    ("ulspec_timer_mark", C.c_int, [P, U32]),
+    ("ulspec_timer_elapsed_ms", C.c_int, [P, U32, U32, C.POINTER(C.c_float)]),
+    ("ulspec_weight_upload", C.c_int, [P, U32, P, C.c_size_t, U32, U32, C.POINTER(U32)]),
+    ("ulspec_weight_info", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32),
+                                     C.POINTER(C.c_size_t)]),
+    ("ulspec_verify_gemm", C.c_int, [P, U32, P, U32, P]),
+    ("ulspec_verify_attention", C.c_int, [P, P, P, P, U32, U32, P, U32, U32, U32, C.c_float, P]),
+    ("ulspec_accept", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P]),
+    ("ulspec_sample", C.c_int, [P, C.POINTER(Sampling), U32, U32, P, P, P]),
+    ("ulspec_uniforms", C.c_int, [P, C.c_uint64, C.c_uint64, U32, P]),
+]
+
+
+def _declare(L):
+    for name, res, args in ABI:
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+class DeviceBuffer:
+    """A device allocation made through ulspec_alloc on one context."""
+
+    def __init__(self, ctx, nbytes):
+        self.ctx = ctx
+        self.nbytes = int(nbytes)
+        p = P()
+        ctx._check(lib().ulspec_alloc(ctx.handle, max(1, self.nbytes), C.byref(p)))
+        self.ptr = p.value
+
+    def free(self):
+        if self.ptr:
+            self.ctx._check(lib().ulspec_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+    def __int__(self):
+        return self.ptr
+
+
+class Context:
+    """ulspec_ctx: one device, one HIP stream."""
+
+    def __init__(self, device=0):
+        h = P()
+        st = lib().ulspec_create(device, C.byref(h))
+        if st != OK:
+            raise UlspecError(st, f"ulspec_create(device={device}) failed: "
+                                  f"{lib().ulspec_status_str(st).decode()}")
+        self.handle = h.value
+        self._bufs = []
+
+    def close(self):
+        if self.handle:
+            for b in self._bufs:
+                b.ptr = None
+            lib().ulspec_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, st):
+        if st != OK:
+            raise UlspecError(st, lib().ulspec_last_error(self.handle).decode())
+
+    # -- memory --------------------------------------------------------------
+    def alloc(self, nbytes):
+        b = DeviceBuffer(self, nbytes)
+        return b
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        b = DeviceBuffer(self, arr.nbytes)
+        if arr.nbytes:
+            self._check(lib().ulspec_memcpy(self.handle, b.ptr, arr.ctypes.data_as(P), arr.nbytes, 0))
+        return b
+
+    def download(self, buf, dtype, shape):
+        out = np.empty(shape, dtype=dtype)
+        if out.nbytes:
+            self._check(lib().ulspec_memcpy(self.handle, out.ctypes.data_as(P), buf.ptr if hasattr(buf, "ptr")
+                                            else int(buf), out.nbytes, 1))
+        return out
+
+    def copy_in(self, buf, arr, offset=0):
+        arr = np.ascontiguousarray(arr)
+        self._check(lib().ulspec_memcpy(self.handle, int(buf.ptr) + offset, arr.ctypes.data_as(P), arr.nbytes, 0))
+
+    def sync(self):
+        self._check(lib().ulspec_sync(self.handle))
+
+    # -- capture / timing ------------------------------------------------------
+    def capture_begin(self):
+        self._check(lib().ulspec_capture_begin(self.handle))
+
+    def capture_end(self):
+        g = U32()
+        self._check(lib().ulspec_capture_end(self.handle, C.byref(g)))
+        return g.value
+
+    def graph_replay(self, gid, times=1):
+        self._check(lib().ulspec_graph_replay(self.handle, gid, times))
+
+    def graph_destroy(self, gid):
+        self._check(lib().ulspec_graph_destroy(self.handle, gid))
+
+    def timer_mark(self, slot):
+        self._check(lib().ulspec_timer_mark(self.handle, slot))
+
+    def timer_elapsed_ms(self, a, b):
+        ms = C.c_float()
+        self._check(lib().ulspec_timer_elapsed_ms(self.handle, a, b, C.byref(ms)))
+        return ms.value
+
+    # -- K1 ------------------------------------------------------------------
+    def weight_upload(self, wtype, blocks, n_rows, k):
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        wid = U32()
+        self._check(lib().ulspec_weight_upload(self.handle, wtype, blocks.ctypes.data_as(P), blocks.nbytes,
+                                               n_rows, k, C.byref(wid)))
+        return wid.value
+
+    def weight_info(self, wid):
+        t, n, k, b = U32(), U32(), U32(), C.c_size_t()
+        self._check(lib().ulspec_weight_info(self.handle, wid, C.byref(t), C.byref(n), C.byref(k), C.byref(b)))
+        return t.value, n.value, k.value, b.value
+
+    def verify_gemm(self, wid, x, M, y):
+        self._check(lib().ulspec_verify_gemm(self.handle, wid, int(x.ptr if hasattr(x, "ptr") else x), M,
+                                             int(y.ptr if hasattr(y, "ptr") else y)))
+
+    # -- K2 ------------------------------------------------------------------
+    def verify_attention(self, q, k_cache, v_cache, n_prefix, nq, parent, H, Hkv, D, scale, out):
+        par = None
+        if parent is not None:
+            par = np.ascontiguousarray(parent, dtype=np.int32)
+        self._check(lib().ulspec_verify_attention(
+            self.handle, _ptr(q), _ptr(k_cache), _ptr(v_cache), n_prefix, nq,
+            par.ctypes.data_as(P) if par is not None else None, H, Hkv, D, scale, _ptr(out)))
+
+    # -- K3 ------------------------------------------------------------------
+    def accept(self, s, B, k, V, target, draft, draft_tokens, uniforms, out_tokens, out_nacc):
+        self._check(lib().ulspec_accept(self.handle, C.byref(s), B, k, V, _ptr(target), _ptr(draft),
+                                        _ptr(draft_tokens), _ptr(uniforms), _ptr(out_tokens), _ptr(out_nacc)))
+
+    def sample(self, s, R, V, logits, uniforms, out_tokens):
+        self._check(lib().ulspec_sample(self.handle, C.byref(s), R, V, _ptr(logits), _ptr(uniforms),
+                                        _ptr(out_tokens)))
+
+    def uniforms(self, seed, idx0, n, out):
+        self._check(lib().ulspec_uniforms(self.handle, seed, idx0, n, _ptr(out)))
+
+
+def _ptr(b):
+    if b is None:
+        return None
+    return int(b.ptr) if hasattr(b, "ptr") else int(b)

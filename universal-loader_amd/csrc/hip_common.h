@@ -1,0 +1,50 @@
+// hip_common.h -- vector types and small device helpers shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+namespace ulspec {
+
+__device__ __forceinline__ half2_t as_half2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+__device__ __forceinline__ half8_t make_half8(half2_t a, half2_t b, half2_t c, half2_t d)
+{
+    half4_t lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
+    half4_t hi = __builtin_shufflevector(c, d, 0, 1, 2, 3);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ half2_t splat2(float v)
+{
+    half2_t h = {(_Float16)v, (_Float16)v};
+    return h;
+}
+
+// 16x16x32 fp16 MFMA: C[i][j] += sum_k A[i][k] B[k][j].  Lane l supplies row
+// i = l % 16 of A and column j = l % 16 of B (8 k values each, the same k
+// slots in both), and holds C rows 4 * (l / 16) + 0..3 of column l % 16.
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 16x16x16 fp16 MFMA, 4 k values per lane, same row/column/C layout.
+__device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace ulspec

@@ -1,0 +1,883 @@
+// q4_gemm.hip -- K1, the verify dequant-GEMM: Y[M][N] = X[M][K] . W[N][K]^T
+// with W in GGUF Q4_0 / Q4_K blocks and X fp16, fp32 accumulation.
+//
+// The reference runs this as a separate fp32 dequantize pass plus a naive
+// GEMM (src/inference/inference_engine.cpp:532-570, orientation of
+// src/shaders/gemm/gemm_transposed_b_v2.glsl:23-29).  Here the weights are
+// read once, dequantized in registers and fed to 16x16x32 fp16 MFMAs.
+//
+// Device weight layout (re-tiled at upload, same 18 / 144 bytes per block):
+//   Tiles of 16 rows.  Lane l of a wave handles row r = l % 16 of the tile and
+//   k-group g = l / 16 (8 consecutive elements of each 32-element block or
+//   sub-block), so one 16-byte load per lane covers a 1 KB contiguous piece.
+//   Within each 32-bit word the eight 4-bit values of elements e0..e7 sit at
+//   nibble positions (e0,e2,e4,e6,e1,e3,e5,e7), so that masking with
+//   0x000F000F / 0x00F000F0 before and after one 8-bit shift yields fp16 pairs
+//   (e0,e1) (e2,e3) (e4,e5) (e6,e7) via the 0x6400 exponent trick.
+//   Q4_0 chunk (tile t, block quad c) = 1152 B:
+//     [0,1024)    lane l: 4 words (blocks 4c..4c+3) at l*16
+//     [1024,1152) fp16 d of row r, block 4c+j at r*8 + j*2
+//   Q4_K chunk (tile t, super-block s) = 2304 B:
+//     [0,2048)    step j (0..7) of lane l at (j/4)*1024 + l*16 + (j%4)*4; lane
+//                 group g covers qs bytes 32g..32g+31 (sub-blocks 2g, 2g+1);
+//                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
+//     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
+#include "hip_common.h"
+#include "ulspec_internal.h"
+
+#include <algorithm>
+
+using namespace ulspec;
+
+namespace {
+
+constexpr int kQ40Chunk = 1152;
+constexpr int kQ4KChunk = 2304;
+
+__device__ __forceinline__ uint32_t perm_nibbles(const uint32_t q[8])
+{
+    // nibble position p holds element (0,2,4,6,1,3,5,7)[p]
+    return q[0] | (q[2] << 4) | (q[4] << 8) | (q[6] << 12) | (q[1] << 16) | (q[3] << 20) | (q[5] << 24) |
+           (q[7] << 28);
+}
+
+__global__ void repack_q4_0_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
+                                   uint32_t nb, uint32_t nquads, uint64_t total)
+{
+    uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const uint32_t j = id & 3;
+    const uint32_t L = (id >> 2) & 63;
+    const uint64_t tc = id >> 8;  // t * nquads + c
+    const uint32_t c = (uint32_t)(tc % nquads);
+    const uint32_t t = (uint32_t)(tc / nquads);
+    const uint32_t r = L & 15, g = L >> 4;
+    const uint32_t n = 16 * t + r, b = 4 * c + j;
+    uint8_t* chunk = out + tc * kQ40Chunk;
+    uint32_t word = 0;
+    uint16_t d = 0;
+    if (n < N && b < nb) {
+        const uint8_t* blk = raw + ((uint64_t)n * nb + b) * 18;
+        uint32_t q[8];
+        for (int e = 0; e < 8; ++e) {
+            uint32_t el = 8 * g + e;
+            q[e] = el < 16 ? (blk[2 + el] & 15u) : (blk[2 + el - 16] >> 4);
+        }
+        word = perm_nibbles(q);
+        d = (uint16_t)(blk[0] | (blk[1] << 8));
+    }
+    *(uint32_t*)(chunk + L * 16 + j * 4) = word;
+    if (g == 0) *(uint16_t*)(chunk + 1024 + r * 8 + j * 2) = d;
+}
+
+__global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
+                                   uint32_t nsb, uint64_t total)
+{
+    uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const uint32_t j = id & 7;
+    const uint32_t L = (id >> 3) & 63;
+    const uint64_t ts = id >> 9;  // t * nsb + s
+    const uint32_t s = (uint32_t)(ts % nsb);
+    const uint32_t t = (uint32_t)(ts / nsb);
+    const uint32_t r = L & 15, g = L >> 4;
+    const uint32_t n = 16 * t + r;
+    uint8_t* chunk = out + ts * kQ4KChunk;
+    uint32_t word = 0;
+    const uint8_t* blk = n < N ? raw + ((uint64_t)n * nsb + s) * 144 : nullptr;
+    if (blk) {
+        const uint8_t* qs = blk + 16 + 32 * g + 8 * (j & 3);
+        uint32_t q[8];
+        for (int e = 0; e < 8; ++e) q[e] = j < 4 ? (qs[e] & 15u) : (qs[e] >> 4);
+        word = perm_nibbles(q);
+    }
+    *(uint32_t*)(chunk + (j >> 2) * 1024 + L * 16 + (j & 3) * 4) = word;
+    if (g == 0 && j == 0) {
+        uint32_t* dst = (uint32_t*)(chunk + 2048 + r * 16);
+        for (int w = 0; w < 4; ++w) {
+            uint32_t v = 0;
+            if (blk) v = blk[4 * w] | (blk[4 * w + 1] << 8) | (blk[4 * w + 2] << 16) | ((uint32_t)blk[4 * w + 3] << 24);
+            dst[w] = v;
+        }
+    }
+}
+
+// Compiler-only barrier: loads issued before it stay before it (they are not
+// sunk to their first use), so all of a batch's loads are in flight together.
+// The hardware still overlaps them; s_waitcnt is placed at each first use.
+__device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
+
+// Raw buffer loads: 32-bit offsets from a base held in scalar registers, and
+// the hardware returns 0 for offsets at or past num_records instead of
+// faulting.  0x00020000 is the gfx9-family dword-3 of the resource.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ uint2 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+__device__ __forceinline__ half8_t buf_load_h8(__amdgpu_buffer_rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(half8_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// (v & mask) | magic as one v_and_or_b32 (gfx9 VOP3 takes no two literals,
+// so the compiler would otherwise split it).
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t magic)
+{
+    uint32_t o;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(o) : "v"(v), "v"(mask), "v"(magic));
+    return o;
+}
+
+// Masks and the fp16 exponent magic, kept in VGPRs.
+struct NibbleConsts {
+    uint32_t lo, hi, magic;
+};
+
+__device__ __forceinline__ NibbleConsts nibble_consts()
+{
+    NibbleConsts k;
+    k.lo = 0x000F000Fu;
+    k.hi = 0x00F000F0u;
+    k.magic = 0x64006400u;
+    // keep them in registers across the loop
+    asm volatile("" : "+v"(k.lo), "+v"(k.hi), "+v"(k.magic));
+    return k;
+}
+
+// 8 nibbles in the tiled order -> fp16 (1024+q, 1024+16q, 1024+q, 1024+16q) pairs
+struct MagicPairs {
+    half2_t a, b, c, d;  // (e0,e1) q, (e2,e3) 16q, (e4,e5) q, (e6,e7) 16q
+};
+
+__device__ __forceinline__ MagicPairs magic_pairs(uint32_t v, const NibbleConsts& k)
+{
+    const uint32_t v8 = v >> 8;
+    MagicPairs m;
+    m.a = as_half2(and_or(v, k.lo, k.magic));
+    m.b = as_half2(and_or(v, k.hi, k.magic));
+    m.c = as_half2(and_or(v8, k.lo, k.magic));
+    m.d = as_half2(and_or(v8, k.hi, k.magic));
+    return m;
+}
+
+// Q4_0: (q - 8) exactly, elements e0..e7.
+__device__ __forceinline__ half8_t dequant_q4_0(uint32_t v, const NibbleConsts& k)
+{
+    MagicPairs m = magic_pairs(v, k);
+    const half2_t c1032 = splat2(-1032.0f), s16 = splat2(0.0625f), c72 = splat2(-72.0f);
+    half2_t a = m.a + c1032;
+    half2_t b = __builtin_elementwise_fma(m.b, s16, c72);
+    half2_t c = m.c + c1032;
+    half2_t d = __builtin_elementwise_fma(m.d, s16, c72);
+    return make_half8(a, b, c, d);
+}
+
+// Q4_K: q * sc exactly (q <= 15, sc <= 63 -> <= 945).
+struct SubScale {
+    half2_t sc, nsc1024, sc16, nsc64;
+};
+
+__device__ __forceinline__ half8_t dequant_q4_k(uint32_t v, const SubScale& s, const NibbleConsts& k)
+{
+    MagicPairs m = magic_pairs(v, k);
+    half2_t a = __builtin_elementwise_fma(m.a, s.sc, s.nsc1024);
+    half2_t b = __builtin_elementwise_fma(m.b, s.sc16, s.nsc64);
+    half2_t c = __builtin_elementwise_fma(m.c, s.sc, s.nsc1024);
+    half2_t d = __builtin_elementwise_fma(m.d, s.sc16, s.nsc64);
+    return make_half8(a, b, c, d);
+}
+
+// 6-bit scale / min of sub-block j (0..7) from the 12 packed bytes held in
+// words y (bytes 0-3), z (4-7), w (8-11); branch-free in j.
+__device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w, int j, uint32_t& sc, uint32_t& m)
+{
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t by = (y >> sh) & 255u, bz = (z >> sh) & 255u, bw = (w >> sh) & 255u;
+    const uint32_t sc_lo = by & 63u, m_lo = bz & 63u;
+    const uint32_t sc_hi = (bw & 15u) | ((by >> 6) << 4), m_hi = (bw >> 4) | ((bz >> 6) << 4);
+    const bool lo = j < 4;
+    sc = lo ? sc_lo : sc_hi;
+    m = lo ? m_lo : m_hi;
+}
+
+// ---- split-K kernels -------------------------------------------------------
+// Grid (row groups, K slices).  A workgroup of kWaves waves covers kWaves
+// 16-row tiles (one per wave) and one K slice of the weight.  Per batch of up
+// to CMAX chunks (Q4_0 block quads / Q4_K super-blocks) it
+//   1. issues the loads of its X slice (16-byte units, registers),
+//   2. issues every weight load of the batch (all waves, all chunks at once,
+//      so the CU holds its whole share of the weight stream in flight),
+//   3. writes X to LDS (waiting only for the older X loads), barrier,
+//   4. dequantizes in registers and runs the MFMAs, X read back from LDS.
+// Out-of-range chunks (past the slice or the last tile) use an offset past
+// the buffer: the load returns 0 and makes no memory request.  Each wave's
+// chunks are accumulated in K order; slices are summed in slice order by the
+// reduction kernel, so every output row is bitwise independent of M.
+constexpr int kWaves = 16;
+constexpr uint32_t kOOB = 0x80000000u;  // >= any buffer's num_records
+
+template <int MT>
+struct XStage {
+    static constexpr int kUnitsPerRow = 129;  // 128 units of 16 B + 1 pad (bank spread)
+    static constexpr int kRowsPerPass = kWaves * 64 / 128;
+    static constexpr int kXU = (16 * MT) / kRowsPerPass;  // passes = units per thread
+};
+
+// Load this batch's X slice (rows < M, units [0, U) of 16 B starting at
+// element k0, U <= 128) into registers: thread -> (row tid / 128 + pass *
+// rows-per-pass, unit tid % 128).  Units past K load 0.
+template <int MT>
+__device__ __forceinline__ void x_stage_load(__amdgpu_buffer_rsrc_t xr, uint4 (&xv)[XStage<MT>::kXU], int M, int K,
+                                             int k0, int U)
+{
+    const int uu = threadIdx.x & 127, m0 = threadIdx.x >> 7;
+    const int k = k0 + 8 * uu;
+#pragma unroll
+    for (int u = 0; u < XStage<MT>::kXU; ++u) {
+        const int m = m0 + u * XStage<MT>::kRowsPerPass;
+        const bool ok = m < M && uu < U && k < K;
+        xv[u] = buf_load16(xr, ok ? (uint32_t)(m * K + k) * 2u : kOOB);
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void x_stage_store(uint4* xs, const uint4 (&xv)[XStage<MT>::kXU], int M, int U)
+{
+    const int uu = threadIdx.x & 127, m0 = threadIdx.x >> 7;
+#pragma unroll
+    for (int u = 0; u < XStage<MT>::kXU; ++u) {
+        const int m = m0 + u * XStage<MT>::kRowsPerPass;
+        if (m < M && uu < U) xs[m * XStage<MT>::kUnitsPerRow + uu] = xv[u];
+    }
+}
+
+template <int MT>
+__device__ __forceinline__ void store_tile(const float4_t (&acc)[MT], float* __restrict__ out, int M, int N, int t)
+{
+    const int lane = threadIdx.x & 63;
+    const int n = 16 * t + (lane & 15);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = mt * 16 + 4 * (lane >> 4) + i;
+            if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][i];
+        }
+}
+
+struct GemmArgs {
+    const uint8_t* w;
+    uint32_t w_bytes;
+    const _Float16* x;
+    float* out;  // Y when ks_count == 1, else partials [ks_count][M][N]
+    int M, N, K, n_tiles, n_chunks, ks_count;
+    int ks_q, ks_r;  // n_chunks = ks_q * ks_count + ks_r; slice s starts at s * ks_q + min(s, ks_r)
+};
+
+__device__ __forceinline__ void slice_range(const GemmArgs& a, int ks, int& lo, int& hi)
+{
+    lo = ks * a.ks_q + min(ks, a.ks_r);
+    hi = lo + a.ks_q + (ks < a.ks_r ? 1 : 0);
+}
+
+template <int MT, int CMAX>
+__global__ __launch_bounds__(kWaves * 64) void gemm_q4_0_kernel(GemmArgs a)
+{
+    __shared__ uint4 xs[16 * MT * XStage<MT>::kUnitsPerRow];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x * kWaves + wave;
+    const bool tile_live = t < a.n_tiles;
+    const int ks = blockIdx.y;
+    int qa, qb;
+    slice_range(a, ks, qa, qb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
+    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + lane * 16;
+    const uint32_t s_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + 1024 + r * 8;
+    int xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + r, a.M - 1) * XStage<MT>::kUnitsPerRow;
+    const NibbleConsts nk = nibble_consts();
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+    float4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = zero4;
+
+    for (int c0 = qa; c0 < qb; c0 += CMAX) {
+        const int nc = min(CMAX, qb - c0);
+        uint4 xv[XStage<MT>::kXU];
+        x_stage_load<MT>(xr, xv, a.M, a.K, c0 * 128, 16 * nc);
+        pin_loads();
+        uint4 wq[CMAX];
+        uint2 sc[CMAX];
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+            const bool ok = tile_live && i < nc;
+            const uint32_t o = (uint32_t)(c0 + i) * kQ40Chunk;
+            wq[i] = buf_load16(wr, ok ? w_lane + o : kOOB);
+            sc[i] = buf_load8(wr, ok ? s_lane + o : kOOB);
+        }
+        pin_loads();
+        if (c0 != qa) __syncthreads();  // previous batch done reading xs
+        x_stage_store<MT>(xs, xv, a.M, 16 * nc);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+            if (i < nc) {
+                const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+                const uint32_t sw[2] = {sc[i].x, sc[i].y};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const half8_t B = dequant_q4_0(words[j], nk);
+                    const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 16 * i + 4 * j + g]);
+                        const float4_t pr = mfma16x16x32(A, B, zero4);
+                        acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
+                    }
+                }
+            }
+        }
+    }
+    if (tile_live) store_tile<MT>(acc, a.out + (size_t)ks * a.M * a.N, a.M, a.N, t);
+}
+
+template <int MT, int CMAX>
+__global__ __launch_bounds__(kWaves * 64) void gemm_q4_k_kernel(GemmArgs a)
+{
+    __shared__ uint4 xs[16 * MT * XStage<MT>::kUnitsPerRow];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x * kWaves + wave;
+    const bool tile_live = t < a.n_tiles;
+    const int ks = blockIdx.y;
+    int sa, sb;
+    slice_range(a, ks, sa, sb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
+    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + lane * 16;
+    const uint32_t h_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + 2048 + r * 16;
+    int xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + r, a.M - 1) * XStage<MT>::kUnitsPerRow + 8 * g;
+    const NibbleConsts nk = nibble_consts();
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+    float4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = zero4;
+
+    for (int s0 = sa; s0 < sb; s0 += CMAX) {
+        const int nc = min(CMAX, sb - s0);
+        uint4 xv[XStage<MT>::kXU];
+        x_stage_load<MT>(xr, xv, a.M, a.K, s0 * 256, 32 * nc);
+        pin_loads();
+        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+            const bool ok = tile_live && i < nc;
+            const uint32_t o = (uint32_t)(s0 + i) * kQ4KChunk;
+            w0[i] = buf_load16(wr, ok ? w_lane + o : kOOB);
+            w1[i] = buf_load16(wr, ok ? w_lane + o + 1024 : kOOB);
+            hd[i] = buf_load16(wr, ok ? h_lane + o : kOOB);
+        }
+        pin_loads();
+        if (s0 != sa) __syncthreads();
+        x_stage_store<MT>(xs, xv, a.M, 32 * nc);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+            if (i < nc) {
+                const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+                const uint4 h = hd[i];
+                const float d = half_bits_to_float(h.x & 0xffffu);
+                const float dmin = half_bits_to_float(h.x >> 16);
+                SubScale ss[2];
+                half8_t mins[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    uint32_t scv, mn;
+                    q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
+                    const float fs = (float)scv;
+                    ss[e].sc = splat2(fs);
+                    ss[e].nsc1024 = splat2(-1024.0f * fs);
+                    ss[e].sc16 = splat2(fs * 0.0625f);
+                    ss[e].nsc64 = splat2(-64.0f * fs);
+                    const _Float16 hm = (_Float16)(float)mn;
+                    mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
+                }
+                float4_t P1[MT], P2[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    P1[mt] = zero4;
+                    P2[mt] = zero4;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 32 * i + j]);
+                        P1[mt] = mfma16x16x32(A, B, P1[mt]);
+                        P2[mt] = mfma16x16x32(A, mins[j >> 2], P2[mt]);
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
+                    acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
+                }
+            }
+        }
+    }
+    if (tile_live) store_tile<MT>(acc, a.out + (size_t)ks * a.M * a.N, a.M, a.N, t);
+}
+
+// ---- whole-X kernels (small M) ---------------------------------------------
+// One workgroup per 16-row tile; wave p computes canonical part p of K (the
+// same parts as the split-K path, so results match it bit for bit).  The whole
+// X (M rows) is copied into LDS with direct buffer->LDS loads (no registers;
+// row pitch rounded up to 1 KB plus 16 B so a partial last load of a row only
+// touches its own padding, and rows fall on different banks), then every
+// weight load of the part is issued; the wait for X covers only the older
+// X copies.  Parts are summed in part order in LDS.
+constexpr int kParts = 16;
+
+__host__ __device__ constexpr uint32_t wide_pitch(uint32_t K)
+{
+    return ((2u * K + 1023u) / 1024u) * 1024u + 16u;
+}
+
+template <int NW>
+__device__ __forceinline__ void x_copy_to_lds(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes)
+{
+    // M rows x ipr 1 KB copies, spread over the NW waves.  Each workgroup
+    // starts at a different copy (rotation by blockIdx) so the CUs of an XCD,
+    // which all read the same X, do not queue on the same L2 channels.
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KU = a.K / 8;  // 16-byte units per row
+    const int ipr = (KU + 63) / 64;
+    const int total = a.M * ipr;
+    const uint32_t pitch = wide_pitch(a.K);
+    int idx = (int)((blockIdx.x * 7u + wave) % (uint32_t)total);
+    int m = idx / ipr, c = idx - (idx / ipr) * ipr;
+    const int step_m = NW / ipr, step_c = NW - (NW / ipr) * ipr;
+    for (int n = wave; n < total; n += NW) {
+        const int u = c * 64 + lane;
+        const uint32_t off = u < KU ? (uint32_t)(m * KU + u) * 16u : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(xs_bytes + m * pitch + c * 1024), 16, off, 0, 0, 0);
+        // advance by NW copies, wrapping around the M x ipr grid
+        c += step_c;
+        m += step_m;
+        if (c >= ipr) {
+            c -= ipr;
+            ++m;
+        }
+        while (m >= a.M) m -= a.M;
+    }
+}
+
+template <int CMAX>
+__device__ __forceinline__ void q4_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t s_lane, int c0,
+                                                int nc, uint4 (&wq)[CMAX], uint2 (&sc)[CMAX])
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        const uint32_t o = (uint32_t)(c0 + i) * kQ40Chunk;
+        wq[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
+        sc[i] = buf_load8(wr, i < nc ? s_lane + o : kOOB);
+    }
+}
+
+// acc += the batch's chunks; A rows come from LDS (unit index xrow + 4 * block).
+template <int CMAX>
+__device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&wq)[CMAX],
+                                               const uint2 (&sc)[CMAX], const NibbleConsts& nk, float4_t& acc)
+{
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        if (i < nc) {
+            const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+            const uint32_t sw[2] = {sc[i].x, sc[i].y};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half8_t B = dequant_q4_0(words[j], nk);
+                const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]);
+                const float4_t pr = mfma16x16x32(A, B, zero4);
+                acc = __builtin_elementwise_fma((float4_t)d, pr, acc);
+            }
+        }
+    }
+}
+
+// Parts summed in part order 0..kParts-1, then stored (rows < M, cols < N).
+__device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& acc, const GemmArgs& a, int t)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        const int row = threadIdx.x >> 6, l = threadIdx.x & 63;
+        float s = red[row * 64 + l];
+#pragma unroll
+        for (int p = 1; p < kParts; ++p) s += red[(p * 4 + row) * 64 + l];
+        const int m = 4 * (l >> 4) + row, n = 16 * t + (l & 15);
+        if (m < a.M && n < a.N) a.out[(size_t)m * a.N + n] = s;
+    }
+}
+
+template <int CMAX>
+__global__ __launch_bounds__(kParts * 64) void gemm_q4_0_wide_kernel(GemmArgs a)
+{
+    extern __shared__ uint4 xs[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x;
+    int qa, qb;
+    slice_range(a, wave, qa, qb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
+    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + lane * 16;
+    const uint32_t s_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + 1024 + r * 8;
+    const int xrow = min(r, a.M - 1) * (int)(wide_pitch(a.K) / 16) + g;
+    const NibbleConsts nk = nibble_consts();
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+
+    x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
+    pin_loads();
+    {  // first batch, straight-line: the X wait before the barrier covers only the X copies
+        uint4 wq[CMAX];
+        uint2 sc[CMAX];
+        const int nc = max(0, min(CMAX, qb - qa));
+        q4_0_load_batch<CMAX>(wr, w_lane, s_lane, qa, nc, wq, sc);
+        pin_loads();
+        __syncthreads();
+        q4_0_mma_batch<CMAX>(xs, xrow, qa, nc, wq, sc, nk, acc);
+    }
+    for (int c0 = qa + CMAX; c0 < qb; c0 += CMAX) {
+        uint4 wq[CMAX];
+        uint2 sc[CMAX];
+        const int nc = min(CMAX, qb - c0);
+        q4_0_load_batch<CMAX>(wr, w_lane, s_lane, c0, nc, wq, sc);
+        pin_loads();
+        q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, wq, sc, nk, acc);
+    }
+    sum_parts_and_store((float*)xs, acc, a, t);
+}
+
+template <int CMAX>
+__device__ __forceinline__ void q4_k_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t h_lane, int s0,
+                                                int nc, uint4 (&w0)[CMAX], uint4 (&w1)[CMAX], uint4 (&hd)[CMAX])
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        const uint32_t o = (uint32_t)(s0 + i) * kQ4KChunk;
+        w0[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
+        w1[i] = buf_load16(wr, i < nc ? w_lane + o + 1024 : kOOB);
+        hd[i] = buf_load16(wr, i < nc ? h_lane + o : kOOB);
+    }
+}
+
+// acc += the batch's super-blocks; A rows from LDS (unit xrow + 32 * sb + j).
+template <int CMAX>
+__device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, int xrow, int s0, int nc, const uint4 (&w0)[CMAX],
+                                               const uint4 (&w1)[CMAX], const uint4 (&hd)[CMAX], int g,
+                                               const NibbleConsts& nk, float4_t& acc)
+{
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        if (i < nc) {
+            const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+            const uint4 h = hd[i];
+            const float d = half_bits_to_float(h.x & 0xffffu);
+            const float dmin = half_bits_to_float(h.x >> 16);
+            SubScale ss[2];
+            half8_t mins[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                uint32_t scv, mn;
+                q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
+                const float fs = (float)scv;
+                ss[e].sc = splat2(fs);
+                ss[e].nsc1024 = splat2(-1024.0f * fs);
+                ss[e].sc16 = splat2(fs * 0.0625f);
+                ss[e].nsc64 = splat2(-64.0f * fs);
+                const _Float16 hm = (_Float16)(float)mn;
+                mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
+            }
+            float4_t P1 = zero4, P2 = zero4;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
+                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 32 * (s0 + i) + j]);
+                P1 = mfma16x16x32(A, B, P1);
+                P2 = mfma16x16x32(A, mins[j >> 2], P2);
+            }
+            acc = __builtin_elementwise_fma((float4_t)d, P1, acc);
+            acc = __builtin_elementwise_fma((float4_t)(-dmin), P2, acc);
+        }
+    }
+}
+
+template <int CMAX>
+__global__ __launch_bounds__(kParts * 64) void gemm_q4_k_wide_kernel(GemmArgs a)
+{
+    extern __shared__ uint4 xs[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x;
+    int sa, sb;
+    slice_range(a, wave, sa, sb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
+    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + lane * 16;
+    const uint32_t h_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + 2048 + r * 16;
+    const int xrow = min(r, a.M - 1) * (int)(wide_pitch(a.K) / 16) + 8 * g;
+    const NibbleConsts nk = nibble_consts();
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+
+    x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
+    pin_loads();
+    {
+        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
+        const int nc = max(0, min(CMAX, sb - sa));
+        q4_k_load_batch<CMAX>(wr, w_lane, h_lane, sa, nc, w0, w1, hd);
+        pin_loads();
+        __syncthreads();
+        q4_k_mma_batch<CMAX>(xs, xrow, sa, nc, w0, w1, hd, g, nk, acc);
+    }
+    for (int s0 = sa + CMAX; s0 < sb; s0 += CMAX) {
+        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
+        const int nc = min(CMAX, sb - s0);
+        q4_k_load_batch<CMAX>(wr, w_lane, h_lane, s0, nc, w0, w1, hd);
+        pin_loads();
+        q4_k_mma_batch<CMAX>(xs, xrow, s0, nc, w0, w1, hd, g, nk, acc);
+    }
+    sum_parts_and_store((float*)xs, acc, a, t);
+}
+
+// Y[i] = sum over slices in slice order (deterministic); all loads issued
+// before the first add.
+constexpr int kMaxSlices = 32;
+
+__global__ __launch_bounds__(256) void reduce_slices_kernel(const float* __restrict__ part, float* __restrict__ Y,
+                                                            int MN, int ks_count)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= MN) return;
+    float v[kMaxSlices];
+#pragma unroll
+    for (int k = 0; k < kMaxSlices; ++k) v[k] = k < ks_count ? part[(size_t)k * MN + i] : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (int k = 1; k < kMaxSlices; ++k)
+        if (k < ks_count) s += v[k];
+    Y[i] = s;
+}
+
+constexpr int kQ40CMax = 8;
+constexpr int kQ4KCMax = 4;
+
+template <int MT>
+void launch_mt(const Weight& w, const GemmArgs& a, hipStream_t st)
+{
+    const dim3 grid((w.n_tiles + kWaves - 1) / kWaves, w.ksplit);
+    if (w.type == ULSPEC_GGML_Q4_0)
+        hipLaunchKernelGGL((gemm_q4_0_kernel<MT, kQ40CMax>), grid, dim3(kWaves * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_q4_k_kernel<MT, (MT >= 3 ? 2 : kQ4KCMax)>), grid, dim3(kWaves * 64), 0, st, a);
+}
+
+}  // namespace
+
+namespace ulspec {
+
+// LDS available to one workgroup on gfx950.
+constexpr size_t kWideLdsMax = 160 * 1024;
+
+bool wide_fits(int M, uint32_t K)
+{
+    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax;
+}
+
+// Opt the whole-X kernels in to the full 160 KB of LDS.
+ulspec_status gemm_init(ulspec_ctx* ctx)
+{
+    hipError_t e = hipFuncSetAttribute((const void*)gemm_q4_0_wide_kernel<kQ40CMax>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax);
+    if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)gemm_q4_k_wide_kernel<kQ4KCMax>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
+    return ULSPEC_OK;
+}
+
+// K slices per weight: about one workgroup per CU in total.
+uint32_t choose_ksplit(uint32_t n_tiles, uint32_t n_chunks, int n_cu)
+{
+    const uint32_t groups = (n_tiles + kWaves - 1) / kWaves;
+    uint32_t ks = (uint32_t)((n_cu + groups / 2) / groups);
+    if (ks < 1) ks = 1;
+    if (ks > n_chunks) ks = n_chunks;
+    if (ks > (uint32_t)kMaxSlices) ks = kMaxSlices;
+    return ks;
+}
+
+size_t gemm_workspace_bytes(const Weight& w)
+{
+    return w.ksplit > 1 ? (size_t)w.ksplit * 64 * w.n * sizeof(float) : 0;
+}
+
+// Launch the GEMM for one weight; rows of X beyond 64 go in further launches.
+// Never allocates (the slice workspace is sized at upload).
+ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y)
+{
+    const _Float16* X = reinterpret_cast<const _Float16*>(x);
+    if (gemm_workspace_bytes(w) > ctx->ws_bytes)
+        return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
+    for (uint32_t m0 = 0; m0 < M; m0 += 64) {
+        const int mc = (int)std::min<uint32_t>(64, M - m0);
+        GemmArgs a;
+        a.w = w.dev;
+        a.w_bytes = (uint32_t)w.bytes;
+        a.x = X + (size_t)m0 * w.k;
+        a.out = w.ksplit > 1 ? (float*)ctx->ws : y + (size_t)m0 * w.n;
+        a.M = mc;
+        a.N = (int)w.n;
+        a.K = (int)w.k;
+        a.n_tiles = (int)w.n_tiles;
+        a.n_chunks = (int)w.n_chunks;
+        a.ks_count = (int)w.ksplit;
+        a.ks_q = (int)(w.n_chunks / w.ksplit);
+        a.ks_r = (int)(w.n_chunks % w.ksplit);
+        if (wide_fits(mc, w.k)) {
+            // whole X in LDS, canonical kParts parts, summed in the kernel
+            a.out = y + (size_t)m0 * w.n;
+            a.ks_count = kParts;
+            a.ks_q = (int)(w.n_chunks / kParts);
+            a.ks_r = (int)(w.n_chunks % kParts);
+            const size_t lds = std::max<size_t>((size_t)mc * wide_pitch(w.k), kParts * 4 * 64 * sizeof(float));
+            if (w.type == ULSPEC_GGML_Q4_0)
+                hipLaunchKernelGGL(gemm_q4_0_wide_kernel<kQ40CMax>, dim3(w.n_tiles), dim3(kParts * 64), lds,
+                                   ctx->stream, a);
+            else
+                hipLaunchKernelGGL(gemm_q4_k_wide_kernel<kQ4KCMax>, dim3(w.n_tiles), dim3(kParts * 64), lds,
+                                   ctx->stream, a);
+            continue;
+        }
+        switch ((mc + 15) / 16) {
+        case 1: launch_mt<1>(w, a, ctx->stream); break;
+        case 2: launch_mt<2>(w, a, ctx->stream); break;
+        case 3: launch_mt<3>(w, a, ctx->stream); break;
+        default: launch_mt<4>(w, a, ctx->stream); break;
+        }
+        if (w.ksplit > 1) {
+            const int MN = mc * (int)w.n;
+            hipLaunchKernelGGL(reduce_slices_kernel, dim3((MN + 255) / 256), dim3(256), 0, ctx->stream,
+                               (const float*)ctx->ws, y + (size_t)m0 * w.n, MN, (int)w.ksplit);
+        }
+    }
+    return check_launch(ctx, "verify_gemm launch");
+}
+
+}  // namespace ulspec
+
+extern "C" ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes,
+                                              uint32_t N, uint32_t K, uint32_t* out_id)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
+    const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
+    if (bs == 0) return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported", type);
+    if (N == 0 || K == 0 || K % bs) return fail(ctx, ULSPEC_EINVAL, "weight_upload: K=%u must be a positive multiple of %d", K, bs);
+    const size_t expect = (size_t)N * (K / bs) * ts;
+    if (nbytes != expect) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes given, %zu expected", nbytes, expect);
+    Weight w;
+    w.type = type;
+    w.n = N;
+    w.k = K;
+    w.n_tiles = (N + 15) / 16;
+    w.n_chunks = type == ULSPEC_GGML_Q4_0 ? (K / 32 + 3) / 4 : K / 256;
+    w.bytes = (size_t)w.n_tiles * w.n_chunks * (type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
+    if (w.bytes >= kOOB) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes exceeds the 2 GiB per-weight limit", w.bytes);
+    w.ksplit = choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipMalloc(&w.dev, w.bytes);
+    if (e != hipSuccess) return hip_fail(ctx, e, "weight_upload hipMalloc");
+    void* raw = nullptr;
+    ulspec_status st = workspace(ctx, std::max(nbytes, gemm_workspace_bytes(w)), &raw);
+    if (st != ULSPEC_OK) {
+        (void)hipFree(w.dev);
+        return st;
+    }
+    e = hipMemcpyAsync(raw, blocks, nbytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(w.dev);
+        return hip_fail(ctx, e, "weight_upload copy");
+    }
+    if (type == ULSPEC_GGML_Q4_0) {
+        const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
+        hipLaunchKernelGGL(repack_q4_0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const uint8_t*)raw, w.dev, N, K / 32, w.n_chunks, total);
+    } else {
+        const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 512;
+        hipLaunchKernelGGL(repack_q4_k_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const uint8_t*)raw, w.dev, N, w.n_chunks, total);
+    }
+    st = check_launch(ctx, "weight repack launch");
+    if (st == ULSPEC_OK) {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "weight_upload sync");
+    }
+    if (st != ULSPEC_OK) {
+        (void)hipFree(w.dev);
+        return st;
+    }
+    *out_id = (uint32_t)ctx->weights.size();
+    ctx->weights.push_back(w);
+    return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_weight_info(ulspec_ctx* ctx, uint32_t id, uint32_t* type, uint32_t* n, uint32_t* k,
+                                            size_t* bytes)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (id >= ctx->weights.size()) return fail(ctx, ULSPEC_EINVAL, "weight_info: no weight %u", id);
+    const Weight& w = ctx->weights[id];
+    if (type) *type = w.type;
+    if (n) *n = w.n;
+    if (k) *k = w.k;
+    if (bytes) *bytes = w.bytes;
+    return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_verify_gemm(ulspec_ctx* ctx, uint32_t id, const uint16_t* x, uint32_t M, float* y)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (id >= ctx->weights.size()) return fail(ctx, ULSPEC_EINVAL, "verify_gemm: no weight %u", id);
+    if (!x || !y) return fail(ctx, ULSPEC_EINVAL, "verify_gemm: null pointer");
+    if (M == 0) return fail(ctx, ULSPEC_EINVAL, "verify_gemm: M must be >= 1");
+    if (((uintptr_t)x & 15) != 0) return fail(ctx, ULSPEC_EINVAL, "verify_gemm: x must be 16-byte aligned");
+    (void)hipSetDevice(ctx->device);
+    return gemm_launch(ctx, ctx->weights[id], x, M, y);
+}

@@ -1,0 +1,88 @@
+// ulspec_internal.h -- context state shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/ulspec.h"
+
+namespace ulspec {
+
+// One uploaded linear weight, re-tiled for the dequant-GEMM kernels.
+struct Weight {
+    uint32_t type = 0;      // ULSPEC_GGML_Q4_0 / ULSPEC_GGML_Q4_K
+    uint32_t n = 0, k = 0;  // rows (N) and elements per row (K)
+    uint32_t n_tiles = 0;   // ceil(N / 16)
+    uint32_t n_chunks = 0;  // per tile: Q4_0 block quads, Q4_K super-blocks
+    uint32_t ksplit = 1;    // K slices of the split-K launch (fixed per weight)
+    size_t bytes = 0;
+    uint8_t* dev = nullptr;
+};
+
+}  // namespace ulspec
+
+struct ulspec_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int n_cu = 0;
+    std::string err;
+    std::vector<ulspec::Weight> weights;
+    // Reusable device workspace (grown on demand, freed with the context).
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // Host staging for weight uploads.
+    void* staging = nullptr;
+    size_t staging_bytes = 0;
+    // Captured graphs and timing events.
+    std::vector<hipGraphExec_t> graphs;
+    bool capturing = false;
+    hipEvent_t events[16] = {};
+};
+
+namespace ulspec {
+
+inline ulspec_status fail(ulspec_ctx* ctx, ulspec_status st, const char* fmt, ...)
+{
+    if (ctx) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof(buf), fmt, ap);
+        va_end(ap);
+        ctx->err = buf;
+    }
+    return st;
+}
+
+inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
+{
+    return fail(ctx, e == hipErrorOutOfMemory ? ULSPEC_ENOMEM : ULSPEC_EDEVICE, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+// One-time kernel attributes of the dequant-GEMM (called by ulspec_create).
+ulspec_status gemm_init(ulspec_ctx* ctx);
+
+// Grow the context workspace to at least `bytes` (stream-ordered reuse).
+ulspec_status workspace(ulspec_ctx* ctx, size_t bytes, void** out);
+
+// Launch-after checks: reports a failed launch as ULSPEC_EDEVICE.
+inline ulspec_status check_launch(ulspec_ctx* ctx, const char* what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(ctx, e, what);
+    return ULSPEC_OK;
+}
+
+}  // namespace ulspec
+
+#define ULSPEC_CHECK_CTX(ctx)                  \
+    do {                                       \
+        if (!(ctx)) return ULSPEC_EINVAL;      \
+        (ctx)->err.clear();                    \
+    } while (0)
