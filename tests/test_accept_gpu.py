@@ -1,0 +1,170 @@
+"""K3 acceptance sampling on the GPU against the oracle (through the C ABI).
+
+Bar: bit-exact.  Given the same logits, draft tokens and uniforms, the GPU
+must emit exactly the oracle's tokens and accepted counts (the decision
+arithmetic is exact fixed point, so no tolerance applies).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _logits(rng, shape, boost=8.0):
+    """N(0, 3^2) with one random +boost token per row."""
+    x = (rng.standard_normal(shape) * 3.0).astype(np.float32)
+    flat = x.reshape(-1, shape[-1])
+    flat[np.arange(flat.shape[0]), rng.integers(0, shape[-1], flat.shape[0])] += boost
+    return x
+
+
+def _draft_tokens(ora, s, dl, seed):
+    B, k, V = dl.shape
+    if s.greedy:
+        return dl.reshape(B * k, V).argmax(axis=1).astype(np.int32).reshape(B, k)
+    u = ora.uniforms(seed, 0, B * k)
+    return ora.sample(s, dl.reshape(B * k, V), u).reshape(B, k)
+
+
+def _run_gpu(ctx, s, tl, dl, dt, u):
+    B, k1, V = tl.shape
+    k = k1 - 1
+    bt = ctx.upload(tl)
+    bd = ctx.upload(dl) if dl is not None else None
+    bx = ctx.upload(dt.astype(np.int32))
+    bu = ctx.upload(u.astype(np.float32)) if u is not None else None
+    bo = ctx.alloc(B * (k + 1) * 4)
+    bn = ctx.alloc(B * 4)
+    ctx.accept(s, B, k, V, bt, bd, bx, bu, bo, bn)
+    out = ctx.download(bo, np.int32, (B, k + 1))
+    nacc = ctx.download(bn, np.int32, (B,))
+    for b in (bt, bd, bx, bu, bo, bn):
+        if b is not None:
+            b.free()
+    return out, nacc
+
+
+def _check(ctx, ora, pkg, s, tl, dl, dt, u):
+    out, nacc = _run_gpu(ctx, s, tl, dl, dt, u)
+    ref_out, ref_nacc = ora.accept(s, tl, dl, dt, u)
+    assert np.array_equal(nacc, ref_nacc), (nacc, ref_nacc)
+    assert np.array_equal(out, ref_out)
+    return nacc
+
+
+@pytest.mark.parametrize("k", [4, 8])
+@pytest.mark.parametrize("V", [32000, 128256])
+def test_accept_config_sampling_topk_topp(ctx, ora, pkg, rng, k, V):
+    B = 16
+    s = pkg.sampling(0.8, top_k=40, top_p=0.9)
+    so = ora.sampling(0.8, top_k=40, top_p=0.9)
+    tl = _logits(rng, (B, k + 1, V))
+    dl = tl[:, :k] * 0.7 + _logits(rng, (B, k, V)) * 0.5  # correlated draft
+    dl = dl.astype(np.float32)
+    dt = _draft_tokens(ora, so, dl, 5)
+    u = rng.random((B, k + 1)).astype(np.float32)
+    nacc = _check(ctx, ora, pkg, s, tl, dl, dt, u)
+    print(f"k={k} V={V} mean accepted {nacc.mean():.2f}")
+
+
+@pytest.mark.parametrize("k", [4, 8])
+@pytest.mark.parametrize("V", [32000, 128256])
+def test_accept_config_greedy(ctx, ora, pkg, rng, k, V):
+    B = 16
+    s, so = pkg.sampling(greedy=True), ora.sampling(greedy=True)
+    tl = _logits(rng, (B, k + 1, V))
+    dt = tl[:, :k].argmax(axis=2).astype(np.int32)
+    # break the chain at random positions
+    cut = rng.integers(0, k + 1, B)
+    for b in range(B):
+        if cut[b] < k:
+            dt[b, cut[b]] = (dt[b, cut[b]] + 1) % V
+    nacc = _check(ctx, ora, pkg, s, tl, None, dt, None)
+    assert np.array_equal(nacc, np.minimum(cut, k))
+
+
+def test_accept_full_vocabulary(ctx, ora, pkg, rng):
+    B, k, V = 6, 4, 32000
+    s, so = pkg.sampling(0.8), ora.sampling(0.8)
+    tl = _logits(rng, (B, k + 1, V), boost=2.0)
+    dl = (tl[:, :k] + rng.standard_normal((B, k, V)).astype(np.float32)).astype(np.float32)
+    dt = _draft_tokens(ora, so, dl, 9)
+    for trial in range(4):
+        u = rng.random((B, k + 1)).astype(np.float32)
+        _check(ctx, ora, pkg, s, tl, dl, dt, u)
+
+
+def test_accept_edge_cases(ctx, ora, pkg, rng):
+    # ties (every logit equal -> exact fallback of the top-k selection),
+    # top_k >= V (full), top_k = 1, tiny top_p, k = 1 and k = 16, small V,
+    # out-of-range draft tokens, draft token with zero draft mass
+    cases = [
+        dict(V=3000, k=3, s=(1.0, 40, 0.9), tie=True),
+        dict(V=40, k=2, s=(0.8, 40, 1.0)),
+        dict(V=5, k=1, s=(1.3, 0, 1.0)),
+        dict(V=1000, k=16, s=(0.5, 1, 1.0)),
+        dict(V=1000, k=5, s=(2.0, 200, 0.01)),
+        dict(V=50000, k=6, s=(0.8, 256, 0.95)),
+    ]
+    for c in cases:
+        V, k = c["V"], c["k"]
+        B = 4
+        T, tk, tp = c["s"]
+        s, so = pkg.sampling(T, top_k=tk, top_p=tp), ora.sampling(T, top_k=tk, top_p=tp)
+        tl = _logits(rng, (B, k + 1, V), boost=1.0)
+        dl = _logits(rng, (B, k, V), boost=1.0)
+        if c.get("tie"):
+            tl[0] = 1.5
+            dl[0] = 1.5
+            tl[1, :, ::2] = 0.0
+            tl[1, :, 1::2] = -0.0
+        dt = _draft_tokens(ora, so, dl, 3)
+        dt[2, 0] = V + 7          # out of range: never accepted
+        dl[3, 0, :] = -60.0
+        dl[3, 0, int(dt[3, 0])] = -1000.0  # zero draft mass at the drafted token
+        u = rng.random((B, k + 1)).astype(np.float32)
+        u[0, 0] = 0.0
+        u[1, -1] = np.float32(1.0 - 2 ** -24)
+        nacc = _check(ctx, ora, pkg, s, tl, dl, dt, u)
+        assert nacc[2] == 0
+
+
+def test_sample_matches_oracle(ctx, ora, pkg, rng):
+    for (T, tk, tp, greedy), V in [((0.8, 40, 0.9, False), 32000), ((1.0, 0, 1.0, False), 32000),
+                                   ((1.0, 0, 1.0, True), 128256), ((0.7, 5, 1.0, False), 7)]:
+        R = 24
+        s, so = pkg.sampling(T, top_k=tk, top_p=tp, greedy=greedy), ora.sampling(T, top_k=tk, top_p=tp, greedy=greedy)
+        logits = _logits(rng, (R, V), boost=3.0)
+        u = ora.uniforms(77, 0, R)
+        bl, bu, bo = ctx.upload(logits), ctx.upload(u), ctx.alloc(R * 4)
+        ctx.sample(s, R, V, bl, bu, bo)
+        got = ctx.download(bo, np.int32, (R,))
+        assert np.array_equal(got, ora.sample(so, logits, u))
+        for b in (bl, bu, bo):
+            b.free()
+
+
+def test_uniforms_match_oracle(ctx, ora):
+    n = 100003
+    b = ctx.alloc(n * 4)
+    ctx.uniforms(0xC0FFEE, 123456789, n, b)
+    got = ctx.download(b, np.float32, (n,))
+    assert np.array_equal(got.view(np.uint32), ora.uniforms(0xC0FFEE, 123456789, n).view(np.uint32))
+    b.free()
+
+
+def test_accept_argument_errors(ctx, pkg):
+    b = ctx.alloc(1024)
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.accept(pkg.sampling(0.0), 1, 1, 10, b, b, b, b, b, b)
+    assert e.value.status == pkg.EINVAL
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.accept(pkg.sampling(1.0), 1, 17, 10, b, b, b, b, b, b)
+    assert e.value.status == pkg.EINVAL
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.accept(pkg.sampling(1.0, top_k=300), 1, 1, 1000, b, b, b, b, b, b)
+    assert e.value.status == pkg.EUNSUPPORTED
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.accept(pkg.sampling(1.0, top_p=0.9), 1, 1, 1000, b, b, b, b, b, b)
+    assert e.value.status == pkg.EUNSUPPORTED
+    b.free()

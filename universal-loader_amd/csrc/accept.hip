@@ -1,0 +1,587 @@
+// accept.hip -- K3, acceptance sampling of k drafted tokens, and sampling of
+// one token per row.
+//
+// Replaces SpeculativeDecoder::verify_speculation (first-match of token ids,
+// src/inference/speculative_decoder.cpp:89-110) with the speculative-sampling
+// rule (Leviathan, Kalman & Matias, ICML 2023, Alg. 1), and
+// InferenceEngine::sample_token (src/inference/inference_engine.cpp:340-367)
+// with seeded uniforms; its inverse-CDF convention (strict "<" on the running
+// sum, fall back to the last index) is kept.
+//
+// Every decision uses exact arithmetic so that any reduction order gives the
+// same tokens:
+//   warp of a row: lmax = max l; e_i = det_expf((l_i - lmax) * invT) for the
+//   kept tokens (all, or the top_k by (logit desc, index asc)); fixed point
+//   E_i = trunc(e_i * 2^S), S = 63 - bitlen(V); Z = sum E_i in uint64 (exact,
+//   order-free); top_p keeps the shortest (logit desc, index asc) prefix with
+//   (double)cum >= (double)top_p * (double)Z.
+//   accept x iff ((double)u * Q_x) * Zp < (double)P_x * Zq  (u q(x) < p(x)).
+//   residual R_j = trunc(ldexp(max(0, P_j Zq - Q_j Zp), 62 - bitlen(Zp) -
+//   bitlen(Zq))) in double; draw T = trunc(u * Z), first j with T < cumsum.
+//
+// Two kernels: row_stats (one 1024-thread workgroup per logit row: max and
+// argmax, exact top-k, E, Z, top-p; kept tokens stored sorted by index) and
+// decide (one workgroup per sequence: the accept walk, the residual or bonus
+// draw).  The logits are read from HBM once by row_stats; decide touches them
+// again only in full-vocabulary mode (no top_k), for the drawn row.
+#include "detmath.h"
+#include "hip_common.h"
+#include "ulspec_internal.h"
+
+using namespace ulspec;
+
+namespace {
+
+constexpr int kKMax = 256;       // largest supported top_k
+constexpr int kCandMax = 2048;   // candidate buffer of the fast top-k path
+constexpr int kRowThreads = 1024;
+constexpr int kSeqThreads = 256;
+
+struct RowStat {
+    uint64_t Z;
+    float lmax;
+    int32_t argmax;
+    int32_t nk;  // kept tokens; == V in full-vocabulary mode (list unused)
+    int32_t pad;
+    int32_t idx[kKMax];  // kept token ids, ascending
+    uint64_t E[kKMax];
+};
+
+struct WarpParams {
+    float invT;
+    uint32_t top_k;  // 0: full vocabulary
+    float top_p;
+    int32_t greedy;
+    float scale;     // 2^S
+    int32_t pad;
+};
+
+// ---- workgroup reductions (all threads call, all get the result) -----------
+template <int NT>
+__device__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    uint64_t r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; ++w) r = scratch[w] > r ? scratch[w] : r;
+    return r;
+}
+
+template <int NT>
+__device__ uint64_t block_sum_u64(uint64_t v, uint64_t* scratch)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    uint64_t r = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) r += scratch[w];
+    return r;
+}
+
+// Exclusive prefix sum over the workgroup (thread order); returns the total.
+template <int NT>
+__device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t& excl, uint64_t* scratch)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint64_t incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t w = __shfl_up(incl, o);
+        if (lane >= o) incl += w;
+    }
+    __syncthreads();
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    uint64_t before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        if (w < wave) before += scratch[w];
+        total += scratch[w];
+    }
+    excl = before + incl - v;
+    return total;
+}
+
+// Bitonic sort of n (power of two) u64 keys in LDS, descending.
+__device__ void bitonic_desc(uint64_t* a, int n)
+{
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < n; i += blockDim.x) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const uint64_t x = a[i], y = a[j];
+                    if (desc ? (x < y) : (x > y)) {
+                        a[i] = y;
+                        a[j] = x;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// (key desc, index asc) as one descending u64
+__device__ __forceinline__ uint64_t order_key(uint32_t key, uint32_t idx)
+{
+    return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
+}
+
+__device__ __forceinline__ uint64_t fixed_e(float l, float lmax, const WarpParams& p)
+{
+    const float e = det_expf((l - lmax) * p.invT);
+    return (uint64_t)(e * p.scale);
+}
+
+// ---- row statistics ----------------------------------------------------------
+__global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __restrict__ logits, uint32_t V,
+                                                                WarpParams p, RowStat* __restrict__ stats)
+{
+    __shared__ uint64_t red[kRowThreads / 64];
+    __shared__ uint64_t buf[kCandMax];  // thread maxima, then candidates
+    __shared__ uint32_t cand_count;
+    __shared__ uint64_t keptE[kKMax];
+    const int tid = threadIdx.x;
+    const float* row = logits + (size_t)blockIdx.x * V;
+    RowStat* st = stats + blockIdx.x;
+
+    // pass 1: max key with the lowest index (argmax), per-thread max key
+    uint64_t best = 0;
+    for (uint32_t i = tid; i < V; i += kRowThreads) {
+        const uint64_t o = order_key(float_key(row[i]), i);
+        best = o > best ? o : best;
+    }
+    const uint64_t top = block_max_u64<kRowThreads>(best, red);
+    const uint32_t top_key = (uint32_t)(top >> 32);
+    const float lmax = key_float(top_key);
+    if (tid == 0) {
+        st->lmax = lmax;
+        st->argmax = (int32_t)(0xffffffffu - (uint32_t)top);
+    }
+    if (p.greedy) return;
+
+    const bool topk = p.top_k > 0 && p.top_k < V;
+    if (!topk) {  // full vocabulary: Z over every token
+        uint64_t z = 0;
+        for (uint32_t i = tid; i < V; i += kRowThreads) z += fixed_e(row[i], lmax, p);
+        z = block_sum_u64<kRowThreads>(z, red);
+        if (tid == 0) {
+            st->Z = z;
+            st->nk = (int32_t)V;
+        }
+        return;
+    }
+    const uint32_t k = p.top_k;
+
+    // fast path: the k-th largest per-thread maximum is <= the k-th largest
+    // logit, so the tokens with key >= it include the top k
+    buf[tid] = best >> 32;  // per-thread max key (0 if the thread has no token)
+    bitonic_desc(buf, kRowThreads);
+    const uint32_t t0 = (uint32_t)buf[k - 1];
+    if (tid == 0) cand_count = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < V; i += kRowThreads) {
+        const uint32_t key = float_key(row[i]);
+        if (key >= t0) {
+            const uint32_t slot = atomicAdd(&cand_count, 1u);
+            if (slot < kCandMax) buf[slot] = order_key(key, i);
+        }
+    }
+    __syncthreads();
+    const uint32_t nc = cand_count;
+    __syncthreads();
+    if (nc <= kCandMax) {
+        int n2 = 1;
+        while (n2 < (int)nc) n2 <<= 1;
+        for (int i = tid; i < n2; i += kRowThreads)
+            if (i >= (int)nc) buf[i] = 0;  // sorts last
+        bitonic_desc(buf, n2);
+    } else {
+        // exact fallback for heavily tied rows: k-th largest key by bisection
+        // on counts, then ties at that key taken by lowest index
+        uint32_t lo = 0, hi = 0xffffffffu;
+        while (lo < hi) {
+            const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+            uint64_t c = 0;
+            for (uint32_t i = tid; i < V; i += kRowThreads) c += float_key(row[i]) >= mid;
+            c = block_sum_u64<kRowThreads>(c, red);
+            if (c >= k) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint32_t kt = lo;
+        if (tid == 0) cand_count = 0;
+        __syncthreads();
+        for (uint32_t i = tid; i < V; i += kRowThreads) {
+            const uint32_t key = float_key(row[i]);
+            if (key > kt) buf[atomicAdd(&cand_count, 1u)] = order_key(key, i);  // < k of them
+        }
+        __syncthreads();
+        const uint32_t ngt = cand_count;
+        const uint32_t need = k - ngt;
+        // ties in index order: thread t owns the contiguous chunk [t*C, (t+1)*C)
+        const uint32_t C = (V + kRowThreads - 1) / kRowThreads;
+        const uint32_t c0 = tid * C, c1 = min(V, c0 + C);
+        uint64_t mine = 0;
+        for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == kt;
+        uint64_t rank = 0;
+        block_exclusive_scan_u64<kRowThreads>(mine, rank, red);
+        for (uint32_t i = c0; i < c1 && rank < need; ++i)
+            if (float_key(row[i]) == kt) {
+                buf[ngt + rank] = order_key(kt, i);
+                ++rank;
+            }
+        __syncthreads();
+        for (int i = tid; i < kKMax; i += kRowThreads)
+            if (i >= (int)k) buf[i] = 0;
+        bitonic_desc(buf, kKMax);
+    }
+    // buf[0..k) = the kept tokens by (logit desc, index asc)
+    for (uint32_t t = tid; t < k; t += kRowThreads) {
+        const uint32_t key = (uint32_t)(buf[t] >> 32);
+        keptE[t] = fixed_e(key_float(key), lmax, p);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t z = 0;
+        for (uint32_t t = 0; t < k; ++t) z += keptE[t];
+        uint32_t nk = k;
+        if (p.top_p < 1.0f) {
+            const double thr = (double)p.top_p * (double)z;
+            uint64_t c = 0;
+            uint32_t t = 0;
+            for (; t < k; ++t) {
+                c += keptE[t];
+                if ((double)c >= thr) {
+                    ++t;
+                    break;
+                }
+            }
+            nk = t;
+            z = c;
+        }
+        st->Z = z;
+        st->nk = (int32_t)nk;
+        cand_count = nk;
+    }
+    __syncthreads();
+    const uint32_t nk = cand_count;
+    // re-sort the kept tokens by index (ascending) and store them
+    for (int t = tid; t < kKMax; t += kRowThreads)
+        buf[t] = t < (int)nk ? (((uint64_t)(0xffffffffu - (uint32_t)buf[t])) << 32 | (uint32_t)t) : 0;
+    // buf now: (index << 32 | position), positions index keptE; sort ascending by index
+    for (int t = tid; t < kKMax; t += kRowThreads)
+        if (t < (int)nk) buf[t] = ~buf[t];  // descending sort of ~x = ascending of x
+    bitonic_desc(buf, kKMax);
+    for (int t = tid; t < (int)nk; t += kRowThreads) {
+        const uint64_t v = ~buf[t];
+        st->idx[t] = (int32_t)(v >> 32);
+        st->E[t] = keptE[(uint32_t)v];
+    }
+}
+
+// ---- decisions -----------------------------------------------------------------
+// weight of token x in a row's warp (0 if not kept)
+__device__ uint64_t weight_of(const RowStat& st, const float* row, uint32_t V, bool topk, int32_t x,
+                              const WarpParams& p)
+{
+    if (x < 0 || (uint32_t)x >= V) return 0;
+    if (!topk) return fixed_e(row[x], st.lmax, p);
+    int lo = 0, hi = st.nk - 1;
+    while (lo <= hi) {
+        const int mid = (lo + hi) >> 1;
+        const int32_t v = st.idx[mid];
+        if (v == x) return st.E[mid];
+        if (v < x) lo = mid + 1;
+        else hi = mid - 1;
+    }
+    return 0;
+}
+
+// Full-vocabulary inverse-CDF draw of a per-token weight w(j) (j in [0, V)):
+// T = trunc(u * total), first j with T < cumsum, else the last j with w > 0.
+// Thread t owns the contiguous chunk [t*C, (t+1)*C) so the prefix is in index order.
+template <typename WFn>
+__device__ int32_t block_cdf_pick(uint32_t V, float u, WFn w, uint64_t* scratch, int32_t* pick)
+{
+    const int tid = threadIdx.x;
+    const uint32_t C = (V + kSeqThreads - 1) / kSeqThreads;
+    const uint32_t c0 = min(V, (uint32_t)tid * C), c1 = min(V, c0 + C);
+    uint64_t mine = 0;
+    int32_t last = -1;
+    for (uint32_t j = c0; j < c1; ++j) {
+        const uint64_t x = w(j);
+        mine += x;
+        if (x) last = (int32_t)j;
+    }
+    uint64_t before = 0;
+    const uint64_t total = block_exclusive_scan_u64<kSeqThreads>(mine, before, scratch);
+    const uint64_t T = (uint64_t)((double)u * (double)total);
+    if (tid == 0) *pick = -1;
+    __syncthreads();
+    if (T >= before && T < before + mine) {
+        uint64_t c = before;
+        for (uint32_t j = c0; j < c1; ++j) {
+            c += w(j);
+            if (T < c) {
+                *pick = (int32_t)j;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    int32_t r = *pick;
+    if (r < 0) {  // T >= total (rounding): the last token with nonzero weight
+        const uint64_t lastp = block_max_u64<kSeqThreads>((uint64_t)(int64_t)(last + 1), scratch);
+        r = lastp ? (int32_t)lastp - 1 : (int32_t)V - 1;
+    }
+    __syncthreads();
+    return r;
+}
+
+// Inverse-CDF draw over a kept list (index order).
+__device__ int32_t list_cdf_pick(const int32_t* idx, const uint64_t* W, int n, uint64_t Z, float u, uint32_t V)
+{
+    const uint64_t T = (uint64_t)((double)u * (double)Z);
+    uint64_t c = 0;
+    int32_t last = -1;
+    for (int t = 0; t < n; ++t) {
+        if (!W[t]) continue;
+        c += W[t];
+        last = idx[t];
+        if (T < c) return idx[t];
+    }
+    return last < 0 ? (int32_t)V - 1 : last;
+}
+
+// Draw from a row's warp with uniform u (all threads return the token).
+__device__ int32_t draw_row(const RowStat& st, const float* row, uint32_t V, bool topk, float u, const WarpParams& p,
+                            uint64_t* scratch, int32_t* pick)
+{
+    if (topk) return list_cdf_pick(st.idx, st.E, st.nk, st.Z, u, V);
+    const float lmax = st.lmax;
+    return block_cdf_pick(V, u, [&](uint32_t j) { return fixed_e(row[j], lmax, p); }, scratch, pick);
+}
+
+__device__ __forceinline__ uint64_t residual_weight(uint64_t P, uint64_t Q, uint64_t Zp, uint64_t Zq, int sh)
+{
+    const double a = (double)P * (double)Zq;
+    const double c = (double)Q * (double)Zp;
+    const double r = a - c;
+    return r > 0.0 ? (uint64_t)__builtin_ldexp(r, sh) : 0;
+}
+
+__global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __restrict__ stats,
+                                                             const float* __restrict__ tl,
+                                                             const float* __restrict__ dl,
+                                                             const int32_t* __restrict__ draft_tokens,
+                                                             const float* __restrict__ uniforms, uint32_t k,
+                                                             uint32_t V, WarpParams p, int32_t* __restrict__ out,
+                                                             int32_t* __restrict__ nacc)
+{
+    __shared__ uint64_t scratch[kSeqThreads / 64];
+    __shared__ int32_t pick;
+    __shared__ int32_t uidx[2 * kKMax];
+    __shared__ uint64_t uR[2 * kKMax];
+    const int tid = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    const RowStat* ts = stats + (size_t)b * (k + 1);          // target rows
+    const RowStat* ds = stats + (size_t)gridDim.x * (k + 1) + (size_t)b * k;  // draft rows
+    const int32_t* x = draft_tokens + (size_t)b * k;
+    const float* u = p.greedy ? nullptr : uniforms + (size_t)b * (k + 1);
+    int32_t* o = out + (size_t)b * (k + 1);
+    const bool topk = p.top_k > 0 && p.top_k < V;
+
+    for (uint32_t i = tid; i <= k; i += kSeqThreads) o[i] = -1;
+    __syncthreads();
+    for (uint32_t i = 0; i < k; ++i) {
+        const int32_t xi = x[i];
+        if (p.greedy) {
+            const int32_t a = ts[i].argmax;
+            if (tid == 0) o[i] = a;
+            if (a != xi) {
+                if (tid == 0) nacc[b] = (int32_t)i;
+                return;
+            }
+            continue;
+        }
+        const float* trow = tl + ((size_t)b * (k + 1) + i) * V;
+        const float* drow = dl + ((size_t)b * k + i) * V;
+        const uint64_t Zp = ts[i].Z, Zq = ds[i].Z;
+        const uint64_t Px = weight_of(ts[i], trow, V, topk, xi, p);
+        const uint64_t Qx = weight_of(ds[i], drow, V, topk, xi, p);
+        const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
+        const double rhs = (double)Px * (double)Zq;
+        if (lhs < rhs) {
+            if (tid == 0) o[i] = xi;
+            continue;
+        }
+        // first rejection: draw from max(0, p - q) with u[k]
+        const int sh = 62 - bitlen64(Zp) - bitlen64(Zq);
+        int32_t tok;
+        if (topk) {
+            if (tid == 0) {
+                const RowStat& A = ts[i];
+                const RowStat& B = ds[i];
+                int ia = 0, ib = 0, n = 0;
+                uint64_t SR = 0;
+                while (ia < A.nk || ib < B.nk) {
+                    const int32_t ja = ia < A.nk ? A.idx[ia] : 0x7fffffff;
+                    const int32_t jb = ib < B.nk ? B.idx[ib] : 0x7fffffff;
+                    const int32_t j = ja < jb ? ja : jb;
+                    const uint64_t P = ja == j ? A.E[ia++] : 0;
+                    const uint64_t Q = jb == j ? B.E[ib++] : 0;
+                    const uint64_t R = residual_weight(P, Q, Zp, Zq, sh);
+                    uidx[n] = j;
+                    uR[n] = R;
+                    SR += R;
+                    ++n;
+                }
+                pick = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(A.idx, A.E, A.nk, Zp, u[k], V);
+            }
+            __syncthreads();
+            tok = pick;
+        } else {
+            const float lpm = ts[i].lmax, lqm = ds[i].lmax;
+            auto rw = [&](uint32_t j) {
+                return residual_weight(fixed_e(trow[j], lpm, p), fixed_e(drow[j], lqm, p), Zp, Zq, sh);
+            };
+            // total residual first (an all-zero residual draws from p)
+            uint64_t mine = 0;
+            for (uint32_t j = tid; j < V; j += kSeqThreads) mine += rw(j);
+            const uint64_t SR = block_sum_u64<kSeqThreads>(mine, scratch);
+            if (SR) tok = block_cdf_pick(V, u[k], rw, scratch, &pick);
+            else tok = draw_row(ts[i], trow, V, false, u[k], p, scratch, &pick);
+        }
+        if (tid == 0) {
+            o[i] = tok;
+            nacc[b] = (int32_t)i;
+        }
+        return;
+    }
+    // every draft accepted: bonus token from the target row k
+    int32_t tok;
+    if (p.greedy) tok = ts[k].argmax;
+    else tok = draw_row(ts[k], tl + ((size_t)b * (k + 1) + k) * V, V, topk, u[k], p, scratch, &pick);
+    if (tid == 0) {
+        o[k] = tok;
+        nacc[b] = (int32_t)k;
+    }
+}
+
+__global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __restrict__ stats,
+                                                             const float* __restrict__ logits,
+                                                             const float* __restrict__ uniforms, uint32_t V,
+                                                             WarpParams p, int32_t* __restrict__ out)
+{
+    __shared__ uint64_t scratch[kSeqThreads / 64];
+    __shared__ int32_t pick;
+    const uint32_t r = blockIdx.x;
+    int32_t tok;
+    if (p.greedy) tok = stats[r].argmax;
+    else
+        tok = draw_row(stats[r], logits + (size_t)r * V, V, p.top_k > 0 && p.top_k < V, uniforms[r], p, scratch,
+                       &pick);
+    if (threadIdx.x == 0) out[r] = tok;
+}
+
+__global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = counter_uniform(seed, idx0 + i);
+}
+
+ulspec_status make_params(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t V, WarpParams& p)
+{
+    if (!s) return fail(ctx, ULSPEC_EINVAL, "sampling parameters are null");
+    p.greedy = s->greedy != 0;
+    p.top_k = s->top_k;
+    p.top_p = s->top_p;
+    p.invT = 1.0f;
+    p.scale = __builtin_ldexpf(1.0f, warp_shift(V));
+    p.pad = 0;
+    if (p.greedy) return ULSPEC_OK;
+    if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
+        return fail(ctx, ULSPEC_EINVAL, "temperature must be positive and finite (got %g)", (double)s->temperature);
+    if (!(s->top_p == s->top_p)) return fail(ctx, ULSPEC_EINVAL, "top_p is NaN");
+    if (s->top_k > (uint32_t)kKMax && s->top_k < V)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "top_k %u > %d", s->top_k, kKMax);
+    if ((s->top_k == 0 || s->top_k >= V) && s->top_p < 1.0f)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "top_p without top_k (a sort of the whole vocabulary)");
+    p.invT = 1.0f / s->temperature;
+    return ULSPEC_OK;
+}
+
+}  // namespace
+
+extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
+                                       uint32_t V, const float* target_logits, const float* draft_logits,
+                                       const int32_t* draft_tokens, const float* uniforms, int32_t* out_tokens,
+                                       int32_t* out_n_accepted)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    WarpParams p;
+    ulspec_status st = make_params(ctx, s, V, p);
+    if (st != ULSPEC_OK) return st;
+    if (B == 0 || k == 0 || k > 16 || V == 0)
+        return fail(ctx, ULSPEC_EINVAL, "accept: need B >= 1, 1 <= k <= 16, V >= 1 (B=%u k=%u V=%u)", B, k, V);
+    if (!target_logits || !draft_tokens || !out_tokens || !out_n_accepted)
+        return fail(ctx, ULSPEC_EINVAL, "accept: null device pointer");
+    if (!p.greedy && (!draft_logits || !uniforms))
+        return fail(ctx, ULSPEC_EINVAL, "accept: sampling needs draft logits and uniforms");
+    const uint32_t rows_t = B * (k + 1), rows_d = p.greedy ? 0 : B * k;
+    void* ws = nullptr;
+    st = workspace(ctx, (size_t)(B * (k + 1) + B * k) * sizeof(RowStat), &ws);
+    if (st != ULSPEC_OK) return st;
+    RowStat* stats = (RowStat*)ws;
+    (void)hipSetDevice(ctx->device);
+    hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats);
+    if (rows_d)
+        hipLaunchKernelGGL(row_stats_kernel, dim3(rows_d), dim3(kRowThreads), 0, ctx->stream, draft_logits, V, p,
+                           stats + (size_t)B * (k + 1));
+    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, stats, target_logits, draft_logits,
+                       draft_tokens, uniforms, k, V, p, out_tokens, out_n_accepted);
+    return check_launch(ctx, "accept launch");
+}
+
+extern "C" ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
+                                       const float* logits, const float* uniforms, int32_t* out_tokens)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    WarpParams p;
+    ulspec_status st = make_params(ctx, s, V, p);
+    if (st != ULSPEC_OK) return st;
+    if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
+    if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
+    void* ws = nullptr;
+    st = workspace(ctx, (size_t)R * sizeof(RowStat), &ws);
+    if (st != ULSPEC_OK) return st;
+    (void)hipSetDevice(ctx->device);
+    hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws);
+    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)ws, logits,
+                       uniforms, V, p, out_tokens);
+    return check_launch(ctx, "sample launch");
+}
+
+extern "C" ulspec_status ulspec_uniforms(ulspec_ctx* ctx, uint64_t seed, uint64_t idx0, uint32_t n, float* out)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!out || n == 0) return fail(ctx, ULSPEC_EINVAL, "uniforms: null pointer or n == 0");
+    (void)hipSetDevice(ctx->device);
+    hipLaunchKernelGGL(uniforms_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, seed, idx0, n, out);
+    return check_launch(ctx, "uniforms launch");
+}
