@@ -1,0 +1,279 @@
+// attn.hip -- K2, attention of the nq <= 16 verified tokens over an fp16 KV
+// cache (causal chain or draft tree).
+//
+// Replaces the per-token "flash_attention" dispatch of forward_layer_gpu
+// (src/inference/inference_engine.cpp:627-630) and follows the visibility rule
+// of src/shaders/attention/flash_attention_v2_fused.glsl:153-166 (key
+// position <= query position, scale applied after the dot, online softmax).
+//
+// Split-KV ("flash-decoding"): grid (heads, splits); a workgroup of 4 waves
+// owns a contiguous key range of one head, each wave takes every 4th 16-key
+// tile of it.  Per tile:
+//   S^T[key][query] = K_tile . Q^T        16x16x32 fp16 MFMA, K loaded from
+//                                         global straight into the A layout
+//   online softmax per query in the log2 domain (fp32)
+//   O^T[d][query] += V^T[d][key] . P^T    16x16x16 fp16 MFMA; the S^T
+//                                         accumulator layout is exactly the
+//                                         P^T operand layout; P = P_hi + P_lo
+//                                         (two fp16 parts) keeps fp32 accuracy;
+//                                         V goes through LDS for the transpose
+// The 4 waves are merged in LDS; splits are merged by a second kernel in
+// split order (deterministic).  Visibility of the nq new keys (rows
+// n_prefix .. L-1) is a per-query bitmask built on the host from the parent
+// array; prefix keys are visible to every query.
+#include "hip_common.h"
+#include "ulspec_internal.h"
+
+#include <cmath>
+
+using namespace ulspec;
+
+namespace {
+
+constexpr int kAttnWaves = 4;
+constexpr int kMaxQ = 16;
+
+struct AttnArgs {
+    const _Float16* q;  // [nq][H][D]
+    const _Float16* k;  // [L][Hkv][D]
+    const _Float16* v;
+    float* out;         // [nq][H][D]
+    float* part;        // [splits][H][nq][D + 2]: O (unnormalised), m, l
+    int n_prefix, nq, L, H, Hkv, splits, keys_per_split;
+    float scale_log2;   // scale * log2(e)
+    uint32_t mask[kMaxQ];
+};
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int D>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
+{
+    constexpr int VP = D + 8;  // V tile row pitch in halfs (16 B pad spreads banks)
+    __shared__ _Float16 vt[kAttnWaves][16 * VP];
+    __shared__ float red_o[kAttnWaves][D][kMaxQ];
+    __shared__ float red_m[kAttnWaves][kMaxQ], red_l[kAttnWaves][kMaxQ];
+
+    const int h = blockIdx.x, s = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;  // c: query (S^T, O^T columns) / key / d column
+    const int hk = h / (a.H / a.Hkv);
+    const size_t row_stride = (size_t)a.Hkv * D;
+
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i)
+        if (c == i) mask = a.mask[i];
+
+    // Q^T operand: lane (query c, group g) holds Q[c][h][32 st + 8 g .. +7]
+    half8_t qb[D / 32];
+    const bool qvalid = c < a.nq;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st)
+        qb[st] = qvalid ? *(const half8_t*)(a.q + ((size_t)c * a.H + h) * D + 32 * st + 8 * g) : half8_t{};
+
+    const int j0 = s * a.keys_per_split;
+    const int j1 = min(a.L, j0 + a.keys_per_split);
+    float m = -INFINITY, l = 0.0f;
+    float4_t oacc[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    _Float16* myv = vt[wave];
+
+    for (int jt0 = j0; jt0 < j1; jt0 += 16 * kAttnWaves) {
+        const int jt = jt0 + 16 * wave;
+        // K rows (A operand) and V rows (to LDS): lane (key c, group g)
+        const int key = jt + c;
+        const bool kvalid = key < j1;
+        const size_t kbase = (size_t)(kvalid ? key : j0) * row_stride + (size_t)hk * D + 8 * g;
+        half8_t ka[D / 32];
+#pragma unroll
+        for (int st = 0; st < D / 32; ++st) ka[st] = *(const half8_t*)(a.k + kbase + 32 * st);
+#pragma unroll
+        for (int st = 0; st < D / 32; ++st)
+            *(half8_t*)(myv + c * VP + 32 * st + 8 * g) = *(const half8_t*)(a.v + kbase + 32 * st);
+
+        float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < D / 32; ++st) sacc = mfma16x16x32(ka[st], qb[st], sacc);
+
+        // lane holds S^T[key 4g + r][query c]
+        float s2[4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int j = jt + 4 * g + r;
+            const bool vis = j < j1 && (j < a.n_prefix || ((mask >> (j - a.n_prefix)) & 1u));
+            s2[r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
+            tmax = fmaxf(tmax, s2[r]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float muse = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = exp2_fast(m - muse);
+        float p[4], psum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = exp2_fast(s2[r] - muse);
+            psum += p[r];
+        }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l = l * alpha + psum;
+        m = mnew;
+        half4_t phi, plo;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            phi[r] = (_Float16)p[r];
+            plo[r] = (_Float16)(p[r] - (float)phi[r]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt) {
+            oacc[dt] = oacc[dt] * alpha;
+            // V^T operand: lane (d = 16 dt + c, group g) holds V[key 4g + r][d]
+            half4_t va;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) va[r] = myv[(4 * g + r) * VP + 16 * dt + c];
+            oacc[dt] = mfma16x16x16(va, phi, oacc[dt]);
+            oacc[dt] = mfma16x16x16(va, plo, oacc[dt]);
+        }
+    }
+
+    // merge the 4 waves: lane holds O^T[d = 16 dt + 4 g + r][query c]
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red_o[wave][16 * dt + 4 * g + r][c] = oacc[dt][r];
+    if (g == 0) {
+        red_m[wave][c] = m;
+        red_l[wave][c] = l;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < D * kMaxQ; idx += kAttnWaves * 64) {
+        const int d = idx / kMaxQ, qi = idx % kMaxQ;
+        if (qi >= a.nq) continue;
+        float M = red_m[0][qi];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w][qi]);
+        const float Mu = M == -INFINITY ? 0.0f : M;
+        float o = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float f = exp2_fast(red_m[w][qi] - Mu);
+            o += red_o[w][d][qi] * f;
+            L += red_l[w][qi] * f;
+        }
+        if (a.splits == 1) {
+            a.out[((size_t)qi * a.H + h) * D + d] = o / L;
+        } else {
+            float* pp = a.part + (((size_t)s * a.H + h) * a.nq + qi) * (D + 2);
+            pp[d] = o;
+            if (d == 0) {
+                pp[D] = M;
+                pp[D + 1] = L;
+            }
+        }
+    }
+}
+
+// out[qi][h][d] = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits in order
+template <int D>
+__global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
+{
+    const int h = blockIdx.x, qi = blockIdx.y, d = threadIdx.x;
+    const size_t stride = (size_t)a.H * a.nq * (D + 2);
+    const float* base = a.part + ((size_t)h * a.nq + qi) * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[s * stride + D]);
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    float o = 0.0f, L = 0.0f;
+    for (int s = 0; s < a.splits; ++s) {
+        const float* pp = base + s * stride;
+        const float f = exp2_fast(pp[D] - Mu);
+        o += pp[d] * f;
+        L += pp[D + 1] * f;
+    }
+    a.out[((size_t)qi * a.H + h) * D + d] = o / L;
+}
+
+template <int D>
+void launch_attn(const AttnArgs& a, hipStream_t st)
+{
+    hipLaunchKernelGGL(attn_split_kernel<D>, dim3(a.H, a.splits), dim3(kAttnWaves * 64), 0, st, a);
+    if (a.splits > 1) hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.H, a.nq), dim3(D), 0, st, a);
+}
+
+}  // namespace
+
+namespace ulspec {
+
+// Splits so that heads x splits is about two workgroups per CU, each split a
+// multiple of the 64 keys one workgroup step covers.
+void attn_plan(int L, int H, int n_cu, int& splits, int& kps)
+{
+    const int step = 16 * kAttnWaves;
+    int want = (2 * n_cu + H - 1) / H;
+    const int max_splits = (L + step - 1) / step;
+    if (want > max_splits) want = max_splits;
+    if (want < 1) want = 1;
+    kps = ((L + want - 1) / want + step - 1) / step * step;
+    splits = (L + kps - 1) / kps;
+}
+
+size_t attn_workspace_bytes(int splits, int H, int nq, int D)
+{
+    return splits > 1 ? (size_t)splits * H * nq * (D + 2) * sizeof(float) : 0;
+}
+
+}  // namespace ulspec
+
+extern "C" ulspec_status ulspec_verify_attention(ulspec_ctx* ctx, const uint16_t* q, const uint16_t* k_cache,
+                                                 const uint16_t* v_cache, uint32_t n_prefix, uint32_t nq,
+                                                 const int32_t* parent, uint32_t H, uint32_t Hkv, uint32_t D,
+                                                 float scale, float* out)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!q || !k_cache || !v_cache || !out) return fail(ctx, ULSPEC_EINVAL, "verify_attention: null pointer");
+    if (nq == 0 || nq > (uint32_t)kMaxQ) return fail(ctx, ULSPEC_EINVAL, "verify_attention: nq=%u not in [1, 16]", nq);
+    if (D != 64 && D != 128) return fail(ctx, ULSPEC_EUNSUPPORTED, "verify_attention: head dim %u (64 or 128)", D);
+    if (H == 0 || Hkv == 0 || H % Hkv) return fail(ctx, ULSPEC_EINVAL, "verify_attention: H=%u Hkv=%u", H, Hkv);
+    if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(ctx, ULSPEC_EINVAL, "verify_attention: scale");
+    if ((uint64_t)n_prefix + nq > (uint64_t)INT32_MAX) return fail(ctx, ULSPEC_EINVAL, "verify_attention: length");
+    AttnArgs a;
+    a.q = (const _Float16*)q;
+    a.k = (const _Float16*)k_cache;
+    a.v = (const _Float16*)v_cache;
+    a.out = out;
+    a.n_prefix = (int)n_prefix;
+    a.nq = (int)nq;
+    a.L = (int)(n_prefix + nq);
+    a.H = (int)H;
+    a.Hkv = (int)Hkv;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    for (int i = 0; i < kMaxQ; ++i) a.mask[i] = 0;
+    for (uint32_t i = 0; i < nq; ++i) {
+        uint32_t mk = 0;
+        if (!parent) {
+            mk = (i == 31) ? 0xffffffffu : ((1u << (i + 1)) - 1u);
+        } else {
+            if (parent[i] >= (int32_t)i || parent[i] < -1)
+                return fail(ctx, ULSPEC_EINVAL, "verify_attention: parent[%u]=%d must be in [-1, %u)", i, parent[i], i);
+            mk = 1u << i;
+            for (int32_t pnode = parent[i]; pnode >= 0; pnode = parent[pnode]) mk |= 1u << pnode;
+        }
+        a.mask[i] = mk;
+    }
+    attn_plan(a.L, a.H, ctx->n_cu, a.splits, a.keys_per_split);
+    void* ws = nullptr;
+    const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)D);
+    if (wsb) {
+        ulspec_status st = workspace(ctx, wsb, &ws);
+        if (st != ULSPEC_OK) return st;
+    }
+    a.part = (float*)ws;
+    (void)hipSetDevice(ctx->device);
+    if (D == 128) launch_attn<128>(a, ctx->stream);
+    else launch_attn<64>(a, ctx->stream);
+    return check_launch(ctx, "verify_attention launch");
+}
