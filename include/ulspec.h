@@ -145,6 +145,84 @@ ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
 /* uniforms[i] = top 24 bits of splitmix64(seed + (idx0 + i + 1) * golden) * 2^-24 */
 ulspec_status ulspec_uniforms(ulspec_ctx* ctx, uint64_t seed, uint64_t idx0, uint32_t n, float* out);
 
+/* ---- synthetic GGUF weights ---------------------------------------------
+ * Writes N rows of K elements as raw GGUF blocks (Q4_0 / Q4_K) into device
+ * memory `out` (N * K / blck * type_size bytes): element (n, k) is normal
+ * number n*K + k of the counter-based stream (seed, stream) -- Box-Muller in
+ * double on splitmix64 counters, then the GGUF quantizer.  For synthetic
+ * random-init models (no checkpoint is loaded). */
+ulspec_status ulspec_synth_q4(ulspec_ctx* ctx, uint32_t ggml_type, uint64_t seed, uint64_t stream, uint32_t N,
+                              uint32_t K, float std_dev, void* out);
+
+/* ---- Llama-shaped model (target or draft) ---------------------------------
+ * Device weights, fp16 KV cache [max_ctx][n_kv_heads][head_dim] per layer and
+ * activation buffers for up to 16 rows.  Block order of
+ * InferenceEngine::forward_layer_gpu (src/inference/inference_engine.cpp:602-682):
+ * RMSNorm -> QKV -> RoPE -> attention -> O -> +residual -> RMSNorm -> gate/up
+ * -> SiLU(gate) * up -> down -> +residual; final RMSNorm and LM head.  GEMM
+ * inputs are fp16, the residual stream and logits fp32.  Replaces Model /
+ * KVCache (src/inference/model.h:49-115) and forward_layer_gpu (:475-692). */
+typedef struct ulspec_model ulspec_model;
+typedef struct {
+    uint32_t dim, n_layers, n_heads, n_kv_heads, ffn, vocab;
+    uint32_t max_ctx;    /* KV-cache positions */
+    float    rms_eps;    /* RMSNorm epsilon */
+    float    rope_base;  /* RoPE theta base (10000 in src/shaders/rope.glsl) */
+} ulspec_model_cfg;
+ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, ulspec_model** out);
+void          ulspec_model_destroy(ulspec_model* m);
+/* One GGUF tensor by its GGUF name (token_embd.weight, output_norm.weight,
+ * output.weight, blk.<i>.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,
+ * ffn_gate,ffn_up,ffn_down}.weight), as the weight map of Model::load_from_gguf
+ * (src/inference/model.cpp:190-246).  Norms are F32 (type 0), matrices and the
+ * embedding Q4_0 / Q4_K.  ne0 = elements per row (contiguous), ne1 = rows.
+ * `data` is host memory, or device memory when on_device != 0. */
+ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* name, uint32_t ggml_type, const void* data,
+                                      size_t nbytes, uint64_t ne0, uint64_t ne1, int on_device);
+/* Forward M tokens (host ids) at positions pos .. pos+M-1, appending their K/V;
+ * copies the logits of the last n_logits (<= 16) rows to host memory `logits`
+ * (n_logits = 0: none).  Synchronous.  Serves InferenceAPI::get_token_logits
+ * (src/api/inference_api.cpp:277-280) and prefill. */
+ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint32_t M, uint32_t pos,
+                                   float* logits, uint32_t n_logits);
+/* Copy K/V cache rows pos0 .. pos0+n-1 of one layer to (dir 0) or from (dir 1)
+ * host arrays [n][n_kv_heads][head_dim] of fp16 bits.  Synchronous. */
+ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n, uint16_t* k,
+                                 uint16_t* v);
+
+/* ---- speculative decoding loop --------------------------------------------
+ * One step (all on the device, captured once into a HIP graph and replayed):
+ * the draft model takes the last two committed tokens (positions n-2, n-1),
+ * then k-1 single-token forwards, sampling d_1 .. d_k from warp(draft logits)
+ * with uniforms u(seed, s*(2k+1) + j); the target scores [t_{n-1}, d_1 .. d_k]
+ * at positions n-1 .. n-1+k; ulspec_accept's rule with uniforms
+ * u(seed, s*(2k+1) + k + j) emits n_accepted + 1 tokens, which are committed
+ * (stale K/V rows past them are overwritten by the next step).  Replaces
+ * SpeculativeDecoder::generate_with_speculation
+ * (src/inference/speculative_decoder.cpp:25-71). */
+typedef struct ulspec_spec ulspec_spec;
+ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
+                                 uint64_t seed, ulspec_spec** out);
+void          ulspec_spec_destroy(ulspec_spec* sp);
+/* Commit the prompt (n >= 2): both models process tokens 0 .. n-2; token n-1
+ * is pending.  Resets the counters.  Synchronous. */
+ulspec_status ulspec_spec_prefill(ulspec_spec* sp, const int32_t* prompt, uint32_t n);
+/* Enqueue n_steps steps (asynchronous); EINVAL if they could overrun the
+ * context (each step commits at most k+1 tokens). */
+ulspec_status ulspec_spec_steps(ulspec_spec* sp, uint32_t n_steps);
+/* Steps until at least n_new tokens were committed by this call; *n_out = the
+ * number committed (up to n_new + k).  Synchronous. */
+ulspec_status ulspec_spec_generate(ulspec_spec* sp, uint32_t n_new, uint32_t* n_out);
+/* Synchronises, then reports committed tokens (prompt included), steps,
+ * accepted draft tokens and proposed draft tokens since the prefill. */
+ulspec_status ulspec_spec_state(ulspec_spec* sp, uint32_t* n_tokens, uint64_t* steps, uint64_t* accepted,
+                                uint64_t* proposed);
+/* Committed tokens start .. start+n-1 to host memory.  Synchronous. */
+ulspec_status ulspec_spec_tokens(ulspec_spec* sp, uint32_t start, uint32_t n, int32_t* out);
+/* use_graph != 0 (default): replay the step captured as a HIP graph;
+ * 0: launch the step's kernels directly on the stream. */
+ulspec_status ulspec_spec_set_graph(ulspec_spec* sp, int use_graph);
+
 #ifdef __cplusplus
 }
 #endif

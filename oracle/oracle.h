@@ -119,39 +119,60 @@ int ora_accept(const ora_sampling* s, int64_t B, int64_t k, int64_t V,
                const int32_t* draft_tokens, const float* uniforms,
                int32_t* out_tokens, int32_t* out_n_accepted, int nthreads);
 
-/* ---- Llama-shaped model and the speculative loop --------------------------- */
+/* ---- Llama-shaped model and the speculative loop ---------------------------
+ * Block order of InferenceEngine::forward_layer_gpu
+ * (src/inference/inference_engine.cpp:602-682): RMSNorm -> Q, K, V -> RoPE ->
+ * attention -> O -> +residual -> RMSNorm -> gate, up -> SiLU(gate)*up -> down
+ * -> +residual; final RMSNorm, LM head.  The residual stream is fp32; every
+ * GEMM input (normed activations, attention output, SiLU product), Q and the
+ * K/V cache are rounded to fp16 (round to nearest even).
+ *   RMSNorm  x = fp16((h * r) * w), r = 1 / sqrtf(sum(h^2) / dim + eps)
+ *            (src/shaders/ffn/ffn_fused.glsl:23-33)
+ *   RoPE     pairs (2i, 2i+1): y0 = x0 c - x1 s, y1 = x0 s + x1 c with
+ *            (c, s) = fp32(cos, sin)(pos * base^(-2i/D)) evaluated in double
+ *            (src/shaders/rope.glsl:50-73)
+ *   SiLU     g * (1 / (1 + ora_expf(-g))) (src/cpu_backend/activation_cpu.cpp:14-20)
+ *   attention ora_attention_f32, scale 1/sqrt(D), causal over the cache. */
 typedef struct {
-    int32_t dim, n_layers, n_heads, n_kv_heads, ffn, vocab;
-    int32_t wtype;     /* ORA_Q4_0 or ORA_Q4_K, every linear + embedding + lm head */
-    int32_t max_ctx;
-    float   rms_eps;   /* 1e-5 */
-    float   rope_base; /* 10000 */
+    int64_t dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx;
+    float rms_eps, rope_base;
 } ora_llama_cfg;
 
 typedef struct ora_llama ora_llama;
-/* tensor order per layer: wq wk wv wo w_gate w_up w_down; then tok_embd, lm_head.
- * Norm weights are all 1.0. */
 ora_llama* ora_llama_create(const ora_llama_cfg* cfg, int nthreads);
 void       ora_llama_free(ora_llama* m);
-/* Set one linear tensor's GGUF bytes (copied).  layer -1: tok_embd (which=0) / lm_head (which=1). */
-int        ora_llama_set_tensor(ora_llama* m, int layer, int which, const uint8_t* bytes, size_t nbytes);
-void       ora_llama_reset(ora_llama* m);                /* KV length = 0 */
-int64_t    ora_llama_kv_len(const ora_llama* m);
-int        ora_llama_set_kv_len(ora_llama* m, int64_t len);
-/* Forward M tokens at positions kv_len..kv_len+M-1, append their K/V, write
- * logits [M][vocab].  Does not advance kv_len beyond kv_len+M. */
-int        ora_llama_forward(ora_llama* m, const int32_t* tokens, int64_t M, float* logits);
-/* Copy KV rows [0, len) of one layer in/out: fp16 [len][n_kv_heads*head_dim]. */
-int        ora_llama_kv_io(ora_llama* m, int layer, int is_v, int64_t len, uint16_t* buf, int write_into_model);
+/* GGUF tensor by name (token_embd / output_norm / output / blk.<i>.{attn_norm,
+ * attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}
+ * .weight); norms F32 (type 0), the rest Q4_0 / Q4_K; bytes are copied. */
+int        ora_llama_set_tensor(ora_llama* m, const char* name, int type, const void* data, size_t nbytes,
+                                int64_t ne0, int64_t ne1);
+/* Forward M tokens at positions pos .. pos+M-1 (K/V appended); logits of the
+ * last n_logits rows to logits [n_logits][vocab] (NULL when n_logits = 0). */
+int        ora_llama_forward(ora_llama* m, const int32_t* tokens, int64_t M, int64_t pos, float* logits,
+                             int64_t n_logits);
+/* K/V rows pos0 .. pos0+n-1 of one layer out of (dir 0) / into (dir 1) the
+ * model, fp16 bits [n][n_kv_heads * head_dim]. */
+int        ora_llama_kv_io(ora_llama* m, int64_t layer, int dir, int64_t pos0, int64_t n, uint16_t* k, uint16_t* v);
 
-/* Speculative decoding driver (bs = 1).  Emits tokens until n_new reached.
- * uniforms per step s: draft u = ora_uniform(seed, s*(2k+1) + j) j<k,
- *                      verify u = ora_uniform(seed, s*(2k+1) + k + j) j<=k.
- * Returns number of steps; writes emitted tokens, per-step n_accepted. */
-int64_t ora_spec_generate(ora_llama* target, ora_llama* draft, const ora_sampling* s, int32_t k,
-                          const int32_t* prompt, int64_t n_prompt, int64_t n_new, uint64_t seed,
-                          int32_t* out_tokens, int32_t* out_n_acc_per_step, int64_t max_steps,
-                          int64_t step0);
+/* Speculative decoding (one sequence).  seq holds the committed tokens
+ * (capacity cap); st->n of them.  One step, as the device loop:
+ *   u_j = ora_uniform(seed, step*(2k+1) + j), j = 0 .. 2k
+ *   draft forward [seq[n-2], seq[n-1]] at n-2 -> d_1 = sample(row n-1, u_0);
+ *   draft forward [d_j] at n-1+j -> d_{j+1} = sample(.., u_j), j = 1 .. k-1
+ *   target forward [seq[n-1], d_1 .. d_k] at n-1 .. n-1+k
+ *   ora_accept(.., uniforms u_k .. u_2k) -> n_acc + 1 tokens appended. */
+typedef struct {
+    int64_t n, step, accepted, proposed;
+} ora_spec_state;
+/* Both models process prompt[0 .. n-2]; seq = prompt; counters zero. */
+int     ora_spec_prefill(ora_llama* target, ora_llama* draft, const int32_t* prompt, int64_t n, int32_t* seq,
+                         int64_t cap, ora_spec_state* st);
+int     ora_spec_step(ora_llama* target, ora_llama* draft, const ora_sampling* s, int64_t k, uint64_t seed,
+                      int32_t* seq, int64_t cap, ora_spec_state* st);
+/* Steps until at least n_new tokens were committed by this call; returns the
+ * number committed (< 0 on error). */
+int64_t ora_spec_generate(ora_llama* target, ora_llama* draft, const ora_sampling* s, int64_t k, uint64_t seed,
+                          int64_t n_new, int32_t* seq, int64_t cap, ora_spec_state* st);
 
 #ifdef __cplusplus
 }

@@ -38,9 +38,13 @@ class Sampling(C.Structure):
 
 
 class LlamaCfg(C.Structure):
-    _fields_ = [("dim", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
-                ("ffn", C.c_int32), ("vocab", C.c_int32), ("wtype", C.c_int32), ("max_ctx", C.c_int32),
+    _fields_ = [("dim", C.c_int64), ("n_layers", C.c_int64), ("n_heads", C.c_int64), ("n_kv_heads", C.c_int64),
+                ("ffn", C.c_int64), ("vocab", C.c_int64), ("max_ctx", C.c_int64),
                 ("rms_eps", C.c_float), ("rope_base", C.c_float)]
+
+
+class SpecState(C.Structure):
+    _fields_ = [("n", C.c_int64), ("step", C.c_int64), ("accepted", C.c_int64), ("proposed", C.c_int64)]
 
 
 P = C.c_void_p
@@ -79,13 +83,12 @@ def _declare(L):
     d("ora_accept", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, C.c_int)
     d("ora_llama_create", P, P, C.c_int)
     d("ora_llama_free", None, P)
-    d("ora_llama_set_tensor", C.c_int, P, C.c_int, C.c_int, P, C.c_size_t)
-    d("ora_llama_reset", None, P)
-    d("ora_llama_kv_len", I64, P)
-    d("ora_llama_set_kv_len", C.c_int, P, I64)
-    d("ora_llama_forward", C.c_int, P, P, I64, P)
-    d("ora_llama_kv_io", C.c_int, P, C.c_int, C.c_int, I64, P, C.c_int)
-    d("ora_spec_generate", I64, P, P, P, C.c_int32, P, I64, I64, C.c_uint64, P, P, I64, I64)
+    d("ora_llama_set_tensor", C.c_int, P, C.c_char_p, C.c_int, P, C.c_size_t, I64, I64)
+    d("ora_llama_forward", C.c_int, P, P, I64, I64, P, I64)
+    d("ora_llama_kv_io", C.c_int, P, I64, C.c_int, I64, I64, P, P)
+    d("ora_spec_prefill", C.c_int, P, P, P, I64, P, I64, P)
+    d("ora_spec_step", C.c_int, P, P, P, I64, C.c_uint64, P, I64, P)
+    d("ora_spec_generate", I64, P, P, P, I64, C.c_uint64, I64, P, I64, P)
 
 
 def _p(a):
@@ -240,3 +243,82 @@ def accept(s, target, draft, draft_tokens, u, nthreads=None):
                           _p(out), _p(nacc), nthreads or nthreads_default())
     assert rc == 0
     return out, nacc
+
+
+class Llama:
+    """CPU restatement of the Llama-shaped model (ora_llama)."""
+
+    def __init__(self, dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps=1e-5, rope_base=10000.0,
+                 nthreads=8):
+        self.cfg = LlamaCfg(dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps, rope_base)
+        self.handle = lib().ora_llama_create(C.byref(self.cfg), nthreads)
+        if not self.handle:
+            raise ValueError("ora_llama_create rejected the configuration")
+
+    def close(self):
+        if self.handle:
+            lib().ora_llama_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    def set_tensor(self, name, wtype, data, ne0, ne1):
+        data = np.ascontiguousarray(data)
+        if lib().ora_llama_set_tensor(self.handle, name.encode(), wtype, data.ctypes.data_as(P), data.nbytes,
+                                      ne0, ne1):
+            raise ValueError(f"ora_llama_set_tensor rejected {name}")
+
+    def forward(self, tokens, pos, n_logits=0):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((n_logits, self.cfg.vocab), np.float32) if n_logits else None
+        if lib().ora_llama_forward(self.handle, tokens.ctypes.data_as(P), len(tokens), pos,
+                                   out.ctypes.data_as(P) if out is not None else None, n_logits):
+            raise ValueError("ora_llama_forward failed")
+        return out
+
+    def kv_io(self, layer, dir, pos0, n, k=None, v=None):
+        row = self.cfg.n_kv_heads * (self.cfg.dim // self.cfg.n_heads)
+        if dir == 0:
+            k = np.empty((n, row), np.uint16)
+            v = np.empty((n, row), np.uint16)
+        else:
+            k = np.ascontiguousarray(k, dtype=np.uint16)
+            v = np.ascontiguousarray(v, dtype=np.uint16)
+        if lib().ora_llama_kv_io(self.handle, layer, dir, pos0, n, k.ctypes.data_as(P), v.ctypes.data_as(P)):
+            raise ValueError("ora_llama_kv_io failed")
+        return k, v
+
+
+class Speculative:
+    """CPU restatement of the speculative loop (ora_spec_*)."""
+
+    def __init__(self, target, draft, k, s, seed, cap=None):
+        self.target, self.draft, self.k, self.s, self.seed = target, draft, k, s, seed
+        self.cap = cap or min(target.cfg.max_ctx, draft.cfg.max_ctx)
+        self.seq = np.zeros(self.cap, np.int32)
+        self.st = SpecState()
+
+    def prefill(self, prompt):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        if lib().ora_spec_prefill(self.target.handle, self.draft.handle, prompt.ctypes.data_as(P), len(prompt),
+                                  self.seq.ctypes.data_as(P), self.cap, C.byref(self.st)):
+            raise ValueError("ora_spec_prefill failed")
+
+    def step(self):
+        if lib().ora_spec_step(self.target.handle, self.draft.handle, C.byref(self.s), self.k, self.seed,
+                               self.seq.ctypes.data_as(P), self.cap, C.byref(self.st)):
+            raise ValueError("ora_spec_step failed")
+
+    def generate(self, n_new):
+        n = lib().ora_spec_generate(self.target.handle, self.draft.handle, C.byref(self.s), self.k, self.seed, n_new,
+                                    self.seq.ctypes.data_as(P), self.cap, C.byref(self.st))
+        if n < 0:
+            raise ValueError("ora_spec_generate failed")
+        return n
+
+    def state(self):
+        return {"n": self.st.n, "steps": self.st.step, "accepted": self.st.accepted, "proposed": self.st.proposed}
+
+    def tokens(self):
+        return self.seq[:self.st.n].copy()

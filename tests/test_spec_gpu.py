@@ -1,0 +1,183 @@
+"""End-to-end speculative decoding on the GPU (model forward, device loop,
+graph replay) against the oracle, through the C ABI.
+
+Bar: the committed token sequences and acceptance counters are bit-exact with
+the oracle's loop on the same weights, prompt and seed; model logits agree
+within 1e-3 of their RMS (fp32 accumulation in different orders).
+"""
+import numpy as np
+import pytest
+
+from llama_util import load, make_tensors
+
+pytestmark = pytest.mark.gpu
+
+# tiny Llama: dim 512, 8 layers, 8 heads x 64, FFN 1376, vocab 32000, Q4_0;
+# draft: 2 layers of the same dims
+TARGET = dict(dim=512, n_layers=8, n_heads=8, n_kv_heads=8, ffn=1376, vocab=32000, max_ctx=256, rms_eps=1e-5,
+              rope_base=10000.0)
+DRAFT = dict(TARGET, n_layers=2)
+
+
+@pytest.fixture(scope="module")
+def weights(ora):
+    return make_tensors(ora, TARGET, 2, seed=101), make_tensors(ora, DRAFT, 2, seed=202)
+
+
+@pytest.fixture(scope="module")
+def prompt():
+    return np.random.default_rng(77).integers(0, 32000, 64).astype(np.int32)
+
+
+def _gpu_model(pkg, ctx, cfg, tensors):
+    m = pkg.Model(ctx, **cfg)
+    load(m, tensors)
+    return m
+
+
+def _ora_model(ora, cfg, tensors):
+    m = ora.Llama(**cfg, nthreads=ora.nthreads_default())
+    load(m, tensors)
+    return m
+
+
+def test_model_forward_logits_and_cache(pkg, ctx, ora, weights, prompt):
+    tw, _ = weights
+    g, o = _gpu_model(pkg, ctx, TARGET, tw), _ora_model(ora, TARGET, tw)
+    lg = g.forward(prompt[:40], 0, n_logits=16)  # chunks of 16 and a final chunk of 16
+    lo = o.forward(prompt[:40], 0, n_logits=16)
+    scale = np.sqrt((lo.astype(np.float64) ** 2).mean())
+    err = np.abs(lg.astype(np.float64) - lo).max() / scale
+    print(f"  logits max err / rms = {err:.2e}")
+    assert err <= 1e-3
+    assert np.array_equal(np.argmax(lg, axis=1), np.argmax(lo, axis=1))
+    for l in (0, TARGET["n_layers"] - 1):
+        kg, vg = g.kv_io(l, 0, 0, 40)
+        ko, vo = o.kv_io(l, 0, 0, 40)
+        for a, b in ((kg, ko), (vg, vo)):
+            a, b = ora.h2f_fast(a).astype(np.float64), ora.h2f_fast(b).astype(np.float64)
+            assert np.abs(a - b).max() <= 1e-2 * np.sqrt((b ** 2).mean())
+    g.close()
+
+
+def test_forward_rows_are_batch_invariant(pkg, ctx, weights, prompt):
+    tw, _ = weights
+    a, b = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, TARGET, tw)
+    la = a.forward(prompt[:6], 0, n_logits=6)
+    lb = np.concatenate([b.forward(prompt[i:i + 1], i, n_logits=1) for i in range(6)])
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    a.close()
+    b.close()
+
+
+@pytest.mark.parametrize("mode", ["greedy", "t0.8"])
+def test_speculative_tokens_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt, mode):
+    tw, dw = weights
+    k, n_new, seed = 4, 128, 2024
+    s_gpu = pkg.sampling(greedy=True) if mode == "greedy" else pkg.sampling(temperature=0.8)
+    s_ora = ora.sampling(greedy=True) if mode == "greedy" else ora.sampling(temperature=0.8)
+    gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
+    sp = pkg.Speculative(gt, gd, k, s_gpu, seed)
+    sp.prefill(prompt)
+    n = sp.generate(n_new)
+    got, st = sp.tokens(), sp.state()
+    ot, od = _ora_model(ora, TARGET, tw), _ora_model(ora, DRAFT, dw)
+    osp = ora.Speculative(ot, od, k, s_ora, seed)
+    osp.prefill(prompt)
+    on = osp.generate(n_new)
+    want, ost = osp.tokens(), osp.state()
+    print(f"  {mode}: {n} tokens in {st['steps']} steps, accepted {st['accepted']}/{st['proposed']}")
+    assert n == on and n >= n_new
+    assert np.array_equal(got, want)
+    assert st == ost
+    sp.close()
+    gt.close()
+    gd.close()
+
+
+def test_graph_replay_equals_direct_launches(pkg, ctx, weights, prompt):
+    tw, dw = weights
+    outs = []
+    for use_graph in (True, False, True):
+        gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
+        sp = pkg.Speculative(gt, gd, 5, pkg.sampling(temperature=0.8), 7)
+        sp.set_graph(use_graph)
+        sp.prefill(prompt)
+        for _ in range(4):  # several replays with host work and syncs between them
+            sp.steps(3)
+            sp.state()
+        outs.append((sp.tokens(), sp.state()))
+        sp.close()
+        gt.close()
+        gd.close()
+    for t, s in outs[1:]:
+        assert np.array_equal(t, outs[0][0]) and s == outs[0][1]
+
+
+def test_draft_equal_to_target_accepts_everything(pkg, ctx, weights, prompt):
+    _, dw = weights
+    a, b = _gpu_model(pkg, ctx, DRAFT, dw), _gpu_model(pkg, ctx, DRAFT, dw)
+    sp = pkg.Speculative(a, b, 4, pkg.sampling(temperature=0.8), 99)
+    sp.prefill(prompt)
+    sp.steps(10)
+    st = sp.state()
+    assert st["steps"] == 10 and st["accepted"] == st["proposed"] == 40 and st["n"] == 64 + 50
+    sp.close()
+    a.close()
+    b.close()
+
+
+def test_greedy_speculation_equals_autoregressive_argmax(pkg, ctx, weights, prompt):
+    tw, dw = weights
+    gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
+    sp = pkg.Speculative(gt, gd, 3, pkg.sampling(greedy=True), 1)
+    sp.prefill(prompt[:20])
+    sp.generate(24)
+    got = sp.tokens()
+    ref = _gpu_model(pkg, ctx, TARGET, tw)
+    seq = list(prompt[:20])
+    ref.forward(np.array(seq[:-1], np.int32), 0)
+    while len(seq) < len(got):
+        lg = ref.forward(np.array(seq[-1:], np.int32), len(seq) - 1, n_logits=1)[0]
+        seq.append(int(np.argmax(lg)))
+    assert list(got) == seq
+    for m in (sp, gt, gd, ref):
+        m.close()
+
+
+def test_synth_matches_oracle_synthesizer(pkg, ctx, ora):
+    for wtype, N, K in ((2, 64, 4096), (12, 48, 2048)):
+        buf = ctx.alloc(N * pkg.row_bytes(wtype, K))
+        ctx.synth_q4(wtype, 5, 3, N, K, 0.02, buf)
+        got = ctx.download(buf, np.uint8, (N * pkg.row_bytes(wtype, K),))
+        want = ora.synth_q4(wtype, 5, 3, N, K, float(np.float32(0.02)))
+        bs = 18 if wtype == 2 else 144
+        same = (got.reshape(-1, bs) == want.reshape(-1, bs)).all(axis=1).mean()
+        # device double log / cos / sin may round a normal differently from libm
+        assert same >= 0.999, same
+        x = ora.dequantize(wtype, got, N * K)
+        assert abs(x.std() - 0.02) < 0.002 and abs(x.mean()) < 0.002
+        buf.free()
+
+
+def test_model_and_spec_argument_errors(pkg, ctx, weights):
+    tw, _ = weights
+    m = pkg.Model(ctx, **DRAFT)
+    with pytest.raises(pkg.UlspecError) as e:
+        m.set_tensor("blk.0.nonsense.weight", 2, np.zeros(18, np.uint8), 32, 1)
+    assert e.value.status == pkg.EINVAL
+    with pytest.raises(pkg.UlspecError) as e:
+        m.set_tensor("blk.9.attn_q.weight", *tw["blk.0.attn_q.weight"])
+    assert e.value.status == pkg.EINVAL
+    name = "blk.0.attn_output.weight"
+    wtype, data, ne0, ne1 = tw[name]
+    with pytest.raises(pkg.UlspecError) as e:
+        m.set_tensor(name, wtype, data, ne1, ne0)  # transposed shape
+    assert e.value.status == pkg.EINVAL
+    with pytest.raises(pkg.UlspecError) as e:  # tensors missing
+        m.forward(np.array([1, 2], np.int32), 0)
+    assert e.value.status == pkg.EINVAL
+    with pytest.raises(pkg.UlspecError) as e:
+        pkg.Model(ctx, **dict(DRAFT, dim=96 * 8))  # head dim 96
+    assert e.value.status == pkg.EUNSUPPORTED
+    m.close()

@@ -51,6 +51,12 @@ def sampling(temperature=1.0, top_k=0, top_p=1.0, greedy=False):
     return Sampling(temperature, top_k, top_p, 1 if greedy else 0)
 
 
+class ModelCfg(C.Structure):
+    _fields_ = [("dim", C.c_uint32), ("n_layers", C.c_uint32), ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32),
+                ("ffn", C.c_uint32), ("vocab", C.c_uint32), ("max_ctx", C.c_uint32), ("rms_eps", C.c_float),
+                ("rope_base", C.c_float)]
+
+
 _lib = None
 P = C.c_void_p
 U32 = C.c_uint32
@@ -95,6 +101,21 @@ ABI = [
     ("ulspec_accept", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P]),
     ("ulspec_sample", C.c_int, [P, C.POINTER(Sampling), U32, U32, P, P, P]),
     ("ulspec_uniforms", C.c_int, [P, C.c_uint64, C.c_uint64, U32, P]),
+    ("ulspec_synth_q4", C.c_int, [P, U32, C.c_uint64, C.c_uint64, U32, U32, C.c_float, P]),
+    ("ulspec_model_create", C.c_int, [P, C.POINTER(ModelCfg), C.POINTER(P)]),
+    ("ulspec_model_destroy", None, [P]),
+    ("ulspec_model_set_tensor", C.c_int, [P, C.c_char_p, U32, P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_int]),
+    ("ulspec_model_forward", C.c_int, [P, P, U32, U32, P, U32]),
+    ("ulspec_model_kv_io", C.c_int, [P, U32, C.c_int, U32, U32, P, P]),
+    ("ulspec_spec_create", C.c_int, [P, P, U32, C.POINTER(Sampling), C.c_uint64, C.POINTER(P)]),
+    ("ulspec_spec_destroy", None, [P]),
+    ("ulspec_spec_prefill", C.c_int, [P, P, U32]),
+    ("ulspec_spec_steps", C.c_int, [P, U32]),
+    ("ulspec_spec_generate", C.c_int, [P, U32, C.POINTER(U32)]),
+    ("ulspec_spec_state", C.c_int, [P, C.POINTER(U32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                    C.POINTER(C.c_uint64)]),
+    ("ulspec_spec_tokens", C.c_int, [P, U32, U32, P]),
+    ("ulspec_spec_set_graph", C.c_int, [P, C.c_int]),
 ]
 
 
@@ -239,6 +260,103 @@ class Context:
 
     def uniforms(self, seed, idx0, n, out):
         self._check(lib().ulspec_uniforms(self.handle, seed, idx0, n, _ptr(out)))
+
+    # -- synthetic weights -----------------------------------------------------
+    def synth_q4(self, wtype, seed, stream, n_rows, k, std, out):
+        self._check(lib().ulspec_synth_q4(self.handle, wtype, seed, stream, n_rows, k, std, _ptr(out)))
+
+
+def row_bytes(wtype, k):
+    return (k // lib().ulspec_ggml_blck_size(wtype)) * lib().ulspec_ggml_type_size(wtype)
+
+
+class Model:
+    """ulspec_model: a Llama-shaped target or draft model on one context."""
+
+    def __init__(self, ctx, dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps=1e-5,
+                 rope_base=10000.0):
+        self.ctx = ctx
+        self.cfg = ModelCfg(dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps, rope_base)
+        h = P()
+        ctx._check(lib().ulspec_model_create(ctx.handle, C.byref(self.cfg), C.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            lib().ulspec_model_destroy(self.handle)
+            self.handle = None
+
+    def set_tensor(self, name, wtype, data, ne0, ne1):
+        """data: a numpy array (host) or a DeviceBuffer (device) of GGUF bytes."""
+        if hasattr(data, "ptr"):
+            ptr, nbytes, dev = data.ptr, data.nbytes, 1
+        else:
+            data = np.ascontiguousarray(data)
+            ptr, nbytes, dev = data.ctypes.data, data.nbytes, 0
+        self.ctx._check(lib().ulspec_model_set_tensor(self.handle, name.encode(), wtype, ptr, nbytes, ne0, ne1, dev))
+
+    def forward(self, tokens, pos, n_logits=0):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.empty((n_logits, self.cfg.vocab), np.float32) if n_logits else None
+        self.ctx._check(lib().ulspec_model_forward(self.handle, tokens.ctypes.data_as(P), len(tokens), pos,
+                                                   out.ctypes.data_as(P) if out is not None else None, n_logits))
+        return out
+
+    def kv_io(self, layer, dir, pos0, n, k=None, v=None):
+        row = self.cfg.n_kv_heads * (self.cfg.dim // self.cfg.n_heads)
+        if dir == 0:
+            k = np.empty((n, row), np.uint16)
+            v = np.empty((n, row), np.uint16)
+        else:
+            k = np.ascontiguousarray(k, dtype=np.uint16)
+            v = np.ascontiguousarray(v, dtype=np.uint16)
+        self.ctx._check(lib().ulspec_model_kv_io(self.handle, layer, dir, pos0, n, k.ctypes.data_as(P),
+                                                 v.ctypes.data_as(P)))
+        return k, v
+
+
+class Speculative:
+    """ulspec_spec: the device speculative-decoding loop over a target and a draft model."""
+
+    def __init__(self, target, draft, k, s, seed):
+        self.ctx = target.ctx
+        self.target, self.draft, self.k = target, draft, k
+        h = P()
+        self.ctx._check(lib().ulspec_spec_create(target.handle, draft.handle, k, C.byref(s), seed, C.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if self.handle:
+            lib().ulspec_spec_destroy(self.handle)
+            self.handle = None
+
+    def prefill(self, prompt):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        self.ctx._check(lib().ulspec_spec_prefill(self.handle, prompt.ctypes.data_as(P), len(prompt)))
+
+    def steps(self, n):
+        self.ctx._check(lib().ulspec_spec_steps(self.handle, n))
+
+    def generate(self, n_new):
+        n = U32()
+        self.ctx._check(lib().ulspec_spec_generate(self.handle, n_new, C.byref(n)))
+        return n.value
+
+    def state(self):
+        n, steps, acc, prop = U32(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        self.ctx._check(lib().ulspec_spec_state(self.handle, C.byref(n), C.byref(steps), C.byref(acc),
+                                                C.byref(prop)))
+        return {"n": n.value, "steps": steps.value, "accepted": acc.value, "proposed": prop.value}
+
+    def tokens(self, start=0, n=None):
+        if n is None:
+            n = self.state()["n"] - start
+        out = np.empty(n, np.int32)
+        self.ctx._check(lib().ulspec_spec_tokens(self.handle, start, n, out.ctypes.data_as(P)))
+        return out
+
+    def set_graph(self, use_graph):
+        self.ctx._check(lib().ulspec_spec_set_graph(self.handle, 1 if use_graph else 0))
 
 
 def _ptr(b):

@@ -528,12 +528,19 @@ ulspec_status make_params(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t V,
 
 }  // namespace
 
-extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
-                                       uint32_t V, const float* target_logits, const float* draft_logits,
-                                       const int32_t* draft_tokens, const float* uniforms, int32_t* out_tokens,
-                                       int32_t* out_n_accepted)
+namespace ulspec {
+
+size_t accept_workspace_bytes(uint32_t B, uint32_t k)
 {
-    ULSPEC_CHECK_CTX(ctx);
+    return (size_t)(B * (k + 1) + B * k) * sizeof(RowStat);
+}
+
+size_t sample_workspace_bytes(uint32_t R) { return (size_t)R * sizeof(RowStat); }
+
+ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
+                            const float* target_logits, const float* draft_logits, const int32_t* draft_tokens,
+                            const float* uniforms, int32_t* out_tokens, int32_t* out_n_accepted, void* ws)
+{
     WarpParams p;
     ulspec_status st = make_params(ctx, s, V, p);
     if (st != ULSPEC_OK) return st;
@@ -544,11 +551,11 @@ extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s
     if (!p.greedy && (!draft_logits || !uniforms))
         return fail(ctx, ULSPEC_EINVAL, "accept: sampling needs draft logits and uniforms");
     const uint32_t rows_t = B * (k + 1), rows_d = p.greedy ? 0 : B * k;
-    void* ws = nullptr;
-    st = workspace(ctx, (size_t)(B * (k + 1) + B * k) * sizeof(RowStat), &ws);
-    if (st != ULSPEC_OK) return st;
+    if (!ws) {
+        st = workspace(ctx, accept_workspace_bytes(B, k), &ws);
+        if (st != ULSPEC_OK) return st;
+    }
     RowStat* stats = (RowStat*)ws;
-    (void)hipSetDevice(ctx->device);
     hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats);
     if (rows_d)
         hipLaunchKernelGGL(row_stats_kernel, dim3(rows_d), dim3(kRowThreads), 0, ctx->stream, draft_logits, V, p,
@@ -558,23 +565,43 @@ extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s
     return check_launch(ctx, "accept launch");
 }
 
-extern "C" ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
-                                       const float* logits, const float* uniforms, int32_t* out_tokens)
+ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
+                            const float* uniforms, int32_t* out_tokens, void* ws)
 {
-    ULSPEC_CHECK_CTX(ctx);
     WarpParams p;
     ulspec_status st = make_params(ctx, s, V, p);
     if (st != ULSPEC_OK) return st;
     if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
     if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
-    void* ws = nullptr;
-    st = workspace(ctx, (size_t)R * sizeof(RowStat), &ws);
-    if (st != ULSPEC_OK) return st;
-    (void)hipSetDevice(ctx->device);
+    if (!ws) {
+        st = workspace(ctx, sample_workspace_bytes(R), &ws);
+        if (st != ULSPEC_OK) return st;
+    }
     hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws);
     hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)ws, logits,
                        uniforms, V, p, out_tokens);
     return check_launch(ctx, "sample launch");
+}
+
+}  // namespace ulspec
+
+extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
+                                       uint32_t V, const float* target_logits, const float* draft_logits,
+                                       const int32_t* draft_tokens, const float* uniforms, int32_t* out_tokens,
+                                       int32_t* out_n_accepted)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    (void)hipSetDevice(ctx->device);
+    return accept_launch(ctx, s, B, k, V, target_logits, draft_logits, draft_tokens, uniforms, out_tokens,
+                         out_n_accepted, nullptr);
+}
+
+extern "C" ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
+                                       const float* logits, const float* uniforms, int32_t* out_tokens)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    (void)hipSetDevice(ctx->device);
+    return sample_launch(ctx, s, R, V, logits, uniforms, out_tokens, nullptr);
 }
 
 extern "C" ulspec_status ulspec_uniforms(ulspec_ctx* ctx, uint64_t seed, uint64_t idx0, uint32_t n, float* out)

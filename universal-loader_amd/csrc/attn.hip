@@ -37,14 +37,31 @@ struct AttnArgs {
     const _Float16* q;  // [nq][H][D]
     const _Float16* k;  // [L][Hkv][D]
     const _Float16* v;
-    float* out;         // [nq][H][D]
+    void* out;          // [nq][H][D], fp32 or (out_f16) fp16
     float* part;        // [splits][H][nq][D + 2]: O (unnormalised), m, l
+    const int32_t* dyn_prefix;  // if set, n_prefix = *dyn_prefix + prefix_add (read on the device)
+    int prefix_add;
     int n_prefix, nq, L, H, Hkv, splits, keys_per_split;
     float scale_log2;   // scale * log2(e)
+    int out_f16;
     uint32_t mask[kMaxQ];
 };
 
+__device__ __forceinline__ void store_out(const AttnArgs& a, size_t i, float v)
+{
+    if (a.out_f16) ((_Float16*)a.out)[i] = (_Float16)v;
+    else ((float*)a.out)[i] = v;
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Prefix length and total keys of this call (the split plan covers a.L keys;
+// a device-side prefix may make the actual length shorter).
+__device__ __forceinline__ void attn_len(const AttnArgs& a, int& n_prefix, int& L)
+{
+    n_prefix = a.dyn_prefix ? *a.dyn_prefix + a.prefix_add : a.n_prefix;
+    L = n_prefix + a.nq;
+}
 
 template <int D>
 __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
@@ -72,8 +89,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     for (int st = 0; st < D / 32; ++st)
         qb[st] = qvalid ? *(const half8_t*)(a.q + ((size_t)c * a.H + h) * D + 32 * st + 8 * g) : half8_t{};
 
+    int n_prefix, L;
+    attn_len(a, n_prefix, L);
     const int j0 = s * a.keys_per_split;
-    const int j1 = min(a.L, j0 + a.keys_per_split);
+    if (j0 >= L) return;  // only when the prefix is read on the device; merge skips it
+    const int j1 = min(L, j0 + a.keys_per_split);
     float m = -INFINITY, l = 0.0f;
     float4_t oacc[D / 16];
 #pragma unroll
@@ -103,7 +123,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int j = jt + 4 * g + r;
-            const bool vis = j < j1 && (j < a.n_prefix || ((mask >> (j - a.n_prefix)) & 1u));
+            const bool vis = j < j1 && (j < n_prefix || ((mask >> (j - n_prefix)) & 1u));
             s2[r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
             tmax = fmaxf(tmax, s2[r]);
         }
@@ -165,7 +185,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
             L += red_l[w][qi] * f;
         }
         if (a.splits == 1) {
-            a.out[((size_t)qi * a.H + h) * D + d] = o / L;
+            store_out(a, ((size_t)qi * a.H + h) * D + d, o / L);
         } else {
             float* pp = a.part + (((size_t)s * a.H + h) * a.nq + qi) * (D + 2);
             pp[d] = o;
@@ -184,17 +204,20 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
     const int h = blockIdx.x, qi = blockIdx.y, d = threadIdx.x;
     const size_t stride = (size_t)a.H * a.nq * (D + 2);
     const float* base = a.part + ((size_t)h * a.nq + qi) * (D + 2);
+    int n_prefix, len;
+    attn_len(a, n_prefix, len);
+    const int ns = min(a.splits, (len + a.keys_per_split - 1) / a.keys_per_split);
     float M = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, base[s * stride + D]);
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, base[s * stride + D]);
     const float Mu = M == -INFINITY ? 0.0f : M;
     float o = 0.0f, L = 0.0f;
-    for (int s = 0; s < a.splits; ++s) {
+    for (int s = 0; s < ns; ++s) {
         const float* pp = base + s * stride;
         const float f = exp2_fast(pp[D] - Mu);
         o += pp[d] * f;
         L += pp[D + 1] * f;
     }
-    a.out[((size_t)qi * a.H + h) * D + d] = o / L;
+    store_out(a, ((size_t)qi * a.H + h) * D + d, o / L);
 }
 
 template <int D>
@@ -228,52 +251,78 @@ size_t attn_workspace_bytes(int splits, int H, int nq, int D)
 
 }  // namespace ulspec
 
+namespace ulspec {
+
+ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
+{
+    if (!c.q || !c.k_cache || !c.v_cache || !c.out) return fail(ctx, ULSPEC_EINVAL, "verify_attention: null pointer");
+    if (c.nq == 0 || c.nq > (uint32_t)kMaxQ)
+        return fail(ctx, ULSPEC_EINVAL, "verify_attention: nq=%u not in [1, 16]", c.nq);
+    if (c.D != 64 && c.D != 128) return fail(ctx, ULSPEC_EUNSUPPORTED, "verify_attention: head dim %u (64 or 128)", c.D);
+    if (c.H == 0 || c.Hkv == 0 || c.H % c.Hkv) return fail(ctx, ULSPEC_EINVAL, "verify_attention: H=%u Hkv=%u", c.H, c.Hkv);
+    if (!(c.scale > 0.0f) || !std::isfinite(c.scale)) return fail(ctx, ULSPEC_EINVAL, "verify_attention: scale");
+    if ((uint64_t)c.n_prefix + c.nq > (uint64_t)INT32_MAX) return fail(ctx, ULSPEC_EINVAL, "verify_attention: length");
+    AttnArgs a;
+    a.q = (const _Float16*)c.q;
+    a.k = (const _Float16*)c.k_cache;
+    a.v = (const _Float16*)c.v_cache;
+    a.out = c.out;
+    a.out_f16 = c.out_f16 ? 1 : 0;
+    a.dyn_prefix = c.dyn_prefix;
+    a.prefix_add = c.prefix_add;
+    a.n_prefix = (int)c.n_prefix;  // with dyn_prefix: the largest prefix the call may see
+    a.nq = (int)c.nq;
+    a.L = (int)(c.n_prefix + c.nq);
+    a.H = (int)c.H;
+    a.Hkv = (int)c.Hkv;
+    a.scale_log2 = c.scale * 1.4426950408889634f;
+    for (int i = 0; i < kMaxQ; ++i) a.mask[i] = 0;
+    for (uint32_t i = 0; i < c.nq; ++i) {
+        uint32_t mk = 0;
+        if (!c.parent) {
+            mk = (1u << (i + 1)) - 1u;
+        } else {
+            if (c.parent[i] >= (int32_t)i || c.parent[i] < -1)
+                return fail(ctx, ULSPEC_EINVAL, "verify_attention: parent[%u]=%d must be in [-1, %u)", i, c.parent[i], i);
+            mk = 1u << i;
+            for (int32_t pnode = c.parent[i]; pnode >= 0; pnode = c.parent[pnode]) mk |= 1u << pnode;
+        }
+        a.mask[i] = mk;
+    }
+    attn_plan(a.L, a.H, ctx->n_cu, a.splits, a.keys_per_split);
+    if (c.dyn_prefix && a.splits == 1) a.splits = 2;  // keep the merge: the split kernel may return early
+    void* ws = c.part;
+    const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D);
+    if (wsb && !ws) {
+        ulspec_status st = workspace(ctx, wsb, &ws);
+        if (st != ULSPEC_OK) return st;
+    }
+    a.part = (float*)ws;
+    if (c.D == 128) launch_attn<128>(a, ctx->stream);
+    else launch_attn<64>(a, ctx->stream);
+    return check_launch(ctx, "verify_attention launch");
+}
+
+}  // namespace ulspec
+
 extern "C" ulspec_status ulspec_verify_attention(ulspec_ctx* ctx, const uint16_t* q, const uint16_t* k_cache,
                                                  const uint16_t* v_cache, uint32_t n_prefix, uint32_t nq,
                                                  const int32_t* parent, uint32_t H, uint32_t Hkv, uint32_t D,
                                                  float scale, float* out)
 {
     ULSPEC_CHECK_CTX(ctx);
-    if (!q || !k_cache || !v_cache || !out) return fail(ctx, ULSPEC_EINVAL, "verify_attention: null pointer");
-    if (nq == 0 || nq > (uint32_t)kMaxQ) return fail(ctx, ULSPEC_EINVAL, "verify_attention: nq=%u not in [1, 16]", nq);
-    if (D != 64 && D != 128) return fail(ctx, ULSPEC_EUNSUPPORTED, "verify_attention: head dim %u (64 or 128)", D);
-    if (H == 0 || Hkv == 0 || H % Hkv) return fail(ctx, ULSPEC_EINVAL, "verify_attention: H=%u Hkv=%u", H, Hkv);
-    if (!(scale > 0.0f) || !std::isfinite(scale)) return fail(ctx, ULSPEC_EINVAL, "verify_attention: scale");
-    if ((uint64_t)n_prefix + nq > (uint64_t)INT32_MAX) return fail(ctx, ULSPEC_EINVAL, "verify_attention: length");
-    AttnArgs a;
-    a.q = (const _Float16*)q;
-    a.k = (const _Float16*)k_cache;
-    a.v = (const _Float16*)v_cache;
-    a.out = out;
-    a.n_prefix = (int)n_prefix;
-    a.nq = (int)nq;
-    a.L = (int)(n_prefix + nq);
-    a.H = (int)H;
-    a.Hkv = (int)Hkv;
-    a.scale_log2 = scale * 1.4426950408889634f;
-    for (int i = 0; i < kMaxQ; ++i) a.mask[i] = 0;
-    for (uint32_t i = 0; i < nq; ++i) {
-        uint32_t mk = 0;
-        if (!parent) {
-            mk = (i == 31) ? 0xffffffffu : ((1u << (i + 1)) - 1u);
-        } else {
-            if (parent[i] >= (int32_t)i || parent[i] < -1)
-                return fail(ctx, ULSPEC_EINVAL, "verify_attention: parent[%u]=%d must be in [-1, %u)", i, parent[i], i);
-            mk = 1u << i;
-            for (int32_t pnode = parent[i]; pnode >= 0; pnode = parent[pnode]) mk |= 1u << pnode;
-        }
-        a.mask[i] = mk;
-    }
-    attn_plan(a.L, a.H, ctx->n_cu, a.splits, a.keys_per_split);
-    void* ws = nullptr;
-    const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)D);
-    if (wsb) {
-        ulspec_status st = workspace(ctx, wsb, &ws);
-        if (st != ULSPEC_OK) return st;
-    }
-    a.part = (float*)ws;
     (void)hipSetDevice(ctx->device);
-    if (D == 128) launch_attn<128>(a, ctx->stream);
-    else launch_attn<64>(a, ctx->stream);
-    return check_launch(ctx, "verify_attention launch");
+    AttnCall c;
+    c.q = q;
+    c.k_cache = k_cache;
+    c.v_cache = v_cache;
+    c.n_prefix = n_prefix;
+    c.nq = nq;
+    c.parent = parent;
+    c.H = H;
+    c.Hkv = Hkv;
+    c.D = D;
+    c.scale = scale;
+    c.out = out;
+    return attn_launch(ctx, c);
 }

@@ -1,0 +1,389 @@
+// model.cpp -- Llama-shaped model on the device: GGUF tensors by name, fp16
+// KV cache, and the block forward of InferenceEngine::forward_layer_gpu
+// (src/inference/inference_engine.cpp:602-682) over M <= 16 rows, with every
+// linear layer on the Q4 verify dequant-GEMM and attention on the verify
+// attention kernel.
+//
+// Weight map as Model::load_from_gguf (src/inference/model.cpp:190-246):
+// "blk.N." or "layers.N." layer prefixes, GGUF and Meta tensor names.  Q, K, V
+// rows are concatenated into one weight (one GEMM, output [M][(H+2Hkv)D]), and
+// so are gate and up ([M][2F]); GGUF rows are independent block runs, so the
+// concatenation is a byte copy.
+#include "model.h"
+
+#include <cmath>
+#include <cstring>
+
+#include "../layer_ops.h"
+
+using namespace ulspec;
+
+namespace {
+
+__global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
+
+// Which tensor a GGUF name is: layer (or -1 for globals) and a role.
+enum Role { R_NONE, R_EMBED, R_OUT_NORM, R_OUT, R_ATTN_NORM, R_Q, R_K, R_V, R_O, R_FFN_NORM, R_GATE, R_UP, R_DOWN };
+
+Role parse_name(const std::string& full, int& layer)
+{
+    layer = -1;
+    std::string name = full;
+    if (name.size() > 7 && name.compare(name.size() - 7, 7, ".weight") == 0) name.resize(name.size() - 7);
+    if (name == "token_embd" || name == "tok_embeddings") return R_EMBED;
+    if (name == "output_norm" || name == "norm") return R_OUT_NORM;
+    if (name == "output") return R_OUT;
+    size_t start = std::string::npos;
+    if (name.compare(0, 4, "blk.") == 0) start = 4;
+    else if (name.compare(0, 7, "layers.") == 0) start = 7;
+    if (start == std::string::npos) return R_NONE;
+    const size_t dot = name.find('.', start);
+    if (dot == std::string::npos || dot == start) return R_NONE;
+    long v = 0;
+    for (size_t i = start; i < dot; ++i) {
+        if (name[i] < '0' || name[i] > '9' || v > 1000000) return R_NONE;
+        v = v * 10 + (name[i] - '0');
+    }
+    layer = (int)v;
+    const std::string base = name.substr(dot + 1);
+    if (base == "attn_norm" || base == "attention_norm") return R_ATTN_NORM;
+    if (base == "attn_q" || base == "attention.wq") return R_Q;
+    if (base == "attn_k" || base == "attention.wk") return R_K;
+    if (base == "attn_v" || base == "attention.wv") return R_V;
+    if (base == "attn_output" || base == "attention.wo") return R_O;
+    if (base == "ffn_norm") return R_FFN_NORM;
+    if (base == "ffn_gate" || base == "mlp_gate" || base == "feed_forward.w1") return R_GATE;
+    if (base == "ffn_up" || base == "mlp_up" || base == "feed_forward.w3") return R_UP;
+    if (base == "ffn_down" || base == "mlp_down" || base == "feed_forward.w2") return R_DOWN;
+    return R_NONE;
+}
+
+size_t row_bytes(uint32_t type, uint64_t k)
+{
+    const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
+    return bs ? (size_t)(k / bs) * ts : 0;
+}
+
+ulspec_status dev_alloc(ulspec_model* m, size_t bytes, void** p)
+{
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return hip_fail(m->ctx, e, "model hipMalloc");
+    m->allocs.push_back(*p);
+    return ULSPEC_OK;
+}
+
+ulspec_status copy_in(ulspec_model* m, void* dst, const void* src, size_t bytes, bool on_device)
+{
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                  m->ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(m->ctx->stream);
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(m->ctx, e, "set_tensor copy");
+}
+
+}  // namespace
+
+namespace ulspec {
+void launch_set_i32(hipStream_t st, int32_t* p, int32_t v)
+{
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, st, p, v);
+}
+}  // namespace ulspec
+
+bool ulspec_model::complete() const
+{
+    if (!embed || !out_norm || w_out == ~0u) return false;
+    for (const Layer& L : layers)
+        if (L.wqkv == ~0u || L.wo == ~0u || L.wgu == ~0u || L.wdown == ~0u || !L.attn_norm || !L.ffn_norm)
+            return false;
+    return true;
+}
+
+ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
+                                    float* logits_dev, uint32_t n_logits)
+{
+    const ulspec_model_cfg& c = cfg;
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = head_dim, F = c.ffn;
+    hipStream_t st = ctx->stream;
+    const std::vector<Weight>& W = ctx->weights;
+    launch_embed(st, embed, embed_type, c.dim, tok_dev, M, c.vocab, h);
+    ulspec_status s = ULSPEC_OK;
+    for (uint32_t l = 0; l < c.n_layers && s == ULSPEC_OK; ++l) {
+        const Layer& L = layers[l];
+        launch_add_rmsnorm(st, h, l ? delta : nullptr, L.attn_norm, M, c.dim, c.rms_eps, x16);
+        s = gemm_launch(ctx, W[L.wqkv], (const uint16_t*)x16, M, qkv);
+        if (s != ULSPEC_OK) break;
+        launch_rope_append(st, qkv, M, H, Hkv, D, pos_dev, pos_add, rope, q16, L.kc, L.vc);
+        AttnCall a;
+        a.q = (const uint16_t*)q16;
+        a.k_cache = (const uint16_t*)L.kc;
+        a.v_cache = (const uint16_t*)L.vc;
+        a.n_prefix = c.max_ctx - M;
+        a.nq = M;
+        a.H = H;
+        a.Hkv = Hkv;
+        a.D = D;
+        a.scale = 1.0f / std::sqrt((float)D);
+        a.out = att16;
+        a.out_f16 = true;
+        a.dyn_prefix = pos_dev;
+        a.prefix_add = pos_add;
+        a.part = attn_part;
+        s = attn_launch(ctx, a);
+        if (s != ULSPEC_OK) break;
+        s = gemm_launch(ctx, W[L.wo], (const uint16_t*)att16, M, delta);
+        if (s != ULSPEC_OK) break;
+        launch_add_rmsnorm(st, h, delta, L.ffn_norm, M, c.dim, c.rms_eps, x16);
+        s = gemm_launch(ctx, W[L.wgu], (const uint16_t*)x16, M, gu);
+        if (s != ULSPEC_OK) break;
+        launch_silu_mul(st, gu, M, F, act16);
+        s = gemm_launch(ctx, W[L.wdown], (const uint16_t*)act16, M, delta);
+    }
+    if (s != ULSPEC_OK) return s;
+    launch_add_rmsnorm(st, h, delta, out_norm, M, c.dim, c.rms_eps, x16);
+    if (n_logits)
+        s = gemm_launch(ctx, W[w_out], (const uint16_t*)(x16 + (size_t)(M - n_logits) * c.dim), n_logits, logits_dev);
+    if (s != ULSPEC_OK) return s;
+    return check_launch(ctx, "model forward launch");
+}
+
+extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, ulspec_model** out)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!cfg || !out) return fail(ctx, ULSPEC_EINVAL, "model_create: null pointer");
+    const ulspec_model_cfg& c = *cfg;
+    if (c.n_heads == 0 || c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.dim % c.n_heads)
+        return fail(ctx, ULSPEC_EINVAL, "model_create: dim=%u heads=%u kv_heads=%u", c.dim, c.n_heads, c.n_kv_heads);
+    const uint32_t D = c.dim / c.n_heads;
+    if (D != 64 && D != 128) return fail(ctx, ULSPEC_EUNSUPPORTED, "model_create: head dim %u (64 or 128)", D);
+    if (c.n_layers == 0 || c.ffn == 0 || c.vocab == 0 || c.max_ctx < 2 || c.max_ctx > (1u << 24))
+        return fail(ctx, ULSPEC_EINVAL, "model_create: layers=%u ffn=%u vocab=%u max_ctx=%u", c.n_layers, c.ffn,
+                    c.vocab, c.max_ctx);
+    if (!(c.rms_eps > 0.0f) || !(c.rope_base > 1.0f) || !std::isfinite(c.rope_base))
+        return fail(ctx, ULSPEC_EINVAL, "model_create: rms_eps / rope_base");
+    (void)hipSetDevice(ctx->device);
+    ulspec_model* m = new ulspec_model;
+    m->ctx = ctx;
+    m->cfg = c;
+    m->head_dim = D;
+    m->layers.resize(c.n_layers);
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn, R = ulspec_model::kRows;
+    const size_t kv_bytes = (size_t)c.max_ctx * Hkv * D * sizeof(_Float16);
+    int splits = 0, kps = 0;
+    attn_plan((int)c.max_ctx, (int)H, ctx->n_cu, splits, kps);
+    if (splits < 2) splits = 2;
+    struct Want {
+        void** p;
+        size_t bytes;
+    } wants[] = {
+        {(void**)&m->h, (size_t)R * c.dim * 4},
+        {(void**)&m->delta, (size_t)R * c.dim * 4},
+        {(void**)&m->qkv, (size_t)R * (H + 2 * Hkv) * D * 4},
+        {(void**)&m->gu, (size_t)R * 2 * F * 4},
+        {(void**)&m->logits, (size_t)R * c.vocab * 4},
+        {(void**)&m->x16, (size_t)R * std::max(c.dim, F) * 2},
+        {(void**)&m->q16, (size_t)R * H * D * 2},
+        {(void**)&m->att16, (size_t)R * H * D * 2},
+        {(void**)&m->act16, (size_t)R * F * 2},
+        {(void**)&m->tok, (size_t)R * 4},
+        {(void**)&m->pos, 16},
+        {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},
+        {(void**)&m->rope, (size_t)c.max_ctx * (D / 2) * sizeof(float2)},
+    };
+    ulspec_status st = ULSPEC_OK;
+    for (const Want& w : wants)
+        if (st == ULSPEC_OK) st = dev_alloc(m, w.bytes, w.p);
+    for (uint32_t l = 0; l < c.n_layers && st == ULSPEC_OK; ++l) {
+        st = dev_alloc(m, kv_bytes, (void**)&m->layers[l].kc);
+        if (st == ULSPEC_OK) st = dev_alloc(m, kv_bytes, (void**)&m->layers[l].vc);
+    }
+    if (st == ULSPEC_OK) {
+        // RoPE angles theta_i = pos * base^(-2i / D) for pair i (src/shaders/rope.glsl:50-56),
+        // evaluated in double on the host, stored as fp32 (cos, sin).
+        std::vector<float2> tab((size_t)c.max_ctx * (D / 2));
+        for (uint32_t p = 0; p < c.max_ctx; ++p)
+            for (uint32_t i = 0; i < D / 2; ++i) {
+                const double th = (double)p * std::pow((double)c.rope_base, -2.0 * (double)i / (double)D);
+                tab[(size_t)p * (D / 2) + i] = make_float2((float)std::cos(th), (float)std::sin(th));
+            }
+        hipError_t e = hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "model rope table");
+    }
+    if (st != ULSPEC_OK) {
+        ulspec_model_destroy(m);
+        return st;
+    }
+    *out = m;
+    return ULSPEC_OK;
+}
+
+extern "C" void ulspec_model_destroy(ulspec_model* m)
+{
+    if (!m) return;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    for (void* p : m->allocs) (void)hipFree(p);
+    for (auto& kv : m->pending)
+        if (kv.second.dev) (void)hipFree(kv.second.dev);
+    delete m;
+}
+
+extern "C" ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* name, uint32_t type, const void* data,
+                                                 size_t nbytes, uint64_t ne0, uint64_t ne1, int on_device)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    if (!name || !data) return fail(ctx, ULSPEC_EINVAL, "set_tensor: null pointer");
+    const ulspec_model_cfg& c = m->cfg;
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = m->head_dim, F = c.ffn;
+    int layer = -1;
+    const Role role = parse_name(name, layer);
+    if (role == R_NONE) return fail(ctx, ULSPEC_EINVAL, "set_tensor: unknown tensor name '%s'", name);
+    if (layer >= (int)c.n_layers) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' beyond %u layers", name, c.n_layers);
+    const bool is_norm = role == R_OUT_NORM || role == R_ATTN_NORM || role == R_FFN_NORM;
+    // expected shape (ne0 = K, ne1 = rows)
+    uint64_t want0 = c.dim, want1 = 1;
+    switch (role) {
+    case R_EMBED: want1 = c.vocab; break;
+    case R_OUT: want1 = c.vocab; break;
+    case R_Q: want1 = (uint64_t)H * D; break;
+    case R_K:
+    case R_V: want1 = (uint64_t)Hkv * D; break;
+    case R_O: want0 = (uint64_t)H * D; want1 = c.dim; break;
+    case R_GATE:
+    case R_UP: want1 = F; break;
+    case R_DOWN: want0 = F; want1 = c.dim; break;
+    default: break;
+    }
+    if (ne0 != want0 || ne1 != want1)
+        return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' is %llu x %llu, expected %llu x %llu", name,
+                    (unsigned long long)ne0, (unsigned long long)ne1, (unsigned long long)want0,
+                    (unsigned long long)want1);
+    (void)hipSetDevice(ctx->device);
+    if (is_norm) {
+        if (type != 0) return fail(ctx, ULSPEC_EUNSUPPORTED, "set_tensor: norm '%s' must be F32 (type 0)", name);
+        if (nbytes != c.dim * 4) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' size %zu", name, nbytes);
+        float** dst = role == R_OUT_NORM ? &m->out_norm
+                      : role == R_ATTN_NORM ? &m->layers[layer].attn_norm : &m->layers[layer].ffn_norm;
+        if (!*dst) {
+            ulspec_status st = dev_alloc(m, nbytes, (void**)dst);
+            if (st != ULSPEC_OK) return st;
+        }
+        return copy_in(m, *dst, data, nbytes, on_device != 0);
+    }
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "set_tensor: '%s' type %u (Q4_0 / Q4_K only)", name, type);
+    const size_t rb = row_bytes(type, ne0);
+    if (rb == 0 || ne0 % ulspec_ggml_blck_size(type))
+        return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' row length %llu not a multiple of the block", name,
+                    (unsigned long long)ne0);
+    if (nbytes != rb * ne1) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' has %zu bytes, expected %zu", name, nbytes, rb * ne1);
+    if (role == R_EMBED) {
+        if (!m->embed) {
+            ulspec_status st = dev_alloc(m, nbytes, (void**)&m->embed);
+            if (st != ULSPEC_OK) return st;
+        }
+        m->embed_type = type;
+        return copy_in(m, m->embed, data, nbytes, on_device != 0);
+    }
+    if (role == R_OUT || role == R_O || role == R_DOWN) {
+        uint32_t* id = role == R_OUT ? &m->w_out : role == R_O ? &m->layers[layer].wo : &m->layers[layer].wdown;
+        if (*id != ~0u) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
+        return weight_create(ctx, type, data, nbytes, (uint32_t)ne1, (uint32_t)ne0, on_device != 0, id);
+    }
+    // fused groups: Q | K | V and gate | up
+    const bool qkv = role == R_Q || role == R_K || role == R_V;
+    const std::string key = std::to_string(layer) + (qkv ? ".qkv" : ".gu");
+    uint32_t* id = qkv ? &m->layers[layer].wqkv : &m->layers[layer].wgu;
+    if (*id != ~0u) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
+    const uint64_t rows_total = qkv ? (uint64_t)(H + 2 * Hkv) * D : 2ull * F;
+    const uint64_t row0 = role == R_Q ? 0 : role == R_K ? (uint64_t)H * D : role == R_V ? (uint64_t)(H + Hkv) * D
+                          : role == R_GATE ? 0 : F;
+    const uint32_t bit = role == R_Q || role == R_GATE ? 1u : role == R_K || role == R_UP ? 2u : 4u;
+    ulspec_model::Pending& p = m->pending[key];
+    if (!p.dev) {
+        hipError_t e = hipMalloc(&p.dev, rb * rows_total);
+        if (e != hipSuccess) {
+            m->pending.erase(key);
+            return hip_fail(ctx, e, "set_tensor staging");
+        }
+        p.type = type;
+        p.need = qkv ? 7u : 3u;
+    }
+    if (p.type != type) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' type differs from its fused group", name);
+    if (p.have & bit) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
+    ulspec_status st = copy_in(m, p.dev + rb * row0, data, nbytes, on_device != 0);
+    if (st != ULSPEC_OK) return st;
+    p.have |= bit;
+    if (p.have == p.need) {
+        st = weight_create(ctx, type, p.dev, rb * rows_total, (uint32_t)rows_total, (uint32_t)ne0, true, id);
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(p.dev);
+        m->pending.erase(key);
+        if (st != ULSPEC_OK) return st;
+    }
+    return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint32_t M, uint32_t pos,
+                                              float* logits, uint32_t n_logits)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    if (!tokens || M == 0) return fail(ctx, ULSPEC_EINVAL, "model_forward: no tokens");
+    if (n_logits > ulspec_model::kRows || n_logits > M || (n_logits && !logits))
+        return fail(ctx, ULSPEC_EINVAL, "model_forward: n_logits=%u (<= 16 and <= M, with an output)", n_logits);
+    if ((uint64_t)pos + M > m->cfg.max_ctx)
+        return fail(ctx, ULSPEC_EINVAL, "model_forward: positions %u + %u beyond max_ctx %u", pos, M, m->cfg.max_ctx);
+    if (!m->complete()) return fail(ctx, ULSPEC_EINVAL, "model_forward: model tensors missing");
+    for (uint32_t i = 0; i < M; ++i)
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= m->cfg.vocab)
+            return fail(ctx, ULSPEC_EINVAL, "model_forward: token %d out of range", tokens[i]);
+    (void)hipSetDevice(ctx->device);
+    // chunks of 16; the last chunk is the last min(16, M) rows (holds the logit rows)
+    const uint32_t R = ulspec_model::kRows;
+    const uint32_t last = M > R ? M - R : 0;
+    uint32_t m0 = 0;
+    while (true) {
+        const uint32_t mc = m0 < last ? std::min(R, last - m0) : M - m0;
+        const bool final_chunk = m0 + mc == M;
+        hipError_t e = hipMemcpyAsync(m->tok, tokens + m0, mc * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "model_forward tokens");
+        launch_set_i32(ctx->stream, m->pos, (int32_t)(pos + m0));
+        ulspec_status st = m->forward(m->tok, mc, m->pos, 0, m->logits, final_chunk ? n_logits : 0);
+        if (st != ULSPEC_OK) return st;
+        if (final_chunk) break;
+        m0 += mc;
+    }
+    if (n_logits) {
+        hipError_t e = hipMemcpyAsync(logits, m->logits, (size_t)n_logits * m->cfg.vocab * sizeof(float),
+                                      hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "model_forward logits");
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "model_forward sync");
+}
+
+extern "C" ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n,
+                                            uint16_t* k, uint16_t* v)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    if (layer >= m->cfg.n_layers || (uint64_t)pos0 + n > m->cfg.max_ctx || (dir != 0 && dir != 1) || (n && (!k || !v)))
+        return fail(ctx, ULSPEC_EINVAL, "model_kv_io: layer %u rows %u+%u dir %d", layer, pos0, n, dir);
+    (void)hipSetDevice(ctx->device);
+    const size_t row = (size_t)m->cfg.n_kv_heads * m->head_dim;
+    const size_t bytes = (size_t)n * row * sizeof(uint16_t);
+    _Float16* kc = m->layers[layer].kc + (size_t)pos0 * row;
+    _Float16* vc = m->layers[layer].vc + (size_t)pos0 * row;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess && bytes) {
+        if (dir == 0) {
+            e = hipMemcpy(k, kc, bytes, hipMemcpyDeviceToHost);
+            if (e == hipSuccess) e = hipMemcpy(v, vc, bytes, hipMemcpyDeviceToHost);
+        } else {
+            e = hipMemcpy(kc, k, bytes, hipMemcpyHostToDevice);
+            if (e == hipSuccess) e = hipMemcpy(vc, v, bytes, hipMemcpyHostToDevice);
+        }
+    }
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "model_kv_io copy");
+}

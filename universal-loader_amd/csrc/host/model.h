@@ -1,0 +1,64 @@
+// model.h -- device state of one Llama-shaped model and its forward pass
+// (shared by the model and speculative-loop translation units).
+#pragma once
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../ulspec_internal.h"
+
+struct ulspec_model {
+    // One fused weight assembled from several GGUF tensors (rows concatenated).
+    struct Pending {
+        uint8_t* dev = nullptr;   // staging, rows of all parts
+        uint32_t type = 0;
+        uint32_t have = 0;        // bitmask of parts received
+        uint32_t need = 0;
+    };
+    struct Layer {
+        uint32_t wqkv = ~0u, wo = ~0u, wgu = ~0u, wdown = ~0u;  // context weight ids
+        float* attn_norm = nullptr;
+        float* ffn_norm = nullptr;
+        _Float16* kc = nullptr;  // [max_ctx][Hkv][D]
+        _Float16* vc = nullptr;
+    };
+
+    ulspec_ctx* ctx = nullptr;
+    ulspec_model_cfg cfg{};
+    uint32_t head_dim = 0;
+    std::vector<Layer> layers;
+    std::map<std::string, Pending> pending;
+    uint8_t* embed = nullptr;  // raw GGUF [vocab][dim]
+    uint32_t embed_type = 0;
+    float* out_norm = nullptr;
+    uint32_t w_out = ~0u;
+    float2* rope = nullptr;    // [max_ctx][head_dim / 2] (cos, sin)
+
+    // activations, up to kRows rows
+    static constexpr uint32_t kRows = 16;
+    float* h = nullptr;        // [kRows][dim] residual stream
+    float* delta = nullptr;    // [kRows][dim] O / down projection output
+    float* qkv = nullptr;      // [kRows][(H + 2 Hkv) D]
+    float* gu = nullptr;       // [kRows][2 F]
+    float* logits = nullptr;   // [kRows][vocab]
+    _Float16* x16 = nullptr;   // [kRows][max(dim, F)]
+    _Float16* q16 = nullptr;   // [kRows][H D]
+    _Float16* att16 = nullptr; // [kRows][H D]
+    _Float16* act16 = nullptr; // [kRows][F]
+    int32_t* tok = nullptr;    // [kRows]
+    int32_t* pos = nullptr;    // [1]
+    float* attn_part = nullptr;
+    std::vector<void*> allocs;
+
+    bool complete() const;
+    // Forward M <= kRows tokens read from device memory at positions
+    // *pos_dev + pos_add ...; logits of the last n_logits rows to `logits`
+    // (device).  Asynchronous, never allocates or synchronises.
+    ulspec_status forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
+                          float* logits_dev, uint32_t n_logits);
+};
+
+namespace ulspec {
+void launch_set_i32(hipStream_t st, int32_t* p, int32_t v);
+}

@@ -802,10 +802,12 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
 
 }  // namespace ulspec
 
-extern "C" ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes,
-                                              uint32_t N, uint32_t K, uint32_t* out_id)
+namespace ulspec {
+
+// Re-tile raw GGUF blocks (host or device memory) into a new device weight.
+ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes, uint32_t N, uint32_t K,
+                            bool on_device, uint32_t* out_id)
 {
-    ULSPEC_CHECK_CTX(ctx);
     if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
     if (bs == 0) return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported", type);
@@ -825,15 +827,19 @@ extern "C" ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t type, co
     hipError_t e = hipMalloc(&w.dev, w.bytes);
     if (e != hipSuccess) return hip_fail(ctx, e, "weight_upload hipMalloc");
     void* raw = nullptr;
-    ulspec_status st = workspace(ctx, std::max(nbytes, gemm_workspace_bytes(w)), &raw);
+    ulspec_status st = workspace(ctx, std::max(on_device ? 0 : nbytes, gemm_workspace_bytes(w)), &raw);
     if (st != ULSPEC_OK) {
         (void)hipFree(w.dev);
         return st;
     }
-    e = hipMemcpyAsync(raw, blocks, nbytes, hipMemcpyHostToDevice, ctx->stream);
-    if (e != hipSuccess) {
-        (void)hipFree(w.dev);
-        return hip_fail(ctx, e, "weight_upload copy");
+    if (on_device) {
+        raw = const_cast<void*>(blocks);
+    } else {
+        e = hipMemcpyAsync(raw, blocks, nbytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(w.dev);
+            return hip_fail(ctx, e, "weight_upload copy");
+        }
     }
     if (type == ULSPEC_GGML_Q4_0) {
         const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
@@ -856,6 +862,15 @@ extern "C" ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t type, co
     *out_id = (uint32_t)ctx->weights.size();
     ctx->weights.push_back(w);
     return ULSPEC_OK;
+}
+
+}  // namespace ulspec
+
+extern "C" ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes,
+                                              uint32_t N, uint32_t K, uint32_t* out_id)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    return weight_create(ctx, type, blocks, nbytes, N, K, false, out_id);
 }
 
 extern "C" ulspec_status ulspec_weight_info(ulspec_ctx* ctx, uint32_t id, uint32_t* type, uint32_t* n, uint32_t* k,

@@ -68,6 +68,38 @@ inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
 // One-time kernel attributes of the dequant-GEMM (called by ulspec_create).
 ulspec_status gemm_init(ulspec_ctx* ctx);
 
+// Kernel launchers shared by the C ABI and the host engine (no validation of
+// device pointers; arguments checked as in the corresponding ABI entry point).
+ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y);
+size_t gemm_workspace_bytes(const Weight& w);
+ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes, uint32_t N, uint32_t K,
+                            bool on_device, uint32_t* out_id);
+struct AttnCall {
+    const uint16_t* q = nullptr;
+    const uint16_t* k_cache = nullptr;
+    const uint16_t* v_cache = nullptr;
+    uint32_t n_prefix = 0;   // with dyn_prefix: an upper bound of the prefix (sizes the split plan)
+    uint32_t nq = 0;
+    const int32_t* parent = nullptr;  // host array, NULL = causal
+    uint32_t H = 0, Hkv = 0, D = 0;
+    float scale = 0.0f;
+    void* out = nullptr;
+    bool out_f16 = false;
+    const int32_t* dyn_prefix = nullptr;  // device int: prefix = *dyn_prefix + prefix_add
+    int prefix_add = 0;
+    void* part = nullptr;    // split partials; NULL = the context workspace
+};
+ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c);
+void attn_plan(int L, int H, int n_cu, int& splits, int& kps);
+size_t attn_workspace_bytes(int splits, int H, int nq, int D);
+size_t accept_workspace_bytes(uint32_t B, uint32_t k);
+size_t sample_workspace_bytes(uint32_t R);
+ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
+                            const float* target_logits, const float* draft_logits, const int32_t* draft_tokens,
+                            const float* uniforms, int32_t* out_tokens, int32_t* out_n_accepted, void* ws);
+ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
+                            const float* uniforms, int32_t* out_tokens, void* ws);
+
 // Grow the context workspace to at least `bytes` (stream-ordered reuse).
 ulspec_status workspace(ulspec_ctx* ctx, size_t bytes, void** out);
 
