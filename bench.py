@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Benchmark: accepted tokens/sec of the speculative decoding loop at 7B shape.
+
+Workload: random-init (synthetic) Llama target -- dim 4096, 32 layers, 32
+heads, FFN 11008, vocab 32000 -- and draft -- dim 2048, 16 layers, 16 heads,
+FFN 5632 -- all linear layers, the embedding and the LM head GGUF Q4_K; a
+seeded prompt of 2048 tokens (prefill untimed); k = 5 draft tokens per step;
+batch 1; temperature 0.8 over the full vocabulary (--greedy: argmax rule).
+One step = 5 draft forwards + one target forward over 6 rows + acceptance +
+commit, replayed from a captured HIP graph.  Inputs live in HBM before the
+timed region starts.
+
+Printed (one JSON line): value = committed tokens / wall seconds over exactly
+--steps steps, bracketed by stream synchronisations; "roofline" for the verify
+dequant-GEMM (the dominant kernel): algorithmic bytes of the target's 129
+verify GEMMs at M = 6 over their average duration, measured with HIP events
+on the context stream; "cpu_baseline": the CPU restatement timed on the host
+on the first recorded steps (from the GPU's post-prefill KV cache), with the
+step-by-step parity of the draws and accept decisions.
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(REPO, "universal-loader_amd")
+
+TARGET = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=32, ffn=11008, vocab=32000, rms_eps=1e-5,
+              rope_base=10000.0)
+DRAFT = dict(dim=2048, n_layers=16, n_heads=16, n_kv_heads=16, ffn=5632, vocab=32000, rms_eps=1e-5,
+             rope_base=10000.0)
+CONTEXT = 2048
+K_SPEC = 5
+HBM_PEAK_GBS = 8000.0
+METRIC = "accepted tokens/sec, 7B-shape Q4_K k=5 bs=1; verify-GEMM HBM GB/s % of peak"
+
+
+def load_package():
+    spec = importlib.util.spec_from_file_location("universal_loader_amd", os.path.join(PKG_DIR, "__init__.py"),
+                                                  submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["universal_loader_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def weight_ids(pkg, ctx):
+    """Ids and (type, N, K) of every weight on the context, in creation order."""
+    out = []
+    while True:
+        try:
+            out.append((len(out), ctx.weight_info(len(out))))
+        except pkg.UlspecError:
+            return out
+
+
+def gemm_roofline(pkg, ctx, ids, M, reps=10):
+    """Average duration and algorithmic bytes of the verify GEMM over the given
+    weights at M rows: reps rounds of back-to-back launches over all weights
+    (direct launches, so that a profiler sees every dispatch), HIP events on
+    the context stream around them."""
+    kmax = max(info[2] for _, info in ids)
+    nmax = max(info[1] for _, info in ids)
+    rng = np.random.default_rng(0)
+    x = ctx.upload(rng.standard_normal((M, kmax)).astype(np.float16).view(np.uint16))
+    y = ctx.alloc(M * nmax * 4)
+    for wid, _ in ids:  # warm-up round
+        ctx.verify_gemm(wid, x, M, y)
+    ctx.sync()
+    ctx.timer_mark(2)
+    for _ in range(reps):
+        for wid, _ in ids:
+            ctx.verify_gemm(wid, x, M, y)
+    ctx.timer_mark(3)
+    ms = ctx.timer_elapsed_ms(2, 3)
+    x.free()
+    y.free()
+    launches = reps * len(ids)
+    alg = 0.0
+    for _, (wtype, n, k, _) in ids:
+        w_bytes = n * k * (144 / 256 if wtype == pkg.Q4_K else 18 / 32)
+        alg += w_bytes + 2 * M * k + 4 * M * n
+    us = ms * 1e3 / launches
+    return us, alg / len(ids)
+
+
+def read_traffic():
+    """HBM bytes per launch of the verify GEMM from the committed PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(REPO, "profiles", "verify_gemm_q4k_7b_m6_pmc.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, n0):
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as ora
+    nt = ora.nthreads_default()
+    s = ora.sampling(greedy=True) if args.greedy else ora.sampling(temperature=args.temperature)
+    models = []
+    for cfg, host, kv in ((TARGET, target_host, kv_t), (DRAFT, draft_host, kv_d)):
+        m = ora.Llama(**cfg, max_ctx=cap, nthreads=nt)
+        for name, (wtype, data, ne0, ne1) in host.items():
+            m.set_tensor(name, wtype, data, ne0, ne1)
+        for l, (k, v) in enumerate(kv):
+            m.kv_io(l, 1, 0, n0 - 1, k, v)
+        models.append(m)
+    ot, od = models
+    k = K_SPEC
+    busy = 0.0
+    steps = tokens = 0
+    draws_exact = accept_exact = own_agree = True
+    worst = 0.0
+    for n, r in recorded:
+        if busy > args.cpu_seconds:
+            break
+        d, u = r["draft_tokens"], r["uniforms"]
+        t0 = time.perf_counter()
+        # the CPU path's own step on the GPU's committed tokens and draft tokens
+        dl = [od.forward(seq[n - 2:n], n - 2, n_logits=1)[0]]
+        own_d = [ora.sample(s, dl[0][None], u[0:1])[0]]
+        for j in range(1, k):
+            dl.append(od.forward(d[j - 1:j], n - 1 + j, n_logits=1)[0])
+            own_d.append(ora.sample(s, dl[j][None], u[j:j + 1])[0])
+        dl = np.array(dl)
+        tl = ot.forward(np.concatenate([[seq[n - 1]], d]).astype(np.int32), n - 1, n_logits=k + 1)
+        out_c, nacc_c = ora.accept(s, tl[None], dl[None], d[None], u[k:][None])
+        busy += time.perf_counter() - t0
+        steps += 1
+        tokens += int(nacc_c[0]) + 1
+        # parity against the GPU step (checker, untimed)
+        for j in range(k):
+            draws_exact &= bool(ora.sample(s, r["draft_logits"][j:j + 1], u[j:j + 1])[0] == d[j])
+        out_g, nacc_g = ora.accept(s, r["target_logits"][None], r["draft_logits"][None], d[None], u[k:][None])
+        accept_exact &= bool(int(nacc_g[0]) == r["n_accepted"] and np.array_equal(out_g[0], r["out_tokens"]))
+        own_agree &= bool(int(nacc_c[0]) == r["n_accepted"] and list(own_d) == list(d))
+        for a, b in ((r["draft_logits"], dl), (r["target_logits"], tl)):
+            b64 = b.astype(np.float64)
+            worst = max(worst, float(np.abs(a - b64).max() / np.sqrt((b64 ** 2).mean())))
+    for m in models:
+        m.close()
+    mode = "greedy" if args.greedy else f"T={args.temperature}"
+    return {
+        "value": tokens / busy if busy else None, "unit": "tokens/s", "cores": nt, "kind": "port",
+        "sample": f"{steps} speculative steps (k=5, {mode}) of the 7B-shape Q4_K target/draft pair at context "
+                  f"{n0}, from the GPU's post-prefill KV cache; oracle/ C restatement, AVX2 f32 GEMM, {nt} threads",
+        "parity": {"steps": steps, "draft_draws_bit_exact": draws_exact, "accept_bit_exact": accept_exact,
+                   "cpu_decisions_equal_gpu": own_agree, "logits_max_err_over_rms": worst},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--greedy", action="store_true")
+    ap.add_argument("--temperature", type=float, default=0.8)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch each step's kernels directly instead of replaying the captured graph")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build measures the single-GPU "
+              "speculative step; sharding across GPUs is not implemented.", file=sys.stderr)
+        return 2
+    pkg = load_package()
+    synthetic_llama = importlib.import_module("universal_loader_amd.synthetic").synthetic_llama
+    ctx = pkg.Context(0)
+    use_cpu = not args.no_cpu
+    cpu_steps = args.cpu_steps if use_cpu else 0
+    cap = CONTEXT + (cpu_steps + args.warmup + args.steps) * (K_SPEC + 1) + 32
+    t0 = time.perf_counter()
+    target, th = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=cap), pkg.Q4_K, seed=1, keep_host=use_cpu)
+    n_target_w = len(weight_ids(pkg, ctx))
+    draft, dh = synthetic_llama(pkg, ctx, dict(DRAFT, max_ctx=cap), pkg.Q4_K, seed=2, keep_host=use_cpu)
+    t_synth = time.perf_counter() - t0
+    log(f"weights synthesized and uploaded in {t_synth:.1f} s")
+    prompt = np.random.default_rng(args.seed).integers(0, TARGET["vocab"], CONTEXT).astype(np.int32)
+    s = pkg.sampling(greedy=True) if args.greedy else pkg.sampling(temperature=args.temperature)
+    sp = pkg.Speculative(target, draft, K_SPEC, s, args.seed)
+    sp.set_graph(not args.no_graph)
+    t0 = time.perf_counter()
+    sp.prefill(prompt)
+    t_prefill = time.perf_counter() - t0
+    log(f"prefill of {CONTEXT} tokens in {t_prefill:.1f} s")
+    recorded, kv_t, kv_d = [], None, None
+    if use_cpu:
+        kv_t = [target.kv_io(l, 0, 0, CONTEXT - 1) for l in range(TARGET["n_layers"])]
+        kv_d = [draft.kv_io(l, 0, 0, CONTEXT - 1) for l in range(DRAFT["n_layers"])]
+        for _ in range(cpu_steps):
+            n = sp.state()["n"]
+            sp.steps(1)
+            recorded.append((n, sp.last_step()))
+    sp.steps(args.warmup)
+    st0 = sp.state()
+    ctx.sync()
+    ctx.timer_mark(0)
+    t0 = time.perf_counter()
+    sp.steps(args.steps)
+    ctx.timer_mark(1)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    ev_ms = ctx.timer_elapsed_ms(0, 1)
+    st1 = sp.state()
+    tokens = st1["n"] - st0["n"]
+    accepted = st1["accepted"] - st0["accepted"]
+    proposed = st1["proposed"] - st0["proposed"]
+    log(f"{args.steps} steps: {tokens} tokens in {wall * 1e3:.1f} ms (events {ev_ms:.1f} ms), "
+        f"accepted {accepted}/{proposed}")
+    ids = [(i, info) for i, info in weight_ids(pkg, ctx)[:n_target_w]]
+    us, alg = gemm_roofline(pkg, ctx, ids, K_SPEC + 1)
+    achieved = alg / (us * 1e-6) / 1e9
+    log(f"verify GEMM (target, M=6): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
+        f"{achieved:.0f} GB/s")
+    seq = sp.tokens() if use_cpu else None
+    sp.close()
+    cpu = None
+    if use_cpu:
+        cpu = cpu_leg(pkg, args, th, dh, kv_t, kv_d, recorded, seq, cap, CONTEXT)
+        log(f"cpu baseline: {cpu}")
+    mode = "greedy" if args.greedy else f"temperature {args.temperature}, full vocabulary"
+    out = {
+        "metric": METRIC, "value": tokens / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights x fp16 activations, fp32 accumulate",
+        "data": "synthetic: random-init N(0, 0.02^2) weights quantized to Q4_K on the device, seeded prompt",
+        "config": {"workload": f"speculative decoding step, 7B-shape Q4_K target (dim 4096, 32 layers, 32 heads, "
+                               f"FFN 11008, vocab 32000) + draft (dim 2048, 16 layers, 16 heads, FFN 5632), k=5, "
+                               f"bs=1, context {CONTEXT}, {mode}",
+                   "k": K_SPEC, "batch": 1, "context": CONTEXT, "acceptance": accepted / max(1, proposed),
+                   "tokens": tokens, "event_ms": ev_ms},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
+                     "kernel": "verify dequant-GEMM (gemm_q4_k_wide_kernel), target weights, M=6",
+                     "avg_us": us, "algorithmic_bytes": alg},
+        "cpu_baseline": cpu,
+    }
+    target.close()
+    draft.close()
+    ctx.close()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

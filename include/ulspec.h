@@ -219,6 +219,13 @@ ulspec_status ulspec_spec_state(ulspec_spec* sp, uint32_t* n_tokens, uint64_t* s
                                 uint64_t* proposed);
 /* Committed tokens start .. start+n-1 to host memory.  Synchronous. */
 ulspec_status ulspec_spec_tokens(ulspec_spec* sp, uint32_t start, uint32_t n, int32_t* out);
+/* Inputs and outputs of the last step, copied to host arrays (any may be
+ * NULL): target logits [k+1][V], draft logits [k][V], draft tokens [k],
+ * uniforms [2k+1], emitted tokens [k+1] (-1 padded), n_accepted.
+ * Synchronous.  For checking a step against a CPU restatement. */
+ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
+                                    int32_t* draft_tokens, float* uniforms, int32_t* out_tokens,
+                                    int32_t* n_accepted);
 /* use_graph != 0 (default): replay the step captured as a HIP graph;
  * 0: launch the step's kernels directly on the stream. */
 ulspec_status ulspec_spec_set_graph(ulspec_spec* sp, int use_graph);

@@ -2,8 +2,10 @@
 graph replay) against the oracle, through the C ABI.
 
 Bar: the committed token sequences and acceptance counters are bit-exact with
-the oracle's loop on the same weights, prompt and seed; model logits agree
-within 1e-3 of their RMS (fp32 accumulation in different orders).
+the oracle's loop on the same weights, prompt and seed.  Model logits agree
+within 1e-2 of their RMS: every layer rounds its GEMM inputs to fp16, and an
+fp32 sum taken in another order lands on the other side of an fp16 rounding
+now and then; such one-ulp flips (5e-4 relative) carry through the layers.
 """
 import numpy as np
 import pytest
@@ -48,8 +50,8 @@ def test_model_forward_logits_and_cache(pkg, ctx, ora, weights, prompt):
     lo = o.forward(prompt[:40], 0, n_logits=16)
     scale = np.sqrt((lo.astype(np.float64) ** 2).mean())
     err = np.abs(lg.astype(np.float64) - lo).max() / scale
-    print(f"  logits max err / rms = {err:.2e}")
-    assert err <= 1e-3
+    print(f"  logits max err / rms = {err:.2e}, mean {np.abs(lg - lo).mean() / scale:.2e}")
+    assert err <= 1e-2
     assert np.array_equal(np.argmax(lg, axis=1), np.argmax(lo, axis=1))
     for l in (0, TARGET["n_layers"] - 1):
         kg, vg = g.kv_io(l, 0, 0, 40)
@@ -70,29 +72,82 @@ def test_forward_rows_are_batch_invariant(pkg, ctx, weights, prompt):
     b.close()
 
 
-@pytest.mark.parametrize("mode", ["greedy", "t0.8"])
-def test_speculative_tokens_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt, mode):
+def test_greedy_tokens_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
+    """Free-running greedy decoding: the whole committed sequence and the
+    counters equal the oracle's (argmax decisions are robust to the fp32
+    summation order)."""
     tw, dw = weights
     k, n_new, seed = 4, 128, 2024
-    s_gpu = pkg.sampling(greedy=True) if mode == "greedy" else pkg.sampling(temperature=0.8)
-    s_ora = ora.sampling(greedy=True) if mode == "greedy" else ora.sampling(temperature=0.8)
     gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
-    sp = pkg.Speculative(gt, gd, k, s_gpu, seed)
+    sp = pkg.Speculative(gt, gd, k, pkg.sampling(greedy=True), seed)
     sp.prefill(prompt)
     n = sp.generate(n_new)
     got, st = sp.tokens(), sp.state()
     ot, od = _ora_model(ora, TARGET, tw), _ora_model(ora, DRAFT, dw)
-    osp = ora.Speculative(ot, od, k, s_ora, seed)
+    osp = ora.Speculative(ot, od, k, ora.sampling(greedy=True), seed)
     osp.prefill(prompt)
     on = osp.generate(n_new)
-    want, ost = osp.tokens(), osp.state()
-    print(f"  {mode}: {n} tokens in {st['steps']} steps, accepted {st['accepted']}/{st['proposed']}")
+    print(f"  greedy: {n} tokens in {st['steps']} steps, accepted {st['accepted']}/{st['proposed']}")
     assert n == on and n >= n_new
-    assert np.array_equal(got, want)
-    assert st == ost
-    sp.close()
-    gt.close()
-    gd.close()
+    assert np.array_equal(got, osp.tokens())
+    assert st == osp.state()
+    for m in (sp, gt, gd):
+        m.close()
+
+
+def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
+    """Temperature 0.8 over the full vocabulary, step by step: the oracle runs
+    the same step on the GPU's committed sequence and draft tokens (teacher
+    forcing).  Every draft draw and every accept decision is bit-exact with the
+    oracle's rule on the step's logits; the oracle's own logits for the same
+    tokens agree within 1e-2 of their RMS.  (Free-running sequences are not
+    compared token for token: an inverse-CDF draw over 32000 tokens moves when
+    the logits move by 1e-4, so fp32 order differences change some draws.)"""
+    tw, dw = weights
+    k, n_new, seed = 4, 128, 2024
+    s_gpu, s_ora = pkg.sampling(temperature=0.8), ora.sampling(temperature=0.8)
+    gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
+    sp = pkg.Speculative(gt, gd, k, s_gpu, seed)
+    sp.prefill(prompt)
+    ot, od = _ora_model(ora, TARGET, tw), _ora_model(ora, DRAFT, dw)
+    ot.forward(prompt[:-1], 0)
+    od.forward(prompt[:-1], 0)
+    seq = list(prompt)
+    worst = 0.0
+    steps = accepted = 0
+    while len(seq) - len(prompt) < n_new:
+        n = len(seq)
+        sp.steps(1)
+        r = sp.last_step()
+        u = r["uniforms"]
+        want_u = np.array([ora.uniforms(seed, steps * (2 * k + 1) + j, 1)[0] for j in range(2 * k + 1)], np.float32)
+        assert np.array_equal(u.view(np.uint32), want_u.view(np.uint32))
+        # draft draws
+        for j in range(k):
+            assert ora.sample(s_ora, r["draft_logits"][j:j + 1], u[j:j + 1])[0] == r["draft_tokens"][j], (steps, j)
+        # accept rule on the step's logits
+        out, nacc = ora.accept(s_ora, r["target_logits"][None], r["draft_logits"][None], r["draft_tokens"][None],
+                               u[k:][None])
+        assert int(nacc[0]) == r["n_accepted"] and np.array_equal(out[0], r["out_tokens"]), steps
+        # the oracle's logits for the same tokens
+        d = r["draft_tokens"]
+        dl = [od.forward(np.array(seq[n - 2:n], np.int32), n - 2, n_logits=1)[0]]
+        for j in range(1, k):
+            dl.append(od.forward(d[j - 1:j], n - 1 + j, n_logits=1)[0])
+        tl = ot.forward(np.concatenate([[seq[n - 1]], d]).astype(np.int32), n - 1, n_logits=k + 1)
+        for a, b in ((r["draft_logits"], np.array(dl)), (r["target_logits"], tl)):
+            worst = max(worst, np.abs(a.astype(np.float64) - b).max() / np.sqrt((b.astype(np.float64) ** 2).mean()))
+        seq += list(r["out_tokens"][:r["n_accepted"] + 1])
+        steps += 1
+        accepted += r["n_accepted"]
+    st = sp.state()
+    assert np.array_equal(sp.tokens(), np.array(seq, np.int32))
+    assert st["steps"] == steps and st["accepted"] == accepted and st["proposed"] == k * steps
+    print(f"  t0.8: {len(seq) - len(prompt)} tokens in {steps} steps, accepted {accepted}/{k * steps}, "
+          f"logits max err / rms {worst:.2e}")
+    assert worst <= 1e-2
+    for m in (sp, gt, gd):
+        m.close()
 
 
 def test_graph_replay_equals_direct_launches(pkg, ctx, weights, prompt):
@@ -169,7 +224,7 @@ def test_model_and_spec_argument_errors(pkg, ctx, weights):
     with pytest.raises(pkg.UlspecError) as e:
         m.set_tensor("blk.9.attn_q.weight", *tw["blk.0.attn_q.weight"])
     assert e.value.status == pkg.EINVAL
-    name = "blk.0.attn_output.weight"
+    name = "blk.0.ffn_down.weight"
     wtype, data, ne0, ne1 = tw[name]
     with pytest.raises(pkg.UlspecError) as e:
         m.set_tensor(name, wtype, data, ne1, ne0)  # transposed shape

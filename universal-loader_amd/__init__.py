@@ -115,6 +115,7 @@ ABI = [
     ("ulspec_spec_state", C.c_int, [P, C.POINTER(U32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                     C.POINTER(C.c_uint64)]),
     ("ulspec_spec_tokens", C.c_int, [P, U32, U32, P]),
+    ("ulspec_spec_last_step", C.c_int, [P, P, P, P, P, P, P]),
     ("ulspec_spec_set_graph", C.c_int, [P, C.c_int]),
 ]
 
@@ -354,6 +355,16 @@ class Speculative:
         out = np.empty(n, np.int32)
         self.ctx._check(lib().ulspec_spec_tokens(self.handle, start, n, out.ctypes.data_as(P)))
         return out
+
+    def last_step(self):
+        """Inputs and outputs of the last step (host copies)."""
+        k, V = self.k, self.target.cfg.vocab
+        r = {"target_logits": np.empty((k + 1, V), np.float32), "draft_logits": np.empty((k, V), np.float32),
+             "draft_tokens": np.empty(k, np.int32), "uniforms": np.empty(2 * k + 1, np.float32),
+             "out_tokens": np.empty(k + 1, np.int32), "n_accepted": np.empty(1, np.int32)}
+        self.ctx._check(lib().ulspec_spec_last_step(self.handle, *[a.ctypes.data_as(P) for a in r.values()]))
+        r["n_accepted"] = int(r["n_accepted"][0])
+        return r
 
     def set_graph(self, use_graph):
         self.ctx._check(lib().ulspec_spec_set_graph(self.handle, 1 if use_graph else 0))

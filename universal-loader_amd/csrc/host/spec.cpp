@@ -333,6 +333,29 @@ extern "C" ulspec_status ulspec_spec_tokens(ulspec_spec* sp, uint32_t start, uin
     return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_tokens copy");
 }
 
+extern "C" ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
+                                               int32_t* draft_tokens, float* uniforms, int32_t* out_tokens,
+                                               int32_t* n_accepted)
+{
+    if (!sp) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = sp->ctx;
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    const size_t k = sp->k, V = sp->V;
+    struct Copy {
+        void* dst;
+        const void* src;
+        size_t bytes;
+    } copies[] = {
+        {target_logits, sp->tlogits, (k + 1) * V * 4}, {draft_logits, sp->dlogits, k * V * 4},
+        {draft_tokens, sp->dtok, k * 4},                {uniforms, sp->unif, (2 * k + 1) * 4},
+        {out_tokens, sp->out_tok, (k + 1) * 4},         {n_accepted, sp->nacc, 4},
+    };
+    for (const Copy& c : copies)
+        if (e == hipSuccess && c.dst) e = hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_last_step copy");
+}
+
 extern "C" ulspec_status ulspec_spec_set_graph(ulspec_spec* sp, int use_graph)
 {
     if (!sp) return ULSPEC_EINVAL;
