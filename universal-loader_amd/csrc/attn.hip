@@ -8,7 +8,8 @@
 //
 // Split-KV ("flash-decoding"): grid (heads, splits); a workgroup of 4 waves
 // owns a contiguous key range of one head, each wave takes every 4th 16-key
-// tile of it.  Per tile:
+// tile of it and issues the loads of all its tiles before the first MFMA (one
+// memory round trip per wave).  Per tile:
 //   S^T[key][query] = K_tile . Q^T        16x16x32 fp16 MFMA, K loaded from
 //                                         global straight into the A layout
 //   online softmax per query in the log2 domain (fp32)
@@ -17,8 +18,10 @@
 //                                         P^T operand layout; P = P_hi + P_lo
 //                                         (two fp16 parts) keeps fp32 accuracy;
 //                                         V goes through LDS for the transpose
-// The 4 waves are merged in LDS; splits are merged by a second kernel in
-// split order (deterministic).  Visibility of the nq new keys (rows
+// The 4 waves are merged in LDS; each workgroup writes its partial (O, m, l)
+// and a second kernel merges the splits in split order (deterministic).  (A
+// merge by the last workgroup to finish, behind an atomic counter, costs more
+// here: the device-scope release before the count writes back the L2.)  Visibility of the nq new keys (rows
 // n_prefix .. L-1) is a per-query bitmask built on the host from the parent
 // array; prefix keys are visible to every query.
 #include "hip_common.h"
@@ -32,13 +35,14 @@ namespace {
 
 constexpr int kAttnWaves = 4;
 constexpr int kMaxQ = 16;
+constexpr int kAttnMaxSplits = 64;
 
 struct AttnArgs {
     const _Float16* q;  // [nq][H][D]
     const _Float16* k;  // [L][Hkv][D]
     const _Float16* v;
     void* out;          // [nq][H][D], fp32 or (out_f16) fp16
-    float* part;        // [splits][H][nq][D + 2]: O (unnormalised), m, l
+    float* part;        // [H][splits][nq][D + 2]: O (unnormalised), m, l
     const int32_t* dyn_prefix;  // if set, n_prefix = *dyn_prefix + prefix_add (read on the device)
     int prefix_add;
     int n_prefix, nq, L, H, Hkv, splits, keys_per_split;
@@ -63,8 +67,8 @@ __device__ __forceinline__ void attn_len(const AttnArgs& a, int& n_prefix, int& 
     L = n_prefix + a.nq;
 }
 
-template <int D>
-__global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
+template <int D, int T>
+__global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 {
     constexpr int VP = D + 8;  // V tile row pitch in halfs (16 B pad spreads banks)
     __shared__ _Float16 vt[kAttnWaves][16 * VP];
@@ -77,10 +81,11 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
     const int hk = h / (a.H / a.Hkv);
     const size_t row_stride = (size_t)a.Hkv * D;
 
-    uint32_t mask = 0;
-#pragma unroll
-    for (int i = 0; i < kMaxQ; ++i)
-        if (c == i) mask = a.mask[i];
+    int n_prefix, L;
+    attn_len(a, n_prefix, L);
+    const int j0 = s * a.keys_per_split;
+    if (j0 >= L) return;  // only when the prefix is read on the device
+    const int j1 = min(L, j0 + a.keys_per_split);
 
     // Q^T operand: lane (query c, group g) holds Q[c][h][32 st + 8 g .. +7]
     half8_t qb[D / 32];
@@ -88,75 +93,84 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
     for (int st = 0; st < D / 32; ++st)
         qb[st] = qvalid ? *(const half8_t*)(a.q + ((size_t)c * a.H + h) * D + 32 * st + 8 * g) : half8_t{};
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxQ; ++i)
+        if (c == i) mask = a.mask[i];
 
-    int n_prefix, L;
-    attn_len(a, n_prefix, L);
-    const int j0 = s * a.keys_per_split;
-    if (j0 >= L) return;  // only when the prefix is read on the device; merge skips it
-    const int j1 = min(L, j0 + a.keys_per_split);
     float m = -INFINITY, l = 0.0f;
     float4_t oacc[D / 16];
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
     _Float16* myv = vt[wave];
 
-    for (int jt0 = j0; jt0 < j1; jt0 += 16 * kAttnWaves) {
-        const int jt = jt0 + 16 * wave;
-        // K rows (A operand) and V rows (to LDS): lane (key c, group g)
-        const int key = jt + c;
-        const bool kvalid = key < j1;
-        const size_t kbase = (size_t)(kvalid ? key : j0) * row_stride + (size_t)hk * D + 8 * g;
-        half8_t ka[D / 32];
+    // rounds of 64 T keys; in each, every K / V load of the wave is issued
+    // first: tile i covers keys jr + 16 (wave + 4 i) ..
+    for (int jr = j0; jr < j1; jr += 16 * kAttnWaves * T) {
+        half8_t ka[T][D / 32], va[T][D / 32];
 #pragma unroll
-        for (int st = 0; st < D / 32; ++st) ka[st] = *(const half8_t*)(a.k + kbase + 32 * st);
+        for (int i = 0; i < T; ++i) {
+            const int key = jr + 16 * (wave + kAttnWaves * i) + c;
+            const size_t kbase = (size_t)(key < j1 ? key : j0) * row_stride + (size_t)hk * D + 8 * g;
 #pragma unroll
-        for (int st = 0; st < D / 32; ++st)
-            *(half8_t*)(myv + c * VP + 32 * st + 8 * g) = *(const half8_t*)(a.v + kbase + 32 * st);
+            for (int st = 0; st < D / 32; ++st) {
+                ka[i][st] = *(const half8_t*)(a.k + kbase + 32 * st);
+                va[i][st] = *(const half8_t*)(a.v + kbase + 32 * st);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            const int jt = jr + 16 * (wave + kAttnWaves * i);
+            if (jt < j1) {  // uniform in the wave
+                // V rows to LDS (the wave's own slot; LDS ops of one wave stay in order)
+#pragma unroll
+                for (int st = 0; st < D / 32; ++st) *(half8_t*)(myv + c * VP + 32 * st + 8 * g) = va[i][st];
+                float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < D / 32; ++st) sacc = mfma16x16x32(ka[i][st], qb[st], sacc);
 
-        float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+                // lane holds S^T[key 4g + r][query c]
+                float s2[4];
+                float tmax = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < D / 32; ++st) sacc = mfma16x16x32(ka[st], qb[st], sacc);
-
-        // lane holds S^T[key 4g + r][query c]
-        float s2[4];
-        float tmax = -INFINITY;
+                for (int r = 0; r < 4; ++r) {
+                    const int j = jt + 4 * g + r;
+                    const bool vis = j < j1 && (j < n_prefix || ((mask >> (j - n_prefix)) & 1u));
+                    s2[r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
+                    tmax = fmaxf(tmax, s2[r]);
+                }
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+                const float mnew = fmaxf(m, tmax);
+                const float muse = mnew == -INFINITY ? 0.0f : mnew;
+                const float alpha = exp2_fast(m - muse);
+                float p[4], psum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int j = jt + 4 * g + r;
-            const bool vis = j < j1 && (j < n_prefix || ((mask >> (j - n_prefix)) & 1u));
-            s2[r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
-            tmax = fmaxf(tmax, s2[r]);
-        }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float mnew = fmaxf(m, tmax);
-        const float muse = mnew == -INFINITY ? 0.0f : mnew;
-        const float alpha = exp2_fast(m - muse);
-        float p[4], psum = 0.0f;
+                for (int r = 0; r < 4; ++r) {
+                    p[r] = exp2_fast(s2[r] - muse);
+                    psum += p[r];
+                }
+                psum += __shfl_xor(psum, 16);
+                psum += __shfl_xor(psum, 32);
+                l = l * alpha + psum;
+                m = mnew;
+                half4_t phi, plo;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            p[r] = exp2_fast(s2[r] - muse);
-            psum += p[r];
-        }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        l = l * alpha + psum;
-        m = mnew;
-        half4_t phi, plo;
+                for (int r = 0; r < 4; ++r) {
+                    phi[r] = (_Float16)p[r];
+                    plo[r] = (_Float16)(p[r] - (float)phi[r]);
+                }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            phi[r] = (_Float16)p[r];
-            plo[r] = (_Float16)(p[r] - (float)phi[r]);
-        }
+                for (int dt = 0; dt < D / 16; ++dt) {
+                    oacc[dt] = oacc[dt] * alpha;
+                    // V^T operand: lane (d = 16 dt + c, group g) holds V[key 4g + r][d]
+                    half4_t vv;
 #pragma unroll
-        for (int dt = 0; dt < D / 16; ++dt) {
-            oacc[dt] = oacc[dt] * alpha;
-            // V^T operand: lane (d = 16 dt + c, group g) holds V[key 4g + r][d]
-            half4_t va;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) va[r] = myv[(4 * g + r) * VP + 16 * dt + c];
-            oacc[dt] = mfma16x16x16(va, phi, oacc[dt]);
-            oacc[dt] = mfma16x16x16(va, plo, oacc[dt]);
+                    for (int r = 0; r < 4; ++r) vv[r] = myv[(4 * g + r) * VP + 16 * dt + c];
+                    oacc[dt] = mfma16x16x16(vv, phi, oacc[dt]);
+                    oacc[dt] = mfma16x16x16(vv, plo, oacc[dt]);
+                }
+            }
         }
     }
 
@@ -170,6 +184,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
         red_l[wave][c] = l;
     }
     __syncthreads();
+    float* pp = a.part + ((size_t)h * a.splits + s) * a.nq * (D + 2);
     for (int idx = threadIdx.x; idx < D * kMaxQ; idx += kAttnWaves * 64) {
         const int d = idx / kMaxQ, qi = idx % kMaxQ;
         if (qi >= a.nq) continue;
@@ -177,53 +192,71 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_split_kernel(AttnArgs a)
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w][qi]);
         const float Mu = M == -INFINITY ? 0.0f : M;
-        float o = 0.0f, L = 0.0f;
+        float o = 0.0f, Lw = 0.0f;
 #pragma unroll
         for (int w = 0; w < kAttnWaves; ++w) {
             const float f = exp2_fast(red_m[w][qi] - Mu);
             o += red_o[w][d][qi] * f;
-            L += red_l[w][qi] * f;
+            Lw += red_l[w][qi] * f;
         }
         if (a.splits == 1) {
-            store_out(a, ((size_t)qi * a.H + h) * D + d, o / L);
+            store_out(a, ((size_t)qi * a.H + h) * D + d, o / Lw);
         } else {
-            float* pp = a.part + (((size_t)s * a.H + h) * a.nq + qi) * (D + 2);
-            pp[d] = o;
+            pp[qi * (D + 2) + d] = o;
             if (d == 0) {
-                pp[D] = M;
-                pp[D + 1] = L;
+                pp[qi * (D + 2) + D] = M;
+                pp[qi * (D + 2) + D + 1] = Lw;
             }
         }
     }
 }
 
-// out[qi][h][d] = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M), splits in order
+// out[qi][h][d] = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the
+// splits that hold keys, in split order (deterministic).  Grid (H, nq), D
+// threads; (m, l) of every split staged in LDS, O loads 16 splits at a time.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
 {
+    __shared__ float sm[kAttnMaxSplits], sl[kAttnMaxSplits];
     const int h = blockIdx.x, qi = blockIdx.y, d = threadIdx.x;
-    const size_t stride = (size_t)a.H * a.nq * (D + 2);
-    const float* base = a.part + ((size_t)h * a.nq + qi) * (D + 2);
-    int n_prefix, len;
-    attn_len(a, n_prefix, len);
-    const int ns = min(a.splits, (len + a.keys_per_split - 1) / a.keys_per_split);
-    float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, base[s * stride + D]);
-    const float Mu = M == -INFINITY ? 0.0f : M;
-    float o = 0.0f, L = 0.0f;
-    for (int s = 0; s < ns; ++s) {
-        const float* pp = base + s * stride;
-        const float f = exp2_fast(pp[D] - Mu);
-        o += pp[d] * f;
-        L += pp[D + 1] * f;
+    int n_prefix, L;
+    attn_len(a, n_prefix, L);
+    const int ns = min(a.splits, (L + a.keys_per_split - 1) / a.keys_per_split);
+    const size_t stride = (size_t)a.nq * (D + 2);
+    const float* q0 = a.part + (size_t)h * a.splits * stride + qi * (D + 2);
+    if (d < ns) {
+        sm[d] = q0[d * stride + D];
+        sl[d] = q0[d * stride + D + 1];
     }
-    store_out(a, ((size_t)qi * a.H + h) * D + d, o / L);
+    __syncthreads();
+    float M = -INFINITY;
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, sm[sp]);
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    float o = 0.0f, Ls = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += 16) {
+        float ov[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) ov[u] = s0 + u < ns ? q0[(s0 + u) * stride + d] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (s0 + u < ns) {
+                const float f = exp2_fast(sm[s0 + u] - Mu);
+                o += ov[u] * f;
+                Ls += sl[s0 + u] * f;
+            }
+    }
+    store_out(a, ((size_t)qi * a.H + h) * D + d, o / Ls);
 }
 
 template <int D>
-void launch_attn(const AttnArgs& a, hipStream_t st)
+void launch_attn(const AttnArgs& a, int T, hipStream_t st)
 {
-    hipLaunchKernelGGL(attn_split_kernel<D>, dim3(a.H, a.splits), dim3(kAttnWaves * 64), 0, st, a);
+    const dim3 grid(a.H, a.splits), block(kAttnWaves * 64);
+    switch (T) {
+    case 1: hipLaunchKernelGGL((attn_kernel<D, 1>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<D, 2>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((attn_kernel<D, 4>), grid, block, 0, st, a); break;
+    }
     if (a.splits > 1) hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.H, a.nq), dim3(D), 0, st, a);
 }
 
@@ -231,17 +264,23 @@ void launch_attn(const AttnArgs& a, hipStream_t st)
 
 namespace ulspec {
 
-// Splits so that heads x splits is about two workgroups per CU, each split a
-// multiple of the 64 keys one workgroup step covers.
+// Splits so that heads x splits is about two workgroups per CU, at most
+// kAttnMaxSplits; a workgroup covers rounds of 64 T keys (T = 1, 2 or 4
+// tiles of 16 keys per wave, all loaded before the round's first MFMA).
 void attn_plan(int L, int H, int n_cu, int& splits, int& kps)
 {
-    const int step = 16 * kAttnWaves;
     int want = (2 * n_cu + H - 1) / H;
-    const int max_splits = (L + step - 1) / step;
-    if (want > max_splits) want = max_splits;
-    if (want < 1) want = 1;
-    kps = ((L + want - 1) / want + step - 1) / step * step;
+    want = want < 1 ? 1 : (want > kAttnMaxSplits ? kAttnMaxSplits : want);
+    const int need = (L + want - 1) / want;
+    int T = 1;
+    while (T < 4 && 64 * T < need) T *= 2;
+    kps = (need + 64 * T - 1) / (64 * T) * (64 * T);
     splits = (L + kps - 1) / kps;
+}
+
+int attn_tiles(int kps)
+{
+    return kps % 256 == 0 ? 4 : (kps % 128 == 0 ? 2 : 1);
 }
 
 size_t attn_workspace_bytes(int splits, int H, int nq, int D)
@@ -290,7 +329,7 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
         a.mask[i] = mk;
     }
     attn_plan(a.L, a.H, ctx->n_cu, a.splits, a.keys_per_split);
-    if (c.dyn_prefix && a.splits == 1) a.splits = 2;  // keep the merge: the split kernel may return early
+    if (c.dyn_prefix && a.splits == 1) a.splits = 2;  // keep the merge: a split may return early
     void* ws = c.part;
     const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D);
     if (wsb && !ws) {
@@ -298,8 +337,9 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
         if (st != ULSPEC_OK) return st;
     }
     a.part = (float*)ws;
-    if (c.D == 128) launch_attn<128>(a, ctx->stream);
-    else launch_attn<64>(a, ctx->stream);
+    const int T = attn_tiles(a.keys_per_split);
+    if (c.D == 128) launch_attn<128>(a, T, ctx->stream);
+    else launch_attn<64>(a, T, ctx->stream);
     return check_launch(ctx, "verify_attention launch");
 }
 

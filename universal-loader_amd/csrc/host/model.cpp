@@ -1,14 +1,25 @@
 // model.cpp -- Llama-shaped model on the device: GGUF tensors by name, fp16
 // KV cache, and the block forward of InferenceEngine::forward_layer_gpu
-// (src/inference/inference_engine.cpp:602-682) over M <= 16 rows, with every
+// (src/inference/inference_engine.cpp:602-682) over M <= 16 rows (fewer when
+// the FFN is wide: every GEMM keeps its whole X in LDS), with every
 // linear layer on the Q4 verify dequant-GEMM and attention on the verify
 // attention kernel.
 //
 // Weight map as Model::load_from_gguf (src/inference/model.cpp:190-246):
 // "blk.N." or "layers.N." layer prefixes, GGUF and Meta tensor names.  Q, K, V
-// rows are concatenated into one weight (one GEMM, output [M][(H+2Hkv)D]), and
-// so are gate and up ([M][2F]); GGUF rows are independent block runs, so the
-// concatenation is a byte copy.
+// rows are concatenated into one weight (one GEMM over (H+2Hkv)D rows), and
+// gate and up rows are interleaved into another (row 2i = gate i, 2i+1 = up
+// i); GGUF rows are independent block runs, so both are byte copies.
+//
+// Five kernels per layer, each a dequant-GEMM with fused steps, plus the
+// attention:
+//   QKV   X = RMSNorm(h) in the prologue; RoPE, fp16 Q, K / V cache append in
+//         the epilogue
+//   attention over the cache -> fp16
+//   O     epilogue h += Y, with the per-tile sums of h^2 the next norm needs
+//   GU    X = RMSNorm(h); epilogue fp16 SiLU(gate) * up
+//   down  epilogue h += Y (+ sums of h^2)
+// and the LM head with the final RMSNorm in its prologue.
 #include "model.h"
 
 #include <cmath>
@@ -102,17 +113,33 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
                                     float* logits_dev, uint32_t n_logits)
 {
     const ulspec_model_cfg& c = cfg;
-    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = head_dim, F = c.ffn;
-    hipStream_t st = ctx->stream;
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = head_dim;
+    if (M == 0 || M > rows_max || n_logits > M) return fail(ctx, ULSPEC_EINVAL, "forward: %u rows (max %u)", M, rows_max);
     const std::vector<Weight>& W = ctx->weights;
-    launch_embed(st, embed, embed_type, c.dim, tok_dev, M, c.vocab, h);
+    launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss);
+    int P = (int)embed_partials(c.dim);
     ulspec_status s = ULSPEC_OK;
     for (uint32_t l = 0; l < c.n_layers && s == ULSPEC_OK; ++l) {
         const Layer& L = layers[l];
-        launch_add_rmsnorm(st, h, l ? delta : nullptr, L.attn_norm, M, c.dim, c.rms_eps, x16);
-        s = gemm_launch(ctx, W[L.wqkv], (const uint16_t*)x16, M, qkv);
+        GemmFuse q;
+        q.pro = kProNorm;
+        q.v = h;
+        q.pss = pss;
+        q.P = P;
+        q.norm_w = L.attn_norm;
+        q.eps = c.rms_eps;
+        q.epi = kEpiRope;
+        q.pos_dev = pos_dev;
+        q.pos_add = pos_add;
+        q.rope = rope;
+        q.q16 = q16;
+        q.kc = L.kc;
+        q.vc = L.vc;
+        q.qdim = (int)(H * D);
+        q.kvdim = (int)(Hkv * D);
+        q.hd = (int)D;
+        s = gemm_fused(ctx, W[L.wqkv], q, nullptr, M, nullptr);
         if (s != ULSPEC_OK) break;
-        launch_rope_append(st, qkv, M, H, Hkv, D, pos_dev, pos_add, rope, q16, L.kc, L.vc);
         AttnCall a;
         a.q = (const uint16_t*)q16;
         a.k_cache = (const uint16_t*)L.kc;
@@ -130,18 +157,42 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         a.part = attn_part;
         s = attn_launch(ctx, a);
         if (s != ULSPEC_OK) break;
-        s = gemm_launch(ctx, W[L.wo], (const uint16_t*)att16, M, delta);
+        GemmFuse o;
+        o.epi = kEpiResid;
+        o.h = h;
+        o.pss_out = pss;
+        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att16, M, nullptr);
         if (s != ULSPEC_OK) break;
-        launch_add_rmsnorm(st, h, delta, L.ffn_norm, M, c.dim, c.rms_eps, x16);
-        s = gemm_launch(ctx, W[L.wgu], (const uint16_t*)x16, M, gu);
+        P = (int)W[L.wo].n_tiles;
+        GemmFuse u;
+        u.pro = kProNorm;
+        u.v = h;
+        u.pss = pss;
+        u.P = P;
+        u.norm_w = L.ffn_norm;
+        u.eps = c.rms_eps;
+        u.epi = kEpiSilu;
+        u.act = act16;
+        s = gemm_fused(ctx, W[L.wgu], u, nullptr, M, nullptr);
         if (s != ULSPEC_OK) break;
-        launch_silu_mul(st, gu, M, F, act16);
-        s = gemm_launch(ctx, W[L.wdown], (const uint16_t*)act16, M, delta);
+        GemmFuse d;
+        d.epi = kEpiResid;
+        d.h = h;
+        d.pss_out = pss;
+        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act16, M, nullptr);
+        P = (int)W[L.wdown].n_tiles;
     }
     if (s != ULSPEC_OK) return s;
-    launch_add_rmsnorm(st, h, delta, out_norm, M, c.dim, c.rms_eps, x16);
-    if (n_logits)
-        s = gemm_launch(ctx, W[w_out], (const uint16_t*)(x16 + (size_t)(M - n_logits) * c.dim), n_logits, logits_dev);
+    if (n_logits) {
+        GemmFuse z;
+        z.pro = kProNorm;
+        z.v = h + (size_t)(M - n_logits) * c.dim;
+        z.pss = pss + (size_t)(M - n_logits) * P;
+        z.P = P;
+        z.norm_w = out_norm;
+        z.eps = c.rms_eps;
+        s = gemm_fused(ctx, W[w_out], z, nullptr, n_logits, logits_dev);
+    }
     if (s != ULSPEC_OK) return s;
     return check_launch(ctx, "model forward launch");
 }
@@ -155,18 +206,25 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         return fail(ctx, ULSPEC_EINVAL, "model_create: dim=%u heads=%u kv_heads=%u", c.dim, c.n_heads, c.n_kv_heads);
     const uint32_t D = c.dim / c.n_heads;
     if (D != 64 && D != 128) return fail(ctx, ULSPEC_EUNSUPPORTED, "model_create: head dim %u (64 or 128)", D);
+    if (c.dim > 4096 || c.dim % 16)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "model_create: dim %u (a multiple of 16, at most 4096)", c.dim);
     if (c.n_layers == 0 || c.ffn == 0 || c.vocab == 0 || c.max_ctx < 2 || c.max_ctx > (1u << 24))
         return fail(ctx, ULSPEC_EINVAL, "model_create: layers=%u ffn=%u vocab=%u max_ctx=%u", c.n_layers, c.ffn,
                     c.vocab, c.max_ctx);
     if (!(c.rms_eps > 0.0f) || !(c.rope_base > 1.0f) || !std::isfinite(c.rope_base))
         return fail(ctx, ULSPEC_EINVAL, "model_create: rms_eps / rope_base");
     (void)hipSetDevice(ctx->device);
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn, R = ulspec_model::kRows;
+    uint32_t rows = R;
+    while (rows > 0 && !(wide_fits((int)rows, c.dim) && wide_fits((int)rows, F))) --rows;
+    if (rows < 2) return fail(ctx, ULSPEC_EUNSUPPORTED, "model_create: FFN %u too wide for the whole-X GEMM", F);
     ulspec_model* m = new ulspec_model;
     m->ctx = ctx;
     m->cfg = c;
     m->head_dim = D;
     m->layers.resize(c.n_layers);
-    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn, R = ulspec_model::kRows;
+    m->rows_max = rows;
+    m->pss_stride = std::max(embed_partials(c.dim), (c.dim + 15) / 16);
     const size_t kv_bytes = (size_t)c.max_ctx * Hkv * D * sizeof(_Float16);
     int splits = 0, kps = 0;
     attn_plan((int)c.max_ctx, (int)H, ctx->n_cu, splits, kps);
@@ -176,11 +234,8 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         size_t bytes;
     } wants[] = {
         {(void**)&m->h, (size_t)R * c.dim * 4},
-        {(void**)&m->delta, (size_t)R * c.dim * 4},
-        {(void**)&m->qkv, (size_t)R * (H + 2 * Hkv) * D * 4},
-        {(void**)&m->gu, (size_t)R * 2 * F * 4},
+        {(void**)&m->pss, (size_t)R * m->pss_stride * 4},
         {(void**)&m->logits, (size_t)R * c.vocab * 4},
-        {(void**)&m->x16, (size_t)R * std::max(c.dim, F) * 2},
         {(void**)&m->q16, (size_t)R * H * D * 2},
         {(void**)&m->att16, (size_t)R * H * D * 2},
         {(void**)&m->act16, (size_t)R * F * 2},
@@ -296,8 +351,7 @@ extern "C" ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* na
     uint32_t* id = qkv ? &m->layers[layer].wqkv : &m->layers[layer].wgu;
     if (*id != ~0u) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
     const uint64_t rows_total = qkv ? (uint64_t)(H + 2 * Hkv) * D : 2ull * F;
-    const uint64_t row0 = role == R_Q ? 0 : role == R_K ? (uint64_t)H * D : role == R_V ? (uint64_t)(H + Hkv) * D
-                          : role == R_GATE ? 0 : F;
+    const uint64_t row0 = role == R_Q ? 0 : role == R_K ? (uint64_t)H * D : (uint64_t)(H + Hkv) * D;
     const uint32_t bit = role == R_Q || role == R_GATE ? 1u : role == R_K || role == R_UP ? 2u : 4u;
     ulspec_model::Pending& p = m->pending[key];
     if (!p.dev) {
@@ -311,7 +365,15 @@ extern "C" ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* na
     }
     if (p.type != type) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' type differs from its fused group", name);
     if (p.have & bit) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
-    ulspec_status st = copy_in(m, p.dev + rb * row0, data, nbytes, on_device != 0);
+    ulspec_status st = ULSPEC_OK;
+    if (qkv) {
+        st = copy_in(m, p.dev + rb * row0, data, nbytes, on_device != 0);
+    } else {  // gate row i -> fused row 2i, up row i -> 2i + 1
+        hipError_t e = hipMemcpy2DAsync(p.dev + (role == R_UP ? rb : 0), 2 * rb, data, rb, rb, F,
+                                        on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "set_tensor copy");
+    }
     if (st != ULSPEC_OK) return st;
     p.have |= bit;
     if (p.have == p.need) {
@@ -330,8 +392,9 @@ extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* to
     if (!m) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = m->ctx;
     if (!tokens || M == 0) return fail(ctx, ULSPEC_EINVAL, "model_forward: no tokens");
-    if (n_logits > ulspec_model::kRows || n_logits > M || (n_logits && !logits))
-        return fail(ctx, ULSPEC_EINVAL, "model_forward: n_logits=%u (<= 16 and <= M, with an output)", n_logits);
+    if (n_logits > m->rows_max || n_logits > M || (n_logits && !logits))
+        return fail(ctx, ULSPEC_EINVAL, "model_forward: n_logits=%u (<= %u and <= M, with an output)", n_logits,
+                    m->rows_max);
     if ((uint64_t)pos + M > m->cfg.max_ctx)
         return fail(ctx, ULSPEC_EINVAL, "model_forward: positions %u + %u beyond max_ctx %u", pos, M, m->cfg.max_ctx);
     if (!m->complete()) return fail(ctx, ULSPEC_EINVAL, "model_forward: model tensors missing");
@@ -339,8 +402,8 @@ extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* to
         if (tokens[i] < 0 || (uint32_t)tokens[i] >= m->cfg.vocab)
             return fail(ctx, ULSPEC_EINVAL, "model_forward: token %d out of range", tokens[i]);
     (void)hipSetDevice(ctx->device);
-    // chunks of 16; the last chunk is the last min(16, M) rows (holds the logit rows)
-    const uint32_t R = ulspec_model::kRows;
+    // chunks of rows_max; the last chunk is the last min(rows_max, M) rows (holds the logit rows)
+    const uint32_t R = m->rows_max;
     const uint32_t last = M > R ? M - R : 0;
     uint32_t m0 = 0;
     while (true) {

@@ -35,14 +35,14 @@ struct ulspec_model {
     uint32_t w_out = ~0u;
     float2* rope = nullptr;    // [max_ctx][head_dim / 2] (cos, sin)
 
-    // activations, up to kRows rows
+    // activations, up to kRows rows (rows_max per forward: every GEMM's X
+    // must fit in LDS)
     static constexpr uint32_t kRows = 16;
-    float* h = nullptr;        // [kRows][dim] residual stream
-    float* delta = nullptr;    // [kRows][dim] O / down projection output
-    float* qkv = nullptr;      // [kRows][(H + 2 Hkv) D]
-    float* gu = nullptr;       // [kRows][2 F]
+    uint32_t rows_max = 0;
+    float* h = nullptr;        // [kRows][dim] residual stream (fp32)
+    float* pss = nullptr;      // [kRows][pss_stride] RMSNorm partial sums of h^2
+    uint32_t pss_stride = 0;
     float* logits = nullptr;   // [kRows][vocab]
-    _Float16* x16 = nullptr;   // [kRows][max(dim, F)]
     _Float16* q16 = nullptr;   // [kRows][H D]
     _Float16* att16 = nullptr; // [kRows][H D]
     _Float16* act16 = nullptr; // [kRows][F]
@@ -52,7 +52,7 @@ struct ulspec_model {
     std::vector<void*> allocs;
 
     bool complete() const;
-    // Forward M <= kRows tokens read from device memory at positions
+    // Forward M <= rows_max tokens read from device memory at positions
     // *pos_dev + pos_add ...; logits of the last n_logits rows to `logits`
     // (device).  Asynchronous, never allocates or synchronises.
     ulspec_status forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,

@@ -173,7 +173,8 @@ extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* 
     ulspec_ctx* ctx = target->ctx;
     if (draft->ctx != ctx) return fail(ctx, ULSPEC_EINVAL, "spec_create: models on different contexts");
     if (!s || !out) return fail(ctx, ULSPEC_EINVAL, "spec_create: null pointer");
-    if (k == 0 || k + 1 > ulspec_model::kRows) return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u not in [1, 15]", k);
+    if (k == 0 || k + 1 > target->rows_max || draft->rows_max < 2)
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u (k + 1 <= %u rows of the target)", k, target->rows_max);
     if (target->cfg.vocab != draft->cfg.vocab) return fail(ctx, ULSPEC_EINVAL, "spec_create: vocabularies differ");
     if (!target->complete() || !draft->complete()) return fail(ctx, ULSPEC_EINVAL, "spec_create: model tensors missing");
     const uint32_t V = target->cfg.vocab;

@@ -22,6 +22,7 @@
 //                 group g covers qs bytes 32g..32g+31 (sub-blocks 2g, 2g+1);
 //                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
 //     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
+#include "detmath.h"
 #include "hip_common.h"
 #include "ulspec_internal.h"
 
@@ -283,6 +284,7 @@ struct GemmArgs {
     float* out;  // Y when ks_count == 1, else partials [ks_count][M][N]
     int M, N, K, n_tiles, n_chunks, ks_count;
     int ks_q, ks_r;  // n_chunks = ks_q * ks_count + ks_r; slice s starts at s * ks_q + min(s, ks_r)
+    GemmFuse f;      // whole-X kernels only
 };
 
 __device__ __forceinline__ void slice_range(const GemmArgs& a, int ks, int& lo, int& hi)
@@ -525,7 +527,17 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
     }
 }
 
-// Parts summed in part order 0..kParts-1, then stored (rows < M, cols < N).
+// Parts summed in part order 0..kParts-1; then the epilogue (rows < M, cols
+// < N).  Thread (row group, lane l) holds output (m = 4 (l / 16) + row,
+// n = 16 t + l % 16); columns n and n ^ 1 sit in lanes l and l ^ 1.
+//   store: Y[m][n] = s
+//   rope:  RoPE pair (n, n+1) at position pos0 + m (Q and K rows), then fp16
+//          Q -> q16[m][n], K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim]
+//          (y0 = x0 c - x1 s, y1 = x0 s + x1 c; src/shaders/rope.glsl:50-73)
+//   silu:  rows interleaved (2i = gate i, 2i+1 = up i):
+//          act[m][i] = fp16(g * (1 / (1 + e^-g)) * u)
+//   resid: h[m][n] += s (in place); pss[m][t] = sum over the tile's 16 columns
+//          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m
 __device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& acc, const GemmArgs& a, int t)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -533,13 +545,116 @@ __device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& 
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
     __syncthreads();
-    if (threadIdx.x < 256) {
-        const int row = threadIdx.x >> 6, l = threadIdx.x & 63;
-        float s = red[row * 64 + l];
+    if (threadIdx.x >= 256) return;
+    const int row = threadIdx.x >> 6, l = threadIdx.x & 63;
+    float s = red[row * 64 + l];
 #pragma unroll
-        for (int p = 1; p < kParts; ++p) s += red[(p * 4 + row) * 64 + l];
-        const int m = 4 * (l >> 4) + row, n = 16 * t + (l & 15);
-        if (m < a.M && n < a.N) a.out[(size_t)m * a.N + n] = s;
+    for (int p = 1; p < kParts; ++p) s += red[(p * 4 + row) * 64 + l];
+    const int m = 4 * (l >> 4) + row, n = 16 * t + (l & 15);
+    const bool ok = m < a.M && n < a.N;
+    const GemmFuse& f = a.f;
+    switch (f.epi) {
+    case kEpiRope: {
+        const float other = __shfl_xor(s, 1);
+        if (!ok) break;
+        const bool odd = n & 1;
+        const int pos = *f.pos_dev + f.pos_add + m;
+        if (n < f.qdim + f.kvdim) {
+            const int nn = n < f.qdim ? n : n - f.qdim;
+            const float2 cs = f.rope[(size_t)pos * (f.hd / 2) + (nn % f.hd) / 2];
+            const float x0 = odd ? other : s, x1 = odd ? s : other;
+            float y;
+            if (!odd) {
+                const float p0 = x0 * cs.x, p1 = x1 * cs.y;
+                y = p0 - p1;
+            } else {
+                const float p0 = x0 * cs.y, p1 = x1 * cs.x;
+                y = p0 + p1;
+            }
+            if (n < f.qdim) f.q16[(size_t)m * f.qdim + nn] = (_Float16)y;
+            else f.kc[(size_t)pos * f.kvdim + nn] = (_Float16)y;
+        } else {
+            f.vc[(size_t)pos * f.kvdim + (n - f.qdim - f.kvdim)] = (_Float16)s;
+        }
+        break;
+    }
+    case kEpiSilu: {
+        const float u = __shfl_xor(s, 1);
+        if (ok && !(n & 1)) {
+            const float sg = s * (1.0f / (1.0f + det_expf(-s)));
+            f.act[(size_t)m * (a.N / 2) + n / 2] = (_Float16)(sg * u);
+        }
+        break;
+    }
+    case kEpiResid: {
+        float v = 0.0f;
+        if (ok) {
+            float* hp = f.h + (size_t)m * a.N + n;
+            v = *hp + s;
+            *hp = v;
+        }
+        float sq = v * v;
+        sq += __shfl_xor(sq, 1);
+        sq += __shfl_xor(sq, 2);
+        sq += __shfl_xor(sq, 4);
+        sq += __shfl_xor(sq, 8);
+        if (m < a.M && (l & 15) == 0) f.pss_out[(size_t)m * a.n_tiles + t] = sq;
+        break;
+    }
+    default:
+        if (ok) a.out[(size_t)m * a.N + n] = s;
+    }
+}
+
+// X[m][k] = fp16((v[m][k] * r_m) * w[k]) into the LDS rows, r_m = 1 /
+// sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
+// Wave m sums row m's P partials (lane-strided, then an xor tree); each thread
+// converts one float4 column group (K <= 4096) of 4 rows at a time, the first
+// group's loads issued before the partial sums are read.
+constexpr int kNormGroup = 4;
+
+__device__ __forceinline__ void norm_prologue(const GemmArgs& a, uint8_t* xs, uint32_t pitch, float* rs)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const GemmFuse& f = a.f;
+    const int K4 = a.K >> 2;
+    const bool col = tid < K4;
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
+    float4 vv[kNormGroup];
+#pragma unroll
+    for (int i = 0; i < kNormGroup; ++i)
+        vv[i] = __builtin_bit_cast(float4, buf_load16(vr, i < a.M && col ? (uint32_t)(i * K4 + tid) * 16u : kOOB));
+    const float4 w = col ? ((const float4*)f.norm_w)[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (wave < a.M) {
+        float ss = 0.0f;
+        for (int p = lane; p < f.P; p += 64) ss += f.pss[(size_t)wave * f.P + p];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) rs[wave] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
+    }
+    __syncthreads();
+    for (int m0 = 0; m0 < a.M; m0 += kNormGroup) {
+        if (m0) {
+#pragma unroll
+            for (int i = 0; i < kNormGroup; ++i)
+                vv[i] = __builtin_bit_cast(
+                    float4, buf_load16(vr, m0 + i < a.M && col ? (uint32_t)((m0 + i) * K4 + tid) * 16u : kOOB));
+        }
+        if (col) {
+#pragma unroll
+            for (int i = 0; i < kNormGroup; ++i) {
+                const int m = m0 + i;
+                if (m < a.M) {
+                    const float r = rs[m];
+                    half4_t x;
+                    x[0] = (_Float16)((vv[i].x * r) * w.x);
+                    x[1] = (_Float16)((vv[i].y * r) * w.y);
+                    x[2] = (_Float16)((vv[i].z * r) * w.z);
+                    x[3] = (_Float16)((vv[i].w * r) * w.w);
+                    *(half4_t*)(xs + m * pitch + 8 * tid) = x;
+                }
+            }
+        }
     }
 }
 
@@ -547,6 +662,7 @@ template <int CMAX>
 __global__ __launch_bounds__(kParts * 64) void gemm_q4_0_wide_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
+    __shared__ float rs[kNormMaxRows];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -561,7 +677,7 @@ __global__ __launch_bounds__(kParts * 64) void gemm_q4_0_wide_kernel(GemmArgs a)
     const NibbleConsts nk = nibble_consts();
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 
-    x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
+    if (a.f.pro == kProCopy) x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
     pin_loads();
     {  // first batch, straight-line: the X wait before the barrier covers only the X copies
         uint4 wq[CMAX];
@@ -569,6 +685,7 @@ __global__ __launch_bounds__(kParts * 64) void gemm_q4_0_wide_kernel(GemmArgs a)
         const int nc = max(0, min(CMAX, qb - qa));
         q4_0_load_batch<CMAX>(wr, w_lane, s_lane, qa, nc, wq, sc);
         pin_loads();
+        if (a.f.pro == kProNorm) norm_prologue(a, (uint8_t*)xs, wide_pitch(a.K), rs);
         __syncthreads();
         q4_0_mma_batch<CMAX>(xs, xrow, qa, nc, wq, sc, nk, acc);
     }
@@ -642,6 +759,7 @@ template <int CMAX>
 __global__ __launch_bounds__(kParts * 64) void gemm_q4_k_wide_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
+    __shared__ float rs[kNormMaxRows];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -656,13 +774,14 @@ __global__ __launch_bounds__(kParts * 64) void gemm_q4_k_wide_kernel(GemmArgs a)
     const NibbleConsts nk = nibble_consts();
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
 
-    x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
+    if (a.f.pro == kProCopy) x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
     pin_loads();
     {
         uint4 w0[CMAX], w1[CMAX], hd[CMAX];
         const int nc = max(0, min(CMAX, sb - sa));
         q4_k_load_batch<CMAX>(wr, w_lane, h_lane, sa, nc, w0, w1, hd);
         pin_loads();
+        if (a.f.pro == kProNorm) norm_prologue(a, (uint8_t*)xs, wide_pitch(a.K), rs);
         __syncthreads();
         q4_k_mma_batch<CMAX>(xs, xrow, sa, nc, w0, w1, hd, g, nk, acc);
     }
@@ -715,19 +834,20 @@ namespace ulspec {
 // LDS available to one workgroup on gfx950.
 constexpr size_t kWideLdsMax = 160 * 1024;
 
+// (less 256 B for the kernels' static LDS)
 bool wide_fits(int M, uint32_t K)
 {
-    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax;
+    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax - 256;
 }
 
 // Opt the whole-X kernels in to the full 160 KB of LDS.
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
     hipError_t e = hipFuncSetAttribute((const void*)gemm_q4_0_wide_kernel<kQ40CMax>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax - 256);
     if (e == hipSuccess)
         e = hipFuncSetAttribute((const void*)gemm_q4_k_wide_kernel<kQ4KCMax>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax);
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax - 256);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
     return ULSPEC_OK;
 }
@@ -770,6 +890,7 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
         a.ks_count = (int)w.ksplit;
         a.ks_q = (int)(w.n_chunks / w.ksplit);
         a.ks_r = (int)(w.n_chunks % w.ksplit);
+        a.f = GemmFuse();
         if (wide_fits(mc, w.k)) {
             // whole X in LDS, canonical kParts parts, summed in the kernel
             a.out = y + (size_t)m0 * w.n;
@@ -798,6 +919,33 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
         }
     }
     return check_launch(ctx, "verify_gemm launch");
+}
+
+ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y)
+{
+    if (M == 0 || !wide_fits((int)M, w.k)) return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows of K=%u do not fit", M, w.k);
+    if (f.pro == kProNorm && (M > (uint32_t)kNormMaxRows || w.k > 4096 || w.k % 4))
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs M <= 16 and K <= 4096");
+    GemmArgs a;
+    a.w = w.dev;
+    a.w_bytes = (uint32_t)w.bytes;
+    a.x = reinterpret_cast<const _Float16*>(x);
+    a.out = y;
+    a.M = (int)M;
+    a.N = (int)w.n;
+    a.K = (int)w.k;
+    a.n_tiles = (int)w.n_tiles;
+    a.n_chunks = (int)w.n_chunks;
+    a.ks_count = kParts;
+    a.ks_q = (int)(w.n_chunks / kParts);
+    a.ks_r = (int)(w.n_chunks % kParts);
+    a.f = f;
+    const size_t lds = std::max<size_t>((size_t)M * wide_pitch(w.k), kParts * 4 * 64 * sizeof(float));
+    if (w.type == ULSPEC_GGML_Q4_0)
+        hipLaunchKernelGGL(gemm_q4_0_wide_kernel<kQ40CMax>, dim3(w.n_tiles), dim3(kParts * 64), lds, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(gemm_q4_k_wide_kernel<kQ4KCMax>, dim3(w.n_tiles), dim3(kParts * 64), lds, ctx->stream, a);
+    return check_launch(ctx, "fused gemm launch");
 }
 
 }  // namespace ulspec

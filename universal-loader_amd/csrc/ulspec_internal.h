@@ -68,9 +68,39 @@ inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
 // One-time kernel attributes of the dequant-GEMM (called by ulspec_create).
 ulspec_status gemm_init(ulspec_ctx* ctx);
 
+// Fusions of the whole-X dequant-GEMM used by the model forward.
+enum { kProCopy = 0, kProNorm = 1 };
+enum { kEpiStore = 0, kEpiRope = 1, kEpiSilu = 2, kEpiResid = 3 };
+constexpr int kNormMaxRows = 16;
+struct GemmFuse {
+    int pro = kProCopy, epi = kEpiStore;
+    // kProNorm: X = fp16(v * rsqrt(sum_p pss[m][p] / K + eps) * norm_w), K <= 4096
+    const float* v = nullptr;
+    const float* pss = nullptr;
+    int P = 0;
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+    // kEpiRope: Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc at positions *pos_dev + pos_add + m
+    const int32_t* pos_dev = nullptr;
+    int pos_add = 0;
+    const float2* rope = nullptr;
+    _Float16* q16 = nullptr;
+    _Float16* kc = nullptr;
+    _Float16* vc = nullptr;
+    int qdim = 0, kvdim = 0, hd = 0;
+    // kEpiSilu: rows interleaved gate / up -> act [M][N / 2]
+    _Float16* act = nullptr;
+    // kEpiResid: h [M][N] += Y; pss_out [M][n_tiles] = per-tile sums of h^2
+    float* h = nullptr;
+    float* pss_out = nullptr;
+};
+
 // Kernel launchers shared by the C ABI and the host engine (no validation of
 // device pointers; arguments checked as in the corresponding ABI entry point).
 ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y);
+// The whole-X kernel with a fused prologue / epilogue (M rows must fit in LDS).
+ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y);
+bool wide_fits(int M, uint32_t K);
 size_t gemm_workspace_bytes(const Weight& w);
 ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes, uint32_t N, uint32_t K,
                             bool on_device, uint32_t* out_id);
