@@ -71,7 +71,10 @@ def test_gemm_row_independence_and_determinism(ctx, ora, rng, wtype):
     W = ora.synth_q4(wtype, 5, 99, N, K)
     wid = ctx.weight_upload(wtype, W, N, K)
     X = _x(rng, ora, 48, K)
-    m_small = 7 if wtype == 2 else 9  # largest M whose X fits in LDS
+    # largest M whose X fits in LDS: M * pitch <= 160 KiB - 16.5 KiB, pitch =
+    # 2K rounded up to 1 KiB, + 16
+    pitch = (2 * K + 1023) // 1024 * 1024 + 16
+    m_small = min(16, (160 * 1024 - 16896) // pitch)
     small = _run(ctx, wid, X[:m_small], N)
     assert np.array_equal(small.view(np.uint32), _run(ctx, wid, X[:m_small], N).view(np.uint32))
     for M in (1, 2, 5):

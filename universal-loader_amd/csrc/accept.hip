@@ -35,7 +35,9 @@ namespace {
 constexpr int kKMax = 256;       // largest supported top_k
 constexpr int kCandMax = 2048;   // candidate buffer of the fast top-k path
 constexpr int kRowThreads = 1024;
-constexpr int kSeqThreads = 256;
+constexpr int kSeqThreads = 1024;
+constexpr int kRound = 8;         // float4 rounds in flight per thread in the vocabulary scans
+constexpr int kMaxRounds = 256;   // rounds of the CDF draw: V <= 256 * 4 * kSeqThreads
 
 struct RowStat {
     uint64_t Z;
@@ -142,10 +144,52 @@ __device__ __forceinline__ uint64_t order_key(uint32_t key, uint32_t idx)
     return ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - idx);
 }
 
+// The four values of float4 group q of a row (elements 4q .. 4q+3; past V
+// they read element V-1).  Rows of a V % 4 != 0 vocabulary are not 16-byte
+// aligned: scalar loads then.
+__device__ __forceinline__ float4 load4(const float* __restrict__ row, uint32_t V, uint32_t q)
+{
+    if ((V & 3u) == 0) return ((const float4*)row)[q];
+    const uint32_t e = 4 * q;
+    return make_float4(row[min(e, V - 1)], row[min(e + 1, V - 1)], row[min(e + 2, V - 1)], row[min(e + 3, V - 1)]);
+}
+
+// body(i, value) for every i < V, thread t taking float4 groups t, t + NT, ..
+// (coalesced), kRound groups loaded before their values are used.
+template <int NT, typename Body>
+__device__ __forceinline__ void scan_row(const float* __restrict__ row, uint32_t V, Body body)
+{
+    const uint32_t V4 = (V + 3) / 4;
+    for (uint32_t q0 = threadIdx.x; q0 < V4; q0 += kRound * NT) {
+        float4 v[kRound];
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) v[r] = load4(row, V, min(q0 + (uint32_t)(r * NT), V4 - 1));
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) {
+            const uint32_t q = q0 + (uint32_t)(r * NT);
+            if (q < V4) {
+                const float e[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (4 * q + c < V) body(4 * q + c, e[c]);
+            }
+        }
+    }
+}
+
 __device__ __forceinline__ uint64_t fixed_e(float l, float lmax, const WarpParams& p)
 {
     const float e = det_expf((l - lmax) * p.invT);
     return (uint64_t)(e * p.scale);
+}
+
+struct W4 {
+    uint64_t a, b, c, d;
+};
+
+__device__ __forceinline__ W4 fixed_e4(float4 l, float lmax, const WarpParams& p)
+{
+    return W4{fixed_e(l.x, lmax, p), fixed_e(l.y, lmax, p), fixed_e(l.z, lmax, p), fixed_e(l.w, lmax, p)};
 }
 
 // ---- row statistics ----------------------------------------------------------
@@ -162,10 +206,10 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
 
     // pass 1: max key with the lowest index (argmax), per-thread max key
     uint64_t best = 0;
-    for (uint32_t i = tid; i < V; i += kRowThreads) {
-        const uint64_t o = order_key(float_key(row[i]), i);
+    scan_row<kRowThreads>(row, V, [&](uint32_t i, float l) {
+        const uint64_t o = order_key(float_key(l), i);
         best = o > best ? o : best;
-    }
+    });
     const uint64_t top = block_max_u64<kRowThreads>(best, red);
     const uint32_t top_key = (uint32_t)(top >> 32);
     const float lmax = key_float(top_key);
@@ -178,7 +222,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
     const bool topk = p.top_k > 0 && p.top_k < V;
     if (!topk) {  // full vocabulary: Z over every token
         uint64_t z = 0;
-        for (uint32_t i = tid; i < V; i += kRowThreads) z += fixed_e(row[i], lmax, p);
+        scan_row<kRowThreads>(row, V, [&](uint32_t, float l) { z += fixed_e(l, lmax, p); });
         z = block_sum_u64<kRowThreads>(z, red);
         if (tid == 0) {
             st->Z = z;
@@ -195,13 +239,13 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
     const uint32_t t0 = (uint32_t)buf[k - 1];
     if (tid == 0) cand_count = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < V; i += kRowThreads) {
-        const uint32_t key = float_key(row[i]);
+    scan_row<kRowThreads>(row, V, [&](uint32_t i, float l) {
+        const uint32_t key = float_key(l);
         if (key >= t0) {
             const uint32_t slot = atomicAdd(&cand_count, 1u);
             if (slot < kCandMax) buf[slot] = order_key(key, i);
         }
-    }
+    });
     __syncthreads();
     const uint32_t nc = cand_count;
     __syncthreads();
@@ -312,34 +356,103 @@ __device__ uint64_t weight_of(const RowStat& st, const float* row, uint32_t V, b
     return 0;
 }
 
-// Full-vocabulary inverse-CDF draw of a per-token weight w(j) (j in [0, V)):
+// Full-vocabulary inverse-CDF draw of per-token weights (u64, exact):
 // T = trunc(u * total), first j with T < cumsum, else the last j with w > 0.
-// Thread t owns the contiguous chunk [t*C, (t+1)*C) so the prefix is in index order.
-template <typename WFn>
-__device__ int32_t block_cdf_pick(uint32_t V, float u, WFn w, uint64_t* scratch, int32_t* pick)
+// w4(q) gives the weights of elements 4q .. 4q+3 (0 past V).  Round r covers
+// float4 groups [r NT, (r+1) NT) (thread t takes group r NT + t, coalesced).
+// Round totals first (kRound rounds per pass, wave xor trees, then LDS), the
+// round holding T, one block scan inside it, then the 4 elements of the
+// owning thread.
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t x)
 {
-    const int tid = threadIdx.x;
-    const uint32_t C = (V + kSeqThreads - 1) / kSeqThreads;
-    const uint32_t c0 = min(V, (uint32_t)tid * C), c1 = min(V, c0 + C);
-    uint64_t mine = 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+template <typename F4>
+__device__ int32_t block_cdf_pick(uint32_t V, float u, F4 w4, uint64_t* scratch, int32_t* pick)
+{
+    constexpr int NW = kSeqThreads / 64;
+    __shared__ uint64_t rt[kMaxRounds];
+    __shared__ uint64_t wpart[NW][kRound];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t V4 = (V + 3) / 4;
+    const uint32_t R = (V4 + kSeqThreads - 1) / kSeqThreads;
     int32_t last = -1;
-    for (uint32_t j = c0; j < c1; ++j) {
-        const uint64_t x = w(j);
-        mine += x;
-        if (x) last = (int32_t)j;
+    for (uint32_t g0 = 0; g0 < R; g0 += kRound) {
+        W4 x[kRound];
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) x[r] = w4(min((g0 + r) * kSeqThreads + tid, V4 - 1));
+        uint64_t sr[kRound];
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) {
+            const uint32_t q = (g0 + r) * kSeqThreads + tid;
+            sr[r] = 0;
+            if (g0 + r < R && q < V4) {
+                const uint64_t e[4] = {x[r].a, x[r].b, x[r].c, x[r].d};
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (4 * q + c < V && e[c]) {
+                        sr[r] += e[c];
+                        last = (int32_t)(4 * q + c);
+                    }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) sr[r] = wave_sum_u64(sr[r]);
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < kRound; ++r) wpart[wave][r] = sr[r];
+        __syncthreads();
+        if (tid < kRound && g0 + tid < R) {
+            uint64_t t = 0;
+#pragma unroll
+            for (int v = 0; v < NW; ++v) t += wpart[v][tid];
+            rt[g0 + tid] = t;
+        }
+        __syncthreads();
     }
-    uint64_t before = 0;
-    const uint64_t total = block_exclusive_scan_u64<kSeqThreads>(mine, before, scratch);
+    uint64_t total = 0;
+    for (uint32_t r = 0; r < R; ++r) total += rt[r];
     const uint64_t T = (uint64_t)((double)u * (double)total);
+    uint32_t rstar = R;
+    uint64_t rbefore = 0;
+    {
+        uint64_t c = 0;
+        for (uint32_t r = 0; r < R; ++r) {
+            if (rt[r] && T < c + rt[r]) {
+                rstar = r;
+                rbefore = c;
+                break;
+            }
+            c += rt[r];
+        }
+    }
     if (tid == 0) *pick = -1;
     __syncthreads();
-    if (T >= before && T < before + mine) {
-        uint64_t c = before;
-        for (uint32_t j = c0; j < c1; ++j) {
-            c += w(j);
-            if (T < c) {
-                *pick = (int32_t)j;
-                break;
+    if (rstar < R) {  // uniform: every thread read the same round totals
+        const uint32_t q = rstar * kSeqThreads + tid;
+        W4 x = w4(min(q, V4 - 1));
+        const uint64_t e[4] = {x.a, x.b, x.c, x.d};
+        uint64_t mine = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q < V4 && 4 * q + c < V) mine += e[c];
+        uint64_t before = 0;
+        block_exclusive_scan_u64<kSeqThreads>(mine, before, scratch);
+        before += rbefore;
+        if (mine && T >= before && T < before + mine) {
+            uint64_t c = before;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (4 * q + k < V) {
+                    c += e[k];
+                    if (T < c) {
+                        *pick = (int32_t)(4 * q + k);
+                        break;
+                    }
+                }
             }
         }
     }
@@ -374,7 +487,7 @@ __device__ int32_t draw_row(const RowStat& st, const float* row, uint32_t V, boo
 {
     if (topk) return list_cdf_pick(st.idx, st.E, st.nk, st.Z, u, V);
     const float lmax = st.lmax;
-    return block_cdf_pick(V, u, [&](uint32_t j) { return fixed_e(row[j], lmax, p); }, scratch, pick);
+    return block_cdf_pick(V, u, [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); }, scratch, pick);
 }
 
 __device__ __forceinline__ uint64_t residual_weight(uint64_t P, uint64_t Q, uint64_t Zp, uint64_t Zq, int sh)
@@ -457,12 +570,30 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
             tok = pick;
         } else {
             const float lpm = ts[i].lmax, lqm = ds[i].lmax;
-            auto rw = [&](uint32_t j) {
-                return residual_weight(fixed_e(trow[j], lpm, p), fixed_e(drow[j], lqm, p), Zp, Zq, sh);
+            auto rw = [&](uint32_t q) {
+                const W4 a = fixed_e4(load4(trow, V, q), lpm, p), b = fixed_e4(load4(drow, V, q), lqm, p);
+                return W4{residual_weight(a.a, b.a, Zp, Zq, sh), residual_weight(a.b, b.b, Zp, Zq, sh),
+                          residual_weight(a.c, b.c, Zp, Zq, sh), residual_weight(a.d, b.d, Zp, Zq, sh)};
             };
             // total residual first (an all-zero residual draws from p)
             uint64_t mine = 0;
-            for (uint32_t j = tid; j < V; j += kSeqThreads) mine += rw(j);
+            {
+                const uint32_t V4 = (V + 3) / 4;
+                for (uint32_t q0 = tid; q0 < V4; q0 += kRound * kSeqThreads) {
+                    W4 x[kRound];
+#pragma unroll
+                    for (int r = 0; r < kRound; ++r) x[r] = rw(min(q0 + (uint32_t)(r * kSeqThreads), V4 - 1));
+#pragma unroll
+                    for (int r = 0; r < kRound; ++r) {
+                        const uint32_t q = q0 + (uint32_t)(r * kSeqThreads);
+                        const uint64_t e[4] = {x[r].a, x[r].b, x[r].c, x[r].d};
+                        if (q < V4)
+#pragma unroll
+                            for (int c = 0; c < 4; ++c)
+                                if (4 * q + c < V) mine += e[c];
+                    }
+                }
+            }
             const uint64_t SR = block_sum_u64<kSeqThreads>(mine, scratch);
             if (SR) tok = block_cdf_pick(V, u[k], rw, scratch, &pick);
             else tok = draw_row(ts[i], trow, V, false, u[k], p, scratch, &pick);
@@ -499,6 +630,32 @@ __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __re
     if (threadIdx.x == 0) out[r] = tok;
 }
 
+// Full-vocabulary (or greedy) draw in one kernel: max / argmax, then the
+// inverse-CDF draw of fixed_e(l - lmax) -- the same draw as row_stats +
+// sample_kernel.
+__global__ __launch_bounds__(kSeqThreads) void sample_full_kernel(const float* __restrict__ logits,
+                                                                  const float* __restrict__ uniforms, uint32_t V,
+                                                                  WarpParams p, int32_t* __restrict__ out)
+{
+    __shared__ uint64_t scratch[kSeqThreads / 64];
+    __shared__ int32_t pick;
+    const uint32_t r = blockIdx.x;
+    const float* row = logits + (size_t)r * V;
+    uint64_t best = 0;
+    scan_row<kSeqThreads>(row, V, [&](uint32_t i, float l) {
+        const uint64_t o = order_key(float_key(l), i);
+        best = o > best ? o : best;
+    });
+    const uint64_t top = block_max_u64<kSeqThreads>(best, scratch);
+    int32_t tok = (int32_t)(0xffffffffu - (uint32_t)top);
+    if (!p.greedy) {
+        const float lmax = key_float((uint32_t)(top >> 32));
+        tok = block_cdf_pick(V, uniforms[r], [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); }, scratch,
+                             &pick);
+    }
+    if (threadIdx.x == 0) out[r] = tok;
+}
+
 __global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
 {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
@@ -514,6 +671,8 @@ ulspec_status make_params(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t V,
     p.invT = 1.0f;
     p.scale = __builtin_ldexpf(1.0f, warp_shift(V));
     p.pad = 0;
+    if (V > (uint32_t)(kMaxRounds * 4 * kSeqThreads))
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "vocabulary %u > %d", V, kMaxRounds * 4 * kSeqThreads);
     if (p.greedy) return ULSPEC_OK;
     if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
         return fail(ctx, ULSPEC_EINVAL, "temperature must be positive and finite (got %g)", (double)s->temperature);
@@ -573,6 +732,11 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (st != ULSPEC_OK) return st;
     if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
     if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
+    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
+        hipLaunchKernelGGL(sample_full_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, logits, uniforms, V, p,
+                           out_tokens);
+        return check_launch(ctx, "sample launch");
+    }
     if (!ws) {
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
         if (st != ULSPEC_OK) return st;

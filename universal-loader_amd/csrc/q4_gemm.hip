@@ -447,15 +447,20 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_q4_k_kernel(GemmArgs a)
     if (tile_live) store_tile<MT>(acc, a.out + (size_t)ks * a.M * a.N, a.M, a.N, t);
 }
 
-// ---- whole-X kernels (small M) ---------------------------------------------
-// One workgroup per 16-row tile; wave p computes canonical part p of K (the
-// same parts as the split-K path, so results match it bit for bit).  The whole
-// X (M rows) is copied into LDS with direct buffer->LDS loads (no registers;
-// row pitch rounded up to 1 KB plus 16 B so a partial last load of a row only
-// touches its own padding, and rows fall on different banks), then every
-// weight load of the part is issued; the wait for X covers only the older
-// X copies.  Parts are summed in part order in LDS.
-constexpr int kParts = 16;
+// ---- whole-X streaming kernels (small M) --------------------------------------
+// The whole X (M rows) sits in LDS, copied once per workgroup with direct
+// buffer->LDS loads (no registers; row pitch rounded up to 1 KB plus 16 B so a
+// partial last load of a row only touches its own padding, and rows fall on
+// different banks) or built there by the RMSNorm prologue.  Per iteration the
+// NW waves of a workgroup cover tpi = NW / P tiles x P parts of K (P a power of
+// two, at most NW and at most the chunks per row).  When there are more
+// iterations than CUs, a grid of one 8-wave workgroup per CU walks them and
+// loads the first batch of the next iteration's weights while the current one
+// is multiplied, so each CU keeps a continuous stream of weight loads in
+// flight; otherwise 16-wave workgroups run one iteration each.  Parts are
+// summed in part order in LDS, then the epilogue runs.
+constexpr int kStreamWaves = 8;
+constexpr int kWideWaves = 16;
 
 __host__ __device__ constexpr uint32_t wide_pitch(uint32_t K)
 {
@@ -527,9 +532,8 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
     }
 }
 
-// Parts summed in part order 0..kParts-1; then the epilogue (rows < M, cols
-// < N).  Thread (row group, lane l) holds output (m = 4 (l / 16) + row,
-// n = 16 t + l % 16); columns n and n ^ 1 sit in lanes l and l ^ 1.
+// Epilogue of output (m, n) of tile t, value s.  Thread lanes l and l ^ 1 hold
+// columns n and n ^ 1 of the same row m (whole waves call this).
 //   store: Y[m][n] = s
 //   rope:  RoPE pair (n, n+1) at position pos0 + m (Q and K rows), then fp16
 //          Q -> q16[m][n], K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim]
@@ -538,19 +542,8 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
 //          act[m][i] = fp16(g * (1 / (1 + e^-g)) * u)
 //   resid: h[m][n] += s (in place); pss[m][t] = sum over the tile's 16 columns
 //          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m
-__device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& acc, const GemmArgs& a, int t)
+__device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
-    __syncthreads();
-    if (threadIdx.x >= 256) return;
-    const int row = threadIdx.x >> 6, l = threadIdx.x & 63;
-    float s = red[row * 64 + l];
-#pragma unroll
-    for (int p = 1; p < kParts; ++p) s += red[(p * 4 + row) * 64 + l];
-    const int m = 4 * (l >> 4) + row, n = 16 * t + (l & 15);
     const bool ok = m < a.M && n < a.N;
     const GemmFuse& f = a.f;
     switch (f.epi) {
@@ -598,7 +591,7 @@ __device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& 
         sq += __shfl_xor(sq, 2);
         sq += __shfl_xor(sq, 4);
         sq += __shfl_xor(sq, 8);
-        if (m < a.M && (l & 15) == 0) f.pss_out[(size_t)m * a.n_tiles + t] = sq;
+        if (m < a.M && t < a.n_tiles && (l & 15) == 0) f.pss_out[(size_t)m * a.n_tiles + t] = sq;
         break;
     }
     default:
@@ -608,96 +601,64 @@ __device__ __forceinline__ void sum_parts_and_store(float* red, const float4_t& 
 
 // X[m][k] = fp16((v[m][k] * r_m) * w[k]) into the LDS rows, r_m = 1 /
 // sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
-// Wave m sums row m's P partials (lane-strided, then an xor tree); each thread
-// converts one float4 column group (K <= 4096) of 4 rows at a time, the first
-// group's loads issued before the partial sums are read.
+// Wave w sums the P partials of rows w, w + NW, .. (lane-strided, then an xor
+// tree); each thread converts float4 column groups tid and tid + 64 NW (K <=
+// 4096) of 4 rows at a time, the first group's loads issued before the partial
+// sums are read.
 constexpr int kNormGroup = 4;
 
+template <int NW>
 __device__ __forceinline__ void norm_prologue(const GemmArgs& a, uint8_t* xs, uint32_t pitch, float* rs)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const GemmFuse& f = a.f;
     const int K4 = a.K >> 2;
-    const bool col = tid < K4;
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
-    float4 vv[kNormGroup];
+    float4 vv[kNormGroup][2];
+    float4 w[2];
 #pragma unroll
-    for (int i = 0; i < kNormGroup; ++i)
-        vv[i] = __builtin_bit_cast(float4, buf_load16(vr, i < a.M && col ? (uint32_t)(i * K4 + tid) * 16u : kOOB));
-    const float4 w = col ? ((const float4*)f.norm_w)[tid] : make_float4(0.f, 0.f, 0.f, 0.f);
-    if (wave < a.M) {
+    for (int j = 0; j < 2; ++j) {
+        const int c = tid + NW * 64 * j;
+#pragma unroll
+        for (int i = 0; i < kNormGroup; ++i)
+            vv[i][j] = __builtin_bit_cast(float4, buf_load16(vr, i < a.M && c < K4 ? (uint32_t)(i * K4 + c) * 16u : kOOB));
+        w[j] = c < K4 ? ((const float4*)f.norm_w)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int m = wave; m < a.M; m += NW) {
         float ss = 0.0f;
-        for (int p = lane; p < f.P; p += 64) ss += f.pss[(size_t)wave * f.P + p];
+        for (int p = lane; p < f.P; p += 64) ss += f.pss[(size_t)m * f.P + p];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) rs[wave] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
+        if (lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
     }
     __syncthreads();
     for (int m0 = 0; m0 < a.M; m0 += kNormGroup) {
-        if (m0) {
 #pragma unroll
-            for (int i = 0; i < kNormGroup; ++i)
-                vv[i] = __builtin_bit_cast(
-                    float4, buf_load16(vr, m0 + i < a.M && col ? (uint32_t)((m0 + i) * K4 + tid) * 16u : kOOB));
-        }
-        if (col) {
+        for (int j = 0; j < 2; ++j) {
+            const int c = tid + NW * 64 * j;
+            if (m0) {
 #pragma unroll
-            for (int i = 0; i < kNormGroup; ++i) {
-                const int m = m0 + i;
-                if (m < a.M) {
-                    const float r = rs[m];
-                    half4_t x;
-                    x[0] = (_Float16)((vv[i].x * r) * w.x);
-                    x[1] = (_Float16)((vv[i].y * r) * w.y);
-                    x[2] = (_Float16)((vv[i].z * r) * w.z);
-                    x[3] = (_Float16)((vv[i].w * r) * w.w);
-                    *(half4_t*)(xs + m * pitch + 8 * tid) = x;
+                for (int i = 0; i < kNormGroup; ++i)
+                    vv[i][j] = __builtin_bit_cast(
+                        float4, buf_load16(vr, m0 + i < a.M && c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
+            }
+            if (c < K4) {
+#pragma unroll
+                for (int i = 0; i < kNormGroup; ++i) {
+                    const int m = m0 + i;
+                    if (m < a.M) {
+                        const float r = rs[m];
+                        half4_t x;
+                        x[0] = (_Float16)((vv[i][j].x * r) * w[j].x);
+                        x[1] = (_Float16)((vv[i][j].y * r) * w[j].y);
+                        x[2] = (_Float16)((vv[i][j].z * r) * w[j].z);
+                        x[3] = (_Float16)((vv[i][j].w * r) * w[j].w);
+                        *(half4_t*)(xs + m * pitch + 8 * c) = x;
+                    }
                 }
             }
         }
     }
-}
-
-template <int CMAX>
-__global__ __launch_bounds__(kParts * 64) void gemm_q4_0_wide_kernel(GemmArgs a)
-{
-    extern __shared__ uint4 xs[];
-    __shared__ float rs[kNormMaxRows];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = lane & 15, g = lane >> 4;
-    const int t = blockIdx.x;
-    int qa, qb;
-    slice_range(a, wave, qa, qb);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + lane * 16;
-    const uint32_t s_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + 1024 + r * 8;
-    const int xrow = min(r, a.M - 1) * (int)(wide_pitch(a.K) / 16) + g;
-    const NibbleConsts nk = nibble_consts();
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-
-    if (a.f.pro == kProCopy) x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
-    pin_loads();
-    {  // first batch, straight-line: the X wait before the barrier covers only the X copies
-        uint4 wq[CMAX];
-        uint2 sc[CMAX];
-        const int nc = max(0, min(CMAX, qb - qa));
-        q4_0_load_batch<CMAX>(wr, w_lane, s_lane, qa, nc, wq, sc);
-        pin_loads();
-        if (a.f.pro == kProNorm) norm_prologue(a, (uint8_t*)xs, wide_pitch(a.K), rs);
-        __syncthreads();
-        q4_0_mma_batch<CMAX>(xs, xrow, qa, nc, wq, sc, nk, acc);
-    }
-    for (int c0 = qa + CMAX; c0 < qb; c0 += CMAX) {
-        uint4 wq[CMAX];
-        uint2 sc[CMAX];
-        const int nc = min(CMAX, qb - c0);
-        q4_0_load_batch<CMAX>(wr, w_lane, s_lane, c0, nc, wq, sc);
-        pin_loads();
-        q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, wq, sc, nk, acc);
-    }
-    sum_parts_and_store((float*)xs, acc, a, t);
 }
 
 template <int CMAX>
@@ -755,44 +716,125 @@ __device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, int xrow, int s0
     }
 }
 
+// One batch of up to CMAX chunks of one tile, in registers.
+template <int TYPE, int CMAX>
+struct WBatch;
 template <int CMAX>
-__global__ __launch_bounds__(kParts * 64) void gemm_q4_k_wide_kernel(GemmArgs a)
+struct WBatch<ULSPEC_GGML_Q4_0, CMAX> {
+    uint4 wq[CMAX];
+    uint2 sc[CMAX];
+};
+template <int CMAX>
+struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
+    uint4 w0[CMAX], w1[CMAX], hd[CMAX];
+};
+
+template <int TYPE, int CMAX>
+__device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, int t, int c0, int nc,
+                                            WBatch<TYPE, CMAX>& b)
+{
+    const int lane = threadIdx.x & 63, r = lane & 15;
+    if (t >= a.n_tiles) nc = 0;
+    const uint32_t tile = (uint32_t)(t < a.n_tiles ? t : 0) * a.n_chunks;
+    if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+        q4_0_load_batch<CMAX>(wr, tile * kQ40Chunk + lane * 16, tile * kQ40Chunk + 1024 + r * 8, c0, nc, b.wq, b.sc);
+    else
+        q4_k_load_batch<CMAX>(wr, tile * kQ4KChunk + lane * 16, tile * kQ4KChunk + 2048 + r * 16, c0, nc, b.w0, b.w1,
+                              b.hd);
+}
+
+template <int TYPE, int CMAX>
+__device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, int nc, const WBatch<TYPE, CMAX>& b,
+                                           const NibbleConsts& nk, float4_t& acc)
+{
+    if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+        q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
+    else
+        q4_k_mma_batch<CMAX>(xs, xrow, c0, nc, b.w0, b.w1, b.hd, (threadIdx.x & 63) >> 4, nk, acc);
+}
+
+// Multiply this wave's part of tile slot tw of iteration `it` (first batch
+// already in `cur`), sum the parts in LDS, run the epilogue.
+template <int TYPE, int CMAX, int NW>
+__device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, const uint4* xs, float* red,
+                                            int xrow, int it, int tw, int P, int tpi, int ca, int cb,
+                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = it * tpi + tw;
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    stream_mma<TYPE, CMAX>(xs, xrow, ca, t < a.n_tiles ? min(CMAX, cb - ca) : 0, cur, nk, acc);
+    for (int c0 = ca + CMAX; c0 < cb; c0 += CMAX) {  // the rest of a long part (not prefetched)
+        const int nc = min(CMAX, cb - c0);
+        stream_load<TYPE, CMAX>(a, wr, t, c0, nc, cur);
+        pin_loads();
+        stream_mma<TYPE, CMAX>(xs, xrow, c0, t < a.n_tiles ? nc : 0, cur, nk, acc);
+    }
+    __syncthreads();  // the previous iteration's epilogue is done with red
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    __syncthreads();
+    // 256 threads per tile slot, NW / 4 slots per pass
+    const int row = (threadIdx.x >> 6) & 3, l = lane;
+    for (int j = threadIdx.x >> 8; j < tpi; j += NW / 4) {
+        float s = red[((j * P) * 4 + row) * 64 + l];
+        for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
+        const int tt = it * tpi + j;
+        epilogue(a, s, 4 * (l >> 4) + row, 16 * tt + (l & 15), tt, l);
+    }
+}
+
+// NW waves per workgroup.  PIPE: the grid is smaller than the iteration count
+// and the next iteration's first batch is prefetched (two register sets);
+// otherwise every workgroup runs exactly one iteration.
+template <int TYPE, int CMAX, int NW, bool PIPE>
+__global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
+    __shared__ float red[NW * 4 * 64];
     __shared__ float rs[kNormMaxRows];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int t = blockIdx.x;
-    int sa, sb;
-    slice_range(a, wave, sa, sb);
+    const int P = a.ks_count, tpi = NW / P;
+    const int tw = wave / P, p = wave - (wave / P) * P;
+    const int ca = p * a.ks_q + min(p, a.ks_r);
+    const int cb = ca + a.ks_q + (p < a.ks_r ? 1 : 0);
+    const int nc0 = max(0, min(CMAX, cb - ca));
+    const int n_iter = (a.n_tiles + tpi - 1) / tpi;
+    const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + lane * 16;
-    const uint32_t h_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + 2048 + r * 16;
-    const int xrow = min(r, a.M - 1) * (int)(wide_pitch(a.K) / 16) + 8 * g;
+    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_0 ? g : 8 * g);
     const NibbleConsts nk = nibble_consts();
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
 
-    if (a.f.pro == kProCopy) x_copy_to_lds<kParts>(a, xr, (uint8_t*)xs);
+    if (a.f.pro == kProCopy) x_copy_to_lds<NW>(a, xr, (uint8_t*)xs);
     pin_loads();
-    {
-        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
-        const int nc = max(0, min(CMAX, sb - sa));
-        q4_k_load_batch<CMAX>(wr, w_lane, h_lane, sa, nc, w0, w1, hd);
-        pin_loads();
-        if (a.f.pro == kProNorm) norm_prologue(a, (uint8_t*)xs, wide_pitch(a.K), rs);
-        __syncthreads();
-        q4_k_mma_batch<CMAX>(xs, xrow, sa, nc, w0, w1, hd, g, nk, acc);
+    WBatch<TYPE, CMAX> A;
+    int it = blockIdx.x;
+    stream_load<TYPE, CMAX>(a, wr, it * tpi + tw, ca, nc0, A);
+    pin_loads();
+    if (a.f.pro == kProNorm) norm_prologue<NW>(a, (uint8_t*)xs, pitch, rs);
+    __syncthreads();
+    if constexpr (!PIPE) {
+        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk);
+    } else {
+        WBatch<TYPE, CMAX> B;
+        while (true) {
+            int nxt = it + gridDim.x;
+            stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, B);
+            pin_loads();
+            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk);
+            it = nxt;
+            if (it >= n_iter) break;
+            nxt = it + gridDim.x;
+            stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, A);
+            pin_loads();
+            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, B, nk);
+            it = nxt;
+            if (it >= n_iter) break;
+        }
     }
-    for (int s0 = sa + CMAX; s0 < sb; s0 += CMAX) {
-        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
-        const int nc = min(CMAX, sb - s0);
-        q4_k_load_batch<CMAX>(wr, w_lane, h_lane, s0, nc, w0, w1, hd);
-        pin_loads();
-        q4_k_mma_batch<CMAX>(xs, xrow, s0, nc, w0, w1, hd, g, nk, acc);
-    }
-    sum_parts_and_store((float*)xs, acc, a, t);
 }
 
 // Y[i] = sum over slices in slice order (deterministic); all loads issued
@@ -816,6 +858,8 @@ __global__ __launch_bounds__(256) void reduce_slices_kernel(const float* __restr
 
 constexpr int kQ40CMax = 8;
 constexpr int kQ4KCMax = 4;
+constexpr int kQ40Stream = 12;
+constexpr int kQ4KStream = 6;
 
 template <int MT>
 void launch_mt(const Weight& w, const GemmArgs& a, hipStream_t st)
@@ -831,25 +875,67 @@ void launch_mt(const Weight& w, const GemmArgs& a, hipStream_t st)
 
 namespace ulspec {
 
-// LDS available to one workgroup on gfx950.
+// LDS available to one workgroup on gfx950, and what the streaming kernel
+// keeps besides X (part sums, norm factors, margin).
 constexpr size_t kWideLdsMax = 160 * 1024;
+constexpr size_t kStreamStatic = kWideWaves * 4 * 64 * sizeof(float) + 512;
 
-// (less 256 B for the kernels' static LDS)
 bool wide_fits(int M, uint32_t K)
 {
-    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax - 256;
+    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax - kStreamStatic;
 }
 
-// Opt the whole-X kernels in to the full 160 KB of LDS.
+// Opt the whole-X kernels in to the LDS they need for X.
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
-    hipError_t e = hipFuncSetAttribute((const void*)gemm_q4_0_wide_kernel<kQ40CMax>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax - 256);
-    if (e == hipSuccess)
-        e = hipFuncSetAttribute((const void*)gemm_q4_k_wide_kernel<kQ4KCMax>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideLdsMax - 256);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
+    const int dyn = (int)(kWideLdsMax - kStreamStatic);
+    const void* fns[] = {
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false>,
+    };
+    for (const void* f : fns) {
+        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
+    }
     return ULSPEC_OK;
+}
+
+// Launch the whole-X kernel.  More tiles than CUs: the pipelined 8-wave grid
+// of one workgroup per CU, P parts per tile (the largest power of two <=
+// min(8, chunks per row)), 8 / P tiles per iteration.  Otherwise one 16-wave
+// workgroup per tile, 16 parts (waves with an empty part idle).
+void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
+{
+    const int n_cu = std::max(1, ctx->n_cu);
+    const bool pipe = (int)w.n_tiles > n_cu;
+    int P = pipe ? kStreamWaves : kWideWaves;
+    if (pipe)
+        while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
+    const int n_iter = ((int)w.n_tiles + (pipe ? kStreamWaves / P : 1) - 1) / (pipe ? kStreamWaves / P : 1);
+    a.ks_count = P;
+    a.ks_q = (int)(w.n_chunks / P);
+    a.ks_r = (int)(w.n_chunks % P);
+    const size_t lds = (size_t)a.M * wide_pitch(w.k);
+    const bool q40 = w.type == ULSPEC_GGML_Q4_0;
+    if (pipe) {
+        const dim3 grid(std::min(n_iter, n_cu)), block(kStreamWaves * 64);
+        if (q40)
+            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true>), grid, block, lds,
+                               ctx->stream, a);
+        else
+            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true>), grid, block, lds,
+                               ctx->stream, a);
+    } else {
+        const dim3 grid(n_iter), block(kWideWaves * 64);
+        if (q40)
+            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false>), grid, block, lds,
+                               ctx->stream, a);
+        else
+            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false>), grid, block, lds,
+                               ctx->stream, a);
+    }
 }
 
 // K slices per weight: about one workgroup per CU in total.
@@ -891,19 +977,9 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
         a.ks_q = (int)(w.n_chunks / w.ksplit);
         a.ks_r = (int)(w.n_chunks % w.ksplit);
         a.f = GemmFuse();
-        if (wide_fits(mc, w.k)) {
-            // whole X in LDS, canonical kParts parts, summed in the kernel
+        if (wide_fits(mc, w.k)) {  // whole X in LDS, parts summed in the kernel
             a.out = y + (size_t)m0 * w.n;
-            a.ks_count = kParts;
-            a.ks_q = (int)(w.n_chunks / kParts);
-            a.ks_r = (int)(w.n_chunks % kParts);
-            const size_t lds = std::max<size_t>((size_t)mc * wide_pitch(w.k), kParts * 4 * 64 * sizeof(float));
-            if (w.type == ULSPEC_GGML_Q4_0)
-                hipLaunchKernelGGL(gemm_q4_0_wide_kernel<kQ40CMax>, dim3(w.n_tiles), dim3(kParts * 64), lds,
-                                   ctx->stream, a);
-            else
-                hipLaunchKernelGGL(gemm_q4_k_wide_kernel<kQ4KCMax>, dim3(w.n_tiles), dim3(kParts * 64), lds,
-                                   ctx->stream, a);
+            stream_launch(ctx, w, a);
             continue;
         }
         switch ((mc + 15) / 16) {
@@ -936,15 +1012,8 @@ ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, co
     a.K = (int)w.k;
     a.n_tiles = (int)w.n_tiles;
     a.n_chunks = (int)w.n_chunks;
-    a.ks_count = kParts;
-    a.ks_q = (int)(w.n_chunks / kParts);
-    a.ks_r = (int)(w.n_chunks % kParts);
     a.f = f;
-    const size_t lds = std::max<size_t>((size_t)M * wide_pitch(w.k), kParts * 4 * 64 * sizeof(float));
-    if (w.type == ULSPEC_GGML_Q4_0)
-        hipLaunchKernelGGL(gemm_q4_0_wide_kernel<kQ40CMax>, dim3(w.n_tiles), dim3(kParts * 64), lds, ctx->stream, a);
-    else
-        hipLaunchKernelGGL(gemm_q4_k_wide_kernel<kQ4KCMax>, dim3(w.n_tiles), dim3(kParts * 64), lds, ctx->stream, a);
+    stream_launch(ctx, w, a);
     return check_launch(ctx, "fused gemm launch");
 }
 
