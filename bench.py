@@ -164,6 +164,187 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
     }
 
 
+def _ora():
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle
+    return oracle
+
+
+def _time_direct(ctx, fn, reps):
+    """Average us per call of fn() over reps back-to-back direct launches (HIP
+    events on the context stream)."""
+    fn()
+    ctx.sync()
+    ctx.timer_mark(4)
+    for _ in range(reps):
+        fn()
+    ctx.timer_mark(5)
+    return ctx.timer_elapsed_ms(4, 5) * 1e3 / reps
+
+
+def workload_gemm(pkg, ctx, args):
+    """Verify dequant-GEMM alone: Q4_0 weights N(0, 0.02^2), fp16 X N(0,1),
+    M in {1,5,9,17}; 24 copies of each weight rotated (> 256 MB, past the
+    MALL).  Headline: N=4096, K=11008, M=5."""
+    ora = _ora()
+    rng = np.random.default_rng(args.seed)
+    rows, head = [], None
+    for N, K in ((4096, 4096), (11008, 4096), (4096, 11008)):
+        nb = N * pkg.row_bytes(pkg.Q4_0, K)
+        buf = ctx.alloc(nb)
+        ctx.synth_q4(pkg.Q4_0, 7, N + K, N, K, 0.02, buf)
+        W = ctx.download(buf, np.uint8, (nb,))
+        buf.free()
+        ids = [ctx.weight_upload(pkg.Q4_0, W, N, K) for _ in range(24)]
+        for M in (1, 5, 9, 17):
+            X = rng.standard_normal((M, K)).astype(np.float16).view(np.uint16)
+            xb, yb = ctx.upload(X), ctx.alloc(M * N * 4)
+            it = iter(range(1 << 30))
+            us = _time_direct(ctx, lambda: ctx.verify_gemm(ids[next(it) % 24], xb, M, yb), 24 * args.reps)
+            alg = nb + 2 * M * K + 4 * M * N
+            gbs = alg / us / 1e3
+            rows.append({"N": N, "K": K, "M": M, "us": us, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS})
+            log(f"Q4_0 N={N} K={K} M={M}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s)")
+            if (N, K, M) == (4096, 11008, 5):
+                head = (us, alg, gbs)
+                Y = ctx.download(yb, np.float32, (M, N))
+                ref = ora.q4_gemm_f64(pkg.Q4_0, W, N, K, X)
+                err = float(np.abs(Y - ref).max() / np.sqrt((ref ** 2).mean()))
+                # CPU baseline: the oracle's AVX2 f32 dequant-GEMM on the same inputs
+                t0, n = time.perf_counter(), 0
+                while time.perf_counter() - t0 < args.cpu_seconds:
+                    ora.q4_gemm_f32(pkg.Q4_0, W, N, K, X)
+                    n += 1
+                cpu_gbs = alg * n / (time.perf_counter() - t0) / 1e9
+            xb.free()
+            yb.free()
+    us, alg, gbs = head
+    return {
+        "metric": "verify-GEMM HBM GB/s (Q4_0 4096x11008, M=5)", "value": gbs, "unit": "GB/s", "ms_per_step": us / 1e3,
+        "dtype": "q4_0 weights x fp16 activations, fp32 accumulate",
+        "config": {"workload": "Q4_0 verify dequant-GEMM N=4096 K=11008 M=5, 24 rotated weight copies", "table": rows},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
+        "cpu_baseline": {"value": cpu_gbs, "unit": "GB/s", "cores": ora.nthreads_default(), "kind": "port",
+                         "sample": "oracle AVX2 f32 dequant-GEMM, N=4096 K=11008 M=5, repeated "
+                                   f"for {args.cpu_seconds:.0f} s"},
+        "parity": {"max_err_over_rms_vs_f64": err},
+    }
+
+
+def workload_attention(pkg, ctx, args):
+    """Verify attention alone: 32 heads x 128, fp16 K/V of 4096 prior tokens
+    N(0,1); 5 causal queries and a 16-node draft tree (branching <= 3, depth
+    <= 5).  Headline: the causal case."""
+    ora = _ora()
+    rng = np.random.default_rng(args.seed)
+    H, D, P = 32, 128, 4096
+    out, head = [], None
+    parents = {"causal5": None, "tree16": np.array([-1, 0, 0, 1, 1, 2, 3, 3, 4, -1, 9, 9, 10, 5, 13, 6], np.int32)}
+    for name, parent in parents.items():
+        nq = 5 if parent is None else 16
+        L = P + nq
+        q = rng.standard_normal((nq, H, D)).astype(np.float16).view(np.uint16)
+        k = rng.standard_normal((L, H, D)).astype(np.float16).view(np.uint16)
+        v = rng.standard_normal((L, H, D)).astype(np.float16).view(np.uint16)
+        bq, bk, bv, bo = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.alloc(nq * H * D * 4)
+        scale = 1.0 / np.sqrt(D)
+        us = _time_direct(ctx, lambda: ctx.verify_attention(bq, bk, bv, P, nq, parent, H, H, D, scale, bo), args.reps)
+        alg = 2 * L * H * D * 2 + nq * H * D * (2 + 4)
+        gbs = alg / us / 1e3
+        o = ctx.download(bo, np.float32, (nq, H, D))
+        ref = ora.attention_f64(q, k, v, P, parent, H, H, D, scale)
+        err = float(np.abs(o - ref).max())
+        out.append({"case": name, "us": us, "GB/s": gbs, "max_abs_err_vs_f64": err})
+        log(f"attention {name}: {us:.2f} us, {gbs:.0f} GB/s, max err {err:.1e}")
+        if name == "causal5":
+            head = (us, alg, gbs)
+            t0, n = time.perf_counter(), 0
+            while time.perf_counter() - t0 < args.cpu_seconds:
+                ora.attention_f32(q, k, v, P, None, H, H, D, scale)
+                n += 1
+            cpu_gbs = alg * n / (time.perf_counter() - t0) / 1e9
+        for b in (bq, bk, bv, bo):
+            b.free()
+    us, alg, gbs = head
+    return {
+        "metric": "verify-attention HBM GB/s (32x128, prefix 4096, 5 causal queries)", "value": gbs, "unit": "GB/s",
+        "ms_per_step": us / 1e3, "dtype": "fp16 K/V, fp32 softmax",
+        "config": {"workload": "verify attention H=32 D=128 prefix 4096, causal nq=5 (and tree nq=16)", "cases": out},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
+        "cpu_baseline": {"value": cpu_gbs, "unit": "GB/s", "cores": ora.nthreads_default(), "kind": "port",
+                         "sample": f"oracle f32 attention, causal nq=5, repeated for {args.cpu_seconds:.0f} s"},
+    }
+
+
+def workload_accept(pkg, ctx, args):
+    """Acceptance sampling alone: B=16 sequences, k in {4, 8}, V in {32000,
+    128256}; logits N(0, 3^2) with one +8 boost per row; T 0.8, top-k 40,
+    top-p 0.9 (and the greedy rule).  Headline: k=4, V=32000."""
+    ora = _ora()
+    rng = np.random.default_rng(args.seed)
+    B = 16
+    cases, head = [], None
+    for k, V in ((4, 32000), (8, 32000), (4, 128256), (8, 128256)):
+        tl = (3.0 * rng.standard_normal((B, k + 1, V))).astype(np.float32)
+        dl = (3.0 * rng.standard_normal((B, k, V))).astype(np.float32)
+        for a in (tl, dl):
+            flat = a.reshape(-1, V)
+            flat[np.arange(flat.shape[0]), rng.integers(0, V, flat.shape[0])] += 8.0
+        s_ora = ora.sampling(temperature=0.8, top_k=40, top_p=0.9)
+        dt = np.stack([ora.sample(s_ora, dl[b], ora.uniforms(args.seed + 1, b * k, k)) for b in range(B)])
+        u = np.stack([ora.uniforms(args.seed + 2, b * (k + 1), k + 1) for b in range(B)])
+        btl, bdl, bdt, bu = ctx.upload(tl), ctx.upload(dl), ctx.upload(dt), ctx.upload(u)
+        bo, bn = ctx.alloc(B * (k + 1) * 4), ctx.alloc(B * 4)
+        for greedy in (False, True):
+            s = pkg.sampling(greedy=True) if greedy else pkg.sampling(temperature=0.8, top_k=40, top_p=0.9)
+            us = _time_direct(ctx, lambda: ctx.accept(s, B, k, V, btl, bdl, bdt, bu, bo, bn), args.reps)
+            alg = 4 * B * (2 * k + 1) * V if not greedy else 4 * B * (k + 1) * V
+            gbs = alg / us / 1e3
+            got = ctx.download(bo, np.int32, (B, k + 1))
+            want, _ = ora.accept(ora.sampling(greedy=True) if greedy else s_ora, tl, dl, dt, u)
+            exact = bool(np.array_equal(got, want))
+            cases.append({"k": k, "V": V, "greedy": greedy, "us": us, "GB/s": gbs, "bit_exact": exact})
+            log(f"accept k={k} V={V} greedy={greedy}: {us:.2f} us, {gbs:.0f} GB/s, bit-exact {exact}")
+            if (k, V, greedy) == (4, 32000, False):
+                head = (us, alg, gbs)
+                t0, n = time.perf_counter(), 0
+                while time.perf_counter() - t0 < args.cpu_seconds:
+                    ora.accept(s_ora, tl, dl, dt, u)
+                    n += 1
+                cpu_gbs = alg * n / (time.perf_counter() - t0) / 1e9
+        for b in (btl, bdl, bdt, bu, bo, bn):
+            b.free()
+    us, alg, gbs = head
+    return {
+        "metric": "acceptance-sampling HBM GB/s (B=16, k=4, V=32000)", "value": gbs, "unit": "GB/s",
+        "ms_per_step": us / 1e3, "dtype": "fp32 logits, exact u64 fixed point",
+        "config": {"workload": "acceptance sampling B=16 k=4 V=32000, T 0.8 top-k 40 top-p 0.9", "cases": cases},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
+        "cpu_baseline": {"value": cpu_gbs, "unit": "GB/s", "cores": ora.nthreads_default(), "kind": "port",
+                         "sample": f"oracle accept rule, same inputs, repeated for {args.cpu_seconds:.0f} s"},
+    }
+
+
+def workload_copy(pkg, ctx, args):
+    """Calibration: device-to-device copies of 25362432 bytes (the size of a
+    4096 x 11008 Q4_0 weight), the reference point that scales the FETCH_SIZE /
+    WRITE_SIZE counters to bytes."""
+    nb = 25362432
+    a, b = ctx.alloc(nb), ctx.alloc(nb)
+    us = _time_direct(ctx, lambda: pkg.lib().ulspec_memcpy(ctx.handle, b.ptr, a.ptr, nb, 2), args.reps)
+    a.free()
+    b.free()
+    gbs = 2 * nb / us / 1e3
+    log(f"copy {nb} B: {us:.2f} us, {gbs:.0f} GB/s (read + write)")
+    return {"metric": "device copy GB/s (read + write), 25362432 B", "value": gbs, "unit": "GB/s",
+            "ms_per_step": us / 1e3, "dtype": "u8", "config": {"workload": "hipMemcpyAsync D2D of 25362432 B"},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None}, "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +356,11 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy"),
+                    default="step",
+                    help="step: the speculative step (default); roofline: only the step's verify-GEMM roofline "
+                         "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration")
+    ap.add_argument("--reps", type=int, default=50, help="launches per timing (kernel workloads)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch each step's kernels directly instead of replaying the captured graph")
     args = ap.parse_args()
@@ -185,6 +371,30 @@ def main():
     pkg = load_package()
     synthetic_llama = importlib.import_module("universal_loader_amd.synthetic").synthetic_llama
     ctx = pkg.Context(0)
+    if args.workload == "roofline":
+        target, _ = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=CONTEXT + 64), pkg.Q4_K, seed=1)
+        ids = weight_ids(pkg, ctx)
+        us, alg = gemm_roofline(pkg, ctx, ids, K_SPEC + 1)
+        achieved = alg / (us * 1e-6) / 1e9
+        log(f"verify GEMM (target, M=6): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
+            f"{achieved:.0f} GB/s")
+        target.close()
+        ctx.close()
+        print(json.dumps({"metric": "verify-GEMM HBM GB/s, 7B-shape Q4_K target weights, M=6", "value": achieved,
+                          "unit": "GB/s", "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                                                       "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                                                       "traffic": read_traffic(), "avg_us": us,
+                                                       "algorithmic_bytes": alg}}), flush=True)
+        return 0
+    if args.workload != "step":
+        fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
+              "copy": workload_copy}[args.workload]
+        out = fn(pkg, ctx, args)
+        base = {"n_gpus": 1, "steps": args.reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
+                "vs_baseline": None, "data": "synthetic, seeded"}
+        ctx.close()
+        print(json.dumps(dict(base, **out)), flush=True)
+        return 0
     use_cpu = not args.no_cpu
     cpu_steps = args.cpu_steps if use_cpu else 0
     cap = CONTEXT + (cpu_steps + args.warmup + args.steps) * (K_SPEC + 1) + 32
