@@ -108,6 +108,21 @@ __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
 // The hardware still overlaps them; s_waitcnt is placed at each first use.
 __device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
 
+// Workgroup barrier after this wave's LDS accesses have completed; no memory
+// fence, so vector loads in flight stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// As lds_barrier, and every vector-memory operation but the N youngest has
+// completed.  After buffer->LDS copies followed by N register loads this
+// waits for the copies only (vmcnt retires in issue order), where a fenced
+// barrier would also wait for the N loads.
+template <int N>
+__device__ __forceinline__ void vm_barrier()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Raw buffer loads: 32-bit offsets from a base held in scalar registers, and
 // the hardware returns 0 for offsets at or past num_records instead of
 // faulting.  0x00020000 is the gfx9-family dword-3 of the resource.
@@ -532,8 +547,50 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
     }
 }
 
-// Epilogue of output (m, n) of tile t, value s.  Thread lanes l and l ^ 1 hold
-// columns n and n ^ 1 of the same row m (whole waves call this).
+// Position of row 0 for the RoPE epilogue: a scalar load through the
+// constant address space (the value is fixed for the whole kernel), so it
+// never waits behind the vector loads in flight.
+__device__ __forceinline__ int epi_pos0(const GemmArgs& a)
+{
+    if (a.f.epi != kEpiRope) return 0;
+    const __attribute__((address_space(4))) int32_t* p = (const __attribute__((address_space(4))) int32_t*)a.f.pos_dev;
+    return *p + a.f.pos_add;
+}
+
+// The memory operands of the epilogue of output (m, n), loaded ahead of it
+// with the weights of the same tile so that the epilogue reads no memory
+// (vmcnt retires in issue order: a load issued in the epilogue would wait for
+// every weight load in flight).  Exactly two 4-byte loads per call whatever
+// the epilogue, out of range when unused:
+//   resid: (h[m][n], -)      rope: (cos, sin) of the pair at position pos0 + m
+__device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int pos0)
+{
+    const GemmFuse& f = a.f;
+    const bool ok = m < a.M && n < a.N;
+    __amdgpu_buffer_rsrc_t r;
+    uint32_t o0 = kOOB, o1 = kOOB;
+    if (f.epi == kEpiResid) {
+        r = make_rsrc(f.h, (uint32_t)a.M * (uint32_t)a.N * 4u);
+        if (ok) o0 = (uint32_t)(m * a.N + n) * 4u;
+    } else if (f.epi == kEpiRope) {
+        r = make_rsrc(f.rope, (uint32_t)(pos0 + a.M) * (uint32_t)(f.hd / 2) * 8u);
+        if (ok && n < f.qdim + f.kvdim) {
+            const int nn = n < f.qdim ? n : n - f.qdim;
+            o0 = (uint32_t)((pos0 + m) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
+            o1 = o0 + 4u;
+        }
+    } else {
+        r = make_rsrc(a.out, 0u);
+    }
+    float2 v;
+    v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o0, 0, 0));
+    v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o1, 0, 0));
+    return v;
+}
+
+// Epilogue of output (m, n) of tile t, value s; pre from epi_load, pos0 from
+// epi_pos0.  Thread lanes l and l ^ 1 hold columns n and n ^ 1 of the same
+// row m (whole waves call this).
 //   store: Y[m][n] = s
 //   rope:  RoPE pair (n, n+1) at position pos0 + m (Q and K rows), then fp16
 //          Q -> q16[m][n], K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim]
@@ -542,7 +599,7 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
 //          act[m][i] = fp16(g * (1 / (1 + e^-g)) * u)
 //   resid: h[m][n] += s (in place); pss[m][t] = sum over the tile's 16 columns
 //          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m
-__device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l)
+__device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l, float2 pre, int pos0)
 {
     const bool ok = m < a.M && n < a.N;
     const GemmFuse& f = a.f;
@@ -551,10 +608,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
         const float other = __shfl_xor(s, 1);
         if (!ok) break;
         const bool odd = n & 1;
-        const int pos = *f.pos_dev + f.pos_add + m;
+        const int pos = pos0 + m;
         if (n < f.qdim + f.kvdim) {
             const int nn = n < f.qdim ? n : n - f.qdim;
-            const float2 cs = f.rope[(size_t)pos * (f.hd / 2) + (nn % f.hd) / 2];
+            const float2 cs = pre;
             const float x0 = odd ? other : s, x1 = odd ? s : other;
             float y;
             if (!odd) {
@@ -582,9 +639,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
     case kEpiResid: {
         float v = 0.0f;
         if (ok) {
-            float* hp = f.h + (size_t)m * a.N + n;
-            v = *hp + s;
-            *hp = v;
+            v = pre.x + s;
+            f.h[(size_t)m * a.N + n] = v;
         }
         float sq = v * v;
         sq += __shfl_xor(sq, 1);
@@ -601,47 +657,89 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
 
 // X[m][k] = fp16((v[m][k] * r_m) * w[k]) into the LDS rows, r_m = 1 /
 // sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
-// Wave w sums the P partials of rows w, w + NW, .. (lane-strided, then an xor
-// tree); each thread converts float4 column groups tid and tid + 64 NW (K <=
-// 4096) of 4 rows at a time, the first group's loads issued before the partial
-// sums are read.
-constexpr int kNormGroup = 4;
+// Two phases so that the weight loads overlap the norm: norm_issue loads the
+// partial sums (rows wave and wave + NW, P <= 256), the norm weights and the
+// first kNormGroup rows of v into registers before the weights' first batch
+// is issued; norm_finish reduces the partials (lane-strided, then an xor
+// tree), then converts float4 column groups tid + 64 NW j (K <= 4096).  Rows
+// past the first group (M > kNormGroup) are loaded in norm_finish.
+constexpr int kNormGroup = 8;
+constexpr int kNormMaxPartials = 256;
 
 template <int NW>
-__device__ __forceinline__ void norm_prologue(const GemmArgs& a, uint8_t* xs, uint32_t pitch, float* rs)
+struct NormRegs {
+    static constexpr int JN = 4096 / (NW * 64 * 4);  // float4 column groups per thread
+    float4 vv[kNormGroup][JN];
+    float4 w[JN];
+    float ps[2][kNormMaxPartials / 64];
+};
+
+template <int NW>
+__device__ __forceinline__ void norm_rows_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t vr, int m0,
+                                               NormRegs<NW>& n)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const GemmFuse& f = a.f;
     const int K4 = a.K >> 2;
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
-    float4 vv[kNormGroup][2];
-    float4 w[2];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int c = tid + NW * 64 * j;
+    for (int j = 0; j < NormRegs<NW>::JN; ++j) {
+        const int c = (int)threadIdx.x + NW * 64 * j;
 #pragma unroll
         for (int i = 0; i < kNormGroup; ++i)
-            vv[i][j] = __builtin_bit_cast(float4, buf_load16(vr, i < a.M && c < K4 ? (uint32_t)(i * K4 + c) * 16u : kOOB));
-        w[j] = c < K4 ? ((const float4*)f.norm_w)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            n.vv[i][j] = __builtin_bit_cast(
+                float4, buf_load16(vr, m0 + i < a.M && c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
     }
-    for (int m = wave; m < a.M; m += NW) {
+}
+
+template <int NW>
+__device__ __forceinline__ void norm_issue(const GemmArgs& a, NormRegs<NW>& n)
+{
+    const GemmFuse& f = a.f;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int K4 = a.K >> 2;
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(f.pss, (uint32_t)a.M * (uint32_t)f.P * 4u);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(f.norm_w, (uint32_t)a.K * 4u);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = wave + NW * i;
+#pragma unroll
+        for (int q = 0; q < kNormMaxPartials / 64; ++q) {
+            const int p = lane + 64 * q;
+            n.ps[i][q] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(pr, m < a.M && p < f.P ? (uint32_t)(m * f.P + p) * 4u : kOOB,
+                                                            0, 0));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NormRegs<NW>::JN; ++j) {
+        const int c = (int)threadIdx.x + NW * 64 * j;
+        n.w[j] = __builtin_bit_cast(float4, buf_load16(wr, c < K4 ? (uint32_t)c * 16u : kOOB));
+    }
+    norm_rows_load<NW>(a, vr, 0, n);
+}
+
+template <int NW>
+__device__ __forceinline__ void norm_finish(const GemmArgs& a, NormRegs<NW>& n, uint8_t* xs, uint32_t pitch, float* rs)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const GemmFuse& f = a.f;
+    const int K4 = a.K >> 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = wave + NW * i;
         float ss = 0.0f;
-        for (int p = lane; p < f.P; p += 64) ss += f.pss[(size_t)m * f.P + p];
+#pragma unroll
+        for (int q = 0; q < kNormMaxPartials / 64; ++q) ss += n.ps[i][q];
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
+        if (m < a.M && lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
     }
-    __syncthreads();
+    lds_barrier();
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
     for (int m0 = 0; m0 < a.M; m0 += kNormGroup) {
+        if (m0) norm_rows_load<NW>(a, vr, m0, n);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int c = tid + NW * 64 * j;
-            if (m0) {
-#pragma unroll
-                for (int i = 0; i < kNormGroup; ++i)
-                    vv[i][j] = __builtin_bit_cast(
-                        float4, buf_load16(vr, m0 + i < a.M && c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
-            }
+        for (int j = 0; j < NormRegs<NW>::JN; ++j) {
+            const int c = (int)threadIdx.x + NW * 64 * j;
             if (c < K4) {
 #pragma unroll
                 for (int i = 0; i < kNormGroup; ++i) {
@@ -649,10 +747,10 @@ __device__ __forceinline__ void norm_prologue(const GemmArgs& a, uint8_t* xs, ui
                     if (m < a.M) {
                         const float r = rs[m];
                         half4_t x;
-                        x[0] = (_Float16)((vv[i][j].x * r) * w[j].x);
-                        x[1] = (_Float16)((vv[i][j].y * r) * w[j].y);
-                        x[2] = (_Float16)((vv[i][j].z * r) * w[j].z);
-                        x[3] = (_Float16)((vv[i][j].w * r) * w[j].w);
+                        x[0] = (_Float16)((n.vv[i][j].x * r) * n.w[j].x);
+                        x[1] = (_Float16)((n.vv[i][j].y * r) * n.w[j].y);
+                        x[2] = (_Float16)((n.vv[i][j].z * r) * n.w[j].z);
+                        x[3] = (_Float16)((n.vv[i][j].w * r) * n.w[j].w);
                         *(half4_t*)(xs + m * pitch + 8 * c) = x;
                     }
                 }
@@ -721,11 +819,13 @@ template <int TYPE, int CMAX>
 struct WBatch;
 template <int CMAX>
 struct WBatch<ULSPEC_GGML_Q4_0, CMAX> {
+    static constexpr int kLoads = 2 * CMAX;  // buffer loads per batch
     uint4 wq[CMAX];
     uint2 sc[CMAX];
 };
 template <int CMAX>
 struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
+    static constexpr int kLoads = 3 * CMAX;
     uint4 w0[CMAX], w1[CMAX], hd[CMAX];
 };
 
@@ -758,7 +858,7 @@ __device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, in
 template <int TYPE, int CMAX, int NW>
 __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, const uint4* xs, float* red,
                                             int xrow, int it, int tw, int P, int tpi, int ca, int cb,
-                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk)
+                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk, int pos0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = it * tpi + tw;
@@ -780,14 +880,18 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_r
         float s = red[((j * P) * 4 + row) * 64 + l];
         for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
         const int tt = it * tpi + j;
-        epilogue(a, s, 4 * (l >> 4) + row, 16 * tt + (l & 15), tt, l);
+        const int m = 4 * (l >> 4) + row, n = 16 * tt + (l & 15);
+        epilogue(a, s, m, n, tt, l, epi_load(a, m, n, pos0), pos0);
     }
 }
 
 // NW waves per workgroup.  PIPE: the grid is smaller than the iteration count
 // and the next iteration's first batch is prefetched (two register sets);
-// otherwise every workgroup runs exactly one iteration.
-template <int TYPE, int CMAX, int NW, bool PIPE>
+// otherwise every workgroup runs exactly one iteration.  NORM: X is built by
+// the RMSNorm prologue, else copied.  Issue order: X (copies or the norm's
+// register loads), then the first weight batch; the barrier waits for X only,
+// so the weights keep streaming in while X is finished.
+template <int TYPE, int CMAX, int NW, bool PIPE, bool NORM>
 __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
@@ -804,35 +908,148 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int n_iter = (a.n_tiles + tpi - 1) / tpi;
     const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
     const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_0 ? g : 8 * g);
     const NibbleConsts nk = nibble_consts();
+    const int pos0 = epi_pos0(a);
 
-    if (a.f.pro == kProCopy) x_copy_to_lds<NW>(a, xr, (uint8_t*)xs);
+    NormRegs<NW> nr;
+    if constexpr (NORM)
+        norm_issue<NW>(a, nr);
+    else
+        x_copy_to_lds<NW>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs);
     pin_loads();
     WBatch<TYPE, CMAX> A;
     int it = blockIdx.x;
     stream_load<TYPE, CMAX>(a, wr, it * tpi + tw, ca, nc0, A);
     pin_loads();
-    if (a.f.pro == kProNorm) norm_prologue<NW>(a, (uint8_t*)xs, pitch, rs);
-    __syncthreads();
+    if constexpr (NORM) {
+        norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
+        lds_barrier();
+    } else {
+        vm_barrier<WBatch<TYPE, CMAX>::kLoads>();
+    }
     if constexpr (!PIPE) {
-        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk);
+        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0);
     } else {
         WBatch<TYPE, CMAX> B;
         while (true) {
             int nxt = it + gridDim.x;
             stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, B);
             pin_loads();
-            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk);
+            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0);
             it = nxt;
             if (it >= n_iter) break;
             nxt = it + gridDim.x;
             stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, A);
             pin_loads();
-            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, B, nk);
+            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, B, nk, pos0);
             it = nxt;
             if (it >= n_iter) break;
+        }
+    }
+}
+
+// ---- ring-buffered whole-X kernel (more tiles than CUs) ----------------------
+// One 8-wave workgroup per CU walks its iterations (tpi = 8 / P tiles x P
+// parts each, as above) with a ring of D register batches: the first D
+// iterations' weights are issued before X is finished, and each iteration
+// refills the batch it has just multiplied with the weights of the iteration
+// D ahead.  So D iterations of weight loads stay in flight behind the
+// arithmetic (one iteration of 16-row tiles over K = 4096 is 36 KB of Q4_K
+// per CU), and a wave never waits to issue before it multiplies.  Part sums
+// go through two alternating LDS buffers, so one barrier per iteration
+// suffices: iteration i + 2 writes the buffer iteration i read, and every
+// wave has finished reading it before the barrier of iteration i + 1.
+constexpr int kRingWaves = 16;
+constexpr int kRingDepth = 2;
+
+// Sum the P part sums of the tpi (<= NW / 4) tiles of global iteration `it` and
+// run their epilogue (threads 256 j .. 256 j + 255 take tile slot j); pre is
+// this thread's epi_load of the same output.
+template <int NW>
+__device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc, float* red, int it, int P, int tpi,
+                                          float2 pre, int pos0)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
+    lds_barrier();
+    const int row = (threadIdx.x >> 6) & 3, l = lane, j = threadIdx.x >> 8;
+    if (j < tpi) {
+        float s = red[((j * P) * 4 + row) * 64 + l];
+        for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
+        const int tt = it * tpi + j;
+        epilogue(a, s, 4 * (l >> 4) + row, 16 * tt + (l & 15), tt, l, pre, pos0);
+    }
+}
+
+// epi_load of this thread's output in global iteration `it` (nothing when its
+// tile slot is unused).
+__device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, int pos0)
+{
+    const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = threadIdx.x >> 8;
+    const int m = j < tpi ? 4 * (l >> 4) + row : a.M;
+    return epi_load(a, m, 16 * (it * tpi + j) + (l & 15), pos0);
+}
+
+template <int TYPE, int C, int D, int NW, bool NORM>
+__global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
+{
+    extern __shared__ uint4 xs[];
+    __shared__ float red[2][NW * 4 * 64];
+    __shared__ float rs[kNormMaxRows];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int P = a.ks_count, tpi = NW / P;
+    const int tw = wave / P, p = wave - (wave / P) * P;
+    const int ca = p * a.ks_q + min(p, a.ks_r);
+    const int nc = a.ks_q + (p < a.ks_r ? 1 : 0);  // <= C (checked by the host)
+    const int n_iter = (a.n_tiles + tpi - 1) / tpi;
+    const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const uint32_t pitch = wide_pitch(a.K);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_0 ? g : 8 * g);
+    const NibbleConsts nk = nibble_consts();
+    // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
+    auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
+
+    const int pos0 = epi_pos0(a);
+    auto git = [&](int li) { return (int)blockIdx.x + li * (int)gridDim.x; };  // global iteration
+
+    NormRegs<NW> nr;
+    if constexpr (NORM)
+        norm_issue<NW>(a, nr);
+    else
+        x_copy_to_lds<NW>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs);
+    pin_loads();
+    WBatch<TYPE, C> ring[D];
+    float2 pre[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        stream_load<TYPE, C>(a, wr, tile_of(k), ca, nc, ring[k]);
+        pre[k] = ring_epi_load(a, git(k), tpi, pos0);
+    }
+    pin_loads();
+    if constexpr (NORM) {
+        norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
+        lds_barrier();
+    } else {
+        vm_barrier<D * (WBatch<TYPE, C>::kLoads + 2)>();
+    }
+    for (int base = 0; base < n_loc; base += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int li = base + k;
+            if (li >= n_loc) break;
+            const int t = tile_of(li);
+            float4_t acc = {0.f, 0.f, 0.f, 0.f};
+            stream_mma<TYPE, C>(xs, xrow, ca, t < a.n_tiles ? nc : 0, ring[k], nk, acc);
+            const float2 pk = pre[k];
+            stream_load<TYPE, C>(a, wr, tile_of(li + D), ca, nc, ring[k]);
+            pre[k] = ring_epi_load(a, git(li + D), tpi, pos0);
+            pin_loads();
+            tile_sums<NW>(a, acc, red[li & 1], git(li), P, tpi, pk, pos0);
         }
     }
 }
@@ -886,56 +1103,105 @@ bool wide_fits(int M, uint32_t K)
 }
 
 // Opt the whole-X kernels in to the LDS they need for X.
+// Static LDS of the ring kernel: two part-sum buffers and the norm factors.
+constexpr size_t kRingStatic = 2 * kRingWaves * 4 * 64 * sizeof(float) + 512;
+
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
     const int dyn = (int)(kWideLdsMax - kStreamStatic);
     const void* fns[] = {
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, false>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, true>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, true>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, true>,
+        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, true>,
     };
     for (const void* f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
         if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
     }
+    const int dyn_ring = (int)(kWideLdsMax - kRingStatic);
+    const void* rings[] = {
+#define ULSPEC_RING_FN(T, C) (const void*)gemm_ring_kernel<T, C, kRingDepth, kRingWaves, false>, \
+                             (const void*)gemm_ring_kernel<T, C, kRingDepth, kRingWaves, true>,
+        ULSPEC_RING_FN(ULSPEC_GGML_Q4_0, 1) ULSPEC_RING_FN(ULSPEC_GGML_Q4_0, 2)
+        ULSPEC_RING_FN(ULSPEC_GGML_Q4_K, 1) ULSPEC_RING_FN(ULSPEC_GGML_Q4_K, 2)
+#undef ULSPEC_RING_FN
+    };
+    for (const void* f : rings) {
+        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn_ring);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
+    }
     return ULSPEC_OK;
 }
 
-// Launch the whole-X kernel.  More tiles than CUs: the pipelined 8-wave grid
-// of one workgroup per CU, P parts per tile (the largest power of two <=
-// min(8, chunks per row)), 8 / P tiles per iteration.  Otherwise one 16-wave
-// workgroup per tile, 16 parts (waves with an empty part idle).
+// Launch the whole-X kernel.  More tiles than CUs and at most two chunks per
+// part: the ring kernel, one 16-wave workgroup per CU, P parts per tile (the
+// largest power of two <= min(16, chunks per row), P >= 4), 16 / P tiles per
+// iteration.  Otherwise the older pipelined 8-wave kernel for more tiles than
+// CUs, else one 16-wave workgroup per tile with 16 parts (waves with an empty
+// part idle).
 void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     const int n_cu = std::max(1, ctx->n_cu);
     const bool pipe = (int)w.n_tiles > n_cu;
+    const size_t lds = (size_t)a.M * wide_pitch(w.k);
+    const bool q40 = w.type == ULSPEC_GGML_Q4_0, norm = a.f.pro == kProNorm;
+    auto split = [&](int P) {
+        a.ks_count = P;
+        a.ks_q = (int)(w.n_chunks / P);
+        a.ks_r = (int)(w.n_chunks % P);
+    };
+    if (pipe) {
+        int P = kRingWaves;
+        while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
+        const int cpp = (int)((w.n_chunks + P - 1) / P);
+        if (P >= 4 && cpp <= 2 && lds + kRingStatic <= kWideLdsMax) {
+            split(P);
+            const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
+            const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
+#define ULSPEC_RING(T, C)                                                                                               \
+    do {                                                                                                                \
+        if (norm) hipLaunchKernelGGL((gemm_ring_kernel<T, C, kRingDepth, kRingWaves, true>), grid, block, lds, ctx->stream, a); \
+        else hipLaunchKernelGGL((gemm_ring_kernel<T, C, kRingDepth, kRingWaves, false>), grid, block, lds, ctx->stream, a);     \
+    } while (0)
+            if (q40 && cpp <= 1) ULSPEC_RING(ULSPEC_GGML_Q4_0, 1);
+            else if (q40) ULSPEC_RING(ULSPEC_GGML_Q4_0, 2);
+            else if (cpp <= 1) ULSPEC_RING(ULSPEC_GGML_Q4_K, 1);
+            else ULSPEC_RING(ULSPEC_GGML_Q4_K, 2);
+#undef ULSPEC_RING
+            return;
+        }
+    }
     int P = pipe ? kStreamWaves : kWideWaves;
     if (pipe)
         while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
+    split(P);
     const int n_iter = ((int)w.n_tiles + (pipe ? kStreamWaves / P : 1) - 1) / (pipe ? kStreamWaves / P : 1);
-    a.ks_count = P;
-    a.ks_q = (int)(w.n_chunks / P);
-    a.ks_r = (int)(w.n_chunks % P);
-    const size_t lds = (size_t)a.M * wide_pitch(w.k);
-    const bool q40 = w.type == ULSPEC_GGML_Q4_0;
+    const dim3 grid(pipe ? std::min(n_iter, n_cu) : n_iter), block((pipe ? kStreamWaves : kWideWaves) * 64);
+#define ULSPEC_STREAM(T, C, W, PI, NO) \
+    hipLaunchKernelGGL((gemm_stream_kernel<T, C, W, PI, NO>), grid, block, lds, ctx->stream, a)
     if (pipe) {
-        const dim3 grid(std::min(n_iter, n_cu)), block(kStreamWaves * 64);
-        if (q40)
-            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true>), grid, block, lds,
-                               ctx->stream, a);
-        else
-            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true>), grid, block, lds,
-                               ctx->stream, a);
+        if (q40) {
+            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, true);
+            else ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, false);
+        } else {
+            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, true);
+            else ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false);
+        }
     } else {
-        const dim3 grid(n_iter), block(kWideWaves * 64);
-        if (q40)
-            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false>), grid, block, lds,
-                               ctx->stream, a);
-        else
-            hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false>), grid, block, lds,
-                               ctx->stream, a);
+        if (q40) {
+            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, true);
+            else ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, false);
+        } else {
+            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, true);
+            else ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, false);
+        }
     }
+#undef ULSPEC_STREAM
 }
 
 // K slices per weight: about one workgroup per CU in total.
@@ -1000,8 +1266,9 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
 ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y)
 {
     if (M == 0 || !wide_fits((int)M, w.k)) return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows of K=%u do not fit", M, w.k);
-    if (f.pro == kProNorm && (M > (uint32_t)kNormMaxRows || w.k > 4096 || w.k % 4))
-        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs M <= 16 and K <= 4096");
+    if (f.pro == kProNorm && (M > (uint32_t)kNormMaxRows || w.k > 4096 || w.k % 4 || f.P < 1 || f.P > kNormMaxPartials))
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs M <= 16, K <= 4096 and 1..%d partial sums",
+                    kNormMaxPartials);
     GemmArgs a;
     a.w = w.dev;
     a.w_bytes = (uint32_t)w.bytes;
