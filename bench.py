@@ -460,7 +460,7 @@ def main():
                    "tokens": tokens, "event_ms": ev_ms},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
-                     "kernel": "verify dequant-GEMM (gemm_q4_k_wide_kernel), target weights, M=6",
+                     "kernel": "verify dequant-GEMM (gemm_ring_kernel for QKV, gate/up, LM head; gemm_stream_kernel for O, down), the 129 target weights, M=6",
                      "avg_us": us, "algorithmic_bytes": alg},
         "cpu_baseline": cpu,
     }

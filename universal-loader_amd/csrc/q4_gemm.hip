@@ -858,7 +858,8 @@ __device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, in
 template <int TYPE, int CMAX, int NW>
 __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, const uint4* xs, float* red,
                                             int xrow, int it, int tw, int P, int tpi, int ca, int cb,
-                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk, int pos0)
+                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk, int pos0,
+                                            const float2* pre0 = nullptr)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int t = it * tpi + tw;
@@ -881,7 +882,7 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_r
         for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
         const int tt = it * tpi + j;
         const int m = 4 * (l >> 4) + row, n = 16 * tt + (l & 15);
-        epilogue(a, s, m, n, tt, l, epi_load(a, m, n, pos0), pos0);
+        epilogue(a, s, m, n, tt, l, pre0 ? *pre0 : epi_load(a, m, n, pos0), pos0);
     }
 }
 
@@ -921,15 +922,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     WBatch<TYPE, CMAX> A;
     int it = blockIdx.x;
     stream_load<TYPE, CMAX>(a, wr, it * tpi + tw, ca, nc0, A);
+    // one tile per workgroup: the epilogue operands of this thread's output
+    // (tile slot 0 is the only one, tpi = 1) load with the weights
+    float2 pre0 = {0.f, 0.f};
+    if constexpr (!PIPE)
+        pre0 = epi_load(a, (threadIdx.x >> 8) == 0 ? 4 * (lane >> 4) + ((threadIdx.x >> 6) & 3) : a.M,
+                        16 * it + (lane & 15), pos0);
     pin_loads();
     if constexpr (NORM) {
         norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
         lds_barrier();
     } else {
-        vm_barrier<WBatch<TYPE, CMAX>::kLoads>();
+        vm_barrier<WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : 2)>();
     }
     if constexpr (!PIPE) {
-        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0);
+        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0, &pre0);
     } else {
         WBatch<TYPE, CMAX> B;
         while (true) {
