@@ -52,9 +52,11 @@ enum { ULSPEC_GGML_Q4_0 = 2, ULSPEC_GGML_Q4_K = 12 };
  * Replaces the Vulkan bring-up of InferenceEngine::initialize
  * (src/inference/inference_engine.cpp:48-148). */
 const char*   ulspec_version(void);
-/* Block sizes of the GGUF types: elements per block (32 / 256) and bytes per
- * block (18 / 144).  Replaces ggml_blck_size / ggml_type_size
- * (src/core/gguf_types.h:35-81, whose Q4 byte sizes 6 / 12 are wrong). */
+/* Block sizes of the GGUF types: elements per block and bytes per block
+ * (Q4_0 32 / 18, Q4_K 256 / 144, Q6_K 256 / 210, Q8_0 32 / 34, F16 1 / 2, ...;
+ * 0 for an unknown id).  Replaces ggml_blck_size / ggml_type_size
+ * (src/core/gguf_types.h:35-81, whose Q4 byte sizes 6 / 12 are wrong).  The
+ * kernels read Q4_0 and Q4_K weights only. */
 int           ulspec_ggml_blck_size(uint32_t ggml_type);
 int           ulspec_ggml_type_size(uint32_t ggml_type);
 ulspec_status ulspec_create(int hip_device, ulspec_ctx** out);
@@ -189,6 +191,54 @@ ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint3
  * host arrays [n][n_kv_heads][head_dim] of fp16 bits.  Synchronous. */
 ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n, uint16_t* k,
                                  uint16_t* v);
+
+/* ---- GGUF files -------------------------------------------------------------
+ * Read-only memory map of a GGUF v2/v3 file: header, metadata and tensor
+ * table parsed with bounds checks; tensor data handed out as pointers into the
+ * mapping.  No device work (usable without a GPU).  Replaces GGUFParser
+ * (src/core/gguf_parser.h:37-90; parse / read_tensor_infos / read_tensor_data_direct,
+ * src/core/gguf_parser.cpp:230-290,348-361, whose byte sizes are wrong, A2). */
+typedef struct ulspec_gguf ulspec_gguf;
+/* metadata value types (src/core/gguf_parser.h:12-26) */
+enum {
+    ULSPEC_GGUF_U8 = 0, ULSPEC_GGUF_I8 = 1, ULSPEC_GGUF_U16 = 2, ULSPEC_GGUF_I16 = 3, ULSPEC_GGUF_U32 = 4,
+    ULSPEC_GGUF_I32 = 5, ULSPEC_GGUF_F32 = 6, ULSPEC_GGUF_BOOL = 7, ULSPEC_GGUF_STRING = 8, ULSPEC_GGUF_ARRAY = 9,
+    ULSPEC_GGUF_U64 = 10, ULSPEC_GGUF_I64 = 11, ULSPEC_GGUF_F64 = 12
+};
+/* On failure *out is NULL and err (if given) holds the reason. */
+ulspec_status ulspec_gguf_open(const char* path, ulspec_gguf** out, char* err, size_t err_len);
+void          ulspec_gguf_close(ulspec_gguf* g);
+const char*   ulspec_gguf_last_error(const ulspec_gguf* g);
+ulspec_status ulspec_gguf_header(const ulspec_gguf* g, uint32_t* version, uint64_t* n_tensors, uint64_t* n_kv,
+                                 uint64_t* alignment, uint64_t* data_offset);
+/* Tensor i: ne[0] = elements per row (contiguous); offset relative to the data
+ * section; nbytes = ne0 / blck * type_size * ne1 * ne2 * ne3, or 0 (and data
+ * NULL) for a type without a fixed block layout.  name / data live until close. */
+ulspec_status ulspec_gguf_tensor(const ulspec_gguf* g, uint64_t i, const char** name, uint32_t* ggml_type,
+                                 uint32_t* n_dims, uint64_t ne[4], uint64_t* offset, uint64_t* nbytes,
+                                 const void** data);
+ulspec_status ulspec_gguf_find_tensor(const ulspec_gguf* g, const char* name, uint64_t* index);
+/* Metadata entry i (array_type / array_len for ULSPEC_GGUF_ARRAY). */
+ulspec_status ulspec_gguf_kv(const ulspec_gguf* g, uint64_t i, const char** key, uint32_t* value_type,
+                             uint32_t* array_type, uint64_t* array_len);
+/* The encoded value bytes of entry i (arrays: from the first element on), for
+ * a caller that decodes string arrays such as tokenizer.ggml.tokens itself. */
+ulspec_status ulspec_gguf_kv_bytes(const ulspec_gguf* g, uint64_t i, const void** data, uint64_t* nbytes);
+/* Scalar lookups by key: integers and bools as int64, floats (and integers)
+ * as double, strings as (pointer, length) into the mapping. */
+ulspec_status ulspec_gguf_get_int(const ulspec_gguf* g, const char* key, int64_t* v);
+ulspec_status ulspec_gguf_get_float(const ulspec_gguf* g, const char* key, double* v);
+ulspec_status ulspec_gguf_get_str(const ulspec_gguf* g, const char* key, const char** v, uint64_t* len);
+/* Llama configuration from the metadata (llama.embedding_length, block_count,
+ * attention.head_count[_kv], feed_forward_length, context_length,
+ * attention.layer_norm_rms_epsilon, rope.freq_base) and the vocabulary from
+ * token_embd.weight; max_ctx 0 = llama.context_length. */
+ulspec_status ulspec_gguf_llama_cfg(const ulspec_gguf* g, uint32_t max_ctx, ulspec_model_cfg* cfg);
+/* Model from a GGUF file: every tensor by name through ulspec_model_set_tensor
+ * (Model::load_from_gguf, src/inference/model.cpp:190-246).  Tensors of types
+ * the kernels do not read (Q6_K, Q8_0, F16 matrices, ...) fail with
+ * ULSPEC_EUNSUPPORTED naming the tensor.  The file may be closed afterwards. */
+ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx, ulspec_model** out);
 
 /* ---- speculative decoding loop --------------------------------------------
  * One step (all on the device, captured once into a HIP graph and replayed):

@@ -56,13 +56,45 @@ private:
     ulspec_ctx* ctx_ = nullptr;
 };
 
+// A memory-mapped GGUF file (GGUFParser, src/core/gguf_parser.h:37-90, with
+// the GGUF block sizes); host only.
+class GGUFFile {
+public:
+    explicit GGUFFile(const std::string& path)
+    {
+        char err[512] = {0};
+        const ulspec_status st = ulspec_gguf_open(path.c_str(), &g_, err, sizeof(err));
+        if (st != ULSPEC_OK) throw Error(st, std::string("ulspec_gguf_open: ") + err);
+    }
+    ~GGUFFile() { ulspec_gguf_close(g_); }
+    GGUFFile(const GGUFFile&) = delete;
+    GGUFFile& operator=(const GGUFFile&) = delete;
+    const ulspec_gguf* get() const { return g_; }
+    ulspec_model_cfg llama_cfg(uint32_t max_ctx = 0) const
+    {
+        ulspec_model_cfg c{};
+        const ulspec_status st = ulspec_gguf_llama_cfg(g_, max_ctx, &c);
+        if (st != ULSPEC_OK) throw Error(st, std::string("ulspec_gguf_llama_cfg: ") + ulspec_gguf_last_error(g_));
+        return c;
+    }
+
+private:
+    ulspec_gguf* g_ = nullptr;
+};
+
 // A Llama-shaped model whose tensors are given by GGUF name and raw block bytes
-// (the weight map of Model::load_from_gguf, src/inference/model.cpp:190-246).
+// (the weight map of Model::load_from_gguf, src/inference/model.cpp:190-246),
+// or read from a GGUF file.
 class Model {
 public:
     Model(Context& ctx, const ulspec_model_cfg& cfg) : ctx_(ctx.get()), cfg_(cfg)
     {
         check(ctx_, ulspec_model_create(ctx_, &cfg, &m_), "ulspec_model_create");
+    }
+    // InferenceEngine::load_model (src/inference/inference_engine.cpp:150-181)
+    Model(Context& ctx, const GGUFFile& file, uint32_t max_ctx = 0) : ctx_(ctx.get()), cfg_(file.llama_cfg(max_ctx))
+    {
+        check(ctx_, ulspec_model_load_gguf(ctx_, file.get(), max_ctx, &m_), "ulspec_model_load_gguf");
     }
     ~Model() { ulspec_model_destroy(m_); }
     Model(const Model&) = delete;

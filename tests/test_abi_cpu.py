@@ -29,7 +29,7 @@ def test_block_sizes(pkg):
     L = pkg.lib()
     assert L.ulspec_ggml_blck_size(2) == 32 and L.ulspec_ggml_type_size(2) == 18
     assert L.ulspec_ggml_blck_size(12) == 256 and L.ulspec_ggml_type_size(12) == 144
-    assert L.ulspec_ggml_blck_size(3) == 0 and L.ulspec_ggml_type_size(99) == 0
+    assert L.ulspec_ggml_blck_size(4) == 0 and L.ulspec_ggml_type_size(99) == 0  # removed / unknown ids
 
 
 def test_null_arguments_are_rejected_without_a_device(pkg):

@@ -1,0 +1,79 @@
+"""The vulkangguf-compatible InferenceAPI (universal-loader_amd/inference_api.py)
+over GGUF files: token-level generation with and without the draft model,
+live acceptance rate and logits."""
+import importlib
+
+import numpy as np
+import pytest
+
+import gguf_io as G
+from llama_util import make_tensors
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=4, ffn=512, vocab=1000, max_ctx=128, rms_eps=1e-5,
+           rope_base=10000.0)
+
+
+@pytest.fixture(scope="module")
+def files(ora, tmp_path_factory):
+    d = tmp_path_factory.mktemp("api")
+    out = []
+    for name, seed, layers in (("target", 31, 2), ("draft", 32, 1)):
+        cfg = dict(CFG, n_layers=layers)
+        kv = G.llama_kv(cfg)
+        kv = [e if e[0] != "tokenizer.ggml.tokens" else
+              ("tokenizer.ggml.tokens", G.ARRAY, (G.STRING, [f"▁w{i}" for i in range(CFG["vocab"])])) for e in kv]
+        p = d / f"{name}.gguf"
+        G.write(p, kv, G.model_tensors(make_tensors(ora, cfg, 12, seed=seed)))
+        out.append(str(p))
+    return out
+
+
+@pytest.fixture(scope="module")
+def api_mod(pkg):
+    return importlib.import_module(pkg.__name__ + ".inference_api")
+
+
+def test_greedy_generation_with_and_without_speculation(pkg, ctx, api_mod, files):
+    target, draft = files
+    api = api_mod.InferenceAPI(ctx=ctx, seed=7)
+    assert api.generate([1, 2, 3]) == "Error: No model loaded"
+    assert api.load_model(target) and api.load_draft_model(draft)
+    info = api.get_model_info()
+    assert (info.vocab_size, info.num_layers, info.hidden_dim, info.context_len, info.architecture) == \
+        (1000, 2, 256, 128, "llama")
+    prompt = list(np.random.default_rng(4).integers(0, 1000, 10))
+    cfg = api_mod.GenerationConfig(max_tokens=20, do_sample=False)
+    assert api.get_acceptance_rate() == 0.5
+    plain = api.generate_tokens(prompt, cfg)
+    api.enable_speculative_decoding(True)
+    spec = api.generate_tokens(prompt, cfg)
+    assert plain.tokens == spec.tokens and spec.num_tokens == 20
+    assert 0.0 <= api.get_acceptance_rate() <= 1.0 and api.get_throughput() > 0
+    # greedy = argmax chain of the target's own logits
+    seq = list(prompt)
+    for _ in range(4):
+        seq.append(int(np.argmax(api.get_token_logits(seq))))
+    assert seq[len(prompt):] == spec.tokens[:4]
+    assert spec.text == "".join(f" w{t}" for t in spec.tokens)
+    api.register_custom_tokenizer(lambda s: [int(x) for x in s.split()])
+    assert api.generate(" ".join(str(t) for t in prompt), cfg) == spec.text
+    api.unload_model()
+    assert api.get_model_architecture() == ""
+
+
+def test_sampled_generation_is_seeded(pkg, ctx, api_mod, files):
+    target, draft = files
+    res = []
+    for _ in range(2):
+        api = api_mod.InferenceAPI(ctx=ctx, seed=99)
+        api.load_model(target)
+        api.load_draft_model(draft)
+        api.enable_speculative_decoding(True)
+        api.set_temperature(0.8)
+        api.set_top_k(40)
+        api.set_top_p(0.9)
+        res.append(api.generate_default([5, 6, 7, 8]).tokens)
+        api.unload_model()
+    assert res[0] == res[1] and len(res[0]) == 100

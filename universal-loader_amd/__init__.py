@@ -117,6 +117,23 @@ ABI = [
     ("ulspec_spec_tokens", C.c_int, [P, U32, U32, P]),
     ("ulspec_spec_last_step", C.c_int, [P, P, P, P, P, P, P]),
     ("ulspec_spec_set_graph", C.c_int, [P, C.c_int]),
+    ("ulspec_gguf_open", C.c_int, [C.c_char_p, C.POINTER(P), C.c_char_p, C.c_size_t]),
+    ("ulspec_gguf_close", None, [P]),
+    ("ulspec_gguf_last_error", C.c_char_p, [P]),
+    ("ulspec_gguf_header", C.c_int, [P, C.POINTER(U32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                     C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    ("ulspec_gguf_tensor", C.c_int, [P, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(U32), C.POINTER(U32),
+                                     C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                     C.POINTER(P)]),
+    ("ulspec_gguf_find_tensor", C.c_int, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    ("ulspec_gguf_kv", C.c_int, [P, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(U32), C.POINTER(U32),
+                                 C.POINTER(C.c_uint64)]),
+    ("ulspec_gguf_kv_bytes", C.c_int, [P, C.c_uint64, C.POINTER(P), C.POINTER(C.c_uint64)]),
+    ("ulspec_gguf_get_int", C.c_int, [P, C.c_char_p, C.POINTER(C.c_int64)]),
+    ("ulspec_gguf_get_float", C.c_int, [P, C.c_char_p, C.POINTER(C.c_double)]),
+    ("ulspec_gguf_get_str", C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(C.c_uint64)]),
+    ("ulspec_gguf_llama_cfg", C.c_int, [P, U32, C.POINTER(ModelCfg)]),
+    ("ulspec_model_load_gguf", C.c_int, [P, P, U32, C.POINTER(P)]),
 ]
 
 
@@ -314,6 +331,134 @@ class Model:
         self.ctx._check(lib().ulspec_model_kv_io(self.handle, layer, dir, pos0, n, k.ctypes.data_as(P),
                                                  v.ctypes.data_as(P)))
         return k, v
+
+
+class GGUFTensor:
+    """One entry of a GGUF tensor table; data is a read-only view into the mapping."""
+
+    def __init__(self, name, ggml_type, shape, offset, nbytes, data):
+        self.name, self.ggml_type, self.shape = name, ggml_type, shape
+        self.offset, self.nbytes, self.data = offset, nbytes, data
+
+    def __repr__(self):
+        return f"GGUFTensor({self.name!r}, type={self.ggml_type}, ne={self.shape}, {self.nbytes} B)"
+
+
+class GGUFFile:
+    """ulspec_gguf: a memory-mapped GGUF v2/v3 file (host only, no GPU needed).
+
+    The reference's GGUFParser (src/core/gguf_parser.h:37-90) with the GGUF
+    block sizes corrected; tensors are views into the mapping, metadata is read
+    by key."""
+
+    def __init__(self, path):
+        L = lib()
+        h = P()
+        err = C.create_string_buffer(512)
+        st = L.ulspec_gguf_open(os.fsencode(path), C.byref(h), err, len(err))
+        if st != OK:
+            raise UlspecError(st, err.value.decode(errors="replace"))
+        self.handle = h.value
+        v, nt, nkv, al, off = U32(), C.c_uint64(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+        L.ulspec_gguf_header(self.handle, C.byref(v), C.byref(nt), C.byref(nkv), C.byref(al), C.byref(off))
+        self.version, self.n_tensors, self.n_kv = v.value, nt.value, nkv.value
+        self.alignment, self.data_offset = al.value, off.value
+
+    def close(self):
+        if self.handle:
+            lib().ulspec_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _check(self, st):
+        if st != OK:
+            raise UlspecError(st, lib().ulspec_gguf_last_error(self.handle).decode(errors="replace"))
+
+    def tensor(self, i):
+        name, t, nd, ne = C.c_char_p(), U32(), U32(), (C.c_uint64 * 4)()
+        off, nb, data = C.c_uint64(), C.c_uint64(), P()
+        self._check(lib().ulspec_gguf_tensor(self.handle, i, C.byref(name), C.byref(t), C.byref(nd), ne, C.byref(off),
+                                             C.byref(nb), C.byref(data)))
+        view = None
+        if data.value:
+            view = np.ctypeslib.as_array(C.cast(data.value, C.POINTER(C.c_uint8)), shape=(nb.value,))
+            view.flags.writeable = False
+        return GGUFTensor(name.value.decode(), t.value, tuple(ne[:nd.value]), off.value, nb.value, view)
+
+    def tensors(self):
+        return [self.tensor(i) for i in range(self.n_tensors)]
+
+    def find(self, name):
+        i = C.c_uint64()
+        if lib().ulspec_gguf_find_tensor(self.handle, name.encode(), C.byref(i)) != OK:
+            return None
+        return self.tensor(i.value)
+
+    def keys(self):
+        out = []
+        for i in range(self.n_kv):
+            k, t, at, n = C.c_char_p(), U32(), U32(), C.c_uint64()
+            self._check(lib().ulspec_gguf_kv(self.handle, i, C.byref(k), C.byref(t), C.byref(at), C.byref(n)))
+            out.append((k.value.decode(), t.value, at.value, n.value))
+        return out
+
+    def get_str_array(self, key):
+        """The strings of an array-of-strings entry (e.g. tokenizer.ggml.tokens)."""
+        for i, (k, t, at, n) in enumerate(self.keys()):
+            if k == key:
+                if t != 9 or at != 8:
+                    raise UlspecError(EINVAL, f"{key} is not an array of strings")
+                p, nb = P(), C.c_uint64()
+                self._check(lib().ulspec_gguf_kv_bytes(self.handle, i, C.byref(p), C.byref(nb)))
+                raw = C.string_at(p.value, nb.value)
+                out, pos = [], 0
+                for _ in range(n):
+                    ln = int.from_bytes(raw[pos:pos + 8], "little")
+                    out.append(raw[pos + 8:pos + 8 + ln].decode(errors="replace"))
+                    pos += 8 + ln
+                return out
+        raise UlspecError(EINVAL, f"no metadata key {key}")
+
+    def get_int(self, key):
+        v = C.c_int64()
+        self._check(lib().ulspec_gguf_get_int(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_float(self, key):
+        v = C.c_double()
+        self._check(lib().ulspec_gguf_get_float(self.handle, key.encode(), C.byref(v)))
+        return v.value
+
+    def get_str(self, key):
+        p, n = P(), C.c_uint64()
+        self._check(lib().ulspec_gguf_get_str(self.handle, key.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p.value, n.value).decode(errors="replace")
+
+    def llama_cfg(self, max_ctx=0):
+        cfg = ModelCfg()
+        self._check(lib().ulspec_gguf_llama_cfg(self.handle, max_ctx, C.byref(cfg)))
+        return cfg
+
+
+def load_gguf_model(ctx, gguf, max_ctx=0):
+    """Model from a GGUFFile (or a path): ulspec_model_load_gguf."""
+    own = not isinstance(gguf, GGUFFile)
+    f = GGUFFile(gguf) if own else gguf
+    try:
+        h = P()
+        ctx._check(lib().ulspec_model_load_gguf(ctx.handle, f.handle, max_ctx, C.byref(h)))
+        m = Model.__new__(Model)
+        m.ctx, m.handle = ctx, h.value
+        m.cfg = f.llama_cfg(max_ctx)
+        return m
+    finally:
+        if own:
+            f.close()
 
 
 class Speculative:

@@ -1300,8 +1300,9 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
                             bool on_device, uint32_t* out_id)
 {
     if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported (Q4_0 / Q4_K)", type);
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
-    if (bs == 0) return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported", type);
     if (N == 0 || K == 0 || K % bs) return fail(ctx, ULSPEC_EINVAL, "weight_upload: K=%u must be a positive multiple of %d", K, bs);
     const size_t expect = (size_t)N * (K / bs) * ts;
     if (nbytes != expect) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes given, %zu expected", nbytes, expect);

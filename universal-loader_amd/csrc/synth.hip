@@ -130,8 +130,9 @@ extern "C" ulspec_status ulspec_synth_q4(ulspec_ctx* ctx, uint32_t type, uint64_
                                          uint32_t K, float std_dev, void* out)
 {
     ULSPEC_CHECK_CTX(ctx);
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "synth_q4: ggml type %u not supported (Q4_0 / Q4_K)", type);
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
-    if (bs == 0) return fail(ctx, ULSPEC_EUNSUPPORTED, "synth_q4: ggml type %u not supported", type);
     if (!out || N == 0 || K == 0 || K % bs) return fail(ctx, ULSPEC_EINVAL, "synth_q4: N=%u K=%u", N, K);
     if (!(std_dev >= 0.0f) || !(std_dev < __builtin_inff())) return fail(ctx, ULSPEC_EINVAL, "synth_q4: std");
     (void)hipSetDevice(ctx->device);

@@ -10,14 +10,57 @@ extern "C" const char* ulspec_version(void)
     return "ulspec 0.1 gfx950";
 }
 
+// Elements and bytes per block of every GGUF tensor type with a fixed block
+// layout (the public ggml definitions; the reference's table,
+// src/core/gguf_types.h:35-81, has wrong byte sizes for most of them).  0 for
+// an unknown id.
+namespace {
+struct GgmlTypeInfo {
+    uint16_t blck, bytes;
+};
+constexpr GgmlTypeInfo kGgmlTypes[] = {
+    {1, 4},     // 0 F32
+    {1, 2},     // 1 F16
+    {32, 18},   // 2 Q4_0: fp16 d, 16 B of nibbles
+    {32, 20},   // 3 Q4_1: fp16 d, m, 16 B
+    {0, 0},     // 4 (removed Q4_2)
+    {0, 0},     // 5 (removed Q4_3)
+    {32, 22},   // 6 Q5_0: d, 4 B high bits, 16 B
+    {32, 24},   // 7 Q5_1
+    {32, 34},   // 8 Q8_0: d, 32 x int8
+    {32, 36},   // 9 Q8_1
+    {256, 84},  // 10 Q2_K
+    {256, 110}, // 11 Q3_K
+    {256, 144}, // 12 Q4_K: d, dmin, 12 B scales, 128 B nibbles
+    {256, 176}, // 13 Q5_K
+    {256, 210}, // 14 Q6_K
+    {256, 292}, // 15 Q8_K
+    {256, 66},  // 16 IQ2_XXS
+    {256, 74},  // 17 IQ2_XS
+    {256, 98},  // 18 IQ3_XXS
+    {256, 50},  // 19 IQ1_S
+    {32, 18},   // 20 IQ4_NL
+    {256, 110}, // 21 IQ3_S
+    {256, 82},  // 22 IQ2_S
+    {256, 136}, // 23 IQ4_XS
+    {1, 1},     // 24 I8
+    {1, 2},     // 25 I16
+    {1, 4},     // 26 I32
+    {1, 8},     // 27 I64
+    {1, 8},     // 28 F64
+    {256, 56},  // 29 IQ1_M
+    {1, 2},     // 30 BF16
+};
+}  // namespace
+
 extern "C" int ulspec_ggml_blck_size(uint32_t t)
 {
-    return t == ULSPEC_GGML_Q4_0 ? 32 : t == ULSPEC_GGML_Q4_K ? 256 : 0;
+    return t < sizeof(kGgmlTypes) / sizeof(kGgmlTypes[0]) ? kGgmlTypes[t].blck : 0;
 }
 
 extern "C" int ulspec_ggml_type_size(uint32_t t)
 {
-    return t == ULSPEC_GGML_Q4_0 ? 18 : t == ULSPEC_GGML_Q4_K ? 144 : 0;
+    return t < sizeof(kGgmlTypes) / sizeof(kGgmlTypes[0]) ? kGgmlTypes[t].bytes : 0;
 }
 
 extern "C" const char* ulspec_status_str(ulspec_status s)

@@ -1,0 +1,248 @@
+"""The speculative-decoding subset of the reference's Python module
+`vulkangguf` (pybind11, src/api/inference_api.cpp:389-473), over the gfx950
+library: same class and method names, argument meaning and result types.
+
+    api = InferenceAPI()
+    api.load_model("target.gguf")            # InferenceAPI::load_model (:21-43)
+    api.load_draft_model("draft.gguf")       # no counterpart: the reference has no draft model
+    api.enable_speculative_decoding(True)    # :214-216 (a no-op there)
+    res = api.generate_tokens(prompt_ids, GenerationConfig(max_tokens=64))
+    api.get_acceptance_rate()                # :222-225 (0.0 there; live here)
+    api.get_token_logits(ids)                # :277-280 (empty there; live here)
+
+Token ids in, token ids out.  Text goes through a tokenizer registered with
+register_custom_tokenizer (:368-370); output text joins the GGUF vocabulary
+strings (tokenizer.ggml.tokens, "▁" read as a space).  Every model call
+runs the HIP kernels of lib/libulspec.so; without a gfx950 device the calls
+raise (no CPU path).  Methods of the reference outside this path (adapters,
+multi-GPU, pipeline caches, quantization switches) are not provided.
+"""
+import threading
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import (EUNSUPPORTED, GGUFFile, Speculative, UlspecError, load_gguf_model, sampling)
+
+
+@dataclass
+class GenerationConfig:
+    """py::GenerationConfig (src/api/inference_api.h:14-22); defaults of the
+    InferenceAPI constructor (inference_api.cpp:8-16)."""
+    max_tokens: int = 100
+    temperature: float = 1.0
+    top_p: float = 0.9
+    top_k: int = 40
+    frequency_penalty: float = 0.0
+    presence_penalty: float = 0.0
+    do_sample: bool = True
+
+
+@dataclass
+class GenerationResult:
+    """py::GenerationResult (inference_api.h:24-30)."""
+    tokens: list = field(default_factory=list)
+    text: str = ""
+    num_tokens: int = 0
+    time_ms: float = 0.0
+    tokens_per_second: float = 0.0
+
+
+@dataclass
+class ModelMetrics:
+    """py::ModelMetrics (inference_api.h:42-50)."""
+    vocab_size: int = 0
+    num_layers: int = 0
+    hidden_dim: int = 0
+    context_len: int = 0
+    num_heads: int = 0
+    model_size_bytes: int = 0
+    architecture: str = ""
+
+
+class InferenceAPI:
+    """py::InferenceAPI (inference_api.h:52-123), speculative-decoding subset.
+    Every public method holds one lock, as the reference's api_mutex_."""
+
+    SPEC_LENGTH = 5  # drafts per step (k)
+
+    def __init__(self, ctx=None, max_ctx=0, seed=0):
+        from . import Context
+        self._ctx = ctx if ctx is not None else Context(0)
+        self._max_ctx = max_ctx
+        self._seed = seed
+        self._lock = threading.RLock()
+        self._config = GenerationConfig()
+        self._target = self._draft = None
+        self._vocab = None
+        self._model_path = ""
+        self._model_bytes = 0
+        self._spec = False
+        self._tokenizer = None
+        self._accepted = self._proposed = 0
+        self._throughput = 0.0
+
+    # -- models ---------------------------------------------------------------
+    def load_model(self, model_path):
+        """Target model from a GGUF file (InferenceAPI::load_model, :21-43)."""
+        with self._lock:
+            self.unload_model()
+            with GGUFFile(model_path) as g:
+                self._target = load_gguf_model(self._ctx, g, self._max_ctx)
+                self._model_bytes = sum(t.nbytes for t in g.tensors())
+                try:
+                    self._vocab = self._read_vocab(g)
+                except UlspecError:
+                    self._vocab = None
+            self._model_path = model_path
+            return True
+
+    def load_draft_model(self, model_path):
+        """Draft model for speculative decoding (same vocabulary as the target)."""
+        with self._lock:
+            if self._target is None:
+                raise UlspecError(EUNSUPPORTED, "load the target model first")
+            d = load_gguf_model(self._ctx, model_path, self._max_ctx)
+            if d.cfg.vocab != self._target.cfg.vocab:
+                d.close()
+                raise ValueError("draft and target vocabularies differ")
+            if self._draft is not None:
+                self._draft.close()
+            self._draft = d
+            return True
+
+    def unload_model(self):
+        with self._lock:
+            for m in (self._draft, self._target):
+                if m is not None:
+                    m.close()
+            self._target = self._draft = None
+            self._model_path, self._vocab, self._model_bytes = "", None, 0
+            return True
+
+    @staticmethod
+    def _read_vocab(g):
+        return g.get_str_array("tokenizer.ggml.tokens")
+
+    # -- configuration -------------------------------------------------------
+    def enable_speculative_decoding(self, enable):
+        with self._lock:
+            self._spec = bool(enable)
+
+    def set_temperature(self, temp):
+        with self._lock:
+            self._config.temperature = float(temp)
+
+    def set_top_p(self, top_p):
+        with self._lock:
+            self._config.top_p = float(top_p)
+
+    def set_top_k(self, top_k):
+        with self._lock:
+            self._config.top_k = int(top_k)
+
+    def enable_gpu(self, enable):
+        """The path runs on the GPU only: enabling succeeds, disabling does not."""
+        return bool(enable)
+
+    def is_gpu_enabled(self):
+        return True
+
+    def register_custom_tokenizer(self, tokenizer_func):
+        """str -> list of token ids, used by generate() for text prompts (:368-370)."""
+        with self._lock:
+            self._tokenizer = tokenizer_func
+
+    # -- queries ---------------------------------------------------------------
+    def get_acceptance_rate(self):
+        """Cumulative accepted / proposed drafts; 0.5 before any speculative
+        step (SpeculativeDecoder's initial value, speculative_decoder.cpp:10)."""
+        with self._lock:
+            return self._accepted / self._proposed if self._proposed else 0.5
+
+    def get_throughput(self):
+        with self._lock:
+            return self._throughput
+
+    def get_model_info(self):
+        with self._lock:
+            if self._target is None:
+                return ModelMetrics()
+            c = self._target.cfg
+            return ModelMetrics(c.vocab, c.n_layers, c.dim, c.max_ctx, c.n_heads, self._model_bytes, "llama")
+
+    def get_model_architecture(self):
+        with self._lock:
+            return "llama" if self._target is not None else ""
+
+    def get_token_logits(self, tokens):
+        """Target logits after `tokens` (positions 0..len-1), as a list of
+        floats (InferenceAPI::get_token_logits, :277-280)."""
+        with self._lock:
+            if self._target is None:
+                return []
+            return self._target.forward(np.asarray(tokens, np.int32), 0, n_logits=1)[0].tolist()
+
+    # -- generation ------------------------------------------------------------
+    def _sampling(self, config):
+        if config.frequency_penalty or config.presence_penalty:
+            raise UlspecError(EUNSUPPORTED, "frequency / presence penalties are not implemented")
+        if not config.do_sample:
+            return sampling(greedy=True)
+        return sampling(temperature=config.temperature, top_k=config.top_k, top_p=config.top_p)
+
+    def generate_tokens(self, prompt_ids, config=None):
+        """max_tokens new token ids after prompt_ids: speculative steps with the
+        draft model when enabled, otherwise k = 1 steps of the same device loop
+        with the target as its own draft."""
+        with self._lock:
+            if self._target is None:
+                raise UlspecError(EUNSUPPORTED, "no model loaded")
+            config = config or self._config
+            s = self._sampling(config)
+            spec = self._spec and self._draft is not None
+            k = self.SPEC_LENGTH if spec else 1
+            loop = Speculative(self._target, self._draft if spec else self._target, k, s, self._seed)
+            try:
+                t0 = time.perf_counter()
+                loop.prefill(np.asarray(prompt_ids, np.int32))
+                n0 = loop.state()["n"]
+                loop.generate(int(config.max_tokens))
+                st = loop.state()
+                toks = loop.tokens(n0, min(int(config.max_tokens), st["n"] - n0)).tolist()
+                dt = time.perf_counter() - t0
+            finally:
+                loop.close()
+            if spec:
+                self._accepted += st["accepted"]
+                self._proposed += st["proposed"]
+            self._throughput = len(toks) / dt if dt > 0 else 0.0
+            return GenerationResult(toks, self.token_text(toks), len(toks), dt * 1e3, self._throughput)
+
+    def generate(self, prompt, config=None):
+        """Text (with a registered tokenizer) or token ids in, text out
+        (InferenceAPI::generate, :45-63, including its error string)."""
+        with self._lock:
+            if self._target is None:
+                return "Error: No model loaded"
+            if isinstance(prompt, str):
+                if self._tokenizer is None:
+                    raise UlspecError(EUNSUPPORTED, "text prompts need register_custom_tokenizer()")
+                prompt = self._tokenizer(prompt)
+            return self.generate_tokens(prompt, config).text
+
+    def generate_default(self, prompt):
+        """generate() with the API's own configuration (:65-77)."""
+        with self._lock:
+            if isinstance(prompt, str):
+                if self._tokenizer is None:
+                    raise UlspecError(EUNSUPPORTED, "text prompts need register_custom_tokenizer()")
+                prompt = self._tokenizer(prompt)
+            return self.generate_tokens(prompt, self._config)
+
+    def token_text(self, tokens):
+        """Decoded text when the GGUF vocabulary covers the ids, else the ids."""
+        if self._vocab is None or any(t >= len(self._vocab) for t in tokens):
+            return " ".join(str(t) for t in tokens)
+        return "".join(self._vocab[t] for t in tokens).replace("\u2581", " ")
