@@ -22,6 +22,9 @@
 //                 group g covers qs bytes 32g..32g+31 (sub-blocks 2g, 2g+1);
 //                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
 //     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
+#include <type_traits>
+#include <vector>
+
 #include "detmath.h"
 #include "hip_common.h"
 #include "ulspec_internal.h"
@@ -123,9 +126,81 @@ __device__ __forceinline__ void vm_barrier()
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// vm_barrier with a wave-uniform count n (0..63) known only at run time.
+__device__ __forceinline__ void vm_barrier_dyn(int n)
+{
+    switch (n) {
+    case 0: vm_barrier<0>(); break;
+    case 1: vm_barrier<1>(); break;
+    case 2: vm_barrier<2>(); break;
+    case 3: vm_barrier<3>(); break;
+    case 4: vm_barrier<4>(); break;
+    case 5: vm_barrier<5>(); break;
+    case 6: vm_barrier<6>(); break;
+    case 7: vm_barrier<7>(); break;
+    case 8: vm_barrier<8>(); break;
+    case 9: vm_barrier<9>(); break;
+    case 10: vm_barrier<10>(); break;
+    case 11: vm_barrier<11>(); break;
+    case 12: vm_barrier<12>(); break;
+    case 13: vm_barrier<13>(); break;
+    case 14: vm_barrier<14>(); break;
+    case 15: vm_barrier<15>(); break;
+    case 16: vm_barrier<16>(); break;
+    case 17: vm_barrier<17>(); break;
+    case 18: vm_barrier<18>(); break;
+    case 19: vm_barrier<19>(); break;
+    case 20: vm_barrier<20>(); break;
+    case 21: vm_barrier<21>(); break;
+    case 22: vm_barrier<22>(); break;
+    case 23: vm_barrier<23>(); break;
+    case 24: vm_barrier<24>(); break;
+    case 25: vm_barrier<25>(); break;
+    case 26: vm_barrier<26>(); break;
+    case 27: vm_barrier<27>(); break;
+    case 28: vm_barrier<28>(); break;
+    case 29: vm_barrier<29>(); break;
+    case 30: vm_barrier<30>(); break;
+    case 31: vm_barrier<31>(); break;
+    case 32: vm_barrier<32>(); break;
+    case 33: vm_barrier<33>(); break;
+    case 34: vm_barrier<34>(); break;
+    case 35: vm_barrier<35>(); break;
+    case 36: vm_barrier<36>(); break;
+    case 37: vm_barrier<37>(); break;
+    case 38: vm_barrier<38>(); break;
+    case 39: vm_barrier<39>(); break;
+    case 40: vm_barrier<40>(); break;
+    case 41: vm_barrier<41>(); break;
+    case 42: vm_barrier<42>(); break;
+    case 43: vm_barrier<43>(); break;
+    case 44: vm_barrier<44>(); break;
+    case 45: vm_barrier<45>(); break;
+    case 46: vm_barrier<46>(); break;
+    case 47: vm_barrier<47>(); break;
+    case 48: vm_barrier<48>(); break;
+    case 49: vm_barrier<49>(); break;
+    case 50: vm_barrier<50>(); break;
+    case 51: vm_barrier<51>(); break;
+    case 52: vm_barrier<52>(); break;
+    case 53: vm_barrier<53>(); break;
+    case 54: vm_barrier<54>(); break;
+    case 55: vm_barrier<55>(); break;
+    case 56: vm_barrier<56>(); break;
+    case 57: vm_barrier<57>(); break;
+    case 58: vm_barrier<58>(); break;
+    case 59: vm_barrier<59>(); break;
+    case 60: vm_barrier<60>(); break;
+    case 61: vm_barrier<61>(); break;
+    case 62: vm_barrier<62>(); break;
+    case 63: vm_barrier<63>(); break;
+    default: vm_barrier<0>();
+    }
+}
+
 // Raw buffer loads: 32-bit offsets from a base held in scalar registers, and
 // the hardware returns 0 for offsets at or past num_records instead of
-// faulting.  0x00020000 is the gfx9-family dword-3 of the resource.
+// faulting (such a load still occupies the texture unit like any other).  0x00020000 is the gfx9-family dword-3 of the resource.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -516,6 +591,9 @@ template <int CMAX>
 __device__ __forceinline__ void q4_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t s_lane, int c0,
                                                 int nc, uint4 (&wq)[CMAX], uint2 (&sc)[CMAX])
 {
+    // every slot is issued (past nc out of range, which moves no data), so
+    // the number of loads in flight is a compile-time constant and each
+    // chunk waits for exactly its own loads; launches pick CMAX to fit
 #pragma unroll
     for (int i = 0; i < CMAX; ++i) {
         const uint32_t o = (uint32_t)(c0 + i) * kQ40Chunk;
@@ -560,8 +638,8 @@ __device__ __forceinline__ int epi_pos0(const GemmArgs& a)
 // The memory operands of the epilogue of output (m, n), loaded ahead of it
 // with the weights of the same tile so that the epilogue reads no memory
 // (vmcnt retires in issue order: a load issued in the epilogue would wait for
-// every weight load in flight).  Exactly two 4-byte loads per call whatever
-// the epilogue, out of range when unused:
+// every weight load in flight).  Two 4-byte loads for the resid and rope
+// epilogues (out of range where a thread has no output), none otherwise:
 //   resid: (h[m][n], -)      rope: (cos, sin) of the pair at position pos0 + m
 __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int pos0)
 {
@@ -582,10 +660,18 @@ __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int 
     } else {
         r = make_rsrc(a.out, 0u);
     }
-    float2 v;
-    v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o0, 0, 0));
-    v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o1, 0, 0));
+    float2 v = {0.f, 0.f};
+    if (f.epi == kEpiResid || f.epi == kEpiRope) {
+        v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o0, 0, 0));
+        v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o1, 0, 0));
+    }
     return v;
+}
+
+// Vector loads epi_load issues (wave-uniform).
+__device__ __forceinline__ int epi_nloads(const GemmArgs& a)
+{
+    return a.f.epi == kEpiResid || a.f.epi == kEpiRope ? 2 : 0;
 }
 
 // Epilogue of output (m, n) of tile t, value s; pre from epi_load, pos0 from
@@ -933,7 +1019,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
         norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
         lds_barrier();
     } else {
-        vm_barrier<WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : 2)>();
+        // the weight loads issued after the copies, then the epilogue's
+        vm_barrier_dyn(WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : epi_nloads(a)));
     }
     if constexpr (!PIPE) {
         stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0, &pre0);
@@ -1042,7 +1129,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
         norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
         lds_barrier();
     } else {
-        vm_barrier<D * (WBatch<TYPE, C>::kLoads + 2)>();
+        vm_barrier_dyn(D * (WBatch<TYPE, C>::kLoads + epi_nloads(a)));  // loads issued after the copies
     }
     for (int base = 0; base < n_loc; base += D) {
 #pragma unroll
@@ -1110,22 +1197,57 @@ bool wide_fits(int M, uint32_t K)
 }
 
 // Opt the whole-X kernels in to the LDS they need for X.
+// Batch sizes (chunks per wave) the one-tile-per-workgroup kernel is built
+// for: a launch takes the smallest that holds a whole part, so no load slot
+// is wasted on chunks past the part (longer parts loop over batches).
+template <int... C>
+struct CList {};
+using WideQ40 = CList<1, 2, 3, 4, 6, 8>;
+using WideQ4K = CList<1, 2, 3, 4>;
+
+template <int TYPE, int... C>
+void wide_kernels(CList<C...>, std::vector<const void*>& out)
+{
+    (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves, false, false>), ...);
+    (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves, false, true>), ...);
+}
+
+// Launch the one-tile kernel with the smallest batch >= cpp (the largest when none is).
+template <int TYPE, int... C>
+void wide_launch(CList<C...>, int cpp, bool norm, dim3 grid, dim3 block, size_t lds, hipStream_t st, GemmArgs& a)
+{
+    constexpr int cs[] = {C...};
+    int pick = cs[sizeof...(C) - 1];
+    for (int c : cs)
+        if (c >= cpp) {
+            pick = c;
+            break;
+        }
+    bool done = false;
+    auto one = [&](auto cmax) {
+        constexpr int CM = decltype(cmax)::value;
+        if (done || CM != pick) return;
+        done = true;
+        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CM, kWideWaves, false, true>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CM, kWideWaves, false, false>), grid, block, lds, st, a);
+    };
+    (one(std::integral_constant<int, C>{}), ...);
+}
+
 // Static LDS of the ring kernel: two part-sum buffers and the norm factors.
 constexpr size_t kRingStatic = 2 * kRingWaves * 4 * 64 * sizeof(float) + 512;
 
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
     const int dyn = (int)(kWideLdsMax - kStreamStatic);
-    const void* fns[] = {
+    std::vector<const void*> fns = {
         (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, false>,
         (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, false>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, false>,
         (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, true>,
         (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, true>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, true>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, true>,
     };
+    wide_kernels<ULSPEC_GGML_Q4_0>(WideQ40{}, fns);
+    wide_kernels<ULSPEC_GGML_Q4_K>(WideQ4K{}, fns);
     for (const void* f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
         if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
@@ -1200,13 +1322,9 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
             else ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false);
         }
     } else {
-        if (q40) {
-            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, true);
-            else ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40CMax, kWideWaves, false, false);
-        } else {
-            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, true);
-            else ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KCMax, kWideWaves, false, false);
-        }
+        const int cpp = a.ks_q + (a.ks_r ? 1 : 0);
+        if (q40) wide_launch<ULSPEC_GGML_Q4_0>(WideQ40{}, cpp, norm, grid, block, lds, ctx->stream, a);
+        else wide_launch<ULSPEC_GGML_Q4_K>(WideQ4K{}, cpp, norm, grid, block, lds, ctx->stream, a);
     }
 #undef ULSPEC_STREAM
 }
