@@ -23,6 +23,7 @@
 //                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
 //     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "detmath.h"
@@ -37,6 +38,9 @@ namespace {
 
 constexpr int kQ40Chunk = 1152;
 constexpr int kQ4KChunk = 2304;
+// 16-byte X units (8 halves) per weight chunk: 128 K for Q4_0, 256 for Q4_K
+template <int TYPE>
+constexpr int kUnitsPerChunk = TYPE == ULSPEC_GGML_Q4_0 ? 16 : 32;
 
 __device__ __forceinline__ uint32_t perm_nibbles(const uint32_t q[8])
 {
@@ -115,87 +119,30 @@ __device__ __forceinline__ void pin_loads() { asm volatile("" ::: "memory"); }
 // fence, so vector loads in flight stay in flight across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// As lds_barrier, and every vector-memory operation but the N youngest has
-// completed.  After buffer->LDS copies followed by N register loads this
-// waits for the copies only (vmcnt retires in issue order), where a fenced
-// barrier would also wait for the N loads.
+// Wait until every vector-memory operation but the N youngest has completed;
+// no barrier.  After this wave's own buffer->LDS copies followed by N register
+// loads, the wave may read what it copied.
 template <int N>
-__device__ __forceinline__ void vm_barrier()
+__device__ __forceinline__ void vm_wait()
 {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// vm_barrier with a wave-uniform count n (0..63) known only at run time.
-__device__ __forceinline__ void vm_barrier_dyn(int n)
+template <int... Ns>
+__device__ __forceinline__ void vm_wait_sel(int n, std::integer_sequence<int, Ns...>)
 {
-    switch (n) {
-    case 0: vm_barrier<0>(); break;
-    case 1: vm_barrier<1>(); break;
-    case 2: vm_barrier<2>(); break;
-    case 3: vm_barrier<3>(); break;
-    case 4: vm_barrier<4>(); break;
-    case 5: vm_barrier<5>(); break;
-    case 6: vm_barrier<6>(); break;
-    case 7: vm_barrier<7>(); break;
-    case 8: vm_barrier<8>(); break;
-    case 9: vm_barrier<9>(); break;
-    case 10: vm_barrier<10>(); break;
-    case 11: vm_barrier<11>(); break;
-    case 12: vm_barrier<12>(); break;
-    case 13: vm_barrier<13>(); break;
-    case 14: vm_barrier<14>(); break;
-    case 15: vm_barrier<15>(); break;
-    case 16: vm_barrier<16>(); break;
-    case 17: vm_barrier<17>(); break;
-    case 18: vm_barrier<18>(); break;
-    case 19: vm_barrier<19>(); break;
-    case 20: vm_barrier<20>(); break;
-    case 21: vm_barrier<21>(); break;
-    case 22: vm_barrier<22>(); break;
-    case 23: vm_barrier<23>(); break;
-    case 24: vm_barrier<24>(); break;
-    case 25: vm_barrier<25>(); break;
-    case 26: vm_barrier<26>(); break;
-    case 27: vm_barrier<27>(); break;
-    case 28: vm_barrier<28>(); break;
-    case 29: vm_barrier<29>(); break;
-    case 30: vm_barrier<30>(); break;
-    case 31: vm_barrier<31>(); break;
-    case 32: vm_barrier<32>(); break;
-    case 33: vm_barrier<33>(); break;
-    case 34: vm_barrier<34>(); break;
-    case 35: vm_barrier<35>(); break;
-    case 36: vm_barrier<36>(); break;
-    case 37: vm_barrier<37>(); break;
-    case 38: vm_barrier<38>(); break;
-    case 39: vm_barrier<39>(); break;
-    case 40: vm_barrier<40>(); break;
-    case 41: vm_barrier<41>(); break;
-    case 42: vm_barrier<42>(); break;
-    case 43: vm_barrier<43>(); break;
-    case 44: vm_barrier<44>(); break;
-    case 45: vm_barrier<45>(); break;
-    case 46: vm_barrier<46>(); break;
-    case 47: vm_barrier<47>(); break;
-    case 48: vm_barrier<48>(); break;
-    case 49: vm_barrier<49>(); break;
-    case 50: vm_barrier<50>(); break;
-    case 51: vm_barrier<51>(); break;
-    case 52: vm_barrier<52>(); break;
-    case 53: vm_barrier<53>(); break;
-    case 54: vm_barrier<54>(); break;
-    case 55: vm_barrier<55>(); break;
-    case 56: vm_barrier<56>(); break;
-    case 57: vm_barrier<57>(); break;
-    case 58: vm_barrier<58>(); break;
-    case 59: vm_barrier<59>(); break;
-    case 60: vm_barrier<60>(); break;
-    case 61: vm_barrier<61>(); break;
-    case 62: vm_barrier<62>(); break;
-    case 63: vm_barrier<63>(); break;
-    default: vm_barrier<0>();
-    }
+    ((n == Ns ? vm_wait<Ns>() : void()), ...);
+}
+
+// vm_wait with a wave-uniform count n known only at run time; counts outside
+// 1..63 wait for everything.
+__device__ __forceinline__ void vm_wait_dyn(int n)
+{
+    if (n <= 0 || n >= 64)
+        vm_wait<0>();
+    else
+        vm_wait_sel(n, std::make_integer_sequence<int, 64>{});
 }
 
 // Raw buffer loads: 32-bit offsets from a base held in scalar registers, and
@@ -557,33 +504,33 @@ __host__ __device__ constexpr uint32_t wide_pitch(uint32_t K)
     return ((2u * K + 1023u) / 1024u) * 1024u + 16u;
 }
 
-template <int NW>
-__device__ __forceinline__ void x_copy_to_lds(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes)
+// This wave's own part of X: rows 0..M-1, chunks [ca, cb) (16-byte units
+// [ua, ub) of each row); element (m, k) goes to LDS byte m * wide_pitch(K) +
+// 2 k.  A wave reads X only inside its own part, so it waits for its own
+// copies (vmcnt) and no other wave's: no barrier before the first multiply.
+// Each copy moves 64 consecutive units; a part that is not a multiple of 64
+// units ends with a copy shifted back to end at ub, and a row shorter than 64
+// units copies units 0..63, the ones past the row end reading as zero into
+// the row's padding.  Units of a neighbouring part written this way receive
+// the same X values that part's own wave writes there.
+template <int UPC>
+__device__ __forceinline__ void x_copy_own(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes, int ca,
+                                           int cb)
 {
-    // M rows x ipr 1 KB copies, spread over the NW waves.  Each workgroup
-    // starts at a different copy (rotation by blockIdx) so the CUs of an XCD,
-    // which all read the same X, do not queue on the same L2 channels.
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int KU = a.K / 8;  // 16-byte units per row
-    const int ipr = (KU + 63) / 64;
-    const int total = a.M * ipr;
+    const int KU = a.K / 8;
+    const int ua = ca * UPC, ub = cb * UPC;
+    const int np = ub > ua ? (ub - ua + 63) / 64 : 0;
     const uint32_t pitch = wide_pitch(a.K);
-    int idx = (int)((blockIdx.x * 7u + wave) % (uint32_t)total);
-    int m = idx / ipr, c = idx - (idx / ipr) * ipr;
-    const int step_m = NW / ipr, step_c = NW - (NW / ipr) * ipr;
-    for (int n = wave; n < total; n += NW) {
-        const int u = c * 64 + lane;
-        const uint32_t off = u < KU ? (uint32_t)(m * KU + u) * 16u : kOOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*)(xs_bytes + m * pitch + c * 1024), 16, off, 0, 0, 0);
-        // advance by NW copies, wrapping around the M x ipr grid
-        c += step_c;
-        m += step_m;
-        if (c >= ipr) {
-            c -= ipr;
-            ++m;
+    for (int m = 0; m < a.M; ++m) {
+        for (int q = 0; q < np; ++q) {
+            int s0 = ua + 64 * q;
+            if (s0 + 64 > ub) s0 = max(ub - 64, 0);
+            const int u = s0 + lane;
+            const uint32_t off = u < KU ? (uint32_t)(m * KU + u) * 16u : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(xs_bytes + m * pitch + s0 * 16), 16, off, 0, 0, 0);
         }
-        while (m >= a.M) m -= a.M;
     }
 }
 
@@ -976,8 +923,9 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_r
 // and the next iteration's first batch is prefetched (two register sets);
 // otherwise every workgroup runs exactly one iteration.  NORM: X is built by
 // the RMSNorm prologue, else copied.  Issue order: X (copies or the norm's
-// register loads), then the first weight batch; the barrier waits for X only,
-// so the weights keep streaming in while X is finished.
+// register loads), then the first weight batch.  A copied X is waited for per
+// wave (vmcnt of its own copies, weights still in flight); the norm's X needs
+// every wave's rows, so it ends in a barrier.
 template <int TYPE, int CMAX, int NW, bool PIPE, bool NORM>
 __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 {
@@ -1003,7 +951,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     if constexpr (NORM)
         norm_issue<NW>(a, nr);
     else
-        x_copy_to_lds<NW>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs);
+        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
+                                         min(cb, a.n_chunks));
     pin_loads();
     WBatch<TYPE, CMAX> A;
     int it = blockIdx.x;
@@ -1019,8 +968,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
         norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
         lds_barrier();
     } else {
-        // the weight loads issued after the copies, then the epilogue's
-        vm_barrier_dyn(WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : epi_nloads(a)));
+        // this wave's copies: issued before its weight loads and the epilogue's
+        vm_wait_dyn(WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : epi_nloads(a)));
     }
     if constexpr (!PIPE) {
         stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0, &pre0);
@@ -1115,7 +1064,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     if constexpr (NORM)
         norm_issue<NW>(a, nr);
     else
-        x_copy_to_lds<NW>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs);
+        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
+                                         ca + nc);
     pin_loads();
     WBatch<TYPE, C> ring[D];
     float2 pre[D];
@@ -1129,7 +1079,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
         norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
         lds_barrier();
     } else {
-        vm_barrier_dyn(D * (WBatch<TYPE, C>::kLoads + epi_nloads(a)));  // loads issued after the copies
+        vm_wait_dyn(D * (WBatch<TYPE, C>::kLoads + epi_nloads(a)));  // this wave's copies
     }
     for (int base = 0; base < n_loc; base += D) {
 #pragma unroll
