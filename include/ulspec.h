@@ -140,6 +140,27 @@ ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
                             uint32_t V, const float* target_logits, const float* draft_logits,
                             const int32_t* draft_tokens, const float* uniforms,
                             int32_t* out_tokens, int32_t* out_n_accepted);
+/* Tree verification, B trees of one shape: nodes 0 .. n-1 (n <= 16), node 0
+ * the root (the last committed token), parent (HOST int32 [n]) with
+ * parent[0] = -1 and parent[i] in [0, i).  target_logits [B][n][V]: row v is
+ * the target's distribution after node v; draft_logits [B][n][V]: row v is the
+ * distribution node v's children were drawn from (rows of leaves are not
+ * read); tokens [B][n] (node 0's unused); uniforms [B][n].  From the root,
+ * the children c of the current node are tested in index order with
+ * u[c-1] against the running residual (multi-draft speculative sampling,
+ * SpecInfer, Miao et al. 2024, Alg. 2): accept iff u q(x) < C(x), else C <-
+ * norm(max(0, C - q)); an accepted child becomes the current node; otherwise
+ * the last token is drawn from C with u[n-1].  Greedy: follow the first child
+ * holding the argmax, else emit it.  On a chain (parent[i] = i-1) this is
+ * ulspec_accept.  out_tokens [B][n]: n_accepted + 1 tokens then -1;
+ * out_path [B][n]: node 0 then the accepted nodes, then -1 (the rows
+ * ulspec_model_kv_compact keeps).  Device memory but parent.  Replaces
+ * TreeSpeculation (src/inference/speculative_decoder.h:62-87, .cpp:118-176),
+ * which builds no real tree. */
+ulspec_status ulspec_accept_tree(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t n, uint32_t V,
+                                 const int32_t* parent, const float* target_logits, const float* draft_logits,
+                                 const int32_t* tokens, const float* uniforms, int32_t* out_tokens,
+                                 int32_t* out_path, int32_t* out_n_accepted);
 /* One token per row from warp(logits[r]) with uniforms[r] (greedy: argmax).
  * Replaces InferenceEngine::sample_token (src/inference/inference_engine.cpp:340-367). */
 ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
@@ -187,6 +208,24 @@ ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* name, uint32_
  * (src/api/inference_api.cpp:277-280) and prefill. */
 ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint32_t M, uint32_t pos,
                                    float* logits, uint32_t n_logits);
+/* Forward a draft tree of M nodes (host ids; M <= 16 and at most the model's
+ * row limit) whose K/V go to slots pos .. pos+M-1: node i (parent[i] in [-1,
+ * i), host array; -1 = child of the prefix) takes RoPE position pos +
+ * depth(i) and attends to positions 0 .. pos-1, its ancestors and itself
+ * (the mask of ulspec_verify_attention).  Logits of all M nodes to host
+ * memory logits [M][vocab].  Synchronous.  Each node's outputs equal those of
+ * a causal forward of its root-to-node path at positions pos, pos+1, .. */
+ulspec_status ulspec_model_forward_tree(ulspec_model* m, const int32_t* tokens, const int32_t* parent, uint32_t M,
+                                        uint32_t pos, float* logits);
+/* Commit an accepted tree path: K/V rows pos + path[j] -> pos + j for j = 1
+ * .. min(*n_accepted + 1, n_max) - 1 in every layer (row pos, the root,
+ * stays).  path and n_accepted are DEVICE memory, as written by
+ * ulspec_accept_tree for one tree (path strictly increasing from 0);
+ * entries outside [0, n_max) are skipped.  Asynchronous on the context
+ * stream.  The rows past the kept ones are stale and are overwritten by the
+ * next forward. */
+ulspec_status ulspec_model_kv_compact(ulspec_model* m, uint32_t pos, const int32_t* path, const int32_t* n_accepted,
+                                      uint32_t n_max);
 /* Copy K/V cache rows pos0 .. pos0+n-1 of one layer to (dir 0) or from (dir 1)
  * host arrays [n][n_kv_heads][head_dim] of fp16 bits.  Synchronous. */
 ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n, uint16_t* k,

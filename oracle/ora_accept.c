@@ -265,3 +265,122 @@ int ora_sample(const ora_sampling* s, int64_t R, int64_t V, const float* logits,
     ora_parallel_for(1, R, sample_range, &j);
     return 0;
 }
+
+/*
+ * Tree acceptance (multi-draft speculative sampling: SpecInfer, Miao et al.
+ * 2024, Alg. 2, sibling drafts drawn with replacement from the draft row of
+ * their parent).  Nodes 0 .. n-1, node 0 the root (the last committed token),
+ * parent[i] < i for i >= 1.  Target row v = distribution after node v; draft
+ * row v = the distribution node v's children were drawn from.  Walk from the
+ * root; at node v, C = warp(target row v) with total Zc, q = warp(draft row v):
+ * the children c of v, in index order, are tested with u[c-1]:
+ *   accept iff ((double)u * (double)Q_x) * (double)Zc < (double)C_x * (double)Zq;
+ *   on rejection C_j <- trunc(ldexp(max(0, C_j*Zq - Q_j*Zc), 62 - bitlen(Zc) -
+ *   bitlen(Zq))) and Zc <- sum C (left unchanged when that sum is 0).
+ * An accepted child becomes v; when no child is accepted (or v is a leaf) the
+ * last token is drawn from C with u[n-1].  On a chain (parent[i] = i-1) this
+ * is ora_accept's rule with the same uniforms.  Greedy: move to the first
+ * child whose token is argmax(target row v), else emit that argmax.
+ * Outputs: tokens [n] = the accepted children's tokens then the drawn one (-1
+ * padded), path [n] = 0 then the accepted nodes (-1 padded), n_accepted.
+ */
+typedef struct {
+    const ora_sampling* s;
+    int64_t n, V;
+    const int32_t* parent;
+    const float *tl, *dl, *u;
+    const int32_t* tok;
+    int32_t *out, *path, *nacc;
+} tree_job;
+
+static void tree_one(const tree_job* j, int64_t b, uint64_t* C, uint64_t* Q)
+{
+    const int64_t n = j->n, V = j->V;
+    const float* tl = j->tl + (size_t)b * (size_t)n * (size_t)V;
+    const float* dl = j->dl ? j->dl + (size_t)b * (size_t)n * (size_t)V : NULL;
+    const int32_t* tok = j->tok + b * n;
+    const float* u = j->u ? j->u + b * n : NULL;
+    int32_t* out = j->out + b * n;
+    int32_t* path = j->path + b * n;
+    for (int64_t i = 0; i < n; ++i) out[i] = path[i] = -1;
+    path[0] = 0;
+    int64_t v = 0, depth = 0;
+    for (;;) {
+        int64_t next = -1;
+        if (j->s->greedy) {
+            const int32_t a = (int32_t)argmax_row(tl + v * V, V);
+            for (int64_t c = v + 1; c < n && next < 0; ++c)
+                if (j->parent[c] == v && tok[c] == a) next = c;
+            out[depth] = a;
+            if (next < 0) break;
+        } else {
+            uint64_t Zc, Zq = 0;
+            int have_q = 0;
+            ora_warp_row(j->s, tl + v * V, V, C, &Zc);
+            for (int64_t c = v + 1; c < n; ++c) {
+                if (j->parent[c] != v) continue;
+                if (!have_q) {
+                    ora_warp_row(j->s, dl + v * V, V, Q, &Zq);
+                    have_q = 1;
+                }
+                const int32_t x = tok[c];
+                const uint64_t Cx = (x >= 0 && x < V) ? C[x] : 0;
+                const uint64_t Qx = (x >= 0 && x < V) ? Q[x] : 0;
+                const double lhs = ((double)u[c - 1] * (double)Qx) * (double)Zc;
+                const double rhs = (double)Cx * (double)Zq;
+                if (lhs < rhs) {
+                    out[depth] = x;
+                    next = c;
+                    break;
+                }
+                const int sh = 62 - bitlen64(Zc) - bitlen64(Zq);
+                uint64_t SR = 0;
+                for (int64_t t = 0; t < V; ++t) {
+                    const double r = (double)C[t] * (double)Zq - (double)Q[t] * (double)Zc;
+                    SR += r > 0.0 ? (uint64_t)ldexp(r, sh) : 0;
+                }
+                if (SR) {
+                    for (int64_t t = 0; t < V; ++t) {
+                        const double r = (double)C[t] * (double)Zq - (double)Q[t] * (double)Zc;
+                        C[t] = r > 0.0 ? (uint64_t)ldexp(r, sh) : 0;
+                    }
+                    Zc = SR;
+                }
+            }
+            if (next < 0) {
+                out[depth] = (int32_t)ora_cdf_pick(C, V, Zc, u[n - 1]);
+                break;
+            }
+        }
+        ++depth;
+        path[depth] = (int32_t)next;
+        v = next;
+    }
+    j->nacc[b] = (int32_t)depth;
+}
+
+static void tree_range(void* arg, int64_t lo, int64_t hi)
+{
+    tree_job* j = (tree_job*)arg;
+    uint64_t* buf = (uint64_t*)malloc(sizeof(uint64_t) * 2u * (size_t)j->V);
+    for (int64_t b = lo; b < hi; ++b) tree_one(j, b, buf, buf + j->V);
+    free(buf);
+}
+
+int ora_accept_tree(const ora_sampling* s, int64_t B, int64_t n, int64_t V, const int32_t* parent,
+                    const float* target_logits, const float* draft_logits, const int32_t* tokens,
+                    const float* uniforms, int32_t* out_tokens, int32_t* out_path, int32_t* out_n_accepted,
+                    int nthreads)
+{
+    if (B <= 0 || n <= 0 || V <= 0 || !s || !parent || !target_logits || !tokens || !out_tokens || !out_path ||
+        !out_n_accepted)
+        return -1;
+    if (parent[0] != -1) return -1;
+    for (int64_t i = 1; i < n; ++i)
+        if (parent[i] < 0 || parent[i] >= i) return -1;
+    if (!s->greedy && (!uniforms || !draft_logits || !(s->temperature > 0.0f))) return -1;
+    tree_job j = { s, n, V, parent, target_logits, draft_logits, uniforms, tokens, out_tokens, out_path,
+                   out_n_accepted };
+    ora_parallel_for(nthreads, B, tree_range, &j);
+    return 0;
+}

@@ -27,6 +27,10 @@
  *     Speculative Decoding", ICML 2023, Algorithm 1; Chen et al. 2023.  The
  *     reference's src/inference/speculative_decoder.cpp:89-110 only matches
  *     token ids and is deliberately not followed.
+ *   - Tree acceptance (sibling drafts tested in turn against the running
+ *     residual): Miao et al., "SpecInfer", ASPLOS 2024, Algorithm 2.  The
+ *     reference's TreeSpeculation (src/inference/speculative_decoder.h:62-87,
+ *     .cpp:118-176) builds no real tree and is not followed.
  *
  * Each function's test pin is listed in tests/ (closed forms, brute force,
  * numpy float64, the compiled reference functions under oracle/_ref).
@@ -118,6 +122,15 @@ int ora_accept(const ora_sampling* s, int64_t B, int64_t k, int64_t V,
                const float* target_logits, const float* draft_logits,
                const int32_t* draft_tokens, const float* uniforms,
                int32_t* out_tokens, int32_t* out_n_accepted, int nthreads);
+/* One tree verification per sequence (rule in ora_accept.c): parent [n]
+ * (parent[0] = -1, parent[i] in [0, i)), shared by the B trees; target and
+ * draft [B][n][V] (row v: after node v / the children's draft distribution),
+ * tokens [B][n], uniforms [B][n]; out_tokens [B][n] and out_path [B][n]
+ * (-1 padded), out_n_accepted [B]. */
+int ora_accept_tree(const ora_sampling* s, int64_t B, int64_t n, int64_t V, const int32_t* parent,
+                    const float* target_logits, const float* draft_logits, const int32_t* tokens,
+                    const float* uniforms, int32_t* out_tokens, int32_t* out_path, int32_t* out_n_accepted,
+                    int nthreads);
 
 /* ---- Llama-shaped model and the speculative loop ---------------------------
  * Block order of InferenceEngine::forward_layer_gpu

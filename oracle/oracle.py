@@ -81,6 +81,7 @@ def _declare(L):
     d("ora_cdf_pick", I64, P, I64, C.c_uint64, C.c_float)
     d("ora_sample", C.c_int, P, I64, I64, P, P, P)
     d("ora_accept", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, C.c_int)
+    d("ora_accept_tree", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, P, P, C.c_int)
     d("ora_llama_create", P, P, C.c_int)
     d("ora_llama_free", None, P)
     d("ora_llama_set_tensor", C.c_int, P, C.c_char_p, C.c_int, P, C.c_size_t, I64, I64)
@@ -243,6 +244,24 @@ def accept(s, target, draft, draft_tokens, u, nthreads=None):
                           _p(out), _p(nacc), nthreads or nthreads_default())
     assert rc == 0
     return out, nacc
+
+
+def accept_tree(s, parent, target, draft, tokens, u, nthreads=None):
+    """Tree verification (ora_accept_tree): target / draft [B][n][V], tokens
+    and uniforms [B][n] -> (tokens [B][n], path [B][n], n_accepted [B])."""
+    target = np.ascontiguousarray(target, dtype=np.float32)
+    B, n, V = target.shape
+    out = np.empty((B, n), dtype=np.int32)
+    path = np.empty((B, n), dtype=np.int32)
+    nacc = np.empty(B, dtype=np.int32)
+    dr = None if draft is None else np.ascontiguousarray(draft, dtype=np.float32)
+    uu = None if u is None else np.ascontiguousarray(u, dtype=np.float32)
+    rc = lib().ora_accept_tree(C.byref(s), B, n, V, _p(np.ascontiguousarray(parent, dtype=np.int32)), _p(target),
+                               _p(dr), _p(np.ascontiguousarray(tokens, dtype=np.int32)), _p(uu), _p(out), _p(path),
+                               _p(nacc), nthreads or nthreads_default())
+    if rc != 0:
+        raise ValueError("ora_accept_tree rejected its arguments")
+    return out, path, nacc
 
 
 class Llama:

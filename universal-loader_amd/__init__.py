@@ -99,6 +99,7 @@ ABI = [
     ("ulspec_verify_gemm", C.c_int, [P, U32, P, U32, P]),
     ("ulspec_verify_attention", C.c_int, [P, P, P, P, U32, U32, P, U32, U32, U32, C.c_float, P]),
     ("ulspec_accept", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P]),
+    ("ulspec_accept_tree", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P, P, P]),
     ("ulspec_sample", C.c_int, [P, C.POINTER(Sampling), U32, U32, P, P, P]),
     ("ulspec_uniforms", C.c_int, [P, C.c_uint64, C.c_uint64, U32, P]),
     ("ulspec_synth_q4", C.c_int, [P, U32, C.c_uint64, C.c_uint64, U32, U32, C.c_float, P]),
@@ -107,6 +108,8 @@ ABI = [
     ("ulspec_model_set_tensor", C.c_int, [P, C.c_char_p, U32, P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_int]),
     ("ulspec_model_forward", C.c_int, [P, P, U32, U32, P, U32]),
     ("ulspec_model_kv_io", C.c_int, [P, U32, C.c_int, U32, U32, P, P]),
+    ("ulspec_model_forward_tree", C.c_int, [P, P, P, U32, U32, P]),
+    ("ulspec_model_kv_compact", C.c_int, [P, U32, P, P, U32]),
     ("ulspec_spec_create", C.c_int, [P, P, U32, C.POINTER(Sampling), C.c_uint64, C.POINTER(P)]),
     ("ulspec_spec_destroy", None, [P]),
     ("ulspec_spec_prefill", C.c_int, [P, P, U32]),
@@ -272,6 +275,13 @@ class Context:
         self._check(lib().ulspec_accept(self.handle, C.byref(s), B, k, V, _ptr(target), _ptr(draft),
                                         _ptr(draft_tokens), _ptr(uniforms), _ptr(out_tokens), _ptr(out_nacc)))
 
+    def accept_tree(self, s, B, n, V, parent, target, draft, tokens, uniforms, out_tokens, out_path, out_nacc):
+        """Tree verification; parent is a host array [n], the rest device buffers."""
+        par = np.ascontiguousarray(parent, dtype=np.int32)
+        self._check(lib().ulspec_accept_tree(self.handle, C.byref(s), B, n, V, par.ctypes.data_as(P), _ptr(target),
+                                             _ptr(draft), _ptr(tokens), _ptr(uniforms), _ptr(out_tokens),
+                                             _ptr(out_path), _ptr(out_nacc)))
+
     def sample(self, s, R, V, logits, uniforms, out_tokens):
         self._check(lib().ulspec_sample(self.handle, C.byref(s), R, V, _ptr(logits), _ptr(uniforms),
                                         _ptr(out_tokens)))
@@ -319,6 +329,20 @@ class Model:
         self.ctx._check(lib().ulspec_model_forward(self.handle, tokens.ctypes.data_as(P), len(tokens), pos,
                                                    out.ctypes.data_as(P) if out is not None else None, n_logits))
         return out
+
+    def forward_tree(self, tokens, parent, pos):
+        """Logits [M][vocab] of the M tree nodes (K/V to slots pos .. pos+M-1)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        parent = np.ascontiguousarray(parent, dtype=np.int32)
+        out = np.empty((len(tokens), self.cfg.vocab), np.float32)
+        self.ctx._check(lib().ulspec_model_forward_tree(self.handle, tokens.ctypes.data_as(P),
+                                                        parent.ctypes.data_as(P), len(tokens), pos,
+                                                        out.ctypes.data_as(P)))
+        return out
+
+    def kv_compact(self, pos, path, n_accepted, n_max):
+        """Keep the accepted path's K/V rows (path, n_accepted: device buffers)."""
+        self.ctx._check(lib().ulspec_model_kv_compact(self.handle, pos, _ptr(path), _ptr(n_accepted), n_max))
 
     def kv_io(self, layer, dir, pos0, n, k=None, v=None):
         row = self.cfg.n_kv_heads * (self.cfg.dim // self.cfg.n_heads)

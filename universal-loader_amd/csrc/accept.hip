@@ -193,16 +193,28 @@ __device__ __forceinline__ W4 fixed_e4(float4 l, float lmax, const WarpParams& p
 }
 
 // ---- row statistics ----------------------------------------------------------
+// Rows a row_stats launch covers: all (n_sel = 0: workgroup r takes row r),
+// or rows row[0 .. n_sel) of every group of n_rows (workgroup g takes row
+// (g / n_sel) * n_rows + row[g % n_sel]); logits and stats share the row index.
+constexpr int kTreeMax = 16;
+struct RowSel {
+    uint32_t n_sel = 0, n_rows = 0;
+    int32_t row[kTreeMax] = {};
+};
+
 __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __restrict__ logits, uint32_t V,
-                                                                WarpParams p, RowStat* __restrict__ stats)
+                                                                WarpParams p, RowStat* __restrict__ stats,
+                                                                RowSel sel)
 {
     __shared__ uint64_t red[kRowThreads / 64];
     __shared__ uint64_t buf[kCandMax];  // thread maxima, then candidates
     __shared__ uint32_t cand_count;
     __shared__ uint64_t keptE[kKMax];
     const int tid = threadIdx.x;
-    const float* row = logits + (size_t)blockIdx.x * V;
-    RowStat* st = stats + blockIdx.x;
+    const size_t r_id = sel.n_sel ? (size_t)(blockIdx.x / sel.n_sel) * sel.n_rows + sel.row[blockIdx.x % sel.n_sel]
+                                   : (size_t)blockIdx.x;
+    const float* row = logits + r_id * V;
+    RowStat* st = stats + r_id;
 
     // pass 1: max key with the lowest index (argmax), per-thread max key
     uint64_t best = 0;
@@ -614,6 +626,195 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
     }
 }
 
+// ---- tree acceptance ------------------------------------------------------------
+// Shape of a draft tree: node 0 the root, parent[i] in [0, i) for i >= 1.
+struct TreeShape {
+    int32_t n;
+    int32_t parent[kTreeMax];
+};
+
+// One workgroup per tree (multi-draft speculative sampling, SpecInfer, Miao
+// et al. 2024, Alg. 2).  At node v: C = warp(target row v) (total Zc), q =
+// warp(draft row v); the children c of v in index order are tested with
+// u[c-1]: accept iff (u Q_x) Zc < C_x Zq; after a rejection C becomes the
+// residual max(0, C Zq - Q Zc) scaled as in decide_kernel (kept when it sums
+// to 0).  An accepted child becomes v; otherwise the token is drawn from C
+// with u[n-1].  Full vocabulary: C is never stored -- level l of the residual
+// chain is recomputed per token from (P_j, Q_j) with the saved (Zc, shift) of
+// the levels before.  top_k: C lives in the merged kept list of the two rows
+// (at most 2 top_k entries, LDS).  On a chain this is decide_kernel's rule.
+__global__ __launch_bounds__(kSeqThreads) void decide_tree_kernel(const RowStat* __restrict__ stats,
+                                                                  const float* __restrict__ tl,
+                                                                  const float* __restrict__ dl,
+                                                                  const int32_t* __restrict__ tokens,
+                                                                  const float* __restrict__ uniforms, uint32_t V,
+                                                                  WarpParams p, TreeShape shape,
+                                                                  int32_t* __restrict__ out,
+                                                                  int32_t* __restrict__ path,
+                                                                  int32_t* __restrict__ nacc)
+{
+    __shared__ uint64_t scratch[kSeqThreads / 64];
+    __shared__ int32_t pick;
+    __shared__ int32_t uidx[2 * kKMax];
+    __shared__ uint64_t uC[2 * kKMax];
+    __shared__ uint64_t uQ[2 * kKMax];
+    __shared__ int32_t un;
+    __shared__ uint64_t sSR;
+    __shared__ uint64_t lvZ[kTreeMax];
+    __shared__ int32_t lvSh[kTreeMax];
+    const int tid = threadIdx.x;
+    const uint32_t b = blockIdx.x;
+    const int n = shape.n;
+    const RowStat* ts = stats + (size_t)b * n;
+    const RowStat* ds = stats + (size_t)gridDim.x * n + (size_t)b * n;
+    const int32_t* tok = tokens + (size_t)b * n;
+    const float* u = p.greedy ? nullptr : uniforms + (size_t)b * n;
+    int32_t* o = out + (size_t)b * n;
+    int32_t* pa = path + (size_t)b * n;
+    const bool topk = p.top_k > 0 && p.top_k < V;
+
+    for (int i = tid; i < n; i += kSeqThreads) {
+        o[i] = -1;
+        pa[i] = i == 0 ? 0 : -1;
+    }
+    __syncthreads();
+    int v = 0, depth = 0;
+    for (;;) {
+        int next = -1;
+        const float* trow = tl + ((size_t)b * n + v) * V;
+        if (p.greedy) {
+            const int32_t a = ts[v].argmax;
+            for (int c = v + 1; c < n; ++c)
+                if (shape.parent[c] == v && tok[c] == a) {
+                    next = c;
+                    break;
+                }
+            if (tid == 0) o[depth] = a;
+            if (next < 0) break;
+        } else {
+            const float* drow = dl + ((size_t)b * n + v) * V;
+            const float lpm = ts[v].lmax, lqm = ds[v].lmax;
+            uint64_t Zc = ts[v].Z;
+            const uint64_t Zq = ds[v].Z;  // read only when v has children (draft stats exist then)
+            int L = 0;                     // levels of the residual chain (full vocabulary)
+            bool have_list = false;
+            // weights of elements 4q..4q+3 at the current level (full vocabulary), and the draft's
+            auto level4 = [&](uint32_t q, W4& qw) {
+                W4 a = fixed_e4(load4(trow, V, q), lpm, p);
+                qw = fixed_e4(load4(drow, V, q), lqm, p);
+                for (int l = 0; l < L; ++l) {
+                    a.a = residual_weight(a.a, qw.a, lvZ[l], Zq, lvSh[l]);
+                    a.b = residual_weight(a.b, qw.b, lvZ[l], Zq, lvSh[l]);
+                    a.c = residual_weight(a.c, qw.c, lvZ[l], Zq, lvSh[l]);
+                    a.d = residual_weight(a.d, qw.d, lvZ[l], Zq, lvSh[l]);
+                }
+                return a;
+            };
+            for (int c = v + 1; c < n; ++c) {
+                if (shape.parent[c] != v) continue;
+                if (topk && !have_list) {
+                    if (tid == 0) {  // merged kept lists, index order
+                        const RowStat& A = ts[v];
+                        const RowStat& B = ds[v];
+                        int ia = 0, ib = 0, m = 0;
+                        while (ia < A.nk || ib < B.nk) {
+                            const int32_t ja = ia < A.nk ? A.idx[ia] : 0x7fffffff;
+                            const int32_t jb = ib < B.nk ? B.idx[ib] : 0x7fffffff;
+                            const int32_t j = ja < jb ? ja : jb;
+                            uC[m] = ja == j ? A.E[ia++] : 0;
+                            uQ[m] = jb == j ? B.E[ib++] : 0;
+                            uidx[m++] = j;
+                        }
+                        un = m;
+                    }
+                    __syncthreads();
+                    have_list = true;
+                }
+                const int32_t x = tok[c];
+                const uint64_t Qx = weight_of(ds[v], drow, V, topk, x, p);
+                uint64_t Cx = 0;
+                if (topk) {
+                    int lo = 0, hi = un - 1;
+                    while (lo <= hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (uidx[mid] == x) {
+                            Cx = uC[mid];
+                            break;
+                        }
+                        if (uidx[mid] < x) lo = mid + 1;
+                        else hi = mid - 1;
+                    }
+                } else {
+                    Cx = weight_of(ts[v], trow, V, false, x, p);
+                    for (int l = 0; l < L; ++l) Cx = residual_weight(Cx, Qx, lvZ[l], Zq, lvSh[l]);
+                }
+                const double lhs = ((double)u[c - 1] * (double)Qx) * (double)Zc;
+                const double rhs = (double)Cx * (double)Zq;
+                if (lhs < rhs) {
+                    if (tid == 0) o[depth] = x;
+                    next = c;
+                    break;
+                }
+                const int sh = 62 - bitlen64(Zc) - bitlen64(Zq);
+                uint64_t SR;
+                if (topk) {
+                    if (tid == 0) {
+                        uint64_t t = 0;
+                        for (int i = 0; i < un; ++i) t += residual_weight(uC[i], uQ[i], Zc, Zq, sh);
+                        if (t)
+                            for (int i = 0; i < un; ++i) uC[i] = residual_weight(uC[i], uQ[i], Zc, Zq, sh);
+                        sSR = t;
+                    }
+                    __syncthreads();
+                    SR = sSR;
+                    __syncthreads();
+                } else {
+                    uint64_t mine = 0;
+                    const uint32_t V4 = (V + 3) / 4;
+                    for (uint32_t q = tid; q < V4; q += kSeqThreads) {
+                        W4 qw;
+                        const W4 a = level4(q, qw);
+                        const uint64_t e[4] = {residual_weight(a.a, qw.a, Zc, Zq, sh), residual_weight(a.b, qw.b, Zc, Zq, sh),
+                                               residual_weight(a.c, qw.c, Zc, Zq, sh), residual_weight(a.d, qw.d, Zc, Zq, sh)};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            if (4 * q + j < V) mine += e[j];
+                    }
+                    SR = block_sum_u64<kSeqThreads>(mine, scratch);
+                    if (SR) {
+                        if (tid == 0) {
+                            lvZ[L] = Zc;
+                            lvSh[L] = sh;
+                        }
+                        __syncthreads();
+                        ++L;
+                    }
+                }
+                if (SR) Zc = SR;
+            }
+            if (next < 0) {
+                int32_t t;
+                const float uf = u[n - 1];
+                if (topk) {
+                    t = have_list ? list_cdf_pick(uidx, uC, un, Zc, uf, V)
+                                  : list_cdf_pick(ts[v].idx, ts[v].E, ts[v].nk, Zc, uf, V);
+                } else if (L == 0) {
+                    t = draw_row(ts[v], trow, V, false, uf, p, scratch, &pick);
+                } else {
+                    t = block_cdf_pick(V, uf, [&](uint32_t q) { W4 qw; return level4(q, qw); }, scratch, &pick);
+                }
+                if (tid == 0) o[depth] = t;
+                break;
+            }
+            __syncthreads();  // the list / levels of v are not reused by the next node before every thread is done
+        }
+        ++depth;
+        if (tid == 0) pa[depth] = next;
+        v = next;
+    }
+    if (tid == 0) nacc[b] = depth;
+}
+
 __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __restrict__ stats,
                                                              const float* __restrict__ logits,
                                                              const float* __restrict__ uniforms, uint32_t V,
@@ -715,13 +916,62 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         if (st != ULSPEC_OK) return st;
     }
     RowStat* stats = (RowStat*)ws;
-    hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats);
+    hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats,
+                       RowSel{});
     if (rows_d)
         hipLaunchKernelGGL(row_stats_kernel, dim3(rows_d), dim3(kRowThreads), 0, ctx->stream, draft_logits, V, p,
-                           stats + (size_t)B * (k + 1));
+                           stats + (size_t)B * (k + 1), RowSel{});
     hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, stats, target_logits, draft_logits,
                        draft_tokens, uniforms, k, V, p, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
+}
+
+size_t accept_tree_workspace_bytes(uint32_t B, uint32_t n) { return (size_t)2 * B * n * sizeof(RowStat); }
+
+ulspec_status accept_tree_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t n, uint32_t V,
+                                 const int32_t* parent, const float* target_logits, const float* draft_logits,
+                                 const int32_t* tokens, const float* uniforms, int32_t* out_tokens,
+                                 int32_t* out_path, int32_t* out_n_accepted, void* ws)
+{
+    WarpParams p;
+    ulspec_status st = make_params(ctx, s, V, p);
+    if (st != ULSPEC_OK) return st;
+    if (B == 0 || n == 0 || n > (uint32_t)kTreeMax || V == 0)
+        return fail(ctx, ULSPEC_EINVAL, "accept_tree: need B >= 1, 1 <= n <= %d, V >= 1 (B=%u n=%u V=%u)", kTreeMax,
+                    B, n, V);
+    if (!parent) return fail(ctx, ULSPEC_EINVAL, "accept_tree: parent (host array) is null");
+    if (!target_logits || !tokens || !out_tokens || !out_path || !out_n_accepted)
+        return fail(ctx, ULSPEC_EINVAL, "accept_tree: null device pointer");
+    if (!p.greedy && (!draft_logits || !uniforms))
+        return fail(ctx, ULSPEC_EINVAL, "accept_tree: sampling needs draft logits and uniforms");
+    TreeShape shape{};
+    shape.n = (int32_t)n;
+    RowSel inner{};  // nodes with children: their draft rows are read
+    bool has_kids[kTreeMax] = {};
+    for (uint32_t i = 0; i < n; ++i) {
+        const int32_t pi = parent[i];
+        if (i == 0 ? pi != -1 : (pi < 0 || pi >= (int32_t)i))
+            return fail(ctx, ULSPEC_EINVAL, "accept_tree: parent[%u]=%d (need parent[0] = -1, parent[i] in [0, i))", i,
+                        pi);
+        shape.parent[i] = pi;
+        if (i) has_kids[pi] = true;
+    }
+    inner.n_rows = n;
+    for (uint32_t i = 0; i < n; ++i)
+        if (has_kids[i]) inner.row[inner.n_sel++] = (int32_t)i;
+    if (!ws) {
+        st = workspace(ctx, accept_tree_workspace_bytes(B, n), &ws);
+        if (st != ULSPEC_OK) return st;
+    }
+    RowStat* stats = (RowStat*)ws;
+    hipLaunchKernelGGL(row_stats_kernel, dim3(B * n), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats,
+                       RowSel{});
+    if (!p.greedy && inner.n_sel)
+        hipLaunchKernelGGL(row_stats_kernel, dim3(B * inner.n_sel), dim3(kRowThreads), 0, ctx->stream, draft_logits,
+                           V, p, stats + (size_t)B * n, inner);
+    hipLaunchKernelGGL(decide_tree_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, stats, target_logits,
+                       draft_logits, tokens, uniforms, V, p, shape, out_tokens, out_path, out_n_accepted);
+    return check_launch(ctx, "accept_tree launch");
 }
 
 ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
@@ -741,7 +991,8 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
         if (st != ULSPEC_OK) return st;
     }
-    hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws);
+    hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws,
+                       RowSel{});
     hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)ws, logits,
                        uniforms, V, p, out_tokens);
     return check_launch(ctx, "sample launch");
@@ -758,6 +1009,17 @@ extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s
     (void)hipSetDevice(ctx->device);
     return accept_launch(ctx, s, B, k, V, target_logits, draft_logits, draft_tokens, uniforms, out_tokens,
                          out_n_accepted, nullptr);
+}
+
+extern "C" ulspec_status ulspec_accept_tree(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t n,
+                                            uint32_t V, const int32_t* parent, const float* target_logits,
+                                            const float* draft_logits, const int32_t* tokens, const float* uniforms,
+                                            int32_t* out_tokens, int32_t* out_path, int32_t* out_n_accepted)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    (void)hipSetDevice(ctx->device);
+    return accept_tree_launch(ctx, s, B, n, V, parent, target_logits, draft_logits, tokens, uniforms, out_tokens,
+                              out_path, out_n_accepted, nullptr);
 }
 
 extern "C" ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,

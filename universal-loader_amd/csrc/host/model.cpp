@@ -33,6 +33,39 @@ namespace {
 
 __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
 
+// Tree compaction of the K/V caches: rows pos + path[j] -> pos + j for j = 1
+// .. cnt - 1, cnt = min(*n_acc + 1, n_max) (row pos, the root, stays), in
+// every layer's K (blockIdx.z = 0) and V (1) cache.  Thread t of the grid
+// moves 16-byte column group t of every row: it reads all its source rows
+// before it writes any (a destination row may be another entry's source),
+// and no other thread touches its columns.  Entries outside [0, n_max) or
+// rows past max_ctx are skipped.
+constexpr int kCompactMax = 16;
+__global__ __launch_bounds__(256) void kv_compact_kernel(_Float16* const* __restrict__ tab, uint32_t n_layers,
+                                                         uint32_t kvdim8, uint32_t max_ctx,
+                                                         const int32_t* __restrict__ pos_dev, int32_t pos_add,
+                                                         const int32_t* __restrict__ path,
+                                                         const int32_t* __restrict__ n_acc, uint32_t n_max)
+{
+    const uint32_t col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= kvdim8) return;
+    uint4* base = (uint4*)tab[blockIdx.z * n_layers + blockIdx.y];
+    const int64_t pos = (int64_t)(pos_dev ? *pos_dev : 0) + pos_add;
+    const int32_t cnt = min(max(*n_acc + 1, 1), (int32_t)n_max);
+    uint4 r[kCompactMax];
+    bool ok[kCompactMax];
+#pragma unroll
+    for (int j = 1; j < kCompactMax; ++j) {
+        const int32_t src = j < cnt ? path[j] : -1;
+        ok[j] = src >= 0 && src < (int32_t)n_max && pos >= 0 && pos + src < (int64_t)max_ctx &&
+                pos + j < (int64_t)max_ctx;
+        if (ok[j]) r[j] = base[(size_t)(pos + src) * kvdim8 + col];
+    }
+#pragma unroll
+    for (int j = 1; j < kCompactMax; ++j)
+        if (ok[j]) base[(size_t)(pos + j) * kvdim8 + col] = r[j];
+}
+
 // Which tensor a GGUF name is: layer (or -1 for globals) and a role.
 enum Role { R_NONE, R_EMBED, R_OUT_NORM, R_OUT, R_ATTN_NORM, R_Q, R_K, R_V, R_O, R_FFN_NORM, R_GATE, R_UP, R_DOWN };
 
@@ -98,6 +131,15 @@ void launch_set_i32(hipStream_t st, int32_t* p, int32_t v)
 {
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, st, p, v);
 }
+
+void launch_kv_compact(hipStream_t st, _Float16* const* kv_tab, uint32_t n_layers, uint32_t kvdim, uint32_t max_ctx,
+                       const int32_t* pos_dev, int32_t pos_add, const int32_t* path, const int32_t* n_acc,
+                       uint32_t n_max)
+{
+    const uint32_t kvdim8 = kvdim / 8;  // kvdim = Hkv * D, a multiple of 64
+    hipLaunchKernelGGL(kv_compact_kernel, dim3((kvdim8 + 255) / 256, n_layers, 2), dim3(256), 0, st, kv_tab,
+                       n_layers, kvdim8, max_ctx, pos_dev, pos_add, path, n_acc, std::min<uint32_t>(n_max, kCompactMax));
+}
 }  // namespace ulspec
 
 bool ulspec_model::complete() const
@@ -110,11 +152,21 @@ bool ulspec_model::complete() const
 }
 
 ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
-                                    float* logits_dev, uint32_t n_logits)
+                                    float* logits_dev, uint32_t n_logits, const int32_t* parent)
 {
     const ulspec_model_cfg& c = cfg;
     const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = head_dim;
     if (M == 0 || M > rows_max || n_logits > M) return fail(ctx, ULSPEC_EINVAL, "forward: %u rows (max %u)", M, rows_max);
+    uint64_t depth_bits = 0;  // 4-bit depth of each tree row (depth <= M - 1 <= 15)
+    if (parent) {
+        uint32_t depth[kRows];
+        for (uint32_t i = 0; i < M; ++i) {
+            if (parent[i] < -1 || parent[i] >= (int32_t)i)
+                return fail(ctx, ULSPEC_EINVAL, "forward: parent[%u]=%d must be in [-1, %u)", i, parent[i], i);
+            depth[i] = parent[i] < 0 ? 0 : depth[parent[i]] + 1;
+            depth_bits |= (uint64_t)depth[i] << (4 * i);
+        }
+    }
     const std::vector<Weight>& W = ctx->weights;
     launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss);
     int P = (int)embed_partials(c.dim);
@@ -131,6 +183,8 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         q.epi = kEpiRope;
         q.pos_dev = pos_dev;
         q.pos_add = pos_add;
+        q.tree = parent != nullptr;
+        q.row_depth = depth_bits;
         q.rope = rope;
         q.q16 = q16;
         q.kc = L.kc;
@@ -146,6 +200,7 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         a.v_cache = (const uint16_t*)L.vc;
         a.n_prefix = c.max_ctx - M;
         a.nq = M;
+        a.parent = parent;
         a.H = H;
         a.Hkv = Hkv;
         a.D = D;
@@ -243,6 +298,7 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         {(void**)&m->pos, 16},
         {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},
         {(void**)&m->rope, (size_t)c.max_ctx * (D / 2) * sizeof(float2)},
+        {(void**)&m->kv_tab, (size_t)2 * c.n_layers * sizeof(_Float16*)},
     };
     ulspec_status st = ULSPEC_OK;
     for (const Want& w : wants)
@@ -250,6 +306,15 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
     for (uint32_t l = 0; l < c.n_layers && st == ULSPEC_OK; ++l) {
         st = dev_alloc(m, kv_bytes, (void**)&m->layers[l].kc);
         if (st == ULSPEC_OK) st = dev_alloc(m, kv_bytes, (void**)&m->layers[l].vc);
+    }
+    if (st == ULSPEC_OK) {
+        std::vector<_Float16*> tab(2 * (size_t)c.n_layers);
+        for (uint32_t l = 0; l < c.n_layers; ++l) {
+            tab[l] = m->layers[l].kc;
+            tab[c.n_layers + l] = m->layers[l].vc;
+        }
+        hipError_t e = hipMemcpy(m->kv_tab, tab.data(), tab.size() * sizeof(_Float16*), hipMemcpyHostToDevice);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "model kv table");
     }
     if (st == ULSPEC_OK) {
         // RoPE angles theta_i = pos * base^(-2i / D) for pair i (src/shaders/rope.glsl:50-56),
@@ -424,6 +489,53 @@ extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* to
     }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "model_forward sync");
+}
+
+extern "C" ulspec_status ulspec_model_forward_tree(ulspec_model* m, const int32_t* tokens, const int32_t* parent,
+                                                   uint32_t M, uint32_t pos, float* logits)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    if (!tokens || !parent || !logits || M == 0)
+        return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: null pointer or no nodes");
+    if (M > m->rows_max)
+        return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: %u nodes (at most %u)", M, m->rows_max);
+    if ((uint64_t)pos + M > m->cfg.max_ctx)
+        return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: slots %u + %u beyond max_ctx %u", pos, M, m->cfg.max_ctx);
+    if (!m->complete()) return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: model tensors missing");
+    for (uint32_t i = 0; i < M; ++i) {
+        if (tokens[i] < 0 || (uint32_t)tokens[i] >= m->cfg.vocab)
+            return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: token %d out of range", tokens[i]);
+        if (parent[i] < -1 || parent[i] >= (int32_t)i)
+            return fail(ctx, ULSPEC_EINVAL, "model_forward_tree: parent[%u]=%d must be in [-1, %u)", i, parent[i], i);
+    }
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipMemcpyAsync(m->tok, tokens, M * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "model_forward_tree tokens");
+    launch_set_i32(ctx->stream, m->pos, (int32_t)pos);
+    ulspec_status st = m->forward(m->tok, M, m->pos, 0, m->logits, M, parent);
+    if (st != ULSPEC_OK) return st;
+    e = hipMemcpyAsync(logits, m->logits, (size_t)M * m->cfg.vocab * sizeof(float), hipMemcpyDeviceToHost,
+                       ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "model_forward_tree logits");
+    e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "model_forward_tree sync");
+}
+
+extern "C" ulspec_status ulspec_model_kv_compact(ulspec_model* m, uint32_t pos, const int32_t* path,
+                                                 const int32_t* n_accepted, uint32_t n_max)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    if (!path || !n_accepted) return fail(ctx, ULSPEC_EINVAL, "model_kv_compact: null device pointer");
+    if (n_max == 0 || n_max > ulspec_model::kRows || (uint64_t)pos + n_max > m->cfg.max_ctx)
+        return fail(ctx, ULSPEC_EINVAL, "model_kv_compact: n_max=%u at %u (1 .. %u rows within max_ctx %u)", n_max,
+                    pos, ulspec_model::kRows, m->cfg.max_ctx);
+    (void)hipSetDevice(ctx->device);
+    launch_set_i32(ctx->stream, m->pos, (int32_t)pos);
+    launch_kv_compact(ctx->stream, m->kv_tab, m->cfg.n_layers, m->cfg.n_kv_heads * m->head_dim, m->cfg.max_ctx,
+                      m->pos, 0, path, n_accepted, n_max);
+    return check_launch(ctx, "model_kv_compact launch");
 }
 
 extern "C" ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n,

@@ -49,16 +49,25 @@ struct ulspec_model {
     int32_t* tok = nullptr;    // [kRows]
     int32_t* pos = nullptr;    // [1]
     float* attn_part = nullptr;
+    _Float16** kv_tab = nullptr;  // device [2][n_layers]: every layer's K cache, then every V cache
     std::vector<void*> allocs;
 
     bool complete() const;
     // Forward M <= rows_max tokens read from device memory at positions
     // *pos_dev + pos_add ...; logits of the last n_logits rows to `logits`
-    // (device).  Asynchronous, never allocates or synchronises.
+    // (device).  With `parent` (host [M], parent[i] in [-1, i)) the rows are
+    // a tree: row i keeps its K/V slot (pos + i) but takes RoPE position pos +
+    // depth(i) and attends to the prefix and its ancestors only.
+    // Asynchronous, never allocates or synchronises.
     ulspec_status forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
-                          float* logits_dev, uint32_t n_logits);
+                          float* logits_dev, uint32_t n_logits, const int32_t* parent = nullptr);
 };
 
 namespace ulspec {
 void launch_set_i32(hipStream_t st, int32_t* p, int32_t v);
+// K/V rows pos + path[j] -> pos + j, j = 1 .. min(*n_acc + 1, n_max) - 1, in
+// every layer (pos = *pos_dev + pos_add); see kv_compact_kernel.
+void launch_kv_compact(hipStream_t st, _Float16* const* kv_tab, uint32_t n_layers, uint32_t kvdim, uint32_t max_ctx,
+                       const int32_t* pos_dev, int32_t pos_add, const int32_t* path, const int32_t* n_acc,
+                       uint32_t n_max);
 }

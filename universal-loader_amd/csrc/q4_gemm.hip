@@ -582,12 +582,19 @@ __device__ __forceinline__ int epi_pos0(const GemmArgs& a)
     return *p + a.f.pos_add;
 }
 
+// RoPE position of row m, relative to pos0: m, or the row's tree depth.
+__device__ __forceinline__ int rope_row(const GemmFuse& f, int m)
+{
+    return f.tree ? (int)((f.row_depth >> (4 * (m & 15))) & 15u) : m;
+}
+
 // The memory operands of the epilogue of output (m, n), loaded ahead of it
 // with the weights of the same tile so that the epilogue reads no memory
 // (vmcnt retires in issue order: a load issued in the epilogue would wait for
 // every weight load in flight).  Two 4-byte loads for the resid and rope
 // epilogues (out of range where a thread has no output), none otherwise:
 //   resid: (h[m][n], -)      rope: (cos, sin) of the pair at position pos0 + m
+//                            (pos0 + depth(m) for a tree)
 __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int pos0)
 {
     const GemmFuse& f = a.f;
@@ -601,7 +608,7 @@ __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int 
         r = make_rsrc(f.rope, (uint32_t)(pos0 + a.M) * (uint32_t)(f.hd / 2) * 8u);
         if (ok && n < f.qdim + f.kvdim) {
             const int nn = n < f.qdim ? n : n - f.qdim;
-            o0 = (uint32_t)((pos0 + m) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
+            o0 = (uint32_t)((pos0 + rope_row(f, m)) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
             o1 = o0 + 4u;
         }
     } else {
@@ -625,8 +632,9 @@ __device__ __forceinline__ int epi_nloads(const GemmArgs& a)
 // epi_pos0.  Thread lanes l and l ^ 1 hold columns n and n ^ 1 of the same
 // row m (whole waves call this).
 //   store: Y[m][n] = s
-//   rope:  RoPE pair (n, n+1) at position pos0 + m (Q and K rows), then fp16
-//          Q -> q16[m][n], K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim]
+//   rope:  RoPE pair (n, n+1) at position pos0 + m, or pos0 + depth(m) for a
+//          tree (Q and K rows, angles from epi_load), then fp16 Q -> q16[m][n],
+//          K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim], pos = pos0 + m
 //          (y0 = x0 c - x1 s, y1 = x0 s + x1 c; src/shaders/rope.glsl:50-73)
 //   silu:  rows interleaved (2i = gate i, 2i+1 = up i):
 //          act[m][i] = fp16(g * (1 / (1 + e^-g)) * u)

@@ -80,9 +80,13 @@ struct GemmFuse {
     int P = 0;
     const float* norm_w = nullptr;
     float eps = 0.0f;
-    // kEpiRope: Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc at positions *pos_dev + pos_add + m
+    // kEpiRope: Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc at slot *pos_dev + pos_add + m;
+    // the RoPE position of row m is *pos_dev + pos_add + m, or with tree != 0
+    // *pos_dev + pos_add + depth(m), depth(m) = bits 4m .. 4m+3 of row_depth
     const int32_t* pos_dev = nullptr;
     int pos_add = 0;
+    int tree = 0;
+    uint64_t row_depth = 0;
     const float2* rope = nullptr;
     _Float16* q16 = nullptr;
     _Float16* kc = nullptr;
@@ -127,6 +131,11 @@ size_t sample_workspace_bytes(uint32_t R);
 ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
                             const float* target_logits, const float* draft_logits, const int32_t* draft_tokens,
                             const float* uniforms, int32_t* out_tokens, int32_t* out_n_accepted, void* ws);
+size_t accept_tree_workspace_bytes(uint32_t B, uint32_t n);
+ulspec_status accept_tree_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t n, uint32_t V,
+                                 const int32_t* parent, const float* target_logits, const float* draft_logits,
+                                 const int32_t* tokens, const float* uniforms, int32_t* out_tokens,
+                                 int32_t* out_path, int32_t* out_n_accepted, void* ws);
 ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
                             const float* uniforms, int32_t* out_tokens, void* ws);
 
