@@ -118,6 +118,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
                 va[i][st] = *(const half8_t*)(a.v + kbase + 32 * st);
             }
         }
+        asm volatile("" ::: "memory");  // keep every load of the round ahead of the first use
 #pragma unroll
         for (int i = 0; i < T; ++i) {
             const int jt = jr + 16 * (wave + kAttnWaves * i);
@@ -224,6 +225,9 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
     const int ns = min(a.splits, (L + a.keys_per_split - 1) / a.keys_per_split);
     const size_t stride = (size_t)a.nq * (D + 2);
     const float* q0 = a.part + (size_t)h * a.splits * stride + qi * (D + 2);
+    float first[16];  // O of the first 16 splits, loaded with (m, l)
+#pragma unroll
+    for (int u = 0; u < 16; ++u) first[u] = u < ns ? q0[u * stride + d] : 0.0f;
     if (d < ns) {
         sm[d] = q0[d * stride + D];
         sl[d] = q0[d * stride + D + 1];
@@ -236,7 +240,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
     for (int s0 = 0; s0 < ns; s0 += 16) {
         float ov[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) ov[u] = s0 + u < ns ? q0[(s0 + u) * stride + d] : 0.0f;
+        for (int u = 0; u < 16; ++u) ov[u] = s0 == 0 ? first[u] : (s0 + u < ns ? q0[(s0 + u) * stride + d] : 0.0f);
 #pragma unroll
         for (int u = 0; u < 16; ++u)
             if (s0 + u < ns) {
@@ -265,16 +269,15 @@ void launch_attn(const AttnArgs& a, int T, hipStream_t st)
 namespace ulspec {
 
 // Splits so that heads x splits is about two workgroups per CU, at most
-// kAttnMaxSplits; a workgroup covers rounds of 64 T keys (T = 1, 2 or 4
-// tiles of 16 keys per wave, all loaded before the round's first MFMA).
+// kAttnMaxSplits; keys per split a multiple of 64, covered in rounds of 64 T
+// keys (T = 4, 2 or 1 tiles of 16 keys per wave, the largest that divides
+// it; all of a round's loads are issued before its first MFMA).
 void attn_plan(int L, int H, int n_cu, int& splits, int& kps)
 {
     int want = (2 * n_cu + H - 1) / H;
     want = want < 1 ? 1 : (want > kAttnMaxSplits ? kAttnMaxSplits : want);
     const int need = (L + want - 1) / want;
-    int T = 1;
-    while (T < 4 && 64 * T < need) T *= 2;
-    kps = (need + 64 * T - 1) / (64 * T) * (64 * T);
+    kps = (need + 63) / 64 * 64;
     splits = (L + kps - 1) / kps;
 }
 
