@@ -17,7 +17,10 @@
 //                                         accumulator layout is exactly the
 //                                         P^T operand layout; P = P_hi + P_lo
 //                                         (two fp16 parts) keeps fp32 accuracy;
-//                                         V goes through LDS for the transpose
+//                                         V goes through LDS and comes back
+//                                         transposed (ds_read_b64_tr_b16)
+// The scores of all tiles of a round come first, then one online-softmax
+// update per round.
 // The 4 waves are merged in LDS; each workgroup writes its partial (O, m, l)
 // and a second kernel merges the splits in split order (deterministic).  (A
 // merge by the last workgroup to finish, behind an atomic counter, costs more
@@ -30,6 +33,8 @@
 #include <cmath>
 
 using namespace ulspec;
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -119,55 +124,70 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
             }
         }
         asm volatile("" ::: "memory");  // keep every load of the round ahead of the first use
+        // scores of every tile of the round, then one softmax update for the
+        // round (rescale, max and sum shuffles once per round, not per tile)
+        float s2[T][4];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            const int jt = jr + 16 * (wave + kAttnWaves * i);
+            float4_t sacc = {0.f, 0.f, 0.f, 0.f};
+            if (jt < j1) {  // uniform in the wave
+#pragma unroll
+                for (int st = 0; st < D / 32; ++st) sacc = mfma16x16x32(ka[i][st], qb[st], sacc);
+            }
+            // lane holds S^T[key 4g + r][query c]
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = jt + 4 * g + r;
+                const bool vis = j < j1 && (j < n_prefix || ((mask >> (j - n_prefix)) & 1u));
+                s2[i][r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
+                tmax = fmaxf(tmax, s2[i][r]);
+            }
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float mnew = fmaxf(m, tmax);
+        const float muse = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = exp2_fast(m - muse);
+        float p[T][4], psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                p[i][r] = exp2_fast(s2[i][r] - muse);
+                psum += p[i][r];
+            }
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        l = l * alpha + psum;
+        m = mnew;
+        if (jr != j0) {  // the first round starts from O = 0: nothing to rescale
+#pragma unroll
+            for (int dt = 0; dt < D / 16; ++dt) oacc[dt] = oacc[dt] * alpha;
+        }
 #pragma unroll
         for (int i = 0; i < T; ++i) {
             const int jt = jr + 16 * (wave + kAttnWaves * i);
             if (jt < j1) {  // uniform in the wave
-                // V rows to LDS (the wave's own slot; LDS ops of one wave stay in order)
+                // V rows to the wave's LDS slot (LDS ops of one wave stay in order)
 #pragma unroll
                 for (int st = 0; st < D / 32; ++st) *(half8_t*)(myv + c * VP + 32 * st + 8 * g) = va[i][st];
-                float4_t sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int st = 0; st < D / 32; ++st) sacc = mfma16x16x32(ka[i][st], qb[st], sacc);
-
-                // lane holds S^T[key 4g + r][query c]
-                float s2[4];
-                float tmax = -INFINITY;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int j = jt + 4 * g + r;
-                    const bool vis = j < j1 && (j < n_prefix || ((mask >> (j - n_prefix)) & 1u));
-                    s2[r] = vis ? sacc[r] * a.scale_log2 : -INFINITY;
-                    tmax = fmaxf(tmax, s2[r]);
-                }
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-                const float mnew = fmaxf(m, tmax);
-                const float muse = mnew == -INFINITY ? 0.0f : mnew;
-                const float alpha = exp2_fast(m - muse);
-                float p[4], psum = 0.0f;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    p[r] = exp2_fast(s2[r] - muse);
-                    psum += p[r];
-                }
-                psum += __shfl_xor(psum, 16);
-                psum += __shfl_xor(psum, 32);
-                l = l * alpha + psum;
-                m = mnew;
                 half4_t phi, plo;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    phi[r] = (_Float16)p[r];
-                    plo[r] = (_Float16)(p[r] - (float)phi[r]);
+                    phi[r] = (_Float16)p[i][r];
+                    plo[r] = (_Float16)(p[i][r] - (float)phi[r]);
                 }
 #pragma unroll
                 for (int dt = 0; dt < D / 16; ++dt) {
-                    oacc[dt] = oacc[dt] * alpha;
-                    // V^T operand: lane (d = 16 dt + c, group g) holds V[key 4g + r][d]
-                    half4_t vv;
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) vv[r] = myv[(4 * g + r) * VP + 16 * dt + c];
+                    // V^T operand: lane (d = 16 dt + c, group g) holds V[key 4g + r][d],
+                    // r = 0..3: one transposing read, lane x = 4r + q of each 16-lane
+                    // group addressing V[key 4g + r][16 dt + 4q .. +3]
+                    const half4_t vv = __builtin_bit_cast(
+                        half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                     (__attribute__((address_space(3))) short4_t*)(myv + (4 * g + (c >> 2)) * VP +
+                                                                                     16 * dt + 4 * (c & 3))));
                     oacc[dt] = mfma16x16x16(vv, phi, oacc[dt]);
                     oacc[dt] = mfma16x16x16(vv, plo, oacc[dt]);
                 }
