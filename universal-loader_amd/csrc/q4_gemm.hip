@@ -1170,6 +1170,15 @@ void wide_kernels(CList<C...>, std::vector<const void*>& out)
     (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves, false, true>), ...);
 }
 
+// One tile per 8-wave workgroup, one chunk per wave: weights of at most 8
+// chunks per row (Q4_K K <= 2048) with 1-2 tiles per CU.  The workgroups of
+// one launch are all resident at once, so every CU works, where the ring
+// kernel's 16-wave workgroups would leave CUs idle (384 tiles of 8 chunks: 192
+// of them).  With more tiles per CU the ring kernel, which normalizes X once
+// per CU instead of once per tile, is faster.
+constexpr int kSmallWaves = 8;
+constexpr int kSmallTilesPerCu = 2;
+
 // Launch the one-tile kernel with the smallest batch >= cpp (the largest when none is).
 template <int TYPE, int... C>
 void wide_launch(CList<C...>, int cpp, bool norm, dim3 grid, dim3 block, size_t lds, hipStream_t st, GemmArgs& a)
@@ -1206,6 +1215,10 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
     };
     wide_kernels<ULSPEC_GGML_Q4_0>(WideQ40{}, fns);
     wide_kernels<ULSPEC_GGML_Q4_K>(WideQ4K{}, fns);
+    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, false>);
+    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, true>);
+    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, false>);
+    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, true>);
     for (const void* f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
         if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
@@ -1242,6 +1255,18 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
         a.ks_q = (int)(w.n_chunks / P);
         a.ks_r = (int)(w.n_chunks % P);
     };
+    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves && (int)w.n_tiles <= kSmallTilesPerCu * n_cu) {
+        split(kSmallWaves);  // one chunk (or none) per wave
+        const dim3 grid(w.n_tiles), block(kSmallWaves * 64);
+        if (q40) {
+            if (norm) hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, true>), grid, block, lds, ctx->stream, a);
+            else hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, false>), grid, block, lds, ctx->stream, a);
+        } else {
+            if (norm) hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, true>), grid, block, lds, ctx->stream, a);
+            else hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, false>), grid, block, lds, ctx->stream, a);
+        }
+        return;
+    }
     if (pipe) {
         int P = kRingWaves;
         while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
