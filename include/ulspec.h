@@ -46,7 +46,7 @@ typedef enum {
 } ulspec_status;
 
 /* GGUF type ids (src/core/gguf_types.h:6-33). */
-enum { ULSPEC_GGML_Q4_0 = 2, ULSPEC_GGML_Q4_K = 12 };
+enum { ULSPEC_GGML_F16 = 1, ULSPEC_GGML_Q4_0 = 2, ULSPEC_GGML_Q8_0 = 8, ULSPEC_GGML_Q4_K = 12, ULSPEC_GGML_Q6_K = 14 };
 
 /* ---- library / context ---------------------------------------------------
  * Replaces the Vulkan bring-up of InferenceEngine::initialize
@@ -91,7 +91,11 @@ ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t
 /* ---- K1: verify dequant-GEMM ------------------------------------------------
  * Upload one linear weight given as GGUF blocks (host memory, rows of K
  * elements, ne[0] = K contiguous; src/core/tensor.h:17-65).  The context keeps
- * a device copy re-tiled for the kernel (same 18 / 144 bytes per block).
+ * a device copy re-tiled for the kernel: Q4_0 / Q4_K in their own 18 / 144
+ * bytes per block; F16 as is; Q8_0 and Q6_K (which Q4_K_M files mix in)
+ * dequantized once to fp16 (d * q, d * scale * q rounded to fp16: the only
+ * inexact step of those two types).  K is a multiple of the block size, and
+ * of 32 for F16.  weight_info reports the uploaded type.
  * Replaces the first-use repack + upload of run_linear_q4k
  * (src/inference/inference_engine.cpp:536-548, repack_q4k_tensor :891-927). */
 ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t ggml_type, const void* gguf_blocks,
@@ -198,7 +202,9 @@ void          ulspec_model_destroy(ulspec_model* m);
  * output.weight, blk.<i>.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,
  * ffn_gate,ffn_up,ffn_down}.weight), as the weight map of Model::load_from_gguf
  * (src/inference/model.cpp:190-246).  Norms are F32 (type 0), matrices and the
- * embedding Q4_0 / Q4_K.  ne0 = elements per row (contiguous), ne1 = rows.
+ * embedding Q4_0, Q4_K, Q6_K, Q8_0 or F16.  The parts of a fused weight (Q | K
+ * | V, gate | up) of one type are fused as they are; parts of mixed types are
+ * fused as fp16 rows.  ne0 = elements per row (contiguous), ne1 = rows.
  * `data` is host memory, or device memory when on_device != 0. */
 ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* name, uint32_t ggml_type, const void* data,
                                       size_t nbytes, uint64_t ne0, uint64_t ne1, int on_device);
@@ -274,9 +280,10 @@ ulspec_status ulspec_gguf_get_str(const ulspec_gguf* g, const char* key, const c
  * token_embd.weight; max_ctx 0 = llama.context_length. */
 ulspec_status ulspec_gguf_llama_cfg(const ulspec_gguf* g, uint32_t max_ctx, ulspec_model_cfg* cfg);
 /* Model from a GGUF file: every tensor by name through ulspec_model_set_tensor
- * (Model::load_from_gguf, src/inference/model.cpp:190-246).  Tensors of types
- * the kernels do not read (Q6_K, Q8_0, F16 matrices, ...) fail with
- * ULSPEC_EUNSUPPORTED naming the tensor.  The file may be closed afterwards. */
+ * (Model::load_from_gguf, src/inference/model.cpp:190-246).  Matrices may be
+ * Q4_0, Q4_K, Q6_K, Q8_0 or F16 (what Q4_K_M files mix); a tensor of another
+ * type fails with ULSPEC_EUNSUPPORTED naming it.  The file may be closed
+ * afterwards. */
 ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx, ulspec_model** out);
 
 /* ---- speculative decoding loop --------------------------------------------

@@ -15,6 +15,23 @@
  *                  m  = (scales[j+4] >> 4) | ((scales[j] >> 6) << 4)
  *        chunk c < 4 uses qs[32c .. 32c+31]: element 64c+l = d*sc_{2c}*(qs[32c+l] & 15) - dmin*m_{2c},
  *        element 64c+32+l = d*sc_{2c+1}*(qs[32c+l] >> 4) - dmin*m_{2c+1}.
+ * Types real Q4_K_M files mix in (ggml's published block layouts; the
+ * reference's own dequantize_q6_k.glsl / dequantize_q8_0.glsl do not read the
+ * GGUF bytes, src/core/gguf_types.h:43,49 has wrong sizes for them):
+ *   F16  (type 1), 1 element, 2 B: IEEE half.
+ *   Q8_0 (type 8), 32 elements, 34 B: { fp16 d; i8 qs[32]; }   x[j] = d * qs[j]
+ *   Q6_K (type 14), 256 elements, 210 B: { u8 ql[128]; u8 qh[64]; i8 scales[16]; fp16 d; }
+ *        for half h < 2 (elements 128h ..), ql += 64h, qh += 32h, sc = scales + 8h, l < 32:
+ *          q1 = ((ql[l]    & 15) | (((qh[l] >> 0) & 3) << 4)) - 32 -> element 128h + l,      scale sc[l/16]
+ *          q2 = ((ql[l+32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32 -> element 128h + 32 + l, scale sc[l/16 + 2]
+ *          q3 = ((ql[l]    >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32 -> element 128h + 64 + l, scale sc[l/16 + 4]
+ *          q4 = ((ql[l+32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32 -> element 128h + 96 + l, scale sc[l/16 + 6]
+ *        x = d * scale * q.
+ *   ggml itself (its ggml-quants.c dequantize_row_q8_0 / _q6_K) is neither in
+ *   the reference tree nor in this image, and no GGUF fixture holding these
+ *   types exists here: the Q8_0 / Q6_K element order is pinned by closed forms
+ *   of the layout above (scale groups, the byte and bit behind each element),
+ *   not against an independent decoder -- parity unpinned against ggml.
  */
 #include "ora_internal.h"
 
@@ -24,12 +41,24 @@
 
 int ora_blck_size(int type)
 {
-    return type == ORA_Q4_0 ? 32 : type == ORA_Q4_K ? 256 : 0;
+    switch (type) {
+    case ORA_F16: return 1;
+    case ORA_Q4_0: case ORA_Q8_0: return 32;
+    case ORA_Q4_K: case ORA_Q6_K: return 256;
+    default: return 0;
+    }
 }
 
 int ora_type_size(int type)
 {
-    return type == ORA_Q4_0 ? 18 : type == ORA_Q4_K ? 144 : 0;
+    switch (type) {
+    case ORA_F16: return 2;
+    case ORA_Q4_0: return 18;
+    case ORA_Q8_0: return 34;
+    case ORA_Q4_K: return 144;
+    case ORA_Q6_K: return 210;
+    default: return 0;
+    }
 }
 
 size_t ora_row_bytes(int type, int64_t k)
@@ -158,15 +187,117 @@ static void dequant_block_q4_k(const uint8_t* blk, float* y)
     }
 }
 
+static void dequant_block_q8_0(const uint8_t* blk, float* y)
+{
+    float d = ora_h2f(rd16(blk));
+    for (int j = 0; j < 32; ++j) y[j] = d * (float)(int8_t)blk[2 + j];
+}
+
+static void dequant_block_q6_k(const uint8_t* blk, float* y)
+{
+    const float d = ora_h2f(rd16(blk + 208));
+    for (int h = 0; h < 2; ++h) {
+        const uint8_t* ql = blk + 64 * h;
+        const uint8_t* qh = blk + 128 + 32 * h;
+        const int8_t* sc = (const int8_t*)(blk + 192 + 8 * h);
+        float* yy = y + 128 * h;
+        for (int l = 0; l < 32; ++l) {
+            const int is = l / 16;
+            const int q1 = ((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = ((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            yy[l] = d * (float)sc[is] * (float)q1;
+            yy[l + 32] = d * (float)sc[is + 2] * (float)q2;
+            yy[l + 64] = d * (float)sc[is + 4] * (float)q3;
+            yy[l + 96] = d * (float)sc[is + 6] * (float)q4;
+        }
+    }
+}
+
+/* Q8_0 quantizer: d = amax / 127, q = round-half-away(x / d), d stored as fp16. */
+static void quant_block_q8_0(const float* x, uint8_t* blk)
+{
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    wr16(blk, ora_f2h(d));
+    for (int j = 0; j < 32; ++j) {
+        int q = (int)roundf(x[j] * id);
+        blk[2 + j] = (uint8_t)(int8_t)(q > 127 ? 127 : (q < -127 ? -127 : q));
+    }
+}
+
+/* Q6_K quantizer (simple, for synthetic tensors): per 16-element group g the
+ * scale s_g = amax_g / 31; d = max_g s_g / 127, sc_g = round(s_g / d)
+ * (int8, <= 127); q = clamp(round(x / (d sc_g)), -32, 31) + 32 split into
+ * ql / qh by the layout above; d stored as fp16. */
+static void quant_block_q6_k(const float* x, uint8_t* blk)
+{
+    float s[16], smax = 0.0f;
+    for (int g = 0; g < 16; ++g) {
+        float amax = 0.0f;
+        for (int l = 0; l < 16; ++l) amax = fmaxf(amax, fabsf(x[16 * g + l]));
+        s[g] = amax / 31.0f;
+        smax = fmaxf(smax, s[g]);
+    }
+    float d = smax / 127.0f;
+    uint16_t dh = ora_f2h(d);
+    float dq = ora_h2f(dh);
+    memset(blk, 0, 210);
+    int8_t sc[16];
+    for (int g = 0; g < 16; ++g) {
+        int v = dq != 0.0f ? (int)roundf(s[g] / dq) : 0;
+        sc[g] = (int8_t)(v > 127 ? 127 : v);
+        blk[192 + g] = (uint8_t)sc[g];
+    }
+    wr16(blk + 208, dh);
+    for (int e = 0; e < 256; ++e) {
+        const int g = e / 16;
+        const float step = dq * (float)sc[g];
+        int q = step != 0.0f ? (int)roundf(x[e] / step) : 0;
+        q = (q > 31 ? 31 : (q < -32 ? -32 : q)) + 32;
+        /* element e: half h, position within the half p = e % 128 -> (quarter, l) */
+        const int h = e / 128, p = e % 128, quarter = p / 32, l = p % 32;
+        uint8_t* ql = blk + 64 * h;
+        uint8_t* qh = blk + 128 + 32 * h;
+        const int lo = q & 15, hi = q >> 4;
+        if (quarter == 0) { ql[l] |= (uint8_t)lo; qh[l] |= (uint8_t)(hi << 0); }
+        if (quarter == 1) { ql[l + 32] |= (uint8_t)lo; qh[l] |= (uint8_t)(hi << 2); }
+        if (quarter == 2) { ql[l] |= (uint8_t)(lo << 4); qh[l] |= (uint8_t)(hi << 4); }
+        if (quarter == 3) { ql[l + 32] |= (uint8_t)(lo << 4); qh[l] |= (uint8_t)(hi << 6); }
+    }
+}
+
+static void quant_block(int type, const float* x, uint8_t* blk)
+{
+    switch (type) {
+    case ORA_F16: wr16(blk, ora_f2h(x[0])); break;
+    case ORA_Q4_0: quant_block_q4_0(x, blk); break;
+    case ORA_Q8_0: quant_block_q8_0(x, blk); break;
+    case ORA_Q4_K: quant_block_q4_k(x, blk); break;
+    default: quant_block_q6_k(x, blk); break;
+    }
+}
+
+static void dequant_block(int type, const uint8_t* blk, float* y)
+{
+    switch (type) {
+    case ORA_F16: y[0] = ora_h2f(rd16(blk)); break;
+    case ORA_Q4_0: dequant_block_q4_0(blk, y); break;
+    case ORA_Q8_0: dequant_block_q8_0(blk, y); break;
+    case ORA_Q4_K: dequant_block_q4_k(blk, y); break;
+    default: dequant_block_q6_k(blk, y); break;
+    }
+}
+
 int ora_quantize(int type, const float* x, int64_t n, uint8_t* out)
 {
     int bs = ora_blck_size(type);
     if (bs == 0 || n % bs) return -1;
     int ts = ora_type_size(type);
-    for (int64_t b = 0; b < n / bs; ++b) {
-        if (type == ORA_Q4_0) quant_block_q4_0(x + b * bs, out + b * ts);
-        else quant_block_q4_k(x + b * bs, out + b * ts);
-    }
+    for (int64_t b = 0; b < n / bs; ++b) quant_block(type, x + b * bs, out + b * ts);
     return 0;
 }
 
@@ -175,10 +306,7 @@ int ora_dequantize(int type, const uint8_t* in, int64_t n, float* out)
     int bs = ora_blck_size(type);
     if (bs == 0 || n % bs) return -1;
     int ts = ora_type_size(type);
-    for (int64_t b = 0; b < n / bs; ++b) {
-        if (type == ORA_Q4_0) dequant_block_q4_0(in + b * ts, out + b * bs);
-        else dequant_block_q4_k(in + b * ts, out + b * bs);
-    }
+    for (int64_t b = 0; b < n / bs; ++b) dequant_block(type, in + b * ts, out + b * bs);
     return 0;
 }
 
@@ -228,7 +356,26 @@ int ora_q4_gemm_f64(int type, const uint8_t* W, int64_t N, int64_t K,
         for (int64_t b = 0; b < K / bs; ++b) {
             const uint8_t* blk = row + b * ts;
             double* wb = w + b * bs;
-            if (type == ORA_Q4_0) {
+            if (type == ORA_F16) {
+                wb[0] = (double)ora_h2f(rd16(blk));
+            } else if (type == ORA_Q8_0) {
+                double d = (double)ora_h2f(rd16(blk));
+                for (int j = 0; j < 32; ++j) wb[j] = d * (double)(int8_t)blk[2 + j];
+            } else if (type == ORA_Q6_K) {
+                double d = (double)ora_h2f(rd16(blk + 208));
+                for (int h = 0; h < 2; ++h) {
+                    const uint8_t* ql = blk + 64 * h;
+                    const uint8_t* qh = blk + 128 + 32 * h;
+                    const int8_t* sc = (const int8_t*)(blk + 192 + 8 * h);
+                    for (int l = 0; l < 32; ++l) {
+                        const int is = l / 16;
+                        wb[128 * h + l] = d * sc[is] * (double)(((ql[l] & 15) | (((qh[l] >> 0) & 3) << 4)) - 32);
+                        wb[128 * h + 32 + l] = d * sc[is + 2] * (double)(((ql[l + 32] & 15) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                        wb[128 * h + 64 + l] = d * sc[is + 4] * (double)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                        wb[128 * h + 96 + l] = d * sc[is + 6] * (double)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+                    }
+                }
+            } else if (type == ORA_Q4_0) {
                 double d = (double)ora_h2f(rd16(blk));
                 for (int j = 0; j < 16; ++j) {
                     wb[j] = (double)((blk[2 + j] & 15) - 8) * d;
@@ -306,7 +453,21 @@ static void gemm_rows(void* arg, int64_t lo, int64_t hi)
             int mc = (int)(M - m0 < ORA_MCHUNK ? M - m0 : ORA_MCHUNK);
             __m256 acc[ORA_MCHUNK];
             for (int i = 0; i < mc; ++i) acc[i] = _mm256_setzero_ps();
-            if (j->type == ORA_Q4_0) {
+            if (j->type != ORA_Q4_0 && j->type != ORA_Q4_K) {
+                /* the other types: the row dequantized to fp32 (ora_dequantize), then fp32 dots */
+                float* w = (float*)malloc(sizeof(float) * (size_t)K);
+                ora_dequantize(j->type, row, K, w);
+                for (int i = 0; i < mc; ++i) {
+                    const float* xp = j->x + (m0 + i) * K;
+                    __m256 a = _mm256_setzero_ps();
+                    int64_t k = 0;
+                    for (; k + 8 <= K; k += 8) a = _mm256_fmadd_ps(_mm256_loadu_ps(xp + k), _mm256_loadu_ps(w + k), a);
+                    float tail = 0.0f;
+                    for (; k < K; ++k) tail = fmaf(xp[k], w[k], tail);
+                    acc[i] = _mm256_add_ps(a, _mm256_set_ps(0, 0, 0, 0, 0, 0, 0, tail));
+                }
+                free(w);
+            } else if (j->type == ORA_Q4_0) {
                 for (int64_t b = 0; b < K / 32; ++b) {
                     const uint8_t* blk = row + b * 18;
                     __m256 w[4];

@@ -9,6 +9,9 @@
  *   - GGUF Q4_0 / Q4_K block formats: type ids and block sizes of
  *     src/core/gguf_types.h:6-33,60-81 with the GGUF byte sizes (18 / 144 B);
  *     Q4_K byte offsets as read by src/inference/inference_engine.cpp:900-921.
+ *   - F16 / Q8_0 / Q6_K rows (the types Q4_K_M files mix in): ggml's
+ *     published block layouts (ggml is absent here; parity of the Q8_0 / Q6_K
+ *     element order against ggml is unpinned, see ora_q4.c).
  *   - fp16 decode: src/inference/inference_engine.cpp:15-37 (half_to_float).
  *   - Weight orientation Y[m][n] = sum_k X[m][k] * W[n][k]:
  *     src/shaders/gemm/gemm_transposed_b_v2.glsl:23-29 with
@@ -45,7 +48,7 @@
 extern "C" {
 #endif
 
-enum { ORA_Q4_0 = 2, ORA_Q4_K = 12 };
+enum { ORA_F16 = 1, ORA_Q4_0 = 2, ORA_Q8_0 = 8, ORA_Q4_K = 12, ORA_Q6_K = 14 };
 
 /* ---- fp16 ---------------------------------------------------------------- */
 float    ora_h2f(uint16_t h);

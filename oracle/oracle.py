@@ -12,8 +12,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
 
-Q4_0 = 2
-Q4_K = 12
+F16, Q4_0, Q8_0, Q4_K, Q6_K = 1, 2, 8, 12, 14
 
 
 def build():

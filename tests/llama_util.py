@@ -109,3 +109,18 @@ class NumpyLlama:
             h = h + a @ W[f"blk.{l}.ffn_down.weight"].T
         x = self._norm(h, W["output_norm.weight"])
         return x @ W["output.weight"].T
+
+
+# Tensors re-encoded as the other GGUF types a Q4_K_M file mixes in: Q6_K
+# output and one V projection (so the fused QKV weight mixes types), Q8_0
+# embedding and one up projection, F16 down projection, Q4_0 query.
+MIXED_TYPES = [("output.weight", 14), ("blk.0.attn_v.weight", 14), ("token_embd.weight", 8),
+               ("blk.1.ffn_down.weight", 1), ("blk.0.ffn_up.weight", 8), ("blk.1.attn_q.weight", 2)]
+
+
+def make_mixed_tensors(ora, cfg, seed, std=0.02, norm_std=0.1):
+    t = make_tensors(ora, cfg, 12, seed, std=std, norm_std=norm_std)
+    for name, nt in MIXED_TYPES:
+        wt, d, ne0, ne1 = t[name]
+        t[name] = (nt, ora.quantize(nt, ora.dequantize(wt, d, ne0 * ne1)), ne0, ne1)
+    return t

@@ -1,0 +1,137 @@
+"""The GGUF types Q4_K_M files mix in (Q6_K, Q8_0, F16) on the GPU: the
+dequant-GEMM against the oracle's float64 product, and a model whose
+tensors mix all five types (one fused QKV weight mixing Q4_K and Q6_K) read
+from a GGUF file against the oracle model.
+
+Bar: the GEMM bound of test_gemm_gpu.py (1e-3 relative plus 1e-3 of the RMS;
+the one fp16 rounding of a dequantized Q8_0 / Q6_K element is 2^-11 relative
+and averages out over K), and the logits bound of test_gguf_gpu.py."""
+import numpy as np
+import pytest
+
+import gguf_io as G
+from llama_util import MIXED_TYPES, load, make_mixed_tensors, make_tensors
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(ctx, wid, X, N):
+    M = X.shape[0]
+    xb, yb = ctx.upload(X), ctx.alloc(M * N * 4)
+    ctx.verify_gemm(wid, xb, M, yb)
+    y = ctx.download(yb, np.float32, (M, N))
+    xb.free()
+    yb.free()
+    return y
+
+
+def _close(y, ref):
+    rms = float(np.sqrt(np.mean(ref ** 2)))
+    err = np.abs(y.astype(np.float64) - ref)
+    worst = float((err / (np.abs(ref) + rms)).max())
+    print(f"  max rel err {worst:.3e}", flush=True)
+    assert np.all(err <= 1e-3 * np.abs(ref) + 1e-3 * rms), worst
+
+
+@pytest.mark.parametrize("wtype", [1, 8, 14], ids=["f16", "q8_0", "q6_k"])
+@pytest.mark.parametrize("N,K,Ms", [(4096, 4096, (1, 6, 17)), (32000, 4096, (6,)), (100, 1536, (1, 3, 33)),
+                                    (40, 512, (2, 65))])
+def test_gemm_matches_oracle(ctx, ora, rng, wtype, N, K, Ms):
+    print(f"type {wtype} N {N} K {K}", flush=True)
+    W = ora.synth_q4(wtype, 13, N + K, N, K)
+    wid = ctx.weight_upload(wtype, W, N, K)
+    assert ctx.weight_info(wid)[:3] == (wtype, N, K)
+    for M in Ms:
+        X = ora.f2h_fast(rng.standard_normal((M, K)).astype(np.float32))
+        y = _gemm(ctx, wid, X, N)
+        _close(y, ora.q4_gemm_f64(wtype, W, N, K, X))
+
+
+@pytest.mark.parametrize("wtype", [1, 8], ids=["f16", "q8_0"])
+def test_gemm_k_tail(ctx, ora, rng, wtype):
+    """K = 1376 = 10.75 chunks of 128: the last chunk is a quarter full."""
+    N, K = 72, 1376
+    W = ora.synth_q4(wtype, 17, 3, N, K)
+    wid = ctx.weight_upload(wtype, W, N, K)
+    for M in (1, 5):
+        X = ora.f2h_fast(rng.standard_normal((M, K)).astype(np.float32))
+        _close(_gemm(ctx, wid, X, N), ora.q4_gemm_f64(wtype, W, N, K, X))
+
+
+def test_f16_gemm_is_exact_in_the_weights(ctx, ora, rng):
+    """F16 weights are taken as they are: with X = e_k rows the product reads
+    back the weight columns bit for bit."""
+    N, K = 48, 256
+    W = (rng.standard_normal((N, K)) * 0.1).astype(np.float16)
+    wid = ctx.weight_upload(1, W.view(np.uint8), N, K)
+    ks = [0, 1, 7, 31, 32, 127, 128, 255]
+    X = np.zeros((len(ks), K), np.float16)
+    X[np.arange(len(ks)), ks] = 1
+    y = _gemm(ctx, wid, X.view(np.uint16), N)
+    assert np.array_equal(y, W[:, ks].T.astype(np.float32))
+
+
+def test_f16_k_must_be_a_multiple_of_32(pkg, ctx):
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.weight_upload(1, np.zeros(4 * 48 * 2, np.uint8), 4, 48)
+    assert e.value.status == pkg.EINVAL
+
+
+CFG = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, ffn=512, vocab=1000, max_ctx=64, rms_eps=1e-5,
+           rope_base=10000.0)
+
+
+@pytest.fixture(scope="module")
+def mixed_file(ora, tmp_path_factory):
+    t = make_mixed_tensors(ora, CFG, seed=21)
+    p = tmp_path_factory.mktemp("gguf") / "tiny_mixed.gguf"
+    G.write(p, G.llama_kv(CFG), G.model_tensors(t))
+    return p, t
+
+
+def test_mixed_type_model_matches_oracle(pkg, ctx, ora, mixed_file):
+    path, tensors = mixed_file
+    assert {tensors[n][0] for n, _ in MIXED_TYPES} == {14, 8, 1, 2}
+    print(f"  loading {path.name}", flush=True)
+    fm = pkg.load_gguf_model(ctx, str(path))
+    sm = pkg.Model(ctx, **CFG)
+    load(sm, tensors)
+    toks = np.random.default_rng(4).integers(0, CFG["vocab"], 12).astype(np.int32)
+    lf, ls = fm.forward(toks, 0, n_logits=12), sm.forward(toks, 0, n_logits=12)
+    assert np.array_equal(lf.view(np.uint32), ls.view(np.uint32))
+    om = ora.Llama(**CFG, nthreads=ora.nthreads_default())
+    load(om, tensors)
+    lo = om.forward(toks, 0, n_logits=12)
+    err = np.abs(lf.astype(np.float64) - lo).max() / np.sqrt((lo.astype(np.float64) ** 2).mean())
+    print(f"  logits max err / rms vs oracle = {err:.2e}", flush=True)
+    assert err <= 1e-2
+    # decode continues on the cache the mixed weights wrote
+    nxt = np.array([int(np.argmax(lo[-1]))], np.int32)
+    lf2, lo2 = fm.forward(nxt, 12, n_logits=1), om.forward(nxt, 12, n_logits=1)
+    err2 = np.abs(lf2.astype(np.float64) - lo2).max() / np.sqrt((lo2.astype(np.float64) ** 2).mean())
+    assert err2 <= 1e-2
+    fm.close()
+    sm.close()
+
+
+def test_mixed_type_speculative_loop(pkg, ctx, ora, mixed_file):
+    """Mixed-type target with a Q4_K draft: the greedy loop commits what the
+    target's own greedy decoding, one token at a time, produces."""
+    path, tensors = mixed_file
+    prompt = list(np.random.default_rng(8).integers(0, CFG["vocab"], 10))
+    t = pkg.load_gguf_model(ctx, str(path))
+    d = pkg.Model(ctx, **CFG)
+    load(d, make_tensors(ora, CFG, 12, seed=22, norm_std=0.1))
+    sp = pkg.Speculative(t, d, 3, pkg.sampling(greedy=True), 5)
+    sp.prefill(np.array(prompt, np.int32))
+    sp.generate(16)
+    got = sp.tokens()
+    ref = pkg.load_gguf_model(ctx, str(path))
+    seq = list(prompt)
+    ref.forward(np.array(seq[:-1], np.int32), 0)
+    while len(seq) < len(got):
+        lg = ref.forward(np.array(seq[-1:], np.int32), len(seq) - 1, n_logits=1)[0]
+        seq.append(int(np.argmax(lg)))
+    assert list(got) == seq
+    for m in (sp, t, d, ref):
+        m.close()

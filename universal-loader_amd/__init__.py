@@ -23,8 +23,11 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libulspec.so")
 CSRC_DIR = os.path.join(PKG_DIR, "csrc")
 
+F16 = 1
 Q4_0 = 2
+Q8_0 = 8
 Q4_K = 12
+Q6_K = 14
 
 OK, EINVAL, ENOMEM, EDEVICE, EUNSUPPORTED = 0, 1, 2, 3, 4
 

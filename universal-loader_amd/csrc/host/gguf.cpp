@@ -434,10 +434,10 @@ extern "C" ulspec_status ulspec_gguf_llama_cfg(const ulspec_gguf* gc, uint32_t m
 
 // Create a model from the file: configuration from the metadata, every
 // tensor through ulspec_model_set_tensor by its GGUF name (the weight map of
-// Model::load_from_gguf, src/inference/model.cpp:190-246).  Tensors of types
-// the kernels do not read (Q6_K, Q8_0, F16, ...) fail with
-// ULSPEC_EUNSUPPORTED naming the tensor; tensors the model does not use
-// (rope_freqs, ...) are skipped.
+// Model::load_from_gguf, src/inference/model.cpp:190-246).  Matrices may be
+// Q4_0, Q4_K, Q6_K, Q8_0 or F16 (the types Q4_K_M files use); a tensor of
+// another type fails with ULSPEC_EUNSUPPORTED naming it; tensors the model
+// does not use (rope_freqs, ...) are skipped.
 extern "C" ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx,
                                                 ulspec_model** out)
 {

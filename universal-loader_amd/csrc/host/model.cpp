@@ -343,7 +343,8 @@ extern "C" void ulspec_model_destroy(ulspec_model* m)
     (void)hipStreamSynchronize(m->ctx->stream);
     for (void* p : m->allocs) (void)hipFree(p);
     for (auto& kv : m->pending)
-        if (kv.second.dev) (void)hipFree(kv.second.dev);
+        for (auto& q : kv.second.part)
+            if (q.dev) (void)hipFree(q.dev);
     delete m;
 }
 
@@ -390,17 +391,21 @@ extern "C" ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* na
         }
         return copy_in(m, *dst, data, nbytes, on_device != 0);
     }
-    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K)
-        return fail(ctx, ULSPEC_EUNSUPPORTED, "set_tensor: '%s' type %u (Q4_0 / Q4_K only)", name, type);
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K && type != ULSPEC_GGML_F16 && type != ULSPEC_GGML_Q8_0 &&
+        type != ULSPEC_GGML_Q6_K)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "set_tensor: '%s' type %u (Q4_0, Q4_K, Q6_K, Q8_0 or F16)", name, type);
     const size_t rb = row_bytes(type, ne0);
     if (rb == 0 || ne0 % ulspec_ggml_blck_size(type))
         return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' row length %llu not a multiple of the block", name,
                     (unsigned long long)ne0);
     if (nbytes != rb * ne1) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' has %zu bytes, expected %zu", name, nbytes, rb * ne1);
     if (role == R_EMBED) {
+        if (m->embed && m->embed_bytes != nbytes)
+            return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set with another type", name);
         if (!m->embed) {
             ulspec_status st = dev_alloc(m, nbytes, (void**)&m->embed);
             if (st != ULSPEC_OK) return st;
+            m->embed_bytes = nbytes;
         }
         m->embed_type = type;
         return copy_in(m, m->embed, data, nbytes, on_device != 0);
@@ -416,39 +421,69 @@ extern "C" ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* na
     uint32_t* id = qkv ? &m->layers[layer].wqkv : &m->layers[layer].wgu;
     if (*id != ~0u) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
     const uint64_t rows_total = qkv ? (uint64_t)(H + 2 * Hkv) * D : 2ull * F;
-    const uint64_t row0 = role == R_Q ? 0 : role == R_K ? (uint64_t)H * D : (uint64_t)(H + Hkv) * D;
-    const uint32_t bit = role == R_Q || role == R_GATE ? 1u : role == R_K || role == R_UP ? 2u : 4u;
+    const int slot = role == R_Q || role == R_GATE ? 0 : role == R_K || role == R_UP ? 1 : 2;
+    const uint32_t bit = 1u << slot;
     ulspec_model::Pending& p = m->pending[key];
-    if (!p.dev) {
-        hipError_t e = hipMalloc(&p.dev, rb * rows_total);
-        if (e != hipSuccess) {
-            m->pending.erase(key);
-            return hip_fail(ctx, e, "set_tensor staging");
-        }
-        p.type = type;
-        p.need = qkv ? 7u : 3u;
-    }
-    if (p.type != type) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' type differs from its fused group", name);
+    p.need = qkv ? 7u : 3u;
     if (p.have & bit) return fail(ctx, ULSPEC_EINVAL, "set_tensor: '%s' already set", name);
-    ulspec_status st = ULSPEC_OK;
-    if (qkv) {
-        st = copy_in(m, p.dev + rb * row0, data, nbytes, on_device != 0);
-    } else {  // gate row i -> fused row 2i, up row i -> 2i + 1
-        hipError_t e = hipMemcpy2DAsync(p.dev + (role == R_UP ? rb : 0), 2 * rb, data, rb, rb, F,
-                                        on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) st = hip_fail(ctx, e, "set_tensor copy");
+    ulspec_model::Pending::Part& part = p.part[slot];
+    hipError_t e = hipMalloc(&part.dev, nbytes);
+    if (e != hipSuccess) {
+        part.dev = nullptr;
+        return hip_fail(ctx, e, "set_tensor staging");
     }
-    if (st != ULSPEC_OK) return st;
+    part.type = type;
+    part.rows = ne1;
+    ulspec_status st = copy_in(m, part.dev, data, nbytes, on_device != 0);
+    if (st != ULSPEC_OK) {
+        (void)hipFree(part.dev);
+        part.dev = nullptr;
+        return st;
+    }
     p.have |= bit;
-    if (p.have == p.need) {
-        st = weight_create(ctx, type, p.dev, rb * rows_total, (uint32_t)rows_total, (uint32_t)ne0, true, id);
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(p.dev);
-        m->pending.erase(key);
-        if (st != ULSPEC_OK) return st;
+    if (p.have != p.need) return ULSPEC_OK;
+    // all parts here: one type -> its blocks fused as they are; mixed types ->
+    // every part as fp16 rows
+    const int n_parts = qkv ? 3 : 2;
+    bool same = true;
+    for (int i = 1; i < n_parts; ++i) same = same && p.part[i].type == p.part[0].type;
+    const uint32_t K = (uint32_t)ne0;
+    uint64_t row0[3] = {0, (uint64_t)H * D, (uint64_t)(H + Hkv) * D};
+    uint8_t* fused = nullptr;
+    size_t fused_bytes = 0;
+    uint32_t fused_type = same ? p.part[0].type : (uint32_t)ULSPEC_GGML_F16;
+    if (same) {
+        const size_t frb = row_bytes(fused_type, K);
+        fused_bytes = frb * rows_total;
+        e = hipMalloc(&fused, fused_bytes);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "set_tensor fused staging");
+        for (int i = 0; i < n_parts && st == ULSPEC_OK; ++i) {
+            const auto& q = p.part[i];
+            if (qkv)
+                e = hipMemcpyAsync(fused + frb * row0[i], q.dev, frb * q.rows, hipMemcpyDeviceToDevice, ctx->stream);
+            else  // gate row r -> fused row 2r, up row r -> 2r + 1
+                e = hipMemcpy2DAsync(fused + (i ? frb : 0), 2 * frb, q.dev, frb, frb, q.rows, hipMemcpyDeviceToDevice,
+                                     ctx->stream);
+            if (e != hipSuccess) st = hip_fail(ctx, e, "set_tensor fuse");
+        }
+    } else {
+        fused_bytes = (size_t)rows_total * K * 2;
+        e = hipMalloc(&fused, fused_bytes);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "set_tensor fused staging");
+        for (int i = 0; i < n_parts && st == ULSPEC_OK; ++i) {
+            const auto& q = p.part[i];
+            st = qkv ? rows_to_f16(ctx, q.type, q.dev, (uint32_t)q.rows, K, (_Float16*)fused, (uint32_t)row0[i], 1)
+                     : rows_to_f16(ctx, q.type, q.dev, (uint32_t)q.rows, K, (_Float16*)fused, (uint32_t)i, 2);
+        }
     }
-    return ULSPEC_OK;
+    if (st == ULSPEC_OK)
+        st = weight_create(ctx, fused_type, fused, fused_bytes, (uint32_t)rows_total, K, true, id);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (fused) (void)hipFree(fused);
+    for (auto& q : p.part)
+        if (q.dev) (void)hipFree(q.dev);
+    m->pending.erase(key);
+    return st;
 }
 
 extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint32_t M, uint32_t pos,

@@ -9,10 +9,16 @@
 #include "../ulspec_internal.h"
 
 struct ulspec_model {
-    // One fused weight assembled from several GGUF tensors (rows concatenated).
+    // One fused weight assembled from several GGUF tensors (Q | K | V rows
+    // concatenated, gate / up rows interleaved); each part is kept as given
+    // until all have arrived.
     struct Pending {
-        uint8_t* dev = nullptr;   // staging, rows of all parts
-        uint32_t type = 0;
+        struct Part {
+            uint8_t* dev = nullptr;  // the part's GGUF blocks (device)
+            uint32_t type = 0;
+            uint64_t rows = 0;
+        };
+        Part part[3];             // Q, K, V or gate, up
         uint32_t have = 0;        // bitmask of parts received
         uint32_t need = 0;
     };
@@ -31,6 +37,7 @@ struct ulspec_model {
     std::map<std::string, Pending> pending;
     uint8_t* embed = nullptr;  // raw GGUF [vocab][dim]
     uint32_t embed_type = 0;
+    size_t embed_bytes = 0;    // its allocation
     float* out_norm = nullptr;
     uint32_t w_out = ~0u;
     float2* rope = nullptr;    // [max_ctx][head_dim / 2] (cos, sin)

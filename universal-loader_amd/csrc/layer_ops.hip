@@ -15,7 +15,8 @@ __device__ __forceinline__ float h2f_bits(uint32_t b) { return (float)__builtin_
 
 // Q4_0 element j of a block: low nibble of qs[j] (j < 16) / high nibble of
 // qs[j-16], value (q - 8) * d.  Q4_K as in the GGUF definition (6-bit
-// sub-scales / mins, chunk c of 64 elements uses qs[32c .. 32c+31]).
+// sub-scales / mins, chunk c of 64 elements uses qs[32c .. 32c+31]).  F16,
+// Q8_0 and Q6_K as ggml defines them (the types Q4_K_M files mix in).
 // Grid (ceil(dim / 256), M); block b of row m also writes pss[m][b], the sum
 // of its 256 values squared (xor tree in each wave, the 4 waves in order).
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w, uint32_t type, uint32_t dim,
@@ -29,7 +30,21 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
     if (tok < 0 || (uint32_t)tok >= V) tok = 0;
     float v = 0.0f;
     if (e < dim) {
-        if (type == 2) {
+        if (type == 1) {  // F16
+            v = h2f_bits(((const uint16_t*)w)[(size_t)tok * dim + e]);
+        } else if (type == 8) {  // Q8_0: d * q
+            const uint8_t* blk = w + ((size_t)tok * (dim / 32) + e / 32) * 34;
+            v = h2f_bits(blk[0] | (blk[1] << 8)) * (float)(int8_t)blk[2 + e % 32];
+        } else if (type == 14) {  // Q6_K: (d * scale) * q, ggml's block_q6_K layout
+            const uint8_t* blk = w + ((size_t)tok * (dim / 256) + e / 256) * 210;
+            const uint32_t i = e % 256, hh = i / 128, p = i % 128, quarter = p / 32, l = p % 32;
+            const uint8_t lo = blk[64 * hh + l + (quarter & 1 ? 32 : 0)];
+            const uint32_t nib = quarter < 2 ? (lo & 15u) : (lo >> 4);
+            const uint32_t hb = (blk[128 + 32 * hh + l] >> (2 * quarter)) & 3u;
+            const int q = (int)(nib | (hb << 4)) - 32;
+            const int sc = (int8_t)blk[192 + 8 * hh + l / 16 + 2 * quarter];
+            v = h2f_bits(blk[208] | (blk[209] << 8)) * (float)sc * (float)q;
+        } else if (type == 2) {
             const uint8_t* blk = w + ((size_t)tok * (dim / 32) + e / 32) * 18;
             const uint32_t j = e % 32;
             const uint32_t q = j < 16 ? (blk[2 + j] & 15u) : (blk[2 + j - 16] >> 4);

@@ -38,9 +38,13 @@ namespace {
 
 constexpr int kQ40Chunk = 1152;
 constexpr int kQ4KChunk = 2304;
-// 16-byte X units (8 halves) per weight chunk: 128 K for Q4_0, 256 for Q4_K
+// fp16 weights (GGUF F16, and Q8_0 / Q6_K converted at upload): a chunk is
+// one 16-row tile x 128 K, 4 KB; lane l reads 16 contiguous bytes at
+// 1024 j + 16 l for MFMA j (rows l & 15, K 32 j + 8 (l >> 4) ..).
+constexpr int kF16Chunk = 4096;
+// 16-byte X units (8 halves) per weight chunk: 128 K for Q4_0 and F16, 256 for Q4_K
 template <int TYPE>
-constexpr int kUnitsPerChunk = TYPE == ULSPEC_GGML_Q4_0 ? 16 : 32;
+constexpr int kUnitsPerChunk = TYPE == ULSPEC_GGML_Q4_K ? 32 : 16;
 
 __device__ __forceinline__ uint32_t perm_nibbles(const uint32_t q[8])
 {
@@ -108,6 +112,71 @@ __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
             dst[w] = v;
         }
     }
+}
+
+// GGUF rows -> fp16 rows (row r to out row out_row0 + r * out_row_step).
+// Q8_0: d * q; Q6_K: d * scale * q with the 6-bit q of ggml's block_q6_K (ql
+// low nibbles, qh 2-bit pairs, int8 scales per 16 elements, fp16 d last);
+// Q4_0 / Q4_K (only for fused weights whose parts mix types) as in their own
+// kernels.  Evaluated in fp32 and rounded once to fp16 (the only inexact step).
+__global__ void dequant_rows_f16_kernel(const uint8_t* __restrict__ raw, _Float16* __restrict__ out, uint32_t type,
+                                        uint32_t K, uint64_t row_bytes, uint64_t total, uint32_t out_row0,
+                                        uint32_t out_row_step)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    const uint64_t row = i / K;
+    const uint32_t k = (uint32_t)(i - row * K);
+    const uint8_t* r = raw + row * row_bytes;
+    float v;
+    if (type == ULSPEC_GGML_Q4_0) {  // (q - 8) * d
+        const uint8_t* blk = r + (uint64_t)(k / 32) * 18;
+        const uint32_t j = k % 32, q = j < 16 ? (blk[2 + j] & 15u) : (blk[2 + j - 16] >> 4);
+        v = (float)((int)q - 8) * half_bits_to_float(blk[0] | (blk[1] << 8));
+    } else if (type == ULSPEC_GGML_Q4_K) {  // (d * sc) * q - dmin * m
+        const uint8_t* blk = r + (uint64_t)(k / 256) * 144;
+        const uint32_t e = k % 256, c = e / 64, l = e % 64, sb = 2 * c + (l >= 32);
+        const uint8_t* sx = blk + 4;
+        const uint32_t sc = sb < 4 ? (sx[sb] & 63u) : ((sx[sb + 4] & 15u) | ((sx[sb - 4] >> 6) << 4));
+        const uint32_t mn = sb < 4 ? (sx[sb + 4] & 63u) : ((sx[sb + 4] >> 4) | ((sx[sb] >> 6) << 4));
+        const uint8_t byte = blk[16 + 32 * c + l % 32];
+        const uint32_t q = l < 32 ? (byte & 15u) : (byte >> 4);
+        v = (half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)sc) * (float)q -
+            half_bits_to_float(blk[2] | (blk[3] << 8)) * (float)mn;
+    } else if (type == ULSPEC_GGML_F16) {
+        v = (float)((const _Float16*)r)[k];
+    } else if (type == ULSPEC_GGML_Q8_0) {
+        const uint8_t* blk = r + (uint64_t)(k / 32) * 34;
+        v = half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)(int8_t)blk[2 + k % 32];
+    } else {  // Q6_K
+        const uint8_t* blk = r + (uint64_t)(k / 256) * 210;
+        const uint32_t e = k % 256, h = e / 128, p = e % 128, quarter = p / 32, l = p % 32;
+        const uint8_t lo = blk[64 * h + l + (quarter & 1 ? 32 : 0)];
+        const uint32_t nib = quarter < 2 ? (lo & 15u) : (lo >> 4);
+        const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+        const int q = (int)(nib | (hb << 4)) - 32;
+        const int sc = (int8_t)blk[192 + 8 * h + l / 16 + 2 * quarter];
+        v = half_bits_to_float(blk[208] | (blk[209] << 8)) * (float)sc * (float)q;
+    }
+    out[((uint64_t)out_row0 + row * out_row_step) * K + k] = (_Float16)v;
+}
+
+// fp16 rows [N][K] -> kF16Chunk tiles; one 16-byte lane slot per thread,
+// zero past N or K.
+__global__ void repack_f16_kernel(const _Float16* __restrict__ src, uint8_t* __restrict__ out, uint32_t N,
+                                  uint32_t K, uint32_t n_chunks, uint64_t total)
+{
+    const uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const uint32_t l = (uint32_t)(id & 63), j = (uint32_t)((id >> 6) & 3);
+    const uint64_t tc = id >> 8;  // t * n_chunks + c
+    const uint32_t c = (uint32_t)(tc % n_chunks), t = (uint32_t)(tc / n_chunks);
+    const uint32_t n = 16 * t + (l & 15), k0 = 128 * c + 32 * j + 8 * (l >> 4);
+    half8_t v = {};
+    if (n < N)
+        for (int e = 0; e < 8; ++e)
+            if (k0 + e < K) v[e] = src[(uint64_t)n * K + k0 + e];
+    *(half8_t*)(out + tc * kF16Chunk + j * 1024 + l * 16) = v;
 }
 
 // Compiler-only barrier: loads issued before it stay before it (they are not
@@ -870,6 +939,37 @@ struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
     uint4 w0[CMAX], w1[CMAX], hd[CMAX];
 };
 
+template <int CMAX>
+struct WBatch<ULSPEC_GGML_F16, CMAX> {
+    static constexpr int kLoads = 4 * CMAX;
+    uint4 w[CMAX][4];
+};
+
+template <int CMAX>
+__device__ __forceinline__ void f16_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, int c0, int nc,
+                                               uint4 (&w)[CMAX][4])
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[i][j] = buf_load16(wr, i < nc ? w_lane + (uint32_t)(c0 + i) * kF16Chunk + 1024u * j : kOOB);
+}
+
+// acc += the batch's chunks: four MFMAs of 32 K per chunk, no dequantization
+template <int CMAX>
+__device__ __forceinline__ void f16_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&w)[CMAX][4],
+                                              float4_t& acc)
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i)
+        if (i < nc)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = mfma16x16x32(__builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]),
+                                   __builtin_bit_cast(half8_t, w[i][j]), acc);
+}
+
 template <int TYPE, int CMAX>
 __device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, int t, int c0, int nc,
                                             WBatch<TYPE, CMAX>& b)
@@ -877,7 +977,9 @@ __device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_r
     const int lane = threadIdx.x & 63, r = lane & 15;
     if (t >= a.n_tiles) nc = 0;
     const uint32_t tile = (uint32_t)(t < a.n_tiles ? t : 0) * a.n_chunks;
-    if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+    if constexpr (TYPE == ULSPEC_GGML_F16)
+        f16_load_batch<CMAX>(wr, tile * kF16Chunk + lane * 16, c0, nc, b.w);
+    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
         q4_0_load_batch<CMAX>(wr, tile * kQ40Chunk + lane * 16, tile * kQ40Chunk + 1024 + r * 8, c0, nc, b.wq, b.sc);
     else
         q4_k_load_batch<CMAX>(wr, tile * kQ4KChunk + lane * 16, tile * kQ4KChunk + 2048 + r * 16, c0, nc, b.w0, b.w1,
@@ -888,7 +990,9 @@ template <int TYPE, int CMAX>
 __device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, int nc, const WBatch<TYPE, CMAX>& b,
                                            const NibbleConsts& nk, float4_t& acc)
 {
-    if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+    if constexpr (TYPE == ULSPEC_GGML_F16)
+        f16_mma_batch<CMAX>(xs, xrow, c0, nc, b.w, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
         q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
     else
         q4_k_mma_batch<CMAX>(xs, xrow, c0, nc, b.w0, b.w1, b.hd, (threadIdx.x & 63) >> 4, nk, acc);
@@ -951,7 +1055,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int n_iter = (a.n_tiles + tpi - 1) / tpi;
     const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_0 ? g : 8 * g);
+    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
     const NibbleConsts nk = nibble_consts();
     const int pos0 = epi_pos0(a);
 
@@ -1060,7 +1164,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_0 ? g : 8 * g);
+    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
@@ -1162,6 +1266,26 @@ template <int... C>
 struct CList {};
 using WideQ40 = CList<1, 2, 3, 4, 6, 8>;
 using WideQ4K = CList<1, 2, 3, 4>;
+using WideF16 = CList<1, 2>;  // 16 VGPRs of weights per chunk
+
+// Per type: the one-tile batch sizes and the pipelined kernel's batch.
+template <int TYPE>
+struct GemmCfg;
+template <>
+struct GemmCfg<ULSPEC_GGML_Q4_0> {
+    using Wide = WideQ40;
+    static constexpr int kStream = kQ40Stream;
+};
+template <>
+struct GemmCfg<ULSPEC_GGML_Q4_K> {
+    using Wide = WideQ4K;
+    static constexpr int kStream = kQ4KStream;
+};
+template <>
+struct GemmCfg<ULSPEC_GGML_F16> {
+    using Wide = WideF16;
+    static constexpr int kStream = 2;
+};
 
 template <int TYPE, int... C>
 void wide_kernels(CList<C...>, std::vector<const void*>& out)
@@ -1204,33 +1328,32 @@ void wide_launch(CList<C...>, int cpp, bool norm, dim3 grid, dim3 block, size_t 
 // Static LDS of the ring kernel: two part-sum buffers and the norm factors.
 constexpr size_t kRingStatic = 2 * kRingWaves * 4 * 64 * sizeof(float) + 512;
 
+template <int TYPE>
+void type_kernels(std::vector<const void*>& fns, std::vector<const void*>& rings)
+{
+    fns.push_back((const void*)gemm_stream_kernel<TYPE, GemmCfg<TYPE>::kStream, kStreamWaves, true, false>);
+    fns.push_back((const void*)gemm_stream_kernel<TYPE, GemmCfg<TYPE>::kStream, kStreamWaves, true, true>);
+    wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, fns);
+    fns.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves, false, false>);
+    fns.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves, false, true>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, false>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, true>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, false>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, true>);
+}
+
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
+    std::vector<const void*> fns, rings;
+    type_kernels<ULSPEC_GGML_Q4_0>(fns, rings);
+    type_kernels<ULSPEC_GGML_Q4_K>(fns, rings);
+    type_kernels<ULSPEC_GGML_F16>(fns, rings);
     const int dyn = (int)(kWideLdsMax - kStreamStatic);
-    std::vector<const void*> fns = {
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, false>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, true>,
-        (const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, true>,
-    };
-    wide_kernels<ULSPEC_GGML_Q4_0>(WideQ40{}, fns);
-    wide_kernels<ULSPEC_GGML_Q4_K>(WideQ4K{}, fns);
-    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, false>);
-    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, true>);
-    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, false>);
-    fns.push_back((const void*)gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, true>);
     for (const void* f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
         if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
     }
     const int dyn_ring = (int)(kWideLdsMax - kRingStatic);
-    const void* rings[] = {
-#define ULSPEC_RING_FN(T, C) (const void*)gemm_ring_kernel<T, C, kRingDepth, kRingWaves, false>, \
-                             (const void*)gemm_ring_kernel<T, C, kRingDepth, kRingWaves, true>,
-        ULSPEC_RING_FN(ULSPEC_GGML_Q4_0, 1) ULSPEC_RING_FN(ULSPEC_GGML_Q4_0, 2)
-        ULSPEC_RING_FN(ULSPEC_GGML_Q4_K, 1) ULSPEC_RING_FN(ULSPEC_GGML_Q4_K, 2)
-#undef ULSPEC_RING_FN
-    };
     for (const void* f : rings) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn_ring);
         if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
@@ -1238,18 +1361,21 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
     return ULSPEC_OK;
 }
 
-// Launch the whole-X kernel.  More tiles than CUs and at most two chunks per
+// Launch the whole-X kernel.  1-2 tiles per CU and at most 8 chunks per row:
+// the 8-wave one-tile kernel.  More tiles than CUs and at most two chunks per
 // part: the ring kernel, one 16-wave workgroup per CU, P parts per tile (the
 // largest power of two <= min(16, chunks per row), P >= 4), 16 / P tiles per
 // iteration.  Otherwise the older pipelined 8-wave kernel for more tiles than
 // CUs, else one 16-wave workgroup per tile with 16 parts (waves with an empty
 // part idle).
-void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
+template <int TYPE>
+void stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     const int n_cu = std::max(1, ctx->n_cu);
     const bool pipe = (int)w.n_tiles > n_cu;
     const size_t lds = (size_t)a.M * wide_pitch(w.k);
-    const bool q40 = w.type == ULSPEC_GGML_Q4_0, norm = a.f.pro == kProNorm;
+    const bool norm = a.f.pro == kProNorm;
+    hipStream_t st = ctx->stream;
     auto split = [&](int P) {
         a.ks_count = P;
         a.ks_q = (int)(w.n_chunks / P);
@@ -1258,13 +1384,8 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
     if (pipe && w.n_chunks <= (uint32_t)kSmallWaves && (int)w.n_tiles <= kSmallTilesPerCu * n_cu) {
         split(kSmallWaves);  // one chunk (or none) per wave
         const dim3 grid(w.n_tiles), block(kSmallWaves * 64);
-        if (q40) {
-            if (norm) hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, true>), grid, block, lds, ctx->stream, a);
-            else hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_0, 1, kSmallWaves, false, false>), grid, block, lds, ctx->stream, a);
-        } else {
-            if (norm) hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, true>), grid, block, lds, ctx->stream, a);
-            else hipLaunchKernelGGL((gemm_stream_kernel<ULSPEC_GGML_Q4_K, 1, kSmallWaves, false, false>), grid, block, lds, ctx->stream, a);
-        }
+        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves, false, true>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves, false, false>), grid, block, lds, st, a);
         return;
     }
     if (pipe) {
@@ -1275,16 +1396,13 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
             split(P);
             const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
             const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
-#define ULSPEC_RING(T, C)                                                                                               \
-    do {                                                                                                                \
-        if (norm) hipLaunchKernelGGL((gemm_ring_kernel<T, C, kRingDepth, kRingWaves, true>), grid, block, lds, ctx->stream, a); \
-        else hipLaunchKernelGGL((gemm_ring_kernel<T, C, kRingDepth, kRingWaves, false>), grid, block, lds, ctx->stream, a);     \
-    } while (0)
-            if (q40 && cpp <= 1) ULSPEC_RING(ULSPEC_GGML_Q4_0, 1);
-            else if (q40) ULSPEC_RING(ULSPEC_GGML_Q4_0, 2);
-            else if (cpp <= 1) ULSPEC_RING(ULSPEC_GGML_Q4_K, 1);
-            else ULSPEC_RING(ULSPEC_GGML_Q4_K, 2);
-#undef ULSPEC_RING
+            if (cpp <= 1) {
+                if (norm) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, true>), grid, block, lds, st, a);
+                else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, false>), grid, block, lds, st, a);
+            } else {
+                if (norm) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, true>), grid, block, lds, st, a);
+                else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, false>), grid, block, lds, st, a);
+            }
             return;
         }
     }
@@ -1294,22 +1412,21 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
     split(P);
     const int n_iter = ((int)w.n_tiles + (pipe ? kStreamWaves / P : 1) - 1) / (pipe ? kStreamWaves / P : 1);
     const dim3 grid(pipe ? std::min(n_iter, n_cu) : n_iter), block((pipe ? kStreamWaves : kWideWaves) * 64);
-#define ULSPEC_STREAM(T, C, W, PI, NO) \
-    hipLaunchKernelGGL((gemm_stream_kernel<T, C, W, PI, NO>), grid, block, lds, ctx->stream, a)
     if (pipe) {
-        if (q40) {
-            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, true);
-            else ULSPEC_STREAM(ULSPEC_GGML_Q4_0, kQ40Stream, kStreamWaves, true, false);
-        } else {
-            if (norm) ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, true);
-            else ULSPEC_STREAM(ULSPEC_GGML_Q4_K, kQ4KStream, kStreamWaves, true, false);
-        }
+        constexpr int CS = GemmCfg<TYPE>::kStream;
+        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CS, kStreamWaves, true, true>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CS, kStreamWaves, true, false>), grid, block, lds, st, a);
     } else {
         const int cpp = a.ks_q + (a.ks_r ? 1 : 0);
-        if (q40) wide_launch<ULSPEC_GGML_Q4_0>(WideQ40{}, cpp, norm, grid, block, lds, ctx->stream, a);
-        else wide_launch<ULSPEC_GGML_Q4_K>(WideQ4K{}, cpp, norm, grid, block, lds, ctx->stream, a);
+        wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, cpp, norm, grid, block, lds, st, a);
     }
-#undef ULSPEC_STREAM
+}
+
+void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
+{
+    if (w.type == ULSPEC_GGML_Q4_0) stream_launch_t<ULSPEC_GGML_Q4_0>(ctx, w, a);
+    else if (w.type == ULSPEC_GGML_Q4_K) stream_launch_t<ULSPEC_GGML_Q4_K>(ctx, w, a);
+    else stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
 }
 
 // K slices per weight: about one workgroup per CU in total.
@@ -1335,8 +1452,12 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
     const _Float16* X = reinterpret_cast<const _Float16*>(x);
     if (gemm_workspace_bytes(w) > ctx->ws_bytes)
         return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
-    for (uint32_t m0 = 0; m0 < M; m0 += 64) {
-        const int mc = (int)std::min<uint32_t>(64, M - m0);
+    // fp16 weights have no split-K kernel: rows go in groups that fit in LDS
+    uint32_t group = 64;
+    if (w.type == ULSPEC_GGML_F16)
+        while (group > 1 && !wide_fits((int)group, w.k)) --group;
+    for (uint32_t m0 = 0; m0 < M; m0 += group) {
+        const int mc = (int)std::min<uint32_t>(group, M - m0);
         GemmArgs a;
         a.w = w.dev;
         a.w_bytes = (uint32_t)w.bytes;
@@ -1396,31 +1517,57 @@ ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, co
 
 namespace ulspec {
 
+// Rows of GGUF blocks (device memory) to fp16 rows out[out_row0 + r * step]
+// (asynchronous on the context stream).
+ulspec_status rows_to_f16(ulspec_ctx* ctx, uint32_t type, const void* raw, uint32_t rows, uint32_t K,
+                          _Float16* out, uint32_t out_row0, uint32_t out_row_step)
+{
+    const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
+    const bool ok = type == ULSPEC_GGML_Q4_0 || type == ULSPEC_GGML_Q4_K || type == ULSPEC_GGML_F16 ||
+                    type == ULSPEC_GGML_Q8_0 || type == ULSPEC_GGML_Q6_K;
+    if (!ok || bs <= 0 || K % bs) return fail(ctx, ULSPEC_EUNSUPPORTED, "rows_to_f16: type %u, K=%u", type, K);
+    const uint64_t elems = (uint64_t)rows * K;
+    hipLaunchKernelGGL(dequant_rows_f16_kernel, dim3((unsigned)((elems + 255) / 256)), dim3(256), 0, ctx->stream,
+                       (const uint8_t*)raw, out, type, K, (uint64_t)(K / bs) * ts, elems, out_row0, out_row_step);
+    return check_launch(ctx, "rows_to_f16 launch");
+}
+
 // Re-tile raw GGUF blocks (host or device memory) into a new device weight.
 ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes, uint32_t N, uint32_t K,
                             bool on_device, uint32_t* out_id)
 {
     if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
-    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K)
-        return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported (Q4_0 / Q4_K)", type);
+    const bool f16 = type == ULSPEC_GGML_F16 || type == ULSPEC_GGML_Q8_0 || type == ULSPEC_GGML_Q6_K;
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K && !f16)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported (Q4_0, Q4_K, Q6_K, Q8_0, F16)",
+                    type);
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
-    if (N == 0 || K == 0 || K % bs) return fail(ctx, ULSPEC_EINVAL, "weight_upload: K=%u must be a positive multiple of %d", K, bs);
+    // F16 rows too are taken in multiples of 32 (activation rows stay 64-byte aligned)
+    const int k_mult = std::max(bs, 32);
+    if (N == 0 || K == 0 || K % k_mult)
+        return fail(ctx, ULSPEC_EINVAL, "weight_upload: K=%u must be a positive multiple of %d", K, k_mult);
     const size_t expect = (size_t)N * (K / bs) * ts;
     if (nbytes != expect) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes given, %zu expected", nbytes, expect);
     Weight w;
-    w.type = type;
+    w.type = f16 ? (uint32_t)ULSPEC_GGML_F16 : type;  // Q8_0 / Q6_K are held as fp16
+    w.src_type = type;
     w.n = N;
     w.k = K;
     w.n_tiles = (N + 15) / 16;
-    w.n_chunks = type == ULSPEC_GGML_Q4_0 ? (K / 32 + 3) / 4 : K / 256;
-    w.bytes = (size_t)w.n_tiles * w.n_chunks * (type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
+    w.n_chunks = type == ULSPEC_GGML_Q4_K ? K / 256 : (K + 127) / 128;
+    w.bytes = (size_t)w.n_tiles * w.n_chunks *
+              (f16 ? kF16Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
     if (w.bytes >= kOOB) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes exceeds the 2 GiB per-weight limit", w.bytes);
-    w.ksplit = choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
+    w.ksplit = f16 ? 1 : choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipMalloc(&w.dev, w.bytes);
     if (e != hipSuccess) return hip_fail(ctx, e, "weight_upload hipMalloc");
     void* raw = nullptr;
-    ulspec_status st = workspace(ctx, std::max(on_device ? 0 : nbytes, gemm_workspace_bytes(w)), &raw);
+    // workspace: the host blocks (when not on the device), then for the fp16
+    // formats the fp16 rows
+    const size_t raw_room = on_device ? 0 : (nbytes + 255) / 256 * 256;
+    const size_t need = f16 ? raw_room + (size_t)N * K * 2 : std::max(raw_room, gemm_workspace_bytes(w));
+    ulspec_status st = workspace(ctx, need, &raw);
     if (st != ULSPEC_OK) {
         (void)hipFree(w.dev);
         return st;
@@ -1434,7 +1581,16 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
             return hip_fail(ctx, e, "weight_upload copy");
         }
     }
-    if (type == ULSPEC_GGML_Q4_0) {
+    if (f16) {
+        // to fp16 rows (after the blocks in the workspace), then re-tiled
+        _Float16* half_rows = (_Float16*)((uint8_t*)ctx->ws + raw_room);
+        const uint64_t elems = (uint64_t)N * K;
+        hipLaunchKernelGGL(dequant_rows_f16_kernel, dim3((unsigned)((elems + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const uint8_t*)raw, half_rows, type, K, (uint64_t)(K / bs) * ts, elems, 0u, 1u);
+        const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
+        hipLaunchKernelGGL(repack_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const _Float16*)half_rows, w.dev, N, K, w.n_chunks, total);
+    } else if (type == ULSPEC_GGML_Q4_0) {
         const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
         hipLaunchKernelGGL(repack_q4_0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
                            (const uint8_t*)raw, w.dev, N, K / 32, w.n_chunks, total);
@@ -1472,7 +1628,7 @@ extern "C" ulspec_status ulspec_weight_info(ulspec_ctx* ctx, uint32_t id, uint32
     ULSPEC_CHECK_CTX(ctx);
     if (id >= ctx->weights.size()) return fail(ctx, ULSPEC_EINVAL, "weight_info: no weight %u", id);
     const Weight& w = ctx->weights[id];
-    if (type) *type = w.type;
+    if (type) *type = w.src_type;
     if (n) *n = w.n;
     if (k) *k = w.k;
     if (bytes) *bytes = w.bytes;

@@ -15,10 +15,11 @@ namespace ulspec {
 
 // One uploaded linear weight, re-tiled for the dequant-GEMM kernels.
 struct Weight {
-    uint32_t type = 0;      // ULSPEC_GGML_Q4_0 / ULSPEC_GGML_Q4_K
+    uint32_t type = 0;      // tile format: ULSPEC_GGML_Q4_0 / Q4_K / F16
+    uint32_t src_type = 0;  // the uploaded GGUF type (Q8_0 and Q6_K are held as F16)
     uint32_t n = 0, k = 0;  // rows (N) and elements per row (K)
     uint32_t n_tiles = 0;   // ceil(N / 16)
-    uint32_t n_chunks = 0;  // per tile: Q4_0 block quads, Q4_K super-blocks
+    uint32_t n_chunks = 0;  // per tile: Q4_0 block quads, Q4_K super-blocks, F16 128-element runs
     uint32_t ksplit = 1;    // K slices of the split-K launch (fixed per weight)
     size_t bytes = 0;
     uint8_t* dev = nullptr;
@@ -102,6 +103,9 @@ struct GemmFuse {
 // Kernel launchers shared by the C ABI and the host engine (no validation of
 // device pointers; arguments checked as in the corresponding ABI entry point).
 ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y);
+// Rows of GGUF blocks (device) to fp16 rows out[out_row0 + r * out_row_step][K].
+ulspec_status rows_to_f16(ulspec_ctx* ctx, uint32_t type, const void* raw, uint32_t rows, uint32_t K,
+                          _Float16* out, uint32_t out_row0, uint32_t out_row_step);
 // The whole-X kernel with a fused prologue / epilogue (M rows must fit in LDS).
 ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y);
 bool wide_fits(int M, uint32_t K);
