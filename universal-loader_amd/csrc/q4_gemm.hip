@@ -768,11 +768,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
 // X[m][k] = fp16((v[m][k] * r_m) * w[k]) into the LDS rows, r_m = 1 /
 // sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
 // Two phases so that the weight loads overlap the norm: norm_issue loads the
-// partial sums (rows wave and wave + NW, P <= 256), the norm weights and the
-// first kNormGroup rows of v into registers before the weights' first batch
-// is issued; norm_finish reduces the partials (lane-strided, then an xor
-// tree), then converts float4 column groups tid + 64 NW j (K <= 4096).  Rows
-// past the first group (M > kNormGroup) are loaded in norm_finish.
+// partial sums (rows wave and wave + NW, P <= 256, one 16-byte load per row),
+// the norm weights and the first kNormGroup rows of v into registers before
+// the weights' first batch is issued; norm_finish reduces the partials (four
+// per lane, then an xor tree), then converts float4 column groups
+// tid + 64 NW j (K <= 4096).  Rows past the first group (M > kNormGroup) are
+// loaded in norm_finish.  Rows past M and waves past K issue no loads: an
+// out-of-range buffer load still takes its turn in the texture unit.
 constexpr int kNormGroup = 8;
 constexpr int kNormMaxPartials = 256;
 
@@ -781,7 +783,7 @@ struct NormRegs {
     static constexpr int JN = 4096 / (NW * 64 * 4);  // float4 column groups per thread
     float4 vv[kNormGroup][JN];
     float4 w[JN];
-    float ps[2][kNormMaxPartials / 64];
+    float4 ps[2];
 };
 
 template <int NW>
@@ -789,13 +791,19 @@ __device__ __forceinline__ void norm_rows_load(const GemmArgs& a, __amdgpu_buffe
                                                NormRegs<NW>& n)
 {
     const int K4 = a.K >> 2;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int j = 0; j < NormRegs<NW>::JN; ++j) {
         const int c = (int)threadIdx.x + NW * 64 * j;
+        const bool wave_in = 64 * (wave + NW * j) < K4;  // wave-uniform
 #pragma unroll
-        for (int i = 0; i < kNormGroup; ++i)
-            n.vv[i][j] = __builtin_bit_cast(
-                float4, buf_load16(vr, m0 + i < a.M && c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
+        for (int i = 0; i < kNormGroup; ++i) {
+            // rows past M and waves past K issue no load at all (an out-of-range
+            // buffer load still takes its turn in the texture unit)
+            if (m0 + i < a.M && wave_in)  // else left unset: norm_finish reads rows < M of waves in K
+                n.vv[i][j] = __builtin_bit_cast(
+                    float4, buf_load16(vr, c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
+        }
     }
 }
 
@@ -803,26 +811,27 @@ template <int NW>
 __device__ __forceinline__ void norm_issue(const GemmArgs& a, NormRegs<NW>& n)
 {
     const GemmFuse& f = a.f;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K4 = a.K >> 2;
     const __amdgpu_buffer_rsrc_t pr = make_rsrc(f.pss, (uint32_t)a.M * (uint32_t)f.P * 4u);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(f.norm_w, (uint32_t)a.K * 4u);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
+    // partial sums of rows wave and wave + NW (loads only where the row and
+    // the group of 64 partials exist: the conditions are wave-uniform)
+    // (lane holds partials 4 lane .. 4 lane + 3; those past P belong to the
+    // next row and are dropped in norm_finish)
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int m = wave + NW * i;
-#pragma unroll
-        for (int q = 0; q < kNormMaxPartials / 64; ++q) {
-            const int p = lane + 64 * q;
-            n.ps[i][q] = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(pr, m < a.M && p < f.P ? (uint32_t)(m * f.P + p) * 4u : kOOB,
-                                                            0, 0));
-        }
+        if (m < a.M)  // else left unset: norm_finish uses rows < M only
+            n.ps[i] = __builtin_bit_cast(float4, buf_load16(pr, 4 * lane < f.P ? (uint32_t)(m * f.P + 4 * lane) * 4u
+                                                                               : kOOB));
     }
 #pragma unroll
     for (int j = 0; j < NormRegs<NW>::JN; ++j) {
         const int c = (int)threadIdx.x + NW * 64 * j;
-        n.w[j] = __builtin_bit_cast(float4, buf_load16(wr, c < K4 ? (uint32_t)c * 16u : kOOB));
+        if (64 * (wave + NW * j) < K4)
+            n.w[j] = __builtin_bit_cast(float4, buf_load16(wr, c < K4 ? (uint32_t)c * 16u : kOOB));
     }
     norm_rows_load<NW>(a, vr, 0, n);
 }
@@ -836,12 +845,14 @@ __device__ __forceinline__ void norm_finish(const GemmArgs& a, NormRegs<NW>& n, 
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int m = wave + NW * i;
-        float ss = 0.0f;
-#pragma unroll
-        for (int q = 0; q < kNormMaxPartials / 64; ++q) ss += n.ps[i][q];
+        if (m >= a.M) continue;  // wave-uniform
+        const int p0 = 4 * lane;
+        const float4 v = n.ps[i];
+        float ss = ((p0 < f.P ? v.x : 0.0f) + (p0 + 1 < f.P ? v.y : 0.0f)) +
+                   ((p0 + 2 < f.P ? v.z : 0.0f) + (p0 + 3 < f.P ? v.w : 0.0f));
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (m < a.M && lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
+        if (lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
     }
     lds_barrier();
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
