@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 {
     constexpr int VP = D + 8;  // V tile row pitch in halfs (16 B pad spreads banks)
     __shared__ _Float16 vt[kAttnWaves][16 * VP];
-    __shared__ float red_o[kAttnWaves][D][kMaxQ];
+    __shared__ float red_o[kAttnWaves][kMaxQ][D + 1];  // odd pitch: the MFMA-layout writes spread over banks
     __shared__ float red_m[kAttnWaves][kMaxQ], red_l[kAttnWaves][kMaxQ];
 
     const int h = blockIdx.x, s = blockIdx.y;
@@ -199,16 +199,16 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red_o[wave][16 * dt + 4 * g + r][c] = oacc[dt][r];
+        for (int r = 0; r < 4; ++r) red_o[wave][c][16 * dt + 4 * g + r] = oacc[dt][r];
     if (g == 0) {
         red_m[wave][c] = m;
         red_l[wave][c] = l;
     }
     __syncthreads();
     float* pp = a.part + ((size_t)h * a.splits + s) * a.nq * (D + 2);
-    for (int idx = threadIdx.x; idx < D * kMaxQ; idx += kAttnWaves * 64) {
-        const int d = idx / kMaxQ, qi = idx % kMaxQ;
-        if (qi >= a.nq) continue;
+    // the nq * D outputs only, d fastest (coalesced stores, conflict-free reads)
+    for (int idx = threadIdx.x; idx < a.nq * D; idx += kAttnWaves * 64) {
+        const int qi = idx / D, d = idx - qi * D;
         float M = red_m[0][qi];
 #pragma unroll
         for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red_m[w][qi]);
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 #pragma unroll
         for (int w = 0; w < kAttnWaves; ++w) {
             const float f = exp2_fast(red_m[w][qi] - Mu);
-            o += red_o[w][d][qi] * f;
+            o += red_o[w][qi][d] * f;
             Lw += red_l[w][qi] * f;
         }
         if (a.splits == 1) {
