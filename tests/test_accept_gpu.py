@@ -131,7 +131,9 @@ def test_accept_edge_cases(ctx, ora, pkg, rng):
 
 def test_sample_matches_oracle(ctx, ora, pkg, rng):
     for (T, tk, tp, greedy), V in [((0.8, 40, 0.9, False), 32000), ((1.0, 0, 1.0, False), 32000),
-                                   ((1.0, 0, 1.0, True), 128256), ((0.7, 5, 1.0, False), 7)]:
+                                   ((1.0, 0, 1.0, True), 128256), ((0.7, 5, 1.0, False), 7),
+                                   ((0.8, 0, 1.0, False), 128256), ((0.8, 0, 1.0, False), 1001),
+                                   ((1.0, 0, 1.0, False), 7), ((1.0, 0, 1.0, True), 5), ((1.3, 0, 1.0, False), 16385)]:
         R = 24
         s, so = pkg.sampling(T, top_k=tk, top_p=tp, greedy=greedy), ora.sampling(T, top_k=tk, top_p=tp, greedy=greedy)
         logits = _logits(rng, (R, V), boost=3.0)
@@ -142,6 +144,34 @@ def test_sample_matches_oracle(ctx, ora, pkg, rng):
         assert np.array_equal(got, ora.sample(so, logits, u))
         for b in (bl, bu, bo):
             b.free()
+
+
+def test_sample_full_vocabulary_edges(ctx, ora, pkg, rng):
+    """Rows split over many workgroups: u at 0 and just below 1, rows with one
+    dominant logit (all weight in one token, the rest underflow to 0), a row of
+    equal logits and rows whose mass sits at either end of the vocabulary."""
+    V = 32000
+    s, so = pkg.sampling(0.8), ora.sampling(0.8)
+    logits = _logits(rng, (8, V), boost=3.0)
+    logits[2, :] = -1e4
+    logits[2, 31999] = 50.0
+    logits[3, :] = 0.25
+    logits[4, :] = -1e4
+    logits[4, 0] = 10.0
+    logits[5, :] = -1e4
+    logits[5, 17] = 10.0
+    logits[5, 31990] = 10.0
+    u = ora.uniforms(5, 0, 8)
+    u[0] = 0.0
+    u[1] = np.float32(1.0 - 2 ** -24)
+    u[5] = np.float32(0.5)
+    bl, bu, bo = ctx.upload(logits), ctx.upload(u), ctx.alloc(8 * 4)
+    ctx.sample(s, 8, V, bl, bu, bo)
+    got = ctx.download(bo, np.int32, (8,))
+    assert np.array_equal(got, ora.sample(so, logits, u))
+    assert got[2] == 31999 and got[4] == 0 and got[5] in (17, 31990)
+    for b in (bl, bu, bo):
+        b.free()
 
 
 def test_uniforms_match_oracle(ctx, ora):

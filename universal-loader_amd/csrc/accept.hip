@@ -831,30 +831,176 @@ __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __re
     if (threadIdx.x == 0) out[r] = tok;
 }
 
-// Full-vocabulary (or greedy) draw in one kernel: max / argmax, then the
-// inverse-CDF draw of fixed_e(l - lmax) -- the same draw as row_stats +
-// sample_kernel.
-__global__ __launch_bounds__(kSeqThreads) void sample_full_kernel(const float* __restrict__ logits,
-                                                                  const float* __restrict__ uniforms, uint32_t V,
-                                                                  WarpParams p, int32_t* __restrict__ out)
+// Full-vocabulary (or greedy) draw, each row split over up to kMaxChunks
+// workgroups (one workgroup reading a whole row is bound by what a single CU
+// keeps in flight): chunk maxima; chunk sums of fixed_e(l - lmax) and the last
+// token of nonzero weight; then one workgroup per row takes T = trunc(u * Z),
+// finds the chunk holding T from the chunk sums in chunk order and scans that
+// chunk alone.  Integer weights make this the draw of block_cdf_pick exactly:
+// first j with T < cumsum, else the last j with w > 0.
+constexpr int kChunkThreads = 256;
+constexpr int kMaxChunks = 64;
+
+struct ChunkPart {
+    uint64_t top;  // largest order_key of the chunk
+    uint64_t sum;  // sum of its weights
+    int32_t last;  // last index of nonzero weight, -1 if none
+    int32_t pad;
+};
+
+// Chunks of a row of V elements: G chunks of CG float4 groups (the last one shorter).
+struct ChunkPlan {
+    uint32_t G, CG;
+};
+__host__ __device__ inline ChunkPlan chunk_plan(uint32_t V)
 {
-    __shared__ uint64_t scratch[kSeqThreads / 64];
-    __shared__ int32_t pick;
-    const uint32_t r = blockIdx.x;
+    const uint32_t V4 = (V + 3) / 4;
+    uint32_t G = (V4 + kChunkThreads - 1) / kChunkThreads;
+    G = G < 1 ? 1 : (G > (uint32_t)kMaxChunks ? (uint32_t)kMaxChunks : G);
+    return ChunkPlan{G, (V4 + G - 1) / G};
+}
+
+// Largest order_key of chunk (blockIdx.x) of row (blockIdx.y).
+__global__ __launch_bounds__(kChunkThreads) void chunk_max_kernel(const float* __restrict__ logits, uint32_t V,
+                                                                  ChunkPlan cp, ChunkPart* __restrict__ part)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
     const float* row = logits + (size_t)r * V;
+    const uint32_t q1 = min(V4, (g + 1) * cp.CG);
     uint64_t best = 0;
-    scan_row<kSeqThreads>(row, V, [&](uint32_t i, float l) {
-        const uint64_t o = order_key(float_key(l), i);
-        best = o > best ? o : best;
-    });
-    const uint64_t top = block_max_u64<kSeqThreads>(best, scratch);
-    int32_t tok = (int32_t)(0xffffffffu - (uint32_t)top);
-    if (!p.greedy) {
-        const float lmax = key_float((uint32_t)(top >> 32));
-        tok = block_cdf_pick(V, uniforms[r], [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); }, scratch,
-                             &pick);
+    for (uint32_t q = g * cp.CG + threadIdx.x; q < q1; q += kChunkThreads) {
+        const float4 v = load4(row, V, q);
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * q + c < V) {
+                const uint64_t o = order_key(float_key(e[c]), 4 * q + c);
+                best = o > best ? o : best;
+            }
     }
-    if (threadIdx.x == 0) out[r] = tok;
+    best = block_max_u64<kChunkThreads>(best, scratch);
+    if (threadIdx.x == 0) part[(size_t)r * cp.G + g].top = best;
+}
+
+// The row's largest order_key from its chunk maxima (all threads get it).
+__device__ __forceinline__ uint64_t row_top(const ChunkPart* part, ChunkPlan cp, uint64_t* scratch)
+{
+    uint64_t t = 0;
+    if (threadIdx.x < cp.G) t = part[threadIdx.x].top;
+    return block_max_u64<kChunkThreads>(t, scratch);
+}
+
+// Sum and last nonzero index of the chunk's weights fixed_e(l - lmax).
+__global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(const float* __restrict__ logits, uint32_t V,
+                                                                  ChunkPlan cp, WarpParams p,
+                                                                  ChunkPart* __restrict__ part)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
+    const float* row = logits + (size_t)r * V;
+    ChunkPart* rp = part + (size_t)r * cp.G;
+    const uint32_t q0 = g * cp.CG + threadIdx.x, q1 = min(V4, (g + 1) * cp.CG);
+    // this thread's first group is loaded before the chunk maxima are read
+    const float4 v0 = load4(row, V, min(q0, V4 - 1));
+    const float lmax = key_float((uint32_t)(row_top(rp, cp, scratch) >> 32));
+    uint64_t sum = 0;
+    int32_t last = -1;
+    for (uint32_t q = q0; q < q1; q += kChunkThreads) {
+        const W4 w = fixed_e4(q == q0 ? v0 : load4(row, V, q), lmax, p);
+        const uint64_t e[4] = {w.a, w.b, w.c, w.d};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * q + c < V && e[c]) {
+                sum += e[c];
+                last = (int32_t)(4 * q + c);
+            }
+    }
+    sum = block_sum_u64<kChunkThreads>(sum, scratch);
+    const uint64_t lastp = block_max_u64<kChunkThreads>((uint64_t)(int64_t)(last + 1), scratch);
+    if (threadIdx.x == 0) {
+        rp[g].sum = sum;
+        rp[g].last = (int32_t)lastp - 1;
+    }
+}
+
+// One workgroup per row: the argmax (greedy) or the inverse-CDF draw.
+__global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* __restrict__ logits,
+                                                                   const float* __restrict__ uniforms, uint32_t V,
+                                                                   ChunkPlan cp, WarpParams p,
+                                                                   const ChunkPart* __restrict__ part,
+                                                                   int32_t* __restrict__ out)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    __shared__ int32_t pick;
+    const uint32_t r = blockIdx.x, V4 = (V + 3) / 4;
+    const int tid = threadIdx.x;
+    const ChunkPart* rp = part + (size_t)r * cp.G;
+    const uint64_t top = row_top(rp, cp, scratch);
+    if (p.greedy) {
+        if (tid == 0) out[r] = (int32_t)(0xffffffffu - (uint32_t)top);
+        return;
+    }
+    const float* row = logits + (size_t)r * V;
+    const float lmax = key_float((uint32_t)(top >> 32));
+    // chunk sums in chunk order (G <= 64: the first wave holds them all)
+    uint64_t cs = 0;
+    int32_t cl = -1;
+    if (tid < cp.G) {
+        cs = rp[tid].sum;
+        cl = rp[tid].last;
+    }
+    const uint64_t total = block_sum_u64<kChunkThreads>(cs, scratch);
+    const uint64_t T = (uint64_t)((double)uniforms[r] * (double)total);
+    uint64_t before = 0;
+    const uint64_t ctot = block_exclusive_scan_u64<kChunkThreads>(cs, before, scratch);
+    (void)ctot;
+    // the first chunk with T < before + sum (and sum > 0); G if none
+    const bool hit = tid < (int)cp.G && cs && T >= before && T < before + cs;
+    const uint64_t hitp = block_max_u64<kChunkThreads>(hit ? (uint64_t)(kMaxChunks - tid) : 0, scratch);
+    const uint64_t lastp = block_max_u64<kChunkThreads>((uint64_t)(int64_t)(cl + 1), scratch);
+    if (tid == 0) pick = -1;
+    if (hitp) {  // uniform
+        const uint32_t g = kMaxChunks - (uint32_t)hitp;
+        // the chunk's base: its exclusive prefix
+        __shared__ uint64_t gbase;
+        if (tid == (int)g) gbase = before;
+        __syncthreads();
+        uint64_t base = gbase;
+        const uint32_t q1 = min(V4, (g + 1) * cp.CG);
+        for (uint32_t qb = g * cp.CG; qb < q1; qb += kChunkThreads) {  // uniform
+            const uint32_t q = qb + tid;
+            const W4 w = fixed_e4(load4(row, V, min(q, V4 - 1)), lmax, p);
+            const uint64_t e[4] = {w.a, w.b, w.c, w.d};
+            uint64_t mine = 0;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (q < q1 && 4 * q + c < V) mine += e[c];
+            uint64_t excl = 0;
+            const uint64_t pass = block_exclusive_scan_u64<kChunkThreads>(mine, excl, scratch);
+            excl += base;
+            if (mine && T >= excl && T < excl + mine) {
+                uint64_t c = excl;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (4 * q + k < V) {
+                        c += e[k];
+                        if (T < c) {
+                            pick = (int32_t)(4 * q + k);
+                            break;
+                        }
+                    }
+            }
+            base += pass;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int32_t t = pick;
+        if (t < 0)  // T >= total (rounding): the last token with nonzero weight
+            t = lastp ? (int32_t)lastp - 1 : (int32_t)V - 1;
+        out[r] = t;
+    }
 }
 
 __global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
@@ -895,7 +1041,10 @@ size_t accept_workspace_bytes(uint32_t B, uint32_t k)
     return (size_t)(B * (k + 1) + B * k) * sizeof(RowStat);
 }
 
-size_t sample_workspace_bytes(uint32_t R) { return (size_t)R * sizeof(RowStat); }
+size_t sample_workspace_bytes(uint32_t R)
+{
+    return (size_t)R * std::max(sizeof(RowStat), kMaxChunks * sizeof(ChunkPart));
+}
 
 ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
                             const float* target_logits, const float* draft_logits, const int32_t* draft_tokens,
@@ -982,14 +1131,20 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (st != ULSPEC_OK) return st;
     if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
     if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
-    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
-        hipLaunchKernelGGL(sample_full_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, logits, uniforms, V, p,
-                           out_tokens);
-        return check_launch(ctx, "sample launch");
-    }
     if (!ws) {
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
         if (st != ULSPEC_OK) return st;
+    }
+    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
+        const ChunkPlan cp = chunk_plan(V);
+        ChunkPart* part = (ChunkPart*)ws;
+        hipLaunchKernelGGL(chunk_max_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, logits, V, cp, part);
+        if (!p.greedy)
+            hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, logits, V, cp, p,
+                               part);
+        hipLaunchKernelGGL(chunk_pick_kernel, dim3(R), dim3(kChunkThreads), 0, ctx->stream, logits, uniforms, V, cp,
+                           p, (const ChunkPart*)part, out_tokens);
+        return check_launch(ctx, "sample launch");
     }
     hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws,
                        RowSel{});
