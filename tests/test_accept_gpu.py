@@ -94,6 +94,36 @@ def test_accept_full_vocabulary(ctx, ora, pkg, rng):
         _check(ctx, ora, pkg, s, tl, dl, dt, u)
 
 
+@pytest.mark.parametrize("V,k", [(32000, 16), (1001, 5), (128256, 3), (7, 2)])
+def test_accept_full_vocabulary_edges(ctx, ora, pkg, rng, V, k):
+    """Full vocabulary and greedy, rows split over many workgroups: an
+    all-zero residual (draft row = target row, out-of-range draft token, so the
+    draw falls back to the target row), zero draft mass at the drafted token,
+    a row of equal logits, every draft accepted (bonus draw), u at 0 and just
+    below 1."""
+    B = 5
+    tl = _logits(rng, (B, k + 1, V), boost=2.0)
+    dl = (tl[:, :k] + 0.5 * rng.standard_normal((B, k, V))).astype(np.float32)
+    dl[0] = tl[0, :k]
+    tl[2, 0, :] = 0.75
+    for T, greedy in ((0.8, False), (1.0, True)):
+        s = pkg.sampling(T, greedy=greedy)
+        so = ora.sampling(T, greedy=greedy)
+        dt = _draft_tokens(ora, so, dl, 4)
+        dt[0, 0] = V + 7
+        dl_z = dl.copy()
+        dl_z[1, 0, :] = -60.0
+        dl_z[1, 0, int(dt[1, 0]) % V] = -1000.0
+        dt_all = dt.copy()
+        dt_all[4] = tl[4, :k].argmax(axis=1) if greedy else dt[4]
+        for trial in range(3):
+            u = rng.random((B, k + 1)).astype(np.float32)
+            u[3, :] = 0.0 if trial == 0 else np.float32(1.0 - 2 ** -24)
+            if trial == 2:
+                u[4, :k] = 0.0  # every draft of sequence 4 accepted when its draft mass is positive
+            _check(ctx, ora, pkg, s, tl, dl_z, dt_all, None if greedy else u)
+
+
 def test_accept_edge_cases(ctx, ora, pkg, rng):
     # ties (every logit equal -> exact fallback of the top-k selection),
     # top_k >= V (full), top_k = 1, tiny top_p, k = 1 and k = 16, small V,

@@ -860,13 +860,24 @@ __host__ __device__ inline ChunkPlan chunk_plan(uint32_t V)
     return ChunkPlan{G, (V4 + G - 1) / G};
 }
 
+// Rows of a chunk launch: rows r < na of a, then rows of b.
+struct RowSrc {
+    const float* a;
+    uint32_t na;
+    const float* b;
+    __device__ const float* row(uint32_t r, uint32_t V) const
+    {
+        return r < na ? a + (size_t)r * V : b + (size_t)(r - na) * V;
+    }
+};
+
 // Largest order_key of chunk (blockIdx.x) of row (blockIdx.y).
-__global__ __launch_bounds__(kChunkThreads) void chunk_max_kernel(const float* __restrict__ logits, uint32_t V,
-                                                                  ChunkPlan cp, ChunkPart* __restrict__ part)
+__global__ __launch_bounds__(kChunkThreads) void chunk_max_kernel(RowSrc rs, uint32_t V, ChunkPlan cp,
+                                                                  ChunkPart* __restrict__ part)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
     const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
-    const float* row = logits + (size_t)r * V;
+    const float* row = rs.row(r, V);
     const uint32_t q1 = min(V4, (g + 1) * cp.CG);
     uint64_t best = 0;
     for (uint32_t q = g * cp.CG + threadIdx.x; q < q1; q += kChunkThreads) {
@@ -892,13 +903,12 @@ __device__ __forceinline__ uint64_t row_top(const ChunkPart* part, ChunkPlan cp,
 }
 
 // Sum and last nonzero index of the chunk's weights fixed_e(l - lmax).
-__global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(const float* __restrict__ logits, uint32_t V,
-                                                                  ChunkPlan cp, WarpParams p,
+__global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, WarpParams p,
                                                                   ChunkPart* __restrict__ part)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
     const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
-    const float* row = logits + (size_t)r * V;
+    const float* row = rs.row(r, V);
     ChunkPart* rp = part + (size_t)r * cp.G;
     const uint32_t q0 = g * cp.CG + threadIdx.x, q1 = min(V4, (g + 1) * cp.CG);
     // this thread's first group is loaded before the chunk maxima are read
@@ -924,53 +934,43 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(const float* _
     }
 }
 
-// One workgroup per row: the argmax (greedy) or the inverse-CDF draw.
-__global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* __restrict__ logits,
-                                                                   const float* __restrict__ uniforms, uint32_t V,
-                                                                   ChunkPlan cp, WarpParams p,
-                                                                   const ChunkPart* __restrict__ part,
-                                                                   int32_t* __restrict__ out)
+// Inverse-CDF draw with uniform u over weights w4(q) (float4 group q) whose
+// chunk sums and last nonzero indices are in cparts (the row's G chunks):
+// T = trunc(u * total), the chunk holding T from the sums in chunk order, then
+// a scan of that chunk alone; T >= total (rounding) gives the last index of
+// nonzero weight (V - 1 if none).  All threads of the workgroup call it; the
+// token is valid in thread 0.
+template <typename F4>
+__device__ int32_t chunk_draw(uint32_t V, ChunkPlan cp, float u, F4 w4, const ChunkPart* cparts, uint64_t* scratch)
 {
-    __shared__ uint64_t scratch[kChunkThreads / 64];
     __shared__ int32_t pick;
-    const uint32_t r = blockIdx.x, V4 = (V + 3) / 4;
+    __shared__ uint64_t gbase;
     const int tid = threadIdx.x;
-    const ChunkPart* rp = part + (size_t)r * cp.G;
-    const uint64_t top = row_top(rp, cp, scratch);
-    if (p.greedy) {
-        if (tid == 0) out[r] = (int32_t)(0xffffffffu - (uint32_t)top);
-        return;
-    }
-    const float* row = logits + (size_t)r * V;
-    const float lmax = key_float((uint32_t)(top >> 32));
-    // chunk sums in chunk order (G <= 64: the first wave holds them all)
+    const uint32_t V4 = (V + 3) / 4;
     uint64_t cs = 0;
     int32_t cl = -1;
-    if (tid < cp.G) {
-        cs = rp[tid].sum;
-        cl = rp[tid].last;
+    if (tid < (int)cp.G) {
+        cs = cparts[tid].sum;
+        cl = cparts[tid].last;
     }
     const uint64_t total = block_sum_u64<kChunkThreads>(cs, scratch);
-    const uint64_t T = (uint64_t)((double)uniforms[r] * (double)total);
+    const uint64_t T = (uint64_t)((double)u * (double)total);
     uint64_t before = 0;
-    const uint64_t ctot = block_exclusive_scan_u64<kChunkThreads>(cs, before, scratch);
-    (void)ctot;
-    // the first chunk with T < before + sum (and sum > 0); G if none
+    (void)block_exclusive_scan_u64<kChunkThreads>(cs, before, scratch);
+    // the chunk with before <= T < before + sum (sum > 0): at most one
     const bool hit = tid < (int)cp.G && cs && T >= before && T < before + cs;
     const uint64_t hitp = block_max_u64<kChunkThreads>(hit ? (uint64_t)(kMaxChunks - tid) : 0, scratch);
     const uint64_t lastp = block_max_u64<kChunkThreads>((uint64_t)(int64_t)(cl + 1), scratch);
     if (tid == 0) pick = -1;
     if (hitp) {  // uniform
         const uint32_t g = kMaxChunks - (uint32_t)hitp;
-        // the chunk's base: its exclusive prefix
-        __shared__ uint64_t gbase;
         if (tid == (int)g) gbase = before;
         __syncthreads();
         uint64_t base = gbase;
         const uint32_t q1 = min(V4, (g + 1) * cp.CG);
         for (uint32_t qb = g * cp.CG; qb < q1; qb += kChunkThreads) {  // uniform
             const uint32_t q = qb + tid;
-            const W4 w = fixed_e4(load4(row, V, min(q, V4 - 1)), lmax, p);
+            const W4 w = w4(min(q, V4 - 1));
             const uint64_t e[4] = {w.a, w.b, w.c, w.d};
             uint64_t mine = 0;
 #pragma unroll
@@ -995,12 +995,202 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* 
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        int32_t t = pick;
-        if (t < 0)  // T >= total (rounding): the last token with nonzero weight
-            t = lastp ? (int32_t)lastp - 1 : (int32_t)V - 1;
-        out[r] = t;
+    int32_t t = pick;
+    if (t < 0) t = lastp ? (int32_t)lastp - 1 : (int32_t)V - 1;
+    return t;
+}
+
+// One workgroup per row: the argmax (greedy) or the inverse-CDF draw.
+__global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* __restrict__ logits,
+                                                                   const float* __restrict__ uniforms, uint32_t V,
+                                                                   ChunkPlan cp, WarpParams p,
+                                                                   const ChunkPart* __restrict__ part,
+                                                                   int32_t* __restrict__ out)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t r = blockIdx.x;
+    const ChunkPart* rp = part + (size_t)r * cp.G;
+    const uint64_t top = row_top(rp, cp, scratch);
+    if (p.greedy) {
+        if (threadIdx.x == 0) out[r] = (int32_t)(0xffffffffu - (uint32_t)top);
+        return;
     }
+    const float* row = logits + (size_t)r * V;
+    const float lmax = key_float((uint32_t)(top >> 32));
+    const int32_t t = chunk_draw(V, cp, uniforms[r], [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); },
+                                 rp, scratch);
+    if (threadIdx.x == 0) out[r] = t;
+}
+
+// ---- acceptance, full vocabulary or greedy -------------------------------------
+// Chunk maxima (and sums) of all target rows then all draft rows; a one-wave
+// walk per sequence runs the accept tests of decide_kernel on the row totals
+// and leaves a plan for the final draw; the residual's chunk sums are taken
+// only for a sequence that rejected; then one workgroup per sequence draws.
+enum { kPlanDone = 0, kPlanResidual = 1, kPlanBonus = 2 };
+struct AcceptPlan {
+    int32_t mode, row, sh, pad;
+    uint64_t Zp, Zq;
+    float lpm, lqm;
+};
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Row total and top from the row's chunk parts (one wave, G <= 64).
+__device__ __forceinline__ void row_totals(const ChunkPart* rp, ChunkPlan cp, bool sums, uint64_t& top, uint64_t& Z)
+{
+    const int lane = threadIdx.x;
+    top = wave_max_u64(lane < (int)cp.G ? rp[lane].top : 0);
+    Z = sums ? wave_sum_u64(lane < (int)cp.G ? rp[lane].sum : 0) : 0;
+}
+
+__global__ __launch_bounds__(64) void accept_walk_kernel(const float* __restrict__ tl, const float* __restrict__ dl,
+                                                         const int32_t* __restrict__ draft_tokens,
+                                                         const float* __restrict__ uniforms, uint32_t k, uint32_t V,
+                                                         ChunkPlan cp, WarpParams p,
+                                                         const ChunkPart* __restrict__ part,
+                                                         AcceptPlan* __restrict__ plan, int32_t* __restrict__ out,
+                                                         int32_t* __restrict__ nacc)
+{
+    const uint32_t b = blockIdx.x, B = gridDim.x;
+    const int lane = threadIdx.x;
+    const int32_t* x = draft_tokens + (size_t)b * k;
+    const float* u = p.greedy ? nullptr : uniforms + (size_t)b * (k + 1);
+    int32_t* o = out + (size_t)b * (k + 1);
+    const ChunkPart* tp = part + (size_t)b * (k + 1) * cp.G;
+    const ChunkPart* dp = part + ((size_t)B * (k + 1) + (size_t)b * k) * cp.G;
+    AcceptPlan pl = {};
+    for (uint32_t i = lane; i <= k; i += 64) o[i] = -1;
+    uint32_t i = 0;
+    for (; i < k; ++i) {
+        const int32_t xi = x[i];
+        uint64_t topT, Zp;
+        row_totals(tp + (size_t)i * cp.G, cp, !p.greedy, topT, Zp);
+        if (p.greedy) {
+            const int32_t a = (int32_t)(0xffffffffu - (uint32_t)topT);
+            if (lane == 0) o[i] = a;
+            if (a != xi) break;
+            continue;
+        }
+        uint64_t topQ, Zq;
+        row_totals(dp + (size_t)i * cp.G, cp, true, topQ, Zq);
+        const float lpm = key_float((uint32_t)(topT >> 32)), lqm = key_float((uint32_t)(topQ >> 32));
+        const bool in = xi >= 0 && (uint32_t)xi < V;
+        const uint64_t Px = in ? fixed_e(tl[((size_t)b * (k + 1) + i) * V + xi], lpm, p) : 0;
+        const uint64_t Qx = in ? fixed_e(dl[((size_t)b * k + i) * V + xi], lqm, p) : 0;
+        const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
+        const double rhs = (double)Px * (double)Zq;
+        if (lhs < rhs) {
+            if (lane == 0) o[i] = xi;
+            continue;
+        }
+        pl.mode = kPlanResidual;  // first rejection: draw from max(0, p - q)
+        pl.row = (int32_t)i;
+        pl.sh = 62 - bitlen64(Zp) - bitlen64(Zq);
+        pl.Zp = Zp;
+        pl.Zq = Zq;
+        pl.lpm = lpm;
+        pl.lqm = lqm;
+        break;
+    }
+    if (i == k) {  // every draft accepted: bonus token from the target row k
+        if (p.greedy) {
+            uint64_t topT, Z;
+            row_totals(tp + (size_t)k * cp.G, cp, false, topT, Z);
+            if (lane == 0) o[k] = (int32_t)(0xffffffffu - (uint32_t)topT);
+        } else {
+            pl.mode = kPlanBonus;
+            pl.row = (int32_t)k;
+        }
+    }
+    if (lane == 0) {
+        plan[b] = pl;
+        nacc[b] = (int32_t)i;
+    }
+}
+
+// Chunk sums of the residual max(0, P Zq - Q Zp) (scaled as in decide_kernel)
+// of a sequence that rejected.
+__device__ __forceinline__ W4 residual4(const float* trow, const float* drow, uint32_t V, uint32_t q,
+                                        const AcceptPlan& pl, const WarpParams& p)
+{
+    const W4 a = fixed_e4(load4(trow, V, q), pl.lpm, p), b = fixed_e4(load4(drow, V, q), pl.lqm, p);
+    return W4{residual_weight(a.a, b.a, pl.Zp, pl.Zq, pl.sh), residual_weight(a.b, b.b, pl.Zp, pl.Zq, pl.sh),
+              residual_weight(a.c, b.c, pl.Zp, pl.Zq, pl.sh), residual_weight(a.d, b.d, pl.Zp, pl.Zq, pl.sh)};
+}
+
+__global__ __launch_bounds__(kChunkThreads) void residual_sum_kernel(const float* __restrict__ tl,
+                                                                     const float* __restrict__ dl, uint32_t k,
+                                                                     uint32_t V, ChunkPlan cp, WarpParams p,
+                                                                     const AcceptPlan* __restrict__ plan,
+                                                                     ChunkPart* __restrict__ rpart)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t b = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
+    const AcceptPlan pl = plan[b];
+    if (pl.mode != kPlanResidual) return;  // uniform
+    const float* trow = tl + ((size_t)b * (k + 1) + pl.row) * V;
+    const float* drow = dl + ((size_t)b * k + pl.row) * V;
+    const uint32_t q1 = min(V4, (g + 1) * cp.CG);
+    uint64_t sum = 0;
+    int32_t last = -1;
+    for (uint32_t q = g * cp.CG + threadIdx.x; q < q1; q += kChunkThreads) {
+        const W4 w = residual4(trow, drow, V, q, pl, p);
+        const uint64_t e[4] = {w.a, w.b, w.c, w.d};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * q + c < V && e[c]) {
+                sum += e[c];
+                last = (int32_t)(4 * q + c);
+            }
+    }
+    sum = block_sum_u64<kChunkThreads>(sum, scratch);
+    const uint64_t lastp = block_max_u64<kChunkThreads>((uint64_t)(int64_t)(last + 1), scratch);
+    if (threadIdx.x == 0) {
+        rpart[(size_t)b * cp.G + g].sum = sum;
+        rpart[(size_t)b * cp.G + g].last = (int32_t)lastp - 1;
+    }
+}
+
+// The final draw of each sequence: the residual (or, when it is all zero, the
+// target row of the rejection) with u[k], or the bonus from target row k.
+__global__ __launch_bounds__(kChunkThreads) void accept_pick_kernel(const float* __restrict__ tl,
+                                                                    const float* __restrict__ dl,
+                                                                    const float* __restrict__ uniforms, uint32_t k,
+                                                                    uint32_t V, ChunkPlan cp, WarpParams p,
+                                                                    const ChunkPart* __restrict__ part,
+                                                                    const ChunkPart* __restrict__ rpart,
+                                                                    const AcceptPlan* __restrict__ plan,
+                                                                    int32_t* __restrict__ out)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t b = blockIdx.x;
+    const AcceptPlan pl = plan[b];
+    if (pl.mode == kPlanDone) return;  // uniform
+    const float u = uniforms[(size_t)b * (k + 1) + k];
+    const float* trow = tl + ((size_t)b * (k + 1) + pl.row) * V;
+    const ChunkPart* rp = rpart + (size_t)b * cp.G;
+    uint64_t SR = 0;
+    if (pl.mode == kPlanResidual)
+        SR = block_sum_u64<kChunkThreads>(threadIdx.x < cp.G ? rp[threadIdx.x].sum : 0, scratch);
+    int32_t t;
+    if (SR) {
+        const float* drow = dl + ((size_t)b * k + pl.row) * V;
+        t = chunk_draw(V, cp, u, [&](uint32_t q) { return residual4(trow, drow, V, q, pl, p); }, rp, scratch);
+    } else {  // the bonus, or an all-zero residual: draw from the target row
+        const ChunkPart* tp = part + ((size_t)b * (k + 1) + pl.row) * cp.G;
+        const float lmax = key_float((uint32_t)(row_top(tp, cp, scratch) >> 32));
+        t = chunk_draw(V, cp, u, [&](uint32_t q) { return fixed_e4(load4(trow, V, q), lmax, p); }, tp, scratch);
+    }
+    if (threadIdx.x == 0) out[(size_t)b * (k + 1) + pl.row] = t;
 }
 
 __global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
@@ -1038,7 +1228,9 @@ namespace ulspec {
 
 size_t accept_workspace_bytes(uint32_t B, uint32_t k)
 {
-    return (size_t)(B * (k + 1) + B * k) * sizeof(RowStat);
+    const size_t stats = (size_t)(B * (k + 1) + B * k) * sizeof(RowStat);
+    const size_t chunks = (size_t)(B * (k + 1) + B * k + B) * kMaxChunks * sizeof(ChunkPart) + B * sizeof(AcceptPlan);
+    return std::max(stats, chunks);
 }
 
 size_t sample_workspace_bytes(uint32_t R)
@@ -1063,6 +1255,27 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (!ws) {
         st = workspace(ctx, accept_workspace_bytes(B, k), &ws);
         if (st != ULSPEC_OK) return st;
+    }
+    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
+        const ChunkPlan cp = chunk_plan(V);
+        ChunkPart* part = (ChunkPart*)ws;  // [rows_t + rows_d][G]
+        ChunkPart* rpart = part + (size_t)(rows_t + rows_d) * cp.G;  // [B][G]
+        AcceptPlan* plan = (AcceptPlan*)(rpart + (size_t)B * cp.G);
+        const RowSrc rs{target_logits, rows_t, draft_logits};
+        const dim3 grid(cp.G, rows_t + rows_d), blk(kChunkThreads);
+        hipLaunchKernelGGL(chunk_max_kernel, grid, blk, 0, ctx->stream, rs, V, cp, part);
+        if (!p.greedy) hipLaunchKernelGGL(chunk_sum_kernel, grid, blk, 0, ctx->stream, rs, V, cp, p, part);
+        hipLaunchKernelGGL(accept_walk_kernel, dim3(B), dim3(64), 0, ctx->stream, target_logits, draft_logits,
+                           draft_tokens, uniforms, k, V, cp, p, (const ChunkPart*)part, plan, out_tokens,
+                           out_n_accepted);
+        if (!p.greedy) {
+            hipLaunchKernelGGL(residual_sum_kernel, dim3(cp.G, B), blk, 0, ctx->stream, target_logits, draft_logits, k,
+                               V, cp, p, (const AcceptPlan*)plan, rpart);
+            hipLaunchKernelGGL(accept_pick_kernel, dim3(B), blk, 0, ctx->stream, target_logits, draft_logits, uniforms,
+                               k, V, cp, p, (const ChunkPart*)part, (const ChunkPart*)rpart, (const AcceptPlan*)plan,
+                               out_tokens);
+        }
+        return check_launch(ctx, "accept launch");
     }
     RowStat* stats = (RowStat*)ws;
     hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats,
@@ -1138,9 +1351,10 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (p.greedy || p.top_k == 0 || p.top_k >= V) {
         const ChunkPlan cp = chunk_plan(V);
         ChunkPart* part = (ChunkPart*)ws;
-        hipLaunchKernelGGL(chunk_max_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, logits, V, cp, part);
+        const RowSrc rs{logits, R, nullptr};
+        hipLaunchKernelGGL(chunk_max_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, part);
         if (!p.greedy)
-            hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, logits, V, cp, p,
+            hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, p,
                                part);
         hipLaunchKernelGGL(chunk_pick_kernel, dim3(R), dim3(kChunkThreads), 0, ctx->stream, logits, uniforms, V, cp,
                            p, (const ChunkPart*)part, out_tokens);
