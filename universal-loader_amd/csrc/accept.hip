@@ -192,6 +192,57 @@ __device__ __forceinline__ W4 fixed_e4(float4 l, float lmax, const WarpParams& p
     return W4{fixed_e(l.x, lmax, p), fixed_e(l.y, lmax, p), fixed_e(l.z, lmax, p), fixed_e(l.w, lmax, p)};
 }
 
+// Kept tokens of a row from buf[0..k) (order keys by (logit desc, index asc)):
+// E, Z, the top-p prefix, then the list re-sorted by index into st.  All
+// threads call it; buf holds at least kKMax entries.
+__device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpParams& p, RowStat* st,
+                            uint64_t* keptE, uint32_t& cand_count)
+{
+    const int tid = threadIdx.x;
+    const int NT = blockDim.x;
+    for (uint32_t t = tid; t < k; t += NT) {
+        const uint32_t key = (uint32_t)(buf[t] >> 32);
+        keptE[t] = fixed_e(key_float(key), lmax, p);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint64_t z = 0;
+        for (uint32_t t = 0; t < k; ++t) z += keptE[t];
+        uint32_t nk = k;
+        if (p.top_p < 1.0f) {
+            const double thr = (double)p.top_p * (double)z;
+            uint64_t c = 0;
+            uint32_t t = 0;
+            for (; t < k; ++t) {
+                c += keptE[t];
+                if ((double)c >= thr) {
+                    ++t;
+                    break;
+                }
+            }
+            nk = t;
+            z = c;
+        }
+        st->Z = z;
+        st->nk = (int32_t)nk;
+        cand_count = nk;
+    }
+    __syncthreads();
+    const uint32_t nk = cand_count;
+    // re-sort the kept tokens by index (ascending) and store them
+    for (int t = tid; t < kKMax; t += NT)
+        buf[t] = t < (int)nk ? (((uint64_t)(0xffffffffu - (uint32_t)buf[t])) << 32 | (uint32_t)t) : 0;
+    // buf now: (index << 32 | position), positions index keptE; sort ascending by index
+    for (int t = tid; t < kKMax; t += NT)
+        if (t < (int)nk) buf[t] = ~buf[t];  // descending sort of ~x = ascending of x
+    bitonic_desc(buf, kKMax);
+    for (int t = tid; t < (int)nk; t += NT) {
+        const uint64_t v = ~buf[t];
+        st->idx[t] = (int32_t)(v >> 32);
+        st->E[t] = keptE[(uint32_t)v];
+    }
+}
+
 // ---- row statistics ----------------------------------------------------------
 // Rows a row_stats launch covers: all (n_sel = 0: workgroup r takes row r),
 // or rows row[0 .. n_sel) of every group of n_rows (workgroup g takes row
@@ -306,48 +357,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
             if (i >= (int)k) buf[i] = 0;
         bitonic_desc(buf, kKMax);
     }
-    // buf[0..k) = the kept tokens by (logit desc, index asc)
-    for (uint32_t t = tid; t < k; t += kRowThreads) {
-        const uint32_t key = (uint32_t)(buf[t] >> 32);
-        keptE[t] = fixed_e(key_float(key), lmax, p);
-    }
-    __syncthreads();
-    if (tid == 0) {
-        uint64_t z = 0;
-        for (uint32_t t = 0; t < k; ++t) z += keptE[t];
-        uint32_t nk = k;
-        if (p.top_p < 1.0f) {
-            const double thr = (double)p.top_p * (double)z;
-            uint64_t c = 0;
-            uint32_t t = 0;
-            for (; t < k; ++t) {
-                c += keptE[t];
-                if ((double)c >= thr) {
-                    ++t;
-                    break;
-                }
-            }
-            nk = t;
-            z = c;
-        }
-        st->Z = z;
-        st->nk = (int32_t)nk;
-        cand_count = nk;
-    }
-    __syncthreads();
-    const uint32_t nk = cand_count;
-    // re-sort the kept tokens by index (ascending) and store them
-    for (int t = tid; t < kKMax; t += kRowThreads)
-        buf[t] = t < (int)nk ? (((uint64_t)(0xffffffffu - (uint32_t)buf[t])) << 32 | (uint32_t)t) : 0;
-    // buf now: (index << 32 | position), positions index keptE; sort ascending by index
-    for (int t = tid; t < kKMax; t += kRowThreads)
-        if (t < (int)nk) buf[t] = ~buf[t];  // descending sort of ~x = ascending of x
-    bitonic_desc(buf, kKMax);
-    for (int t = tid; t < (int)nk; t += kRowThreads) {
-        const uint64_t v = ~buf[t];
-        st->idx[t] = (int32_t)(v >> 32);
-        st->E[t] = keptE[(uint32_t)v];
-    }
+    finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
 
 // ---- decisions -----------------------------------------------------------------
@@ -510,6 +520,30 @@ __device__ __forceinline__ uint64_t residual_weight(uint64_t P, uint64_t Q, uint
     return r > 0.0 ? (uint64_t)__builtin_ldexp(r, sh) : 0;
 }
 
+// Kept-list helpers of decide_kernel (top-k mode; all threads call them):
+// copy a row's list into LDS with coalesced loads, and look a token's weight
+// up in one pass instead of a binary search of dependent loads.
+__device__ __forceinline__ int stage_list(const RowStat& st, int32_t* sidx, uint64_t* sE)
+{
+    const int n = st.nk;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+        sidx[t] = st.idx[t];
+        sE[t] = st.E[t];
+    }
+    return n;
+}
+
+__device__ __forceinline__ uint64_t list_weight(const int32_t* sidx, const uint64_t* sE, int n, int32_t x,
+                                                uint64_t* slot)
+{
+    if (threadIdx.x == 0) *slot = 0;
+    __syncthreads();
+    for (int t = threadIdx.x; t < n; t += blockDim.x)
+        if (sidx[t] == x) *slot = sE[t];  // token ids in a list are distinct
+    __syncthreads();
+    return *slot;
+}
+
 __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __restrict__ stats,
                                                              const float* __restrict__ tl,
                                                              const float* __restrict__ dl,
@@ -522,6 +556,9 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
     __shared__ int32_t pick;
     __shared__ int32_t uidx[2 * kKMax];
     __shared__ uint64_t uR[2 * kKMax];
+    __shared__ int32_t aidx[kKMax], bidx[kKMax];  // top-k mode: the position's target / draft lists
+    __shared__ uint64_t aE[kKMax], bE[kKMax];
+    __shared__ uint64_t wslot[2];
     const int tid = threadIdx.x;
     const uint32_t b = blockIdx.x;
     const RowStat* ts = stats + (size_t)b * (k + 1);          // target rows
@@ -547,8 +584,18 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
         const float* trow = tl + ((size_t)b * (k + 1) + i) * V;
         const float* drow = dl + ((size_t)b * k + i) * V;
         const uint64_t Zp = ts[i].Z, Zq = ds[i].Z;
-        const uint64_t Px = weight_of(ts[i], trow, V, topk, xi, p);
-        const uint64_t Qx = weight_of(ds[i], drow, V, topk, xi, p);
+        uint64_t Px, Qx;
+        int na = 0, nb = 0;
+        if (topk) {
+            __syncthreads();  // the previous position's lists are no longer read
+            na = stage_list(ts[i], aidx, aE);
+            nb = stage_list(ds[i], bidx, bE);
+            Px = list_weight(aidx, aE, na, xi, &wslot[0]);
+            Qx = list_weight(bidx, bE, nb, xi, &wslot[1]);
+        } else {
+            Px = weight_of(ts[i], trow, V, false, xi, p);
+            Qx = weight_of(ds[i], drow, V, false, xi, p);
+        }
         const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
         const double rhs = (double)Px * (double)Zq;
         if (lhs < rhs) {
@@ -559,24 +606,22 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
         const int sh = 62 - bitlen64(Zp) - bitlen64(Zq);
         int32_t tok;
         if (topk) {
-            if (tid == 0) {
-                const RowStat& A = ts[i];
-                const RowStat& B = ds[i];
+            if (tid == 0) {  // both lists are in LDS (staged for the weight lookups)
                 int ia = 0, ib = 0, n = 0;
                 uint64_t SR = 0;
-                while (ia < A.nk || ib < B.nk) {
-                    const int32_t ja = ia < A.nk ? A.idx[ia] : 0x7fffffff;
-                    const int32_t jb = ib < B.nk ? B.idx[ib] : 0x7fffffff;
+                while (ia < na || ib < nb) {
+                    const int32_t ja = ia < na ? aidx[ia] : 0x7fffffff;
+                    const int32_t jb = ib < nb ? bidx[ib] : 0x7fffffff;
                     const int32_t j = ja < jb ? ja : jb;
-                    const uint64_t P = ja == j ? A.E[ia++] : 0;
-                    const uint64_t Q = jb == j ? B.E[ib++] : 0;
+                    const uint64_t P = ja == j ? aE[ia++] : 0;
+                    const uint64_t Q = jb == j ? bE[ib++] : 0;
                     const uint64_t R = residual_weight(P, Q, Zp, Zq, sh);
                     uidx[n] = j;
                     uR[n] = R;
                     SR += R;
                     ++n;
                 }
-                pick = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(A.idx, A.E, A.nk, Zp, u[k], V);
+                pick = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(aidx, aE, na, Zp, u[k], V);
             }
             __syncthreads();
             tok = pick;
@@ -618,8 +663,18 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
     }
     // every draft accepted: bonus token from the target row k
     int32_t tok;
-    if (p.greedy) tok = ts[k].argmax;
-    else tok = draw_row(ts[k], tl + ((size_t)b * (k + 1) + k) * V, V, topk, u[k], p, scratch, &pick);
+    if (p.greedy) {
+        tok = ts[k].argmax;
+    } else if (topk) {
+        __syncthreads();
+        const int na = stage_list(ts[k], aidx, aE);
+        __syncthreads();
+        if (tid == 0) pick = list_cdf_pick(aidx, aE, na, ts[k].Z, u[k], V);
+        __syncthreads();
+        tok = pick;
+    } else {
+        tok = draw_row(ts[k], tl + ((size_t)b * (k + 1) + k) * V, V, false, u[k], p, scratch, &pick);
+    }
     if (tid == 0) {
         o[k] = tok;
         nacc[b] = (int32_t)k;
@@ -1192,6 +1247,7 @@ __global__ __launch_bounds__(kChunkThreads) void accept_pick_kernel(const float*
     }
     if (threadIdx.x == 0) out[(size_t)b * (k + 1) + pl.row] = t;
 }
+
 
 __global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
 {
