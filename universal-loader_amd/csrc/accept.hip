@@ -116,13 +116,18 @@ __device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t& excl, uint64_
     return total;
 }
 
-// Bitonic sort of n (power of two) u64 keys in LDS, descending.
+// Bitonic sort of n (power of two) u64 keys in LDS, descending.  Strides of
+// 64 and more exchange through LDS (one barrier each); for each size the
+// strides below 64 pair lanes of one wave (element i on thread i mod NT), so
+// they run in registers with lane shuffles between one LDS read and one write.
 __device__ void bitonic_desc(uint64_t* a, int n)
 {
+    const int NT = blockDim.x, tid = threadIdx.x;
     for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        int stride = size >> 1;
+        for (; stride >= 64; stride >>= 1) {
             __syncthreads();
-            for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            for (int i = tid; i < n; i += NT) {
                 const int j = i ^ stride;
                 if (j > i) {
                     const bool desc = (i & size) == 0;
@@ -133,6 +138,19 @@ __device__ void bitonic_desc(uint64_t* a, int n)
                     }
                 }
             }
+        }
+        __syncthreads();
+        for (int i0 = 0; i0 < n; i0 += NT) {  // uniform
+            const int i = i0 + tid;
+            const bool have = i < n;
+            uint64_t v = have ? a[i] : 0;
+            const bool desc = (i & size) == 0;
+            for (int st = stride; st > 0; st >>= 1) {
+                const uint64_t w = __shfl_xor(v, st);
+                const bool keep_max = ((i & st) == 0) == desc;  // the lower index keeps the larger when descending
+                v = keep_max ? (v > w ? v : w) : (v < w ? v : w);
+            }
+            if (have) a[i] = v;
         }
     }
     __syncthreads();
