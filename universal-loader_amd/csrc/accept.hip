@@ -271,6 +271,52 @@ struct RowSel {
     int32_t row[kTreeMax] = {};
 };
 
+// Exact top k of a row whose candidates overflow kCandMax (heavy ties): the
+// k-th largest key by bisection on counts, then the ties at that key taken by
+// lowest index; buf[0..k) = the kept order keys, sorted.  kRowThreads threads.
+__device__ void topk_tie_fallback(const float* __restrict__ row, uint32_t V, uint32_t k, uint64_t* buf, uint64_t* red,
+                                  uint32_t& cand_count)
+{
+    const int tid = threadIdx.x;
+    // exact fallback for heavily tied rows: k-th largest key by bisection
+    // on counts, then ties at that key taken by lowest index
+    uint32_t lo = 0, hi = 0xffffffffu;
+    while (lo < hi) {
+        const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
+        uint64_t c = 0;
+        for (uint32_t i = tid; i < V; i += kRowThreads) c += float_key(row[i]) >= mid;
+        c = block_sum_u64<kRowThreads>(c, red);
+        if (c >= k) lo = mid;
+        else hi = mid - 1;
+    }
+    const uint32_t kt = lo;
+    if (tid == 0) cand_count = 0;
+    __syncthreads();
+    for (uint32_t i = tid; i < V; i += kRowThreads) {
+        const uint32_t key = float_key(row[i]);
+        if (key > kt) buf[atomicAdd(&cand_count, 1u)] = order_key(key, i);  // < k of them
+    }
+    __syncthreads();
+    const uint32_t ngt = cand_count;
+    const uint32_t need = k - ngt;
+    // ties in index order: thread t owns the contiguous chunk [t*C, (t+1)*C)
+    const uint32_t C = (V + kRowThreads - 1) / kRowThreads;
+    const uint32_t c0 = tid * C, c1 = min(V, c0 + C);
+    uint64_t mine = 0;
+    for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == kt;
+    uint64_t rank = 0;
+    block_exclusive_scan_u64<kRowThreads>(mine, rank, red);
+    for (uint32_t i = c0; i < c1 && rank < need; ++i)
+        if (float_key(row[i]) == kt) {
+            buf[ngt + rank] = order_key(kt, i);
+            ++rank;
+        }
+    __syncthreads();
+    for (int i = tid; i < kKMax; i += kRowThreads)
+        if (i >= (int)k) buf[i] = 0;
+    bitonic_desc(buf, kKMax);
+}
+
 __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __restrict__ logits, uint32_t V,
                                                                 WarpParams p, RowStat* __restrict__ stats,
                                                                 RowSel sel)
@@ -337,43 +383,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
             if (i >= (int)nc) buf[i] = 0;  // sorts last
         bitonic_desc(buf, n2);
     } else {
-        // exact fallback for heavily tied rows: k-th largest key by bisection
-        // on counts, then ties at that key taken by lowest index
-        uint32_t lo = 0, hi = 0xffffffffu;
-        while (lo < hi) {
-            const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
-            uint64_t c = 0;
-            for (uint32_t i = tid; i < V; i += kRowThreads) c += float_key(row[i]) >= mid;
-            c = block_sum_u64<kRowThreads>(c, red);
-            if (c >= k) lo = mid;
-            else hi = mid - 1;
-        }
-        const uint32_t kt = lo;
-        if (tid == 0) cand_count = 0;
-        __syncthreads();
-        for (uint32_t i = tid; i < V; i += kRowThreads) {
-            const uint32_t key = float_key(row[i]);
-            if (key > kt) buf[atomicAdd(&cand_count, 1u)] = order_key(key, i);  // < k of them
-        }
-        __syncthreads();
-        const uint32_t ngt = cand_count;
-        const uint32_t need = k - ngt;
-        // ties in index order: thread t owns the contiguous chunk [t*C, (t+1)*C)
-        const uint32_t C = (V + kRowThreads - 1) / kRowThreads;
-        const uint32_t c0 = tid * C, c1 = min(V, c0 + C);
-        uint64_t mine = 0;
-        for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == kt;
-        uint64_t rank = 0;
-        block_exclusive_scan_u64<kRowThreads>(mine, rank, red);
-        for (uint32_t i = c0; i < c1 && rank < need; ++i)
-            if (float_key(row[i]) == kt) {
-                buf[ngt + rank] = order_key(kt, i);
-                ++rank;
-            }
-        __syncthreads();
-        for (int i = tid; i < kKMax; i += kRowThreads)
-            if (i >= (int)k) buf[i] = 0;
-        bitonic_desc(buf, kKMax);
+        topk_tie_fallback(row, V, k, buf, red, cand_count);
     }
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
@@ -1267,6 +1277,225 @@ __global__ __launch_bounds__(kChunkThreads) void accept_pick_kernel(const float*
 }
 
 
+
+// ---- top-k row statistics over chunk workgroups ---------------------------------
+// As row_stats_kernel (same kept tokens), but the passes over the row run on
+// G chunk workgroups: per-thread maximum keys of every chunk; the k-th
+// largest of those G x 256 maxima (a lower bound of the k-th largest logit,
+// radix-selected in one workgroup per row); the tokens at or above it
+// collected by the chunks; one workgroup per row sorts the candidates (or,
+// past kCandMax of them, runs the exact tie path of row_stats_kernel) and
+// finishes the kept list.
+struct TopkWs {
+    RowStat* stats;   // [rows]
+    ChunkPart* part;  // [rows][G] chunk maxima
+    uint32_t* tm;     // [rows][G][kChunkThreads] per-thread maximum keys
+    uint32_t* t0;     // [rows] candidate threshold
+    uint32_t* cnt;    // [rows][kCntPad] candidates collected (one cache line per row: the atomics of
+                      // different rows do not queue behind each other)
+    uint64_t* cand;   // [rows][kCandMax]
+};
+
+inline size_t topk_align(size_t b) { return (b + 255) / 256 * 256; }
+constexpr uint32_t kCntPad = 32;
+
+inline size_t topk_ws_bytes(uint32_t rows)
+{
+    return topk_align((size_t)rows * sizeof(RowStat)) + topk_align((size_t)rows * kMaxChunks * sizeof(ChunkPart)) +
+           topk_align((size_t)rows * kMaxChunks * kChunkThreads * 4) + topk_align((size_t)rows * 4) +
+           topk_align((size_t)rows * kCntPad * 4) +
+           (size_t)rows * kCandMax * 8;
+}
+
+inline TopkWs topk_ws(void* ws, uint32_t rows)
+{
+    uint8_t* b = (uint8_t*)ws;
+    TopkWs w;
+    w.stats = (RowStat*)b;
+    b += topk_align((size_t)rows * sizeof(RowStat));
+    w.part = (ChunkPart*)b;
+    b += topk_align((size_t)rows * kMaxChunks * sizeof(ChunkPart));
+    w.tm = (uint32_t*)b;
+    b += topk_align((size_t)rows * kMaxChunks * kChunkThreads * 4);
+    w.t0 = (uint32_t*)b;
+    b += topk_align((size_t)rows * 4);
+    w.cnt = (uint32_t*)b;
+    b += topk_align((size_t)rows * kCntPad * 4);
+    w.cand = (uint64_t*)b;
+    return w;
+}
+
+__global__ __launch_bounds__(kChunkThreads) void topk_scan_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, TopkWs w)
+{
+    __shared__ uint64_t scratch[kChunkThreads / 64];
+    const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
+    const float* row = rs.row(r, V);
+    const uint32_t q1 = min(V4, (g + 1) * cp.CG);
+    uint64_t best = 0;  // order key: the thread's largest key, lowest index among equals
+    for (uint32_t q = g * cp.CG + threadIdx.x; q < q1; q += kChunkThreads) {
+        const float4 v = load4(row, V, q);
+        const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (4 * q + c < V) {
+                const uint64_t o = order_key(float_key(e[c]), 4 * q + c);
+                best = o > best ? o : best;
+            }
+    }
+    w.tm[((size_t)r * cp.G + g) * kChunkThreads + threadIdx.x] = (uint32_t)(best >> 32);  // 0: no token
+    best = block_max_u64<kChunkThreads>(best, scratch);
+    if (threadIdx.x == 0) w.part[(size_t)r * cp.G + g].top = best;
+}
+
+// k-th largest of the row's G x 256 per-thread maxima by an 8-bit radix
+// select (four histogram rounds); the row's max / argmax from the chunk maxima.
+__global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan cp, uint32_t k, TopkWs w)
+{
+    constexpr int E = kMaxChunks * kChunkThreads / kRowThreads;  // values per thread
+    constexpr int NWV = kRowThreads / 64 * 4;
+    __shared__ uint32_t whist[NWV][256];  // per (wave, lane & 3) histograms: most values share their top bytes
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sel_bucket, sel_k;
+    __shared__ uint64_t scratch[kRowThreads / 64];
+    const uint32_t r = blockIdx.x, n = cp.G * kChunkThreads;
+    const int tid = threadIdx.x;
+    const uint32_t* tm = w.tm + (size_t)r * cp.G * kChunkThreads;
+    uint32_t v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {  // unconditional loads (clamped index), then masked: all in flight together
+        const uint32_t i = tid + kRowThreads * e;
+        v[e] = tm[min(i, n - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (tid + kRowThreads * e >= n) v[e] = 0u;
+    uint32_t prefix = 0, mask = 0, kk = k;
+    const int wv = (tid >> 6) * 4 + (tid & 3);
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < NWV * 256; b += kRowThreads) (&whist[0][0])[b] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e)
+            if (tid + kRowThreads * e < n && (v[e] & mask) == prefix) atomicAdd(&whist[wv][(v[e] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t t = 0;
+#pragma unroll
+            for (int w2 = 0; w2 < NWV; ++w2) t += whist[w2][tid];
+            hist[tid] = t;
+        }
+        __syncthreads();
+        if (tid < 64) {  // the bucket holding the kk-th largest: lane l holds buckets 4l .. 4l+3
+            const uint32_t h0 = hist[4 * tid], h1 = hist[4 * tid + 1], h2 = hist[4 * tid + 2], h3 = hist[4 * tid + 3];
+            const uint32_t sl = h0 + h1 + h2 + h3;
+            uint32_t suf = sl;  // sum over buckets >= 4l
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t t = __shfl_down(suf, o);
+                if (tid + o < 64) suf += t;
+            }
+            const uint32_t above = suf - sl;
+            if (above < kk && suf >= kk) {
+                uint32_t c = above, b;
+                if (c + h3 >= kk) {
+                    b = 4 * tid + 3;
+                } else if ((c += h3) + h2 >= kk) {
+                    b = 4 * tid + 2;
+                } else if ((c += h2) + h1 >= kk) {
+                    b = 4 * tid + 1;
+                } else {
+                    c += h1;
+                    b = 4 * tid;
+                }
+                sel_bucket = b;
+                sel_k = kk - c;
+            }
+        }
+        __syncthreads();
+        prefix |= sel_bucket << shift;
+        mask |= 255u << shift;
+        kk = sel_k;
+        __syncthreads();
+    }
+    const uint64_t top = block_max_u64<kRowThreads>(tid < (int)cp.G ? w.part[(size_t)r * cp.G + tid].top : 0, scratch);
+    if (tid == 0) {
+        RowStat* st = w.stats + r;
+        st->lmax = key_float((uint32_t)(top >> 32));
+        st->argmax = (int32_t)(0xffffffffu - (uint32_t)top);
+        w.t0[r] = prefix;
+        w.cnt[(size_t)r * kCntPad] = 0;
+    }
+}
+
+__global__ __launch_bounds__(kChunkThreads) void topk_collect_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, TopkWs w)
+{
+    const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
+    const float* row = rs.row(r, V);
+    const uint32_t thr = w.t0[r], q1 = min(V4, (g + 1) * cp.CG);
+    const int lane = threadIdx.x & 63;
+    for (uint32_t qb = g * cp.CG; qb < q1; qb += kChunkThreads) {  // uniform
+        const uint32_t q = qb + threadIdx.x;
+        const float4 v = load4(row, V, min(q, V4 - 1));
+        const float e[4] = {v.x, v.y, v.z, v.w};
+        uint32_t key[4], n = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            key[c] = float_key(e[c]);
+            n += q < q1 && 4 * q + c < V && key[c] >= thr;
+        }
+        // one slot reservation per wave: exclusive prefix of the lanes' counts
+        uint32_t incl = n;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        const uint32_t total = __shfl(incl, 63);
+        uint32_t base = 0;
+        if (lane == 0 && total) base = atomicAdd(&w.cnt[(size_t)r * kCntPad], total);
+        base = __shfl(base, 0);
+        uint32_t slot = base + incl - n;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q < q1 && 4 * q + c < V && key[c] >= thr) {
+                if (slot < (uint32_t)kCandMax) w.cand[(size_t)r * kCandMax + slot] = order_key(key[c], 4 * q + c);
+                ++slot;
+            }
+    }
+}
+
+__global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uint32_t V, WarpParams p, TopkWs w)
+{
+    __shared__ uint64_t red[kRowThreads / 64];
+    __shared__ uint64_t buf[kCandMax];
+    __shared__ uint32_t cand_count;
+    __shared__ uint64_t keptE[kKMax];
+    const uint32_t r = blockIdx.x, k = p.top_k;
+    RowStat* st = w.stats + r;
+    const uint32_t nc = w.cnt[(size_t)r * kCntPad];
+    const float lmax = st->lmax;
+    if (nc <= (uint32_t)kCandMax) {
+        int n2 = 1;
+        while (n2 < (int)nc) n2 <<= 1;
+        const uint64_t* c = w.cand + (size_t)r * kCandMax;
+        for (int i = threadIdx.x; i < n2; i += kRowThreads) buf[i] = i < (int)nc ? c[i] : 0;
+        bitonic_desc(buf, n2);
+    } else {
+        topk_tie_fallback(rs.row(r, V), V, k, buf, red, cand_count);
+    }
+    finish_topk(buf, k, lmax, p, st, keptE, cand_count);
+}
+
+void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w)
+{
+    const ChunkPlan cp = chunk_plan(V);
+    const dim3 grid(cp.G, rows), blk(kChunkThreads);
+    hipLaunchKernelGGL(topk_scan_kernel, grid, blk, 0, s, rs, V, cp, w);
+    hipLaunchKernelGGL(topk_threshold_kernel, dim3(rows), dim3(kRowThreads), 0, s, cp, p.top_k, w);
+    hipLaunchKernelGGL(topk_collect_kernel, grid, blk, 0, s, rs, V, cp, w);
+    hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kRowThreads), 0, s, rs, V, p, w);
+}
+
 __global__ void uniforms_kernel(uint64_t seed, uint64_t idx0, uint32_t n, float* __restrict__ out)
 {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
@@ -1302,14 +1531,14 @@ namespace ulspec {
 
 size_t accept_workspace_bytes(uint32_t B, uint32_t k)
 {
-    const size_t stats = (size_t)(B * (k + 1) + B * k) * sizeof(RowStat);
+    const size_t stats = topk_ws_bytes(B * (k + 1) + B * k);
     const size_t chunks = (size_t)(B * (k + 1) + B * k + B) * kMaxChunks * sizeof(ChunkPart) + B * sizeof(AcceptPlan);
     return std::max(stats, chunks);
 }
 
 size_t sample_workspace_bytes(uint32_t R)
 {
-    return (size_t)R * std::max(sizeof(RowStat), kMaxChunks * sizeof(ChunkPart));
+    return std::max((size_t)R * kMaxChunks * sizeof(ChunkPart), topk_ws_bytes(R));
 }
 
 ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
@@ -1351,12 +1580,9 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         }
         return check_launch(ctx, "accept launch");
     }
-    RowStat* stats = (RowStat*)ws;
-    hipLaunchKernelGGL(row_stats_kernel, dim3(rows_t), dim3(kRowThreads), 0, ctx->stream, target_logits, V, p, stats,
-                       RowSel{});
-    if (rows_d)
-        hipLaunchKernelGGL(row_stats_kernel, dim3(rows_d), dim3(kRowThreads), 0, ctx->stream, draft_logits, V, p,
-                           stats + (size_t)B * (k + 1), RowSel{});
+    const TopkWs tw = topk_ws(ws, rows_t + rows_d);
+    RowStat* stats = tw.stats;
+    launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw);
     hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, stats, target_logits, draft_logits,
                        draft_tokens, uniforms, k, V, p, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
@@ -1434,9 +1660,9 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
                            p, (const ChunkPart*)part, out_tokens);
         return check_launch(ctx, "sample launch");
     }
-    hipLaunchKernelGGL(row_stats_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, logits, V, p, (RowStat*)ws,
-                       RowSel{});
-    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)ws, logits,
+    const TopkWs tw = topk_ws(ws, R);
+    launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw);
+    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, logits,
                        uniforms, V, p, out_tokens);
     return check_launch(ctx, "sample launch");
 }
