@@ -572,19 +572,18 @@ __device__ __forceinline__ uint64_t list_weight(const int32_t* sidx, const uint6
     return *slot;
 }
 
+// Top-k / top-p acceptance of one sequence per workgroup (greedy and
+// full-vocabulary acceptance run in the chunk kernels below): the accept walk
+// on the kept lists, then the residual or bonus draw from the lists.
 __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __restrict__ stats,
-                                                             const float* __restrict__ tl,
-                                                             const float* __restrict__ dl,
                                                              const int32_t* __restrict__ draft_tokens,
                                                              const float* __restrict__ uniforms, uint32_t k,
-                                                             uint32_t V, WarpParams p, int32_t* __restrict__ out,
+                                                             uint32_t V, int32_t* __restrict__ out,
                                                              int32_t* __restrict__ nacc)
 {
-    __shared__ uint64_t scratch[kSeqThreads / 64];
-    __shared__ int32_t pick;
     __shared__ int32_t uidx[2 * kKMax];
     __shared__ uint64_t uR[2 * kKMax];
-    __shared__ int32_t aidx[kKMax], bidx[kKMax];  // top-k mode: the position's target / draft lists
+    __shared__ int32_t aidx[kKMax], bidx[kKMax];  // the position's target / draft lists
     __shared__ uint64_t aE[kKMax], bE[kKMax];
     __shared__ uint64_t wslot[2];
     const int tid = threadIdx.x;
@@ -592,119 +591,52 @@ __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __re
     const RowStat* ts = stats + (size_t)b * (k + 1);          // target rows
     const RowStat* ds = stats + (size_t)gridDim.x * (k + 1) + (size_t)b * k;  // draft rows
     const int32_t* x = draft_tokens + (size_t)b * k;
-    const float* u = p.greedy ? nullptr : uniforms + (size_t)b * (k + 1);
+    const float* u = uniforms + (size_t)b * (k + 1);
     int32_t* o = out + (size_t)b * (k + 1);
-    const bool topk = p.top_k > 0 && p.top_k < V;
 
     for (uint32_t i = tid; i <= k; i += kSeqThreads) o[i] = -1;
-    __syncthreads();
     for (uint32_t i = 0; i < k; ++i) {
         const int32_t xi = x[i];
-        if (p.greedy) {
-            const int32_t a = ts[i].argmax;
-            if (tid == 0) o[i] = a;
-            if (a != xi) {
-                if (tid == 0) nacc[b] = (int32_t)i;
-                return;
-            }
-            continue;
-        }
-        const float* trow = tl + ((size_t)b * (k + 1) + i) * V;
-        const float* drow = dl + ((size_t)b * k + i) * V;
         const uint64_t Zp = ts[i].Z, Zq = ds[i].Z;
-        uint64_t Px, Qx;
-        int na = 0, nb = 0;
-        if (topk) {
-            __syncthreads();  // the previous position's lists are no longer read
-            na = stage_list(ts[i], aidx, aE);
-            nb = stage_list(ds[i], bidx, bE);
-            Px = list_weight(aidx, aE, na, xi, &wslot[0]);
-            Qx = list_weight(bidx, bE, nb, xi, &wslot[1]);
-        } else {
-            Px = weight_of(ts[i], trow, V, false, xi, p);
-            Qx = weight_of(ds[i], drow, V, false, xi, p);
-        }
+        __syncthreads();  // the previous position's lists are no longer read
+        const int na = stage_list(ts[i], aidx, aE);
+        const int nb = stage_list(ds[i], bidx, bE);
+        const uint64_t Px = list_weight(aidx, aE, na, xi, &wslot[0]);
+        const uint64_t Qx = list_weight(bidx, bE, nb, xi, &wslot[1]);
         const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
         const double rhs = (double)Px * (double)Zq;
         if (lhs < rhs) {
             if (tid == 0) o[i] = xi;
             continue;
         }
-        // first rejection: draw from max(0, p - q) with u[k]
+        // first rejection: draw from max(0, p - q) with u[k] (from p when that is all zero)
         const int sh = 62 - bitlen64(Zp) - bitlen64(Zq);
-        int32_t tok;
-        if (topk) {
-            if (tid == 0) {  // both lists are in LDS (staged for the weight lookups)
-                int ia = 0, ib = 0, n = 0;
-                uint64_t SR = 0;
-                while (ia < na || ib < nb) {
-                    const int32_t ja = ia < na ? aidx[ia] : 0x7fffffff;
-                    const int32_t jb = ib < nb ? bidx[ib] : 0x7fffffff;
-                    const int32_t j = ja < jb ? ja : jb;
-                    const uint64_t P = ja == j ? aE[ia++] : 0;
-                    const uint64_t Q = jb == j ? bE[ib++] : 0;
-                    const uint64_t R = residual_weight(P, Q, Zp, Zq, sh);
-                    uidx[n] = j;
-                    uR[n] = R;
-                    SR += R;
-                    ++n;
-                }
-                pick = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(aidx, aE, na, Zp, u[k], V);
+        if (tid == 0) {  // both lists are in LDS
+            int ia = 0, ib = 0, n = 0;
+            uint64_t SR = 0;
+            while (ia < na || ib < nb) {
+                const int32_t ja = ia < na ? aidx[ia] : 0x7fffffff;
+                const int32_t jb = ib < nb ? bidx[ib] : 0x7fffffff;
+                const int32_t j = ja < jb ? ja : jb;
+                const uint64_t P = ja == j ? aE[ia++] : 0;
+                const uint64_t Q = jb == j ? bE[ib++] : 0;
+                const uint64_t R = residual_weight(P, Q, Zp, Zq, sh);
+                uidx[n] = j;
+                uR[n] = R;
+                SR += R;
+                ++n;
             }
-            __syncthreads();
-            tok = pick;
-        } else {
-            const float lpm = ts[i].lmax, lqm = ds[i].lmax;
-            auto rw = [&](uint32_t q) {
-                const W4 a = fixed_e4(load4(trow, V, q), lpm, p), b = fixed_e4(load4(drow, V, q), lqm, p);
-                return W4{residual_weight(a.a, b.a, Zp, Zq, sh), residual_weight(a.b, b.b, Zp, Zq, sh),
-                          residual_weight(a.c, b.c, Zp, Zq, sh), residual_weight(a.d, b.d, Zp, Zq, sh)};
-            };
-            // total residual first (an all-zero residual draws from p)
-            uint64_t mine = 0;
-            {
-                const uint32_t V4 = (V + 3) / 4;
-                for (uint32_t q0 = tid; q0 < V4; q0 += kRound * kSeqThreads) {
-                    W4 x[kRound];
-#pragma unroll
-                    for (int r = 0; r < kRound; ++r) x[r] = rw(min(q0 + (uint32_t)(r * kSeqThreads), V4 - 1));
-#pragma unroll
-                    for (int r = 0; r < kRound; ++r) {
-                        const uint32_t q = q0 + (uint32_t)(r * kSeqThreads);
-                        const uint64_t e[4] = {x[r].a, x[r].b, x[r].c, x[r].d};
-                        if (q < V4)
-#pragma unroll
-                            for (int c = 0; c < 4; ++c)
-                                if (4 * q + c < V) mine += e[c];
-                    }
-                }
-            }
-            const uint64_t SR = block_sum_u64<kSeqThreads>(mine, scratch);
-            if (SR) tok = block_cdf_pick(V, u[k], rw, scratch, &pick);
-            else tok = draw_row(ts[i], trow, V, false, u[k], p, scratch, &pick);
-        }
-        if (tid == 0) {
-            o[i] = tok;
+            o[i] = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(aidx, aE, na, Zp, u[k], V);
             nacc[b] = (int32_t)i;
         }
         return;
     }
     // every draft accepted: bonus token from the target row k
-    int32_t tok;
-    if (p.greedy) {
-        tok = ts[k].argmax;
-    } else if (topk) {
-        __syncthreads();
-        const int na = stage_list(ts[k], aidx, aE);
-        __syncthreads();
-        if (tid == 0) pick = list_cdf_pick(aidx, aE, na, ts[k].Z, u[k], V);
-        __syncthreads();
-        tok = pick;
-    } else {
-        tok = draw_row(ts[k], tl + ((size_t)b * (k + 1) + k) * V, V, false, u[k], p, scratch, &pick);
-    }
+    __syncthreads();
+    const int na = stage_list(ts[k], aidx, aE);
+    __syncthreads();
     if (tid == 0) {
-        o[k] = tok;
+        o[k] = list_cdf_pick(aidx, aE, na, ts[k].Z, u[k], V);
         nacc[b] = (int32_t)k;
     }
 }
@@ -898,20 +830,18 @@ __global__ __launch_bounds__(kSeqThreads) void decide_tree_kernel(const RowStat*
     if (tid == 0) nacc[b] = depth;
 }
 
+// Top-k / top-p draw of one row per workgroup from its kept list (greedy and
+// full-vocabulary draws run in the chunk kernels below).
 __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __restrict__ stats,
-                                                             const float* __restrict__ logits,
                                                              const float* __restrict__ uniforms, uint32_t V,
-                                                             WarpParams p, int32_t* __restrict__ out)
+                                                             int32_t* __restrict__ out)
 {
-    __shared__ uint64_t scratch[kSeqThreads / 64];
-    __shared__ int32_t pick;
+    __shared__ int32_t sidx[kKMax];
+    __shared__ uint64_t sE[kKMax];
     const uint32_t r = blockIdx.x;
-    int32_t tok;
-    if (p.greedy) tok = stats[r].argmax;
-    else
-        tok = draw_row(stats[r], logits + (size_t)r * V, V, p.top_k > 0 && p.top_k < V, uniforms[r], p, scratch,
-                       &pick);
-    if (threadIdx.x == 0) out[r] = tok;
+    const int n = stage_list(stats[r], sidx, sE);
+    __syncthreads();
+    if (threadIdx.x == 0) out[r] = list_cdf_pick(sidx, sE, n, stats[r].Z, uniforms[r], V);
 }
 
 // Full-vocabulary (or greedy) draw, each row split over up to kMaxChunks
@@ -1583,8 +1513,8 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     const TopkWs tw = topk_ws(ws, rows_t + rows_d);
     RowStat* stats = tw.stats;
     launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw);
-    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, stats, target_logits, draft_logits,
-                       draft_tokens, uniforms, k, V, p, out_tokens, out_n_accepted);
+    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)stats, draft_tokens,
+                       uniforms, k, V, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
 }
 
@@ -1662,8 +1592,8 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     }
     const TopkWs tw = topk_ws(ws, R);
     launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw);
-    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, logits,
-                       uniforms, V, p, out_tokens);
+    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, uniforms,
+                       V, out_tokens);
     return check_launch(ctx, "sample launch");
 }
 
