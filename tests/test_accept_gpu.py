@@ -227,4 +227,11 @@ def test_accept_argument_errors(ctx, pkg):
     with pytest.raises(pkg.UlspecError) as e:
         ctx.accept(pkg.sampling(1.0, top_p=0.9), 1, 1, 1000, b, b, b, b, b, b)
     assert e.value.status == pkg.EUNSUPPORTED
+    # rows of one call: B (2k+1) and R at most 65535 (checked before any launch)
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.accept(pkg.sampling(1.0), 5000, 8, 1000, b, b, b, b, b, b)
+    assert e.value.status == pkg.EUNSUPPORTED
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.sample(pkg.sampling(1.0), 70000, 1000, b, b, b)
+    assert e.value.status == pkg.EUNSUPPORTED
     b.free()

@@ -853,6 +853,7 @@ __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __re
 // first j with T < cumsum, else the last j with w > 0.
 constexpr int kChunkThreads = 256;
 constexpr int kMaxChunks = 64;
+constexpr uint32_t kMaxGridRows = 65535;  // rows of a chunk launch run along grid y
 
 struct ChunkPart {
     uint64_t top;  // largest order_key of the chunk
@@ -1485,6 +1486,9 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (!p.greedy && (!draft_logits || !uniforms))
         return fail(ctx, ULSPEC_EINVAL, "accept: sampling needs draft logits and uniforms");
     const uint32_t rows_t = B * (k + 1), rows_d = p.greedy ? 0 : B * k;
+    if ((uint64_t)B * (2 * k + 1) > kMaxGridRows)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "accept: B (2k+1) = %llu logit rows (at most %u per call)",
+                    (unsigned long long)B * (2 * k + 1), kMaxGridRows);
     if (!ws) {
         st = workspace(ctx, accept_workspace_bytes(B, k), &ws);
         if (st != ULSPEC_OK) return st;
@@ -1573,6 +1577,7 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     ulspec_status st = make_params(ctx, s, V, p);
     if (st != ULSPEC_OK) return st;
     if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
+    if (R > kMaxGridRows) return fail(ctx, ULSPEC_EUNSUPPORTED, "sample: R=%u rows (at most %u per call)", R, kMaxGridRows);
     if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
     if (!ws) {
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
