@@ -136,7 +136,8 @@ typedef struct {
  * draw from max(0, p_i - q_i) (renormalised) with u[b][k]; if all k pass, draw
  * the bonus token from p_k with u[b][k].  Greedy: accept while argmax p_i ==
  * x_i and emit the argmax.  out_tokens [B][k+1] holds n_accepted + 1 tokens
- * then -1.  All arrays are device memory.  1 <= k <= 16, top_k <= 256.
+ * then -1.  All arrays are device memory.  1 <= k <= 16, top_k <= 256,
+ * B (2k+1) <= 65535 logit rows per call.
  * Replaces SpeculativeDecoder::verify_speculation and the sampling of
  * InferenceEngine::sample_token (src/inference/speculative_decoder.cpp:89-110,
  * src/inference/inference_engine.cpp:340-367). */
@@ -165,7 +166,8 @@ ulspec_status ulspec_accept_tree(ulspec_ctx* ctx, const ulspec_sampling* s, uint
                                  const int32_t* parent, const float* target_logits, const float* draft_logits,
                                  const int32_t* tokens, const float* uniforms, int32_t* out_tokens,
                                  int32_t* out_path, int32_t* out_n_accepted);
-/* One token per row from warp(logits[r]) with uniforms[r] (greedy: argmax).
+/* One token per row from warp(logits[r]) with uniforms[r] (greedy: argmax);
+ * R <= 65535 rows per call.
  * Replaces InferenceEngine::sample_token (src/inference/inference_engine.cpp:340-367). */
 ulspec_status ulspec_sample(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
                             const float* logits, const float* uniforms, int32_t* out_tokens);
