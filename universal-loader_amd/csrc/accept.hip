@@ -19,11 +19,18 @@
 //   residual R_j = trunc(ldexp(max(0, P_j Zq - Q_j Zp), 62 - bitlen(Zp) -
 //   bitlen(Zq))) in double; draw T = trunc(u * Z), first j with T < cumsum.
 //
-// Two kernels: row_stats (one 1024-thread workgroup per logit row: max and
-// argmax, exact top-k, E, Z, top-p; kept tokens stored sorted by index) and
-// decide (one workgroup per sequence: the accept walk, the residual or bonus
-// draw).  The logits are read from HBM once by row_stats; decide touches them
-// again only in full-vocabulary mode (no top_k), for the drawn row.
+// Every logit row is split over up to 64 chunk workgroups (one workgroup
+// reading a whole row is bound by what a single CU keeps in flight); integer
+// weights make chunked sums and draws equal to a scan of the whole row.
+//   full vocabulary / greedy: chunk maxima, chunk sums of E (and the last
+//   nonzero index), a one-wave accept walk per sequence on the row totals,
+//   the residual's chunk sums for a sequence that rejected, and a final draw
+//   that scans only the chunk holding T;
+//   top-k / top-p: per-chunk thread maxima, a radix-selected lower bound of
+//   the k-th largest logit, candidate collection by the chunks, one
+//   workgroup per row for the candidate sort and the kept list (sorted by
+//   index), then decide (one workgroup per sequence, lists staged in LDS).
+// Tree acceptance keeps one workgroup per row (row_stats) and per tree.
 #include "detmath.h"
 #include "hip_common.h"
 #include "ulspec_internal.h"
