@@ -46,6 +46,8 @@ CASES = [
     (2, 100, 1376, (1, 3, 16, 33)),   # N % 16 != 0, K = 43 blocks (partial quad)
     (12, 40, 512, (2, 64, 65)),       # M > 64 splits into launches
     (2, 32000, 512, (5,)),            # LM-head shape of the small model
+    (12, 11264, 2048, (1, 2, 6)),     # 704 tiles of <= 8 chunks: one-tile kernel, 2.75 tiles per CU
+    (2, 16384, 1024, (1, 5)),         # 1024 tiles of 8 chunks: one-tile kernel, 4 tiles per CU
 ]
 
 

@@ -1312,7 +1312,8 @@ void wide_kernels(CList<C...>, std::vector<const void*>& out)
 // of them).  With more tiles per CU the ring kernel, which normalizes X once
 // per CU instead of once per tile, is faster.
 constexpr int kSmallWaves = 8;
-constexpr int kSmallTilesPerCu = 2;
+constexpr int kSmallTilesPerCu = 4;      // copied X
+constexpr int kSmallTilesPerCuNorm = 2;  // RMSNorm prologue: each workgroup normalises the whole of X
 
 // Launch the one-tile kernel with the smallest batch >= cpp (the largest when none is).
 template <int TYPE, int... C>
@@ -1392,7 +1393,8 @@ void stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
         a.ks_q = (int)(w.n_chunks / P);
         a.ks_r = (int)(w.n_chunks % P);
     };
-    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves && (int)w.n_tiles <= kSmallTilesPerCu * n_cu) {
+    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves &&
+        (int)w.n_tiles <= (norm ? kSmallTilesPerCuNorm : kSmallTilesPerCu) * n_cu) {
         split(kSmallWaves);  // one chunk (or none) per wave
         const dim3 grid(w.n_tiles), block(kSmallWaves * 64);
         if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves, false, true>), grid, block, lds, st, a);
