@@ -113,9 +113,11 @@ class NumpyLlama:
 
 # Tensors re-encoded as the other GGUF types a Q4_K_M file mixes in: Q6_K
 # output and one V projection (so the fused QKV weight mixes types), Q8_0
-# embedding and one up projection, F16 down projection, Q4_0 query.
+# embedding, one up projection (mixed gate/up) and one output projection (a
+# Q8_0 weight of its own), F16 down projection, Q4_0 query.
 MIXED_TYPES = [("output.weight", 14), ("blk.0.attn_v.weight", 14), ("token_embd.weight", 8),
-               ("blk.1.ffn_down.weight", 1), ("blk.0.ffn_up.weight", 8), ("blk.1.attn_q.weight", 2)]
+               ("blk.1.ffn_down.weight", 1), ("blk.0.ffn_up.weight", 8), ("blk.1.attn_q.weight", 2),
+               ("blk.1.attn_output.weight", 8)]
 
 
 def make_mixed_tensors(ora, cfg, seed, std=0.02, norm_std=0.1):

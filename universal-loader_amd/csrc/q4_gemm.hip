@@ -37,6 +37,12 @@ using namespace ulspec;
 namespace {
 
 constexpr int kQ40Chunk = 1152;
+// Q8_0: one 16-row tile x 4 blocks (128 K): lane l holds the 8 int8 values
+// k = 32 j + 8 (l >> 4) .. +7 of row l & 15 for blocks j = 0, 1 at l * 16 and
+// j = 2, 3 at 1024 + l * 16 (two 1 KB coalesced loads per wave), then the
+// 16 rows' 4 fp16 block scales at 2048 + row * 8.  1.0625 B per weight, as
+// in GGUF.
+constexpr int kQ80Chunk = 2176;
 constexpr int kQ4KChunk = 2304;
 // fp16 weights (GGUF F16, and Q8_0 / Q6_K converted at upload): a chunk is
 // one 16-row tile x 128 K, 4 KB; lane l reads 16 contiguous bytes at
@@ -80,6 +86,37 @@ __global__ void repack_q4_0_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
     }
     *(uint32_t*)(chunk + L * 16 + j * 4) = word;
     if (g == 0) *(uint16_t*)(chunk + 1024 + r * 8 + j * 2) = d;
+}
+
+// One thread per (tile, chunk, lane, block j): the lane's 8 values of block
+// 4 c + j and, for lanes 0-15, the row's scale of that block; zeros past N
+// and past the last block.
+__global__ void repack_q8_0_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
+                                   uint32_t nb, uint32_t nquads, uint64_t total)
+{
+    const uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const uint32_t j = id & 3;
+    const uint32_t L = (id >> 2) & 63;
+    const uint64_t tc = id >> 8;  // t * nquads + c
+    const uint32_t c = (uint32_t)(tc % nquads);
+    const uint32_t t = (uint32_t)(tc / nquads);
+    const uint32_t r = L & 15, g = L >> 4;
+    const uint32_t n = 16 * t + r, b = 4 * c + j;
+    uint8_t* chunk = out + tc * kQ80Chunk;
+    uint32_t w0 = 0, w1 = 0;
+    uint16_t d = 0;
+    if (n < N && b < nb) {
+        const uint8_t* blk = raw + ((uint64_t)n * nb + b) * 34;
+        const uint8_t* q = blk + 2 + 8 * g;
+        w0 = q[0] | (q[1] << 8) | (q[2] << 16) | ((uint32_t)q[3] << 24);
+        w1 = q[4] | (q[5] << 8) | (q[6] << 16) | ((uint32_t)q[7] << 24);
+        d = (uint16_t)(blk[0] | (blk[1] << 8));
+    }
+    uint32_t* dst = (uint32_t*)(chunk + (j >> 1) * 1024 + L * 16 + (j & 1) * 8);
+    dst[0] = w0;
+    dst[1] = w1;
+    if (g == 0) *(uint16_t*)(chunk + 2048 + r * 8 + j * 2) = d;
 }
 
 __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
@@ -641,6 +678,54 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
     }
 }
 
+template <int CMAX>
+__device__ __forceinline__ void q8_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t s_lane, int c0,
+                                                int nc, uint4 (&w0)[CMAX], uint4 (&w1)[CMAX], uint2 (&sc)[CMAX])
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        const uint32_t o = (uint32_t)(c0 + i) * kQ80Chunk;
+        w0[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
+        w1[i] = buf_load16(wr, i < nc ? w_lane + o + 1024 : kOOB);
+        sc[i] = buf_load8(wr, i < nc ? s_lane + o : kOOB);
+    }
+}
+
+// Eight int8 values (two words) -> fp16, exactly: each biased byte b ^ 0x80
+// under exponent 0x64 is 1024 + (b + 128); subtracting 1152 leaves b.
+__device__ __forceinline__ half8_t dequant_q8_0(uint32_t lo, uint32_t hi)
+{
+    const uint32_t x0 = lo ^ 0x80808080u, x1 = hi ^ 0x80808080u;
+    const uint4 u = {(x0 & 0xffu) | ((x0 & 0xff00u) << 8) | 0x64006400u,
+                     ((x0 >> 16) & 0xffu) | ((x0 >> 8) & 0xff0000u) | 0x64006400u,
+                     (x1 & 0xffu) | ((x1 & 0xff00u) << 8) | 0x64006400u,
+                     ((x1 >> 16) & 0xffu) | ((x1 >> 8) & 0xff0000u) | 0x64006400u};
+    return __builtin_bit_cast(half8_t, u) - (half8_t)(_Float16)1152.0f;
+}
+
+// acc += d_block * (A . q) per block, as for Q4_0.
+template <int CMAX>
+__device__ __forceinline__ void q8_0_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&w0)[CMAX],
+                                               const uint4 (&w1)[CMAX], const uint2 (&sc)[CMAX], float4_t& acc)
+{
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        if (i < nc) {
+            const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
+            const uint32_t sw[2] = {sc[i].x, sc[i].y};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const half8_t B = dequant_q8_0(words[2 * j], words[2 * j + 1]);
+                const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]);
+                const float4_t pr = mfma16x16x32(A, B, zero4);
+                acc = __builtin_elementwise_fma((float4_t)d, pr, acc);
+            }
+        }
+    }
+}
+
 // Position of row 0 for the RoPE epilogue: a scalar load through the
 // constant address space (the value is fixed for the whole kernel), so it
 // never waits behind the vector loads in flight.
@@ -951,6 +1036,13 @@ struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
 };
 
 template <int CMAX>
+struct WBatch<ULSPEC_GGML_Q8_0, CMAX> {
+    static constexpr int kLoads = 3 * CMAX;
+    uint4 w0[CMAX], w1[CMAX];
+    uint2 sc[CMAX];
+};
+
+template <int CMAX>
 struct WBatch<ULSPEC_GGML_F16, CMAX> {
     static constexpr int kLoads = 4 * CMAX;
     uint4 w[CMAX][4];
@@ -990,6 +1082,9 @@ __device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_r
     const uint32_t tile = (uint32_t)(t < a.n_tiles ? t : 0) * a.n_chunks;
     if constexpr (TYPE == ULSPEC_GGML_F16)
         f16_load_batch<CMAX>(wr, tile * kF16Chunk + lane * 16, c0, nc, b.w);
+    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
+        q8_0_load_batch<CMAX>(wr, tile * kQ80Chunk + lane * 16, tile * kQ80Chunk + 2048 + r * 8, c0, nc, b.w0, b.w1,
+                              b.sc);
     else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
         q4_0_load_batch<CMAX>(wr, tile * kQ40Chunk + lane * 16, tile * kQ40Chunk + 1024 + r * 8, c0, nc, b.wq, b.sc);
     else
@@ -1003,6 +1098,8 @@ __device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, in
 {
     if constexpr (TYPE == ULSPEC_GGML_F16)
         f16_mma_batch<CMAX>(xs, xrow, c0, nc, b.w, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
+        q8_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.w0, b.w1, b.sc, acc);
     else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
         q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
     else
@@ -1278,6 +1375,7 @@ struct CList {};
 using WideQ40 = CList<1, 2, 3, 4, 6, 8>;
 using WideQ4K = CList<1, 2, 3, 4>;
 using WideF16 = CList<1, 2>;  // 16 VGPRs of weights per chunk
+using WideQ80 = CList<1, 2, 3, 4, 6>;  // 10 VGPRs of weights per chunk
 
 // Per type: the one-tile batch sizes and the pipelined kernel's batch.
 template <int TYPE>
@@ -1291,6 +1389,11 @@ template <>
 struct GemmCfg<ULSPEC_GGML_Q4_K> {
     using Wide = WideQ4K;
     static constexpr int kStream = kQ4KStream;
+};
+template <>
+struct GemmCfg<ULSPEC_GGML_Q8_0> {
+    using Wide = WideQ80;
+    static constexpr int kStream = 8;
 };
 template <>
 struct GemmCfg<ULSPEC_GGML_F16> {
@@ -1360,6 +1463,7 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
     type_kernels<ULSPEC_GGML_Q4_0>(fns, rings);
     type_kernels<ULSPEC_GGML_Q4_K>(fns, rings);
     type_kernels<ULSPEC_GGML_F16>(fns, rings);
+    type_kernels<ULSPEC_GGML_Q8_0>(fns, rings);
     const int dyn = (int)(kWideLdsMax - kStreamStatic);
     for (const void* f : fns) {
         hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
@@ -1439,6 +1543,7 @@ void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     if (w.type == ULSPEC_GGML_Q4_0) stream_launch_t<ULSPEC_GGML_Q4_0>(ctx, w, a);
     else if (w.type == ULSPEC_GGML_Q4_K) stream_launch_t<ULSPEC_GGML_Q4_K>(ctx, w, a);
+    else if (w.type == ULSPEC_GGML_Q8_0) stream_launch_t<ULSPEC_GGML_Q8_0>(ctx, w, a);
     else stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
 }
 
@@ -1465,9 +1570,9 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
     const _Float16* X = reinterpret_cast<const _Float16*>(x);
     if (gemm_workspace_bytes(w) > ctx->ws_bytes)
         return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
-    // fp16 weights have no split-K kernel: rows go in groups that fit in LDS
+    // fp16 and Q8_0 weights have no split-K kernel: rows go in groups that fit in LDS
     uint32_t group = 64;
-    if (w.type == ULSPEC_GGML_F16)
+    if (w.type == ULSPEC_GGML_F16 || w.type == ULSPEC_GGML_Q8_0)
         while (group > 1 && !wide_fits((int)group, w.k)) --group;
     for (uint32_t m0 = 0; m0 < M; m0 += group) {
         const int mc = (int)std::min<uint32_t>(group, M - m0);
@@ -1550,8 +1655,9 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
                             bool on_device, uint32_t* out_id)
 {
     if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
-    const bool f16 = type == ULSPEC_GGML_F16 || type == ULSPEC_GGML_Q8_0 || type == ULSPEC_GGML_Q6_K;
-    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K && !f16)
+    const bool f16 = type == ULSPEC_GGML_F16 || type == ULSPEC_GGML_Q6_K;  // held as fp16
+    const bool q80 = type == ULSPEC_GGML_Q8_0;
+    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K && !f16 && !q80)
         return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported (Q4_0, Q4_K, Q6_K, Q8_0, F16)",
                     type);
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
@@ -1562,16 +1668,16 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
     const size_t expect = (size_t)N * (K / bs) * ts;
     if (nbytes != expect) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes given, %zu expected", nbytes, expect);
     Weight w;
-    w.type = f16 ? (uint32_t)ULSPEC_GGML_F16 : type;  // Q8_0 / Q6_K are held as fp16
+    w.type = f16 ? (uint32_t)ULSPEC_GGML_F16 : type;  // Q6_K is held as fp16
     w.src_type = type;
     w.n = N;
     w.k = K;
     w.n_tiles = (N + 15) / 16;
     w.n_chunks = type == ULSPEC_GGML_Q4_K ? K / 256 : (K + 127) / 128;
     w.bytes = (size_t)w.n_tiles * w.n_chunks *
-              (f16 ? kF16Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
+              (f16 ? kF16Chunk : q80 ? kQ80Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
     if (w.bytes >= kOOB) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes exceeds the 2 GiB per-weight limit", w.bytes);
-    w.ksplit = f16 ? 1 : choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
+    w.ksplit = f16 || q80 ? 1 : choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipMalloc(&w.dev, w.bytes);
     if (e != hipSuccess) return hip_fail(ctx, e, "weight_upload hipMalloc");
@@ -1603,6 +1709,10 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
         const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
         hipLaunchKernelGGL(repack_f16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
                            (const _Float16*)half_rows, w.dev, N, K, w.n_chunks, total);
+    } else if (q80) {
+        const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
+        hipLaunchKernelGGL(repack_q8_0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
+                           (const uint8_t*)raw, w.dev, N, K / 32, w.n_chunks, total);
     } else if (type == ULSPEC_GGML_Q4_0) {
         const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 256;
         hipLaunchKernelGGL(repack_q4_0_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
