@@ -44,7 +44,8 @@ constexpr int kQ40Chunk = 1152;
 // in GGUF.
 constexpr int kQ80Chunk = 2176;
 constexpr int kQ4KChunk = 2304;
-// fp16 weights (GGUF F16, and Q8_0 / Q6_K converted at upload): a chunk is
+// fp16 weights (GGUF F16, and Q6_K or mixed-type fused weights converted at
+// upload): a chunk is
 // one 16-row tile x 128 K, 4 KB; lane l reads 16 contiguous bytes at
 // 1024 j + 16 l for MFMA j (rows l & 15, K 32 j + 8 (l >> 4) ..).
 constexpr int kF16Chunk = 4096;
