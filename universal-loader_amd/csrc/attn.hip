@@ -235,22 +235,30 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 // out[qi][h][d] = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the
 // splits that hold keys, in split order (deterministic).  Grid (H, nq), D
 // threads; (m, l) of every split staged in LDS, O loads 16 splits at a time.
+// The first loads do not wait for the device-side prefix length: they read
+// splits 0..min(16, splits)-1 of the workspace (which holds all `splits`
+// partials, so every read is in bounds; a split past the last one holding
+// keys reads stale values that are never used) and the count of live splits
+// masks them afterwards.
 template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
 {
     __shared__ float sm[kAttnMaxSplits], sl[kAttnMaxSplits];
     const int h = blockIdx.x, qi = blockIdx.y, d = threadIdx.x;
+    const int S = a.splits;
+    const size_t stride = (size_t)a.nq * (D + 2);
+    const float* q0 = a.part + (size_t)h * S * stride + qi * (D + 2);
+    float first[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) first[u] = q0[min(u, S - 1) * stride + d];
+    const int ds = min(d, S - 1);
+    const float mv = q0[ds * stride + D], lv = q0[ds * stride + D + 1];
     int n_prefix, L;
     attn_len(a, n_prefix, L);
-    const int ns = min(a.splits, (L + a.keys_per_split - 1) / a.keys_per_split);
-    const size_t stride = (size_t)a.nq * (D + 2);
-    const float* q0 = a.part + (size_t)h * a.splits * stride + qi * (D + 2);
-    float first[16];  // O of the first 16 splits, loaded with (m, l)
-#pragma unroll
-    for (int u = 0; u < 16; ++u) first[u] = u < ns ? q0[u * stride + d] : 0.0f;
-    if (d < ns) {
-        sm[d] = q0[d * stride + D];
-        sl[d] = q0[d * stride + D + 1];
+    const int ns = min(S, (L + a.keys_per_split - 1) / a.keys_per_split);
+    if (d < S) {
+        sm[d] = mv;
+        sl[d] = lv;
     }
     __syncthreads();
     float M = -INFINITY;
@@ -260,7 +268,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
     for (int s0 = 0; s0 < ns; s0 += 16) {
         float ov[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) ov[u] = s0 == 0 ? first[u] : (s0 + u < ns ? q0[(s0 + u) * stride + d] : 0.0f);
+        for (int u = 0; u < 16; ++u) ov[u] = s0 == 0 ? first[u] : q0[min(s0 + u, S - 1) * stride + d];
 #pragma unroll
         for (int u = 0; u < 16; ++u)
             if (s0 + u < ns) {
