@@ -158,6 +158,14 @@ def test_malformed_files(pkg, tmp_path):
     struct.pack_into("<Q", b, b.index(b"q") + 1 + 4, 48)  # ne0 no longer a multiple of 32
     p.write_bytes(bytes(b))
     _expect_open_error(pkg, p, "multiple of the block")
+    # dimensions whose byte count is 2^128 (4 B x 2^62 x 2^63 x 2): a product
+    # wrapped in 128 bits would read 0 bytes and pass the size check
+    b = b"GGUF" + struct.pack("<IQQ", 3, 1, 0)
+    b += struct.pack("<Q", 1) + b"w" + struct.pack("<I", 3) + struct.pack("<3Q", 1 << 62, 1 << 63, 2)
+    b += struct.pack("<IQ", 0, 0)
+    b += b"\0" * ((len(b) + 31) // 32 * 32 - len(b)) + bytes(64)
+    p.write_bytes(b)
+    _expect_open_error(pkg, p, "past the end")
 
 
 def test_unknown_type_is_listed_without_data(pkg, tmp_path):

@@ -198,9 +198,11 @@ ulspec_status parse(ulspec_gguf* g)
         if (t.ne[0] % (uint64_t)bs)
             return gfail(g, ULSPEC_EINVAL, "GGUF tensor '%s': row of %llu not a multiple of the block (%d)",
                          t.name.c_str(), (unsigned long long)t.ne[0], bs);
-        // bytes = ne0 / bs * ts * ne1 * ne2 * ne3, overflow-checked
+        // bytes = ne0 / bs * ts * ne1 * ne2 * ne3; the product stops growing
+        // once it passes the file size, so with every factor below 2^64 it
+        // never wraps in 128 bits
         unsigned __int128 n = (unsigned __int128)(t.ne[0] / (uint64_t)bs) * (uint64_t)ts;
-        for (int d = 1; d < 4; ++d) n *= t.ne[d];
+        for (int d = 1; d < 4 && n <= g->size; ++d) n *= t.ne[d];
         if (n > g->size || g->data_offset > g->size || t.offset > g->size - g->data_offset ||
             (uint64_t)n > g->size - g->data_offset - t.offset)
             return gfail(g, ULSPEC_EINVAL, "GGUF tensor '%s': data past the end of the file", t.name.c_str());
