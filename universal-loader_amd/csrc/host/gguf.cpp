@@ -19,6 +19,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <string>
@@ -146,7 +147,7 @@ ulspec_status parse(ulspec_gguf* g)
     const uint64_t n_tensors = c.get<uint64_t>(), n_kv = c.get<uint64_t>();
     // every entry takes at least 8 bytes: bounds the counts before reserving
     if (!c.ok || n_tensors > g->size / 8 || n_kv > g->size / 8) return gfail(g, ULSPEC_EINVAL, "GGUF header counts");
-    g->kv.reserve((size_t)n_kv);
+    g->kv.reserve((size_t)std::min<uint64_t>(n_kv, 4096));  // a hostile count fails below, before it allocates
     for (uint64_t i = 0; i < n_kv; ++i) {
         ulspec_gguf::Kv e;
         e.key = c.str();
@@ -174,7 +175,7 @@ ulspec_status parse(ulspec_gguf* g)
             return gfail(g, ULSPEC_EINVAL, "general.alignment must be a power of two");
         g->alignment = (uint64_t)a;
     }
-    g->tensors.reserve((size_t)n_tensors);
+    g->tensors.reserve((size_t)std::min<uint64_t>(n_tensors, 4096));
     for (uint64_t i = 0; i < n_tensors; ++i) {
         ulspec_gguf::Tensor t;
         t.name = c.str();
