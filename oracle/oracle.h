@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of the speculative-decoding verification path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/,
+ * TEST INFRASTRUCTURE ONLY: the outputs the HIP path is tested against.  Only tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
  * product (universal-loader_amd/) never links, imports or falls back to it.
  *

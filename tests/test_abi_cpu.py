@@ -46,7 +46,7 @@ def test_create_reports_missing_device(pkg):
     L = pkg.lib()
     h = C.c_void_p()
     st = L.ulspec_create(0, C.byref(h))
-    if st == pkg.OK:  # a gfx950 is present (GPU box): nothing to check here
+    if st == pkg.OK:  # a gfx950 is present: nothing to check here
         L.ulspec_destroy(h)
         pytest.skip("device present")
     assert st == pkg.EDEVICE and not h.value
