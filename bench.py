@@ -365,7 +365,7 @@ def main():
                     help="launch each step's kernels directly instead of replaying the captured graph")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build measures the single-GPU "
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the library measures the single-GPU "
               "speculative step; sharding across GPUs is not implemented.", file=sys.stderr)
         return 2
     pkg = load_package()

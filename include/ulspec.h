@@ -42,7 +42,7 @@ typedef enum {
     ULSPEC_EINVAL = 1,       /* bad argument (checked before any launch) */
     ULSPEC_ENOMEM = 2,       /* device or host allocation failed */
     ULSPEC_EDEVICE = 3,      /* HIP runtime error / no gfx950 device */
-    ULSPEC_EUNSUPPORTED = 4  /* valid request this build does not implement */
+    ULSPEC_EUNSUPPORTED = 4  /* valid request the library does not implement */
 } ulspec_status;
 
 /* GGUF type ids (src/core/gguf_types.h:6-33). */
