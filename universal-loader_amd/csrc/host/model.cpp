@@ -41,6 +41,7 @@ __global__ void set_i32_kernel(int32_t* p, int32_t v) { *p = v; }
 // and no other thread touches its columns.  Entries outside [0, n_max) or
 // rows past max_ctx are skipped.
 constexpr int kCompactMax = 16;
+static_assert(kCompactMax >= (int)ulspec_model::kRows, "a compaction moves every row a tree forward can hold");
 __global__ __launch_bounds__(256) void kv_compact_kernel(_Float16* const* __restrict__ tab, uint32_t n_layers,
                                                          uint32_t kvdim8, uint32_t max_ctx,
                                                          const int32_t* __restrict__ pos_dev, int32_t pos_add,
