@@ -451,7 +451,7 @@ def main():
     out = {
         "metric": METRIC, "value": tokens / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights x fp16 activations, fp32 accumulate",
+        "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights x fp32 activations (split fp16 MFMA operands), fp32 accumulate",
         "data": "synthetic: random-init N(0, 0.02^2) weights quantized to Q4_K on the device, seeded prompt",
         "config": {"workload": f"speculative decoding step, 7B-shape Q4_K target (dim 4096, 32 layers, 32 heads, "
                                f"FFN 11008, vocab 32000) + draft (dim 2048, 16 layers, 16 heads, FFN 5632), k=5, "

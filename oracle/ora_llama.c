@@ -3,8 +3,8 @@
  * baseline); nothing in the product links it.
  *
  * Block order: src/inference/inference_engine.cpp:602-682.  Weight names:
- * src/inference/model.cpp:190-246.  Formulas and fp16 rounding points are
- * listed in oracle.h.  The speculative step replaces the host callback loop
+ * src/inference/model.cpp:190-246.  Formulas and the fp16 rounding points
+ * (Q and the K/V cache only) are listed in oracle.h.  The speculative step replaces the host callback loop
  * of src/inference/speculative_decoder.cpp:25-71 with the draft / verify /
  * accept sequence documented in oracle.h; the cumulative counters follow
  * update_acceptance_stats (:112-116). */
@@ -133,8 +133,8 @@ static void embed_row(const ora_llama* m, int32_t tok, float* h)
     ora_dequantize(m->embed_type, row, dim, h);
 }
 
-/* h += delta (if given); x = fp16((h * r) * w) */
-static void add_rmsnorm(float* h, const float* delta, const float* w, int64_t M, int64_t dim, float eps, uint16_t* x)
+/* h += delta (if given); x = (h * r) * w */
+static void add_rmsnorm(float* h, const float* delta, const float* w, int64_t M, int64_t dim, float eps, float* x)
 {
     for (int64_t r = 0; r < M; ++r) {
         float* hr = h + r * dim;
@@ -144,7 +144,7 @@ static void add_rmsnorm(float* h, const float* delta, const float* w, int64_t M,
             ss = fmaf(hr[i], hr[i], ss);
         }
         float rr = 1.0f / sqrtf(ss / (float)dim + eps);
-        for (int64_t i = 0; i < dim; ++i) x[r * dim + i] = ora_f2h((hr[i] * rr) * w[i]);
+        for (int64_t i = 0; i < dim; ++i) x[r * dim + i] = (hr[i] * rr) * w[i];
     }
 }
 
@@ -171,16 +171,16 @@ int ora_llama_forward(ora_llama* m, const int32_t* tokens, int64_t M, int64_t po
     float* att = (float*)malloc(sizeof(float) * (size_t)(M * H * D));
     float* g = (float*)malloc(sizeof(float) * (size_t)(M * F));
     float* u = (float*)malloc(sizeof(float) * (size_t)(M * F));
-    uint16_t* x16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(M * xw));
+    float* x = (float*)malloc(sizeof(float) * (size_t)(M * xw));
     uint16_t* q16 = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(M * H * D));
     for (int64_t r = 0; r < M; ++r) embed_row(m, tokens[r], h + r * dim);
     float scale = 1.0f / sqrtf((float)D);
     for (int64_t l = 0; l < c->n_layers; ++l) {
         ora_layer* L = &m->L[l];
-        add_rmsnorm(h, l ? delta : NULL, L->attn_norm, M, dim, c->rms_eps, x16);
-        ora_q4_gemm_f32(L->tq, L->wq, H * D, dim, x16, M, q, nt);
-        ora_q4_gemm_f32(L->tk, L->wk, kvw, dim, x16, M, kk, nt);
-        ora_q4_gemm_f32(L->tv, L->wv, kvw, dim, x16, M, vv, nt);
+        add_rmsnorm(h, l ? delta : NULL, L->attn_norm, M, dim, c->rms_eps, x);
+        ora_q4_gemm_x32(L->tq, L->wq, H * D, dim, x, M, q, nt);
+        ora_q4_gemm_x32(L->tk, L->wk, kvw, dim, x, M, kk, nt);
+        ora_q4_gemm_x32(L->tv, L->wv, kvw, dim, x, M, vv, nt);
         for (int64_t r = 0; r < M; ++r) {
             int64_t p = pos + r;
             const float* cs = m->rope + 2 * p * (D / 2);
@@ -191,20 +191,19 @@ int ora_llama_forward(ora_llama* m, const int32_t* tokens, int64_t M, int64_t po
             for (int64_t i = 0; i < kvw; ++i) L->vc[p * kvw + i] = ora_f2h(vv[r * kvw + i]);
         }
         ora_attention_f32(q16, L->kc, L->vc, pos, M, NULL, H, Hkv, D, scale, att, nt);
-        for (int64_t i = 0; i < M * H * D; ++i) q16[i] = ora_f2h(att[i]); /* attention output, fp16 */
-        ora_q4_gemm_f32(L->to, L->wo, dim, H * D, q16, M, delta, nt);
-        add_rmsnorm(h, delta, L->ffn_norm, M, dim, c->rms_eps, x16);
-        ora_q4_gemm_f32(L->tg, L->wg, F, dim, x16, M, g, nt);
-        ora_q4_gemm_f32(L->tu, L->wu, F, dim, x16, M, u, nt);
+        ora_q4_gemm_x32(L->to, L->wo, dim, H * D, att, M, delta, nt);
+        add_rmsnorm(h, delta, L->ffn_norm, M, dim, c->rms_eps, x);
+        ora_q4_gemm_x32(L->tg, L->wg, F, dim, x, M, g, nt);
+        ora_q4_gemm_x32(L->tu, L->wu, F, dim, x, M, u, nt);
         for (int64_t i = 0; i < M * F; ++i) {
             float s = g[i] * (1.0f / (1.0f + ora_expf(-g[i])));
-            x16[i] = ora_f2h(s * u[i]);
+            x[i] = s * u[i];
         }
-        ora_q4_gemm_f32(L->td, L->wd, dim, F, x16, M, delta, nt);
+        ora_q4_gemm_x32(L->td, L->wd, dim, F, x, M, delta, nt);
     }
-    add_rmsnorm(h, delta, m->out_norm, M, dim, c->rms_eps, x16);
-    if (n_logits) ora_q4_gemm_f32(m->tout, m->wout, V, dim, x16 + (M - n_logits) * dim, n_logits, logits, nt);
-    free(h); free(delta); free(q); free(kk); free(vv); free(att); free(g); free(u); free(x16); free(q16);
+    add_rmsnorm(h, delta, m->out_norm, M, dim, c->rms_eps, x);
+    if (n_logits) ora_q4_gemm_x32(m->tout, m->wout, V, dim, x + (M - n_logits) * dim, n_logits, logits, nt);
+    free(h); free(delta); free(q); free(kk); free(vv); free(att); free(g); free(u); free(x); free(q16);
     return 0;
 }
 

@@ -519,14 +519,22 @@ static void gemm_rows(void* arg, int64_t lo, int64_t hi)
     }
 }
 
+int ora_q4_gemm_x32(int type, const uint8_t* W, int64_t N, int64_t K,
+                    const float* X, int64_t M, float* Y, int nthreads)
+{
+    if (ora_row_bytes(type, K) == 0 || N <= 0 || M <= 0) return -1;
+    gemm_job j = { type, W, N, K, M, X, Y };
+    ora_parallel_for(nthreads, N, gemm_rows, &j);
+    return 0;
+}
+
 int ora_q4_gemm_f32(int type, const uint8_t* W, int64_t N, int64_t K,
                     const uint16_t* X, int64_t M, float* Y, int nthreads)
 {
     if (ora_row_bytes(type, K) == 0 || N <= 0 || M <= 0) return -1;
     float* x = (float*)malloc(sizeof(float) * (size_t)(M * K));
     ora_h2f_array(X, x, (size_t)(M * K));
-    gemm_job j = { type, W, N, K, M, x, Y };
-    ora_parallel_for(nthreads, N, gemm_rows, &j);
+    int rc = ora_q4_gemm_x32(type, W, N, K, x, M, Y, nthreads);
     free(x);
-    return 0;
+    return rc;
 }

@@ -85,6 +85,9 @@ int ora_q4_gemm_f64(int type, const uint8_t* W, int64_t N, int64_t K,
                     const uint16_t* X, int64_t M, double* Y);
 int ora_q4_gemm_f32(int type, const uint8_t* W, int64_t N, int64_t K,
                     const uint16_t* X, int64_t M, float* Y, int nthreads);
+/* The same with fp32 X (the model's activations). */
+int ora_q4_gemm_x32(int type, const uint8_t* W, int64_t N, int64_t K,
+                    const float* X, int64_t M, float* Y, int nthreads);
 
 /* ---- verify attention ------------------------------------------------------ */
 /* q: fp16 [nq][H][D]; k, v: fp16 [L][Hkv][D] with L = n_prefix + nq (the nq new
@@ -139,10 +142,11 @@ int ora_accept_tree(const ora_sampling* s, int64_t B, int64_t n, int64_t V, cons
  * Block order of InferenceEngine::forward_layer_gpu
  * (src/inference/inference_engine.cpp:602-682): RMSNorm -> Q, K, V -> RoPE ->
  * attention -> O -> +residual -> RMSNorm -> gate, up -> SiLU(gate)*up -> down
- * -> +residual; final RMSNorm, LM head.  The residual stream is fp32; every
- * GEMM input (normed activations, attention output, SiLU product), Q and the
- * K/V cache are rounded to fp16 (round to nearest even).
- *   RMSNorm  x = fp16((h * r) * w), r = 1 / sqrtf(sum(h^2) / dim + eps)
+ * -> +residual; final RMSNorm, LM head.  Activations are fp32 (the residual
+ * stream and every GEMM input: normed activations, attention output, SiLU
+ * product); only Q and the K/V cache are rounded to fp16 (round to nearest
+ * even), the attention kernel's inputs.
+ *   RMSNorm  x = (h * r) * w, r = 1 / sqrtf(sum(h^2) / dim + eps)
  *            (src/shaders/ffn/ffn_fused.glsl:23-33)
  *   RoPE     pairs (2i, 2i+1): y0 = x0 c - x1 s, y1 = x0 s + x1 c with
  *            (c, s) = fp32(cos, sin)(pos * base^(-2i/D)) evaluated in double

@@ -52,7 +52,8 @@ def _f16(x):
 
 
 class NumpyLlama:
-    """Float64 forward with the same fp16 rounding points as the oracle
+    """Float64 forward with the same fp16 rounding points as the oracle -- the
+    attention's inputs Q, K and V -- and unrounded activations everywhere else
     (independent code: matrix products, explicit softmax, closed-form RoPE)."""
 
     def __init__(self, ora, tensors, cfg):
@@ -65,7 +66,7 @@ class NumpyLlama:
 
     def _norm(self, h, w):
         r = 1.0 / np.sqrt((h * h).sum(axis=1, keepdims=True) / h.shape[1] + self.cfg["rms_eps"])
-        return _f16(h * r * w)
+        return h * r * w
 
     def _rope(self, x, pos):  # x [M][heads][D]
         D = self.D
@@ -101,11 +102,11 @@ class NumpyLlama:
                     s = keys[:, g, :] @ q[r, hh] / np.sqrt(D)
                     p = np.exp(s - s.max())
                     att[r, hh] = (p / p.sum()) @ vals[:, g, :]
-            h = h + _f16(att).reshape(M, H * D) @ W[f"blk.{l}.attn_output.weight"].T
+            h = h + att.reshape(M, H * D) @ W[f"blk.{l}.attn_output.weight"].T
             x = self._norm(h, W[f"blk.{l}.ffn_norm.weight"])
             g = x @ W[f"blk.{l}.ffn_gate.weight"].T
             u = x @ W[f"blk.{l}.ffn_up.weight"].T
-            a = _f16(g / (1.0 + np.exp(-g)) * u)
+            a = g / (1.0 + np.exp(-g)) * u
             h = h + a @ W[f"blk.{l}.ffn_down.weight"].T
         x = self._norm(h, W["output_norm.weight"])
         return x @ W["output.weight"].T

@@ -1,0 +1,125 @@
+"""Speculative decoding at the 7B shape against the oracle, through the C ABI.
+
+Workload: random-init Q4_K target (dim 4096, 32 layers, 32 heads, FFN 11008,
+vocab 32000) and draft (dim 2048, 16 layers, 16 heads, FFN 5632), k = 5,
+batch 1, a seeded prompt of 2048 tokens.  The GPU runs the prefill; the
+oracle starts from the GPU's post-prefill K/V cache (a CPU prefill of 2047
+tokens through both models would take minutes) and then computes every step
+itself.
+
+Bars:
+  - greedy, free-running: the committed tokens and the acceptance counters
+    of 8 steps are bit-exact with the oracle's own loop;
+  - temperature 0.8 over the full vocabulary, teacher-forced on the GPU's
+    committed tokens: every draft draw and accept decision is bit-exact with
+    the oracle's rule on the step's logits, and the oracle's own logits for
+    the same tokens are within LOGIT_TOL of their RMS (max |error| / RMS over
+    all rows of the step).  The activations are fp32 on both sides (split
+    fp16 pairs into the GPU's MFMAs); only Q and the K/V cache are fp16, so
+    the two differ by fp32 summation order and the fp16 roundings that order
+    moves.
+"""
+import importlib
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TARGET = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=32, ffn=11008, vocab=32000, rms_eps=1e-5,
+              rope_base=10000.0)
+DRAFT = dict(dim=2048, n_layers=16, n_heads=16, n_kv_heads=16, ffn=5632, vocab=32000, rms_eps=1e-5,
+             rope_base=10000.0)
+CONTEXT, K_SPEC, STEPS = 2048, 5, 8
+CAP = CONTEXT + 2 * STEPS * (K_SPEC + 1) + 32
+LOGIT_TOL = 1e-2
+Q4_K = 12
+
+
+@pytest.fixture(scope="module")
+def models(pkg, ctx, ora):
+    synthetic_llama = importlib.import_module("universal_loader_amd.synthetic").synthetic_llama
+    gt, th = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=CAP), Q4_K, seed=1, keep_host=True)
+    gd, dh = synthetic_llama(pkg, ctx, dict(DRAFT, max_ctx=CAP), Q4_K, seed=2, keep_host=True)
+    oms = []
+    for cfg, host in ((TARGET, th), (DRAFT, dh)):
+        m = ora.Llama(**cfg, max_ctx=CAP, nthreads=ora.nthreads_default())
+        for name, (wtype, data, ne0, ne1) in host.items():
+            m.set_tensor(name, wtype, data, ne0, ne1)
+        oms.append(m)
+    del th, dh
+    yield gt, gd, oms[0], oms[1]
+    for m in (gt, gd, *oms):
+        m.close()
+
+
+@pytest.fixture(scope="module")
+def prompt():
+    return np.random.default_rng(1234).integers(0, TARGET["vocab"], CONTEXT).astype(np.int32)
+
+
+def _prefill(pkg, models, prompt, s, seed):
+    """GPU prefill, then the oracle models take the GPU's K/V rows 0 .. n-2."""
+    gt, gd, ot, od = models
+    sp = pkg.Speculative(gt, gd, K_SPEC, s, seed)
+    sp.prefill(prompt)
+    for g, o, cfg in ((gt, ot, TARGET), (gd, od, DRAFT)):
+        for l in range(cfg["n_layers"]):
+            k, v = g.kv_io(l, 0, 0, CONTEXT - 1)
+            o.kv_io(l, 1, 0, CONTEXT - 1, k, v)
+    return sp
+
+
+def test_7b_greedy_tokens_bit_exact(pkg, ora, models, prompt):
+    gt, gd, ot, od = models
+    seed = 31
+    sp = _prefill(pkg, models, prompt, pkg.sampling(greedy=True), seed)
+    osp = ora.Speculative(ot, od, K_SPEC, ora.sampling(greedy=True), seed, cap=CAP)
+    osp.seq[:CONTEXT] = prompt
+    osp.st.n = CONTEXT
+    for step in range(STEPS):
+        sp.steps(1)
+        osp.step()
+        print(f"  step {step}: gpu n={sp.state()['n']} oracle n={osp.state()['n']}", flush=True)
+    got, st = sp.tokens(), sp.state()
+    print(f"  greedy 7B: {st['n'] - CONTEXT} tokens in {st['steps']} steps, accepted {st['accepted']}/{st['proposed']}")
+    assert np.array_equal(got, osp.tokens())
+    assert st == osp.state()
+    sp.close()
+
+
+def test_7b_sampling_steps_bit_exact(pkg, ora, models, prompt):
+    gt, gd, ot, od = models
+    seed, k = 2024, K_SPEC
+    s_ora = ora.sampling(temperature=0.8)
+    sp = _prefill(pkg, models, prompt, pkg.sampling(temperature=0.8), seed)
+    seq = list(prompt)
+    worst = 0.0
+    accepted = 0
+    for step in range(STEPS):
+        n = len(seq)
+        sp.steps(1)
+        r = sp.last_step()
+        u, d = r["uniforms"], r["draft_tokens"]
+        for j in range(k):
+            assert ora.sample(s_ora, r["draft_logits"][j:j + 1], u[j:j + 1])[0] == d[j], (step, j)
+        out, nacc = ora.accept(s_ora, r["target_logits"][None], r["draft_logits"][None], d[None], u[k:][None])
+        assert int(nacc[0]) == r["n_accepted"] and np.array_equal(out[0], r["out_tokens"]), step
+        dl = [od.forward(np.array(seq[n - 2:n], np.int32), n - 2, n_logits=1)[0]]
+        for j in range(1, k):
+            dl.append(od.forward(d[j - 1:j], n - 1 + j, n_logits=1)[0])
+        tl = ot.forward(np.concatenate([[seq[n - 1]], d]).astype(np.int32), n - 1, n_logits=k + 1)
+        errs = []
+        for a, b in ((r["draft_logits"], np.array(dl)), (r["target_logits"], tl)):
+            b64 = b.astype(np.float64)
+            errs.append(np.abs(a.astype(np.float64) - b64).max() / np.sqrt((b64 ** 2).mean()))
+        worst = max(worst, *errs)
+        print(f"  step {step}: accepted {r['n_accepted']}, logits max err / rms draft {errs[0]:.2e} "
+              f"target {errs[1]:.2e}", flush=True)
+        seq += list(r["out_tokens"][:r["n_accepted"] + 1])
+        accepted += r["n_accepted"]
+    assert np.array_equal(sp.tokens(), np.array(seq, np.int32))
+    assert sp.state()["accepted"] == accepted
+    print(f"  T=0.8 7B: {len(seq) - CONTEXT} tokens, accepted {accepted}/{k * STEPS}, worst logits err {worst:.2e}")
+    assert worst <= LOGIT_TOL
+    sp.close()

@@ -3,9 +3,10 @@ graph replay) against the oracle, through the C ABI.
 
 Bar: the committed token sequences and acceptance counters are bit-exact with
 the oracle's loop on the same weights, prompt and seed.  Model logits agree
-within 1e-2 of their RMS: every layer rounds its GEMM inputs to fp16, and an
-fp32 sum taken in another order lands on the other side of an fp16 rounding
-now and then; such one-ulp flips (5e-4 relative) carry through the layers.
+within LOGIT_TOL of their RMS (max |error| / RMS): activations are fp32 on both
+sides (split fp16 pairs into the GPU's MFMAs), only Q and the K/V cache are
+fp16, so the two differ by fp32 summation order and the fp16 roundings of Q,
+K and V that it moves (measured 2e-4 on this model).
 """
 import numpy as np
 import pytest
@@ -19,6 +20,7 @@ pytestmark = pytest.mark.gpu
 TARGET = dict(dim=512, n_layers=8, n_heads=8, n_kv_heads=8, ffn=1376, vocab=32000, max_ctx=256, rms_eps=1e-5,
               rope_base=10000.0)
 DRAFT = dict(TARGET, n_layers=2)
+LOGIT_TOL = 2e-3
 
 
 @pytest.fixture(scope="module")
@@ -51,14 +53,14 @@ def test_model_forward_logits_and_cache(pkg, ctx, ora, weights, prompt):
     scale = np.sqrt((lo.astype(np.float64) ** 2).mean())
     err = np.abs(lg.astype(np.float64) - lo).max() / scale
     print(f"  logits max err / rms = {err:.2e}, mean {np.abs(lg - lo).mean() / scale:.2e}")
-    assert err <= 1e-2
+    assert err <= LOGIT_TOL
     assert np.array_equal(np.argmax(lg, axis=1), np.argmax(lo, axis=1))
     for l in (0, TARGET["n_layers"] - 1):
         kg, vg = g.kv_io(l, 0, 0, 40)
         ko, vo = o.kv_io(l, 0, 0, 40)
         for a, b in ((kg, ko), (vg, vo)):
             a, b = ora.h2f_fast(a).astype(np.float64), ora.h2f_fast(b).astype(np.float64)
-            assert np.abs(a - b).max() <= 1e-2 * np.sqrt((b ** 2).mean())
+            assert np.abs(a - b).max() <= LOGIT_TOL * np.sqrt((b ** 2).mean())
     g.close()
 
 
@@ -100,7 +102,7 @@ def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
     the same step on the GPU's committed sequence and draft tokens (teacher
     forcing).  Every draft draw and every accept decision is bit-exact with the
     oracle's rule on the step's logits; the oracle's own logits for the same
-    tokens agree within 1e-2 of their RMS.  (Free-running sequences are not
+    tokens agree within LOGIT_TOL of their RMS.  (Free-running sequences are not
     compared token for token: an inverse-CDF draw over 32000 tokens moves when
     the logits move by 1e-4, so fp32 order differences change some draws.)"""
     tw, dw = weights
@@ -145,7 +147,7 @@ def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
     assert st["steps"] == steps and st["accepted"] == accepted and st["proposed"] == k * steps
     print(f"  t0.8: {len(seq) - len(prompt)} tokens in {steps} steps, accepted {accepted}/{k * steps}, "
           f"logits max err / rms {worst:.2e}")
-    assert worst <= 1e-2
+    assert worst <= LOGIT_TOL
     for m in (sp, gt, gd):
         m.close()
 

@@ -46,20 +46,29 @@ struct AttnArgs {
     const _Float16* q;  // [nq][H][D]
     const _Float16* k;  // [L][Hkv][D]
     const _Float16* v;
-    void* out;          // [nq][H][D], fp32 or (out_f16) fp16
+    void* out;          // [nq][H][D]: fp32, fp16 (out_mode 1) or split fp16 [2][nq][H][D] (2)
     float* part;        // [H][splits][nq][D + 2]: O (unnormalised), m, l
     const int32_t* dyn_prefix;  // if set, n_prefix = *dyn_prefix + prefix_add (read on the device)
     int prefix_add;
     int n_prefix, nq, L, H, Hkv, splits, keys_per_split;
     float scale_log2;   // scale * log2(e)
-    int out_f16;
+    int out_mode;
     uint32_t mask[kMaxQ];
 };
 
+template <int D>
 __device__ __forceinline__ void store_out(const AttnArgs& a, size_t i, float v)
 {
-    if (a.out_f16) ((_Float16*)a.out)[i] = (_Float16)v;
-    else ((float*)a.out)[i] = v;
+    if (a.out_mode == 1) {
+        ((_Float16*)a.out)[i] = (_Float16)v;
+    } else if (a.out_mode == 2) {  // high parts, then low parts (the split X of the next GEMM)
+        _Float16 hi, lo;
+        split_hl(v, hi, lo);
+        ((_Float16*)a.out)[i] = hi;
+        ((_Float16*)a.out)[(size_t)a.nq * a.H * D + i] = lo;
+    } else {
+        ((float*)a.out)[i] = v;
+    }
 }
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
             Lw += red_l[w][qi] * f;
         }
         if (a.splits == 1) {
-            store_out(a, ((size_t)qi * a.H + h) * D + d, o / Lw);
+            store_out<D>(a, ((size_t)qi * a.H + h) * D + d, o / Lw);
         } else {
             pp[qi * (D + 2) + d] = o;
             if (d == 0) {
@@ -277,7 +286,7 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
                 Ls += sl[s0 + u] * f;
             }
     }
-    store_out(a, ((size_t)qi * a.H + h) * D + d, o / Ls);
+    store_out<D>(a, ((size_t)qi * a.H + h) * D + d, o / Ls);
 }
 
 template <int D>
@@ -337,7 +346,7 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
     a.k = (const _Float16*)c.k_cache;
     a.v = (const _Float16*)c.v_cache;
     a.out = c.out;
-    a.out_f16 = c.out_f16 ? 1 : 0;
+    a.out_mode = c.out_split ? 2 : c.out_f16 ? 1 : 0;
     a.dyn_prefix = c.dyn_prefix;
     a.prefix_add = c.prefix_add;
     a.n_prefix = (int)c.n_prefix;  // with dyn_prefix: the largest prefix the call may see

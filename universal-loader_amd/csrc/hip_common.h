@@ -33,6 +33,19 @@ __device__ __forceinline__ half2_t splat2(float v)
     return h;
 }
 
+// Split operand of an fp32 activation for the fp16 MFMAs: hi = fp16(x), lo =
+// fp16((x - hi) * 2^11) (x - hi is exact in fp32), so x = hi + lo * 2^-11 to
+// about 22 bits.  Products of either part with an fp16 weight are exact in
+// fp32, so a GEMM over (hi, lo) accumulates x * w at fp32 precision.
+constexpr float kLoScale = 2048.0f;
+constexpr float kLoUnscale = 1.0f / 2048.0f;
+
+__device__ __forceinline__ void split_hl(float x, _Float16& hi, _Float16& lo)
+{
+    hi = (_Float16)x;
+    lo = (_Float16)((x - (float)hi) * kLoScale);
+}
+
 // 16x16x32 fp16 MFMA: C[i][j] += sum_k A[i][k] B[k][j].  Lane l supplies row
 // i = l % 16 of A and column j = l % 16 of B (8 k values each, the same k
 // slots in both), and holds C rows 4 * (l / 16) + 0..3 of column l % 16.

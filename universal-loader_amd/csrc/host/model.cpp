@@ -1,9 +1,10 @@
 // model.cpp -- Llama-shaped model on the device: GGUF tensors by name, fp16
 // KV cache, and the block forward of InferenceEngine::forward_layer_gpu
-// (src/inference/inference_engine.cpp:602-682) over M <= 16 rows (fewer when
-// the FFN is wide: every GEMM keeps its whole X in LDS), with every
-// linear layer on the Q4 verify dequant-GEMM and attention on the verify
-// attention kernel.
+// (src/inference/inference_engine.cpp:602-682) over M <= 16 rows, with every
+// linear layer on the verify dequant-GEMM and attention on the verify
+// attention kernel.  Activations stay fp32: each GEMM takes its input as
+// split fp16 pairs (hi, lo), so the products are fp32-exact; only the
+// attention queries and the K / V cache are fp16.
 //
 // Weight map as Model::load_from_gguf (src/inference/model.cpp:190-246):
 // "blk.N." or "layers.N." layer prefixes, GGUF and Meta tensor names.  Q, K, V
@@ -11,15 +12,17 @@
 // gate and up rows are interleaved into another (row 2i = gate i, 2i+1 = up
 // i); GGUF rows are independent block runs, so both are byte copies.
 //
-// Five kernels per layer, each a dequant-GEMM with fused steps, plus the
-// attention:
+// Five GEMMs per layer with fused steps, plus the attention:
 //   QKV   X = RMSNorm(h) in the prologue; RoPE, fp16 Q, K / V cache append in
 //         the epilogue
-//   attention over the cache -> fp16
+//   attention over the cache -> split X of O
 //   O     epilogue h += Y, with the per-tile sums of h^2 the next norm needs
-//   GU    X = RMSNorm(h); epilogue fp16 SiLU(gate) * up
+//   GU    X = RMSNorm(h); epilogue SiLU(gate) * up -> split X of down
 //   down  epilogue h += Y (+ sums of h^2)
-// and the LM head with the final RMSNorm in its prologue.
+// and the LM head with the final RMSNorm in its prologue.  Rows up to 8 whose
+// split X fits in LDS run the whole-X kernels with both steps fused; others
+// (the 7B FFN width, trees and prefill chunks past 8 rows) the split-K kernel,
+// a norm kernel before it and the epilogue in its slice reduction.
 #include "model.h"
 
 #include <cmath>
@@ -169,12 +172,20 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         }
     }
     const std::vector<Weight>& W = ctx->weights;
+    // every GEMM: split-K partials and the norm's split X when it takes the split-K path
+    auto fuse = [&]() {
+        GemmFuse f;
+        f.part = part;
+        f.part_bytes = part_bytes;
+        f.x_scratch = xn;
+        return f;
+    };
     launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss);
     int P = (int)embed_partials(c.dim);
     ulspec_status s = ULSPEC_OK;
     for (uint32_t l = 0; l < c.n_layers && s == ULSPEC_OK; ++l) {
         const Layer& L = layers[l];
-        GemmFuse q;
+        GemmFuse q = fuse();
         q.pro = kProNorm;
         q.v = h;
         q.pss = pss;
@@ -206,21 +217,21 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         a.Hkv = Hkv;
         a.D = D;
         a.scale = 1.0f / std::sqrt((float)D);
-        a.out = att16;
-        a.out_f16 = true;
+        a.out = att;
+        a.out_split = true;
         a.dyn_prefix = pos_dev;
         a.prefix_add = pos_add;
         a.part = attn_part;
         s = attn_launch(ctx, a);
         if (s != ULSPEC_OK) break;
-        GemmFuse o;
+        GemmFuse o = fuse();
         o.epi = kEpiResid;
         o.h = h;
         o.pss_out = pss;
-        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att16, M, nullptr);
+        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att, M, nullptr);
         if (s != ULSPEC_OK) break;
         P = (int)W[L.wo].n_tiles;
-        GemmFuse u;
+        GemmFuse u = fuse();
         u.pro = kProNorm;
         u.v = h;
         u.pss = pss;
@@ -228,19 +239,19 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         u.norm_w = L.ffn_norm;
         u.eps = c.rms_eps;
         u.epi = kEpiSilu;
-        u.act = act16;
+        u.act = act;
         s = gemm_fused(ctx, W[L.wgu], u, nullptr, M, nullptr);
         if (s != ULSPEC_OK) break;
-        GemmFuse d;
+        GemmFuse d = fuse();
         d.epi = kEpiResid;
         d.h = h;
         d.pss_out = pss;
-        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act16, M, nullptr);
+        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act, M, nullptr);
         P = (int)W[L.wdown].n_tiles;
     }
     if (s != ULSPEC_OK) return s;
     if (n_logits) {
-        GemmFuse z;
+        GemmFuse z = fuse();
         z.pro = kProNorm;
         z.v = h + (size_t)(M - n_logits) * c.dim;
         z.pss = pss + (size_t)(M - n_logits) * P;
@@ -271,15 +282,23 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         return fail(ctx, ULSPEC_EINVAL, "model_create: rms_eps / rope_base");
     (void)hipSetDevice(ctx->device);
     const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn, R = ulspec_model::kRows;
-    uint32_t rows = R;
-    while (rows > 0 && !(wide_fits((int)rows, c.dim) && wide_fits((int)rows, F))) --rows;
-    if (rows < 2) return fail(ctx, ULSPEC_EUNSUPPORTED, "model_create: FFN %u too wide for the whole-X GEMM", F);
     ulspec_model* m = new ulspec_model;
     m->ctx = ctx;
     m->cfg = c;
     m->head_dim = D;
     m->layers.resize(c.n_layers);
-    m->rows_max = rows;
+    m->rows_max = R;
+    // slice partials of the split-K path: the most any of the model's weights
+    // needs at R rows (slices are chosen at upload from the tile and chunk
+    // counts; ceil(K / 128) bounds the chunks of every weight type)
+    {
+        const uint32_t shapes[5][2] = {{(H + 2 * Hkv) * D, c.dim}, {c.dim, H * D}, {2 * F, c.dim}, {c.dim, F},
+                                       {c.vocab, c.dim}};
+        for (const auto& nk : shapes) {
+            const uint32_t ks = choose_ksplit((nk[0] + 15) / 16, (nk[1] + 127) / 128, ctx->n_cu);
+            m->part_bytes = std::max(m->part_bytes, (size_t)ks * R * nk[0] * sizeof(float));
+        }
+    }
     m->pss_stride = std::max(embed_partials(c.dim), (c.dim + 15) / 16);
     const size_t kv_bytes = (size_t)c.max_ctx * Hkv * D * sizeof(_Float16);
     int splits = 0, kps = 0;
@@ -293,8 +312,10 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         {(void**)&m->pss, (size_t)R * m->pss_stride * 4},
         {(void**)&m->logits, (size_t)R * c.vocab * 4},
         {(void**)&m->q16, (size_t)R * H * D * 2},
-        {(void**)&m->att16, (size_t)R * H * D * 2},
-        {(void**)&m->act16, (size_t)R * F * 2},
+        {(void**)&m->att, (size_t)2 * R * H * D * 2},
+        {(void**)&m->act, (size_t)2 * R * F * 2},
+        {(void**)&m->xn, (size_t)2 * R * c.dim * 2},
+        {(void**)&m->part, m->part_bytes},
         {(void**)&m->tok, (size_t)R * 4},
         {(void**)&m->pos, 16},
         {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},

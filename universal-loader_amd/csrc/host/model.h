@@ -42,17 +42,21 @@ struct ulspec_model {
     uint32_t w_out = ~0u;
     float2* rope = nullptr;    // [max_ctx][head_dim / 2] (cos, sin)
 
-    // activations, up to kRows rows (rows_max per forward: every GEMM's X
-    // must fit in LDS)
+    // activations, up to kRows rows per forward.  GEMM inputs are fp32
+    // activations held as split fp16 pairs [2 rows][width] (high parts, then
+    // low parts): the attention output and SiLU(gate) * up.
     static constexpr uint32_t kRows = 16;
     uint32_t rows_max = 0;
     float* h = nullptr;        // [kRows][dim] residual stream (fp32)
     float* pss = nullptr;      // [kRows][pss_stride] RMSNorm partial sums of h^2
     uint32_t pss_stride = 0;
     float* logits = nullptr;   // [kRows][vocab]
-    _Float16* q16 = nullptr;   // [kRows][H D]
-    _Float16* att16 = nullptr; // [kRows][H D]
-    _Float16* act16 = nullptr; // [kRows][F]
+    _Float16* q16 = nullptr;   // [kRows][H D] (attention queries, fp16)
+    _Float16* att = nullptr;   // split [2 kRows][H D]
+    _Float16* act = nullptr;   // split [2 kRows][F]
+    _Float16* xn = nullptr;    // split [2 kRows][dim]: RMSNorm output of the split-K path
+    float* part = nullptr;     // split-K slice partials
+    size_t part_bytes = 0;
     int32_t* tok = nullptr;    // [kRows]
     int32_t* pos = nullptr;    // [1]
     float* attn_part = nullptr;

@@ -372,55 +372,49 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w
 constexpr int kWaves = 16;
 constexpr uint32_t kOOB = 0x80000000u;  // >= any buffer's num_records
 
-template <int MT>
+// X slice of one split-K batch in LDS: 16 MT rows of UB units (16 bytes =
+// 8 halves) plus one pad unit (bank spread); UB is a power of two <= 128.
+// Thread tid stages unit tid % UB of rows tid / UB + pass * (1024 / UB).
+template <int MT, int UB>
 struct XStage {
-    static constexpr int kUnitsPerRow = 129;  // 128 units of 16 B + 1 pad (bank spread)
-    static constexpr int kRowsPerPass = kWaves * 64 / 128;
-    static constexpr int kXU = (16 * MT) / kRowsPerPass;  // passes = units per thread
+    static constexpr int kUnitsPerRow = UB + 1;
+    static constexpr int kRowsPerPass = kWaves * 64 / UB;
+    static constexpr int kXU = (16 * MT + kRowsPerPass - 1) / kRowsPerPass;  // passes = units per thread
 };
 
-// Load this batch's X slice (rows < M, units [0, U) of 16 B starting at
-// element k0, U <= 128) into registers: thread -> (row tid / 128 + pass *
-// rows-per-pass, unit tid % 128).  Units past K load 0.
-template <int MT>
-__device__ __forceinline__ void x_stage_load(__amdgpu_buffer_rsrc_t xr, uint4 (&xv)[XStage<MT>::kXU], int M, int K,
-                                             int k0, int U)
+// Load this batch's X slice (rows < M, units [0, U) starting at element k0,
+// U <= UB) into registers.  Units past K load 0.
+template <int MT, int UB>
+__device__ __forceinline__ void x_stage_load(__amdgpu_buffer_rsrc_t xr, uint4 (&xv)[XStage<MT, UB>::kXU], int M,
+                                             int K, int k0, int U)
 {
-    const int uu = threadIdx.x & 127, m0 = threadIdx.x >> 7;
+    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
     const int k = k0 + 8 * uu;
 #pragma unroll
-    for (int u = 0; u < XStage<MT>::kXU; ++u) {
-        const int m = m0 + u * XStage<MT>::kRowsPerPass;
+    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
+        const int m = m0 + u * XStage<MT, UB>::kRowsPerPass;
         const bool ok = m < M && uu < U && k < K;
         xv[u] = buf_load16(xr, ok ? (uint32_t)(m * K + k) * 2u : kOOB);
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void x_stage_store(uint4* xs, const uint4 (&xv)[XStage<MT>::kXU], int M, int U)
+template <int MT, int UB>
+__device__ __forceinline__ void x_stage_store(uint4* xs, const uint4 (&xv)[XStage<MT, UB>::kXU], int M, int U)
 {
-    const int uu = threadIdx.x & 127, m0 = threadIdx.x >> 7;
+    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
 #pragma unroll
-    for (int u = 0; u < XStage<MT>::kXU; ++u) {
-        const int m = m0 + u * XStage<MT>::kRowsPerPass;
-        if (m < M && uu < U) xs[m * XStage<MT>::kUnitsPerRow + uu] = xv[u];
+    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
+        const int m = m0 + u * XStage<MT, UB>::kRowsPerPass;
+        if (m < M && uu < U) xs[m * XStage<MT, UB>::kUnitsPerRow + uu] = xv[u];
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void store_tile(const float4_t (&acc)[MT], float* __restrict__ out, int M, int N, int t)
-{
-    const int lane = threadIdx.x & 63;
-    const int n = 16 * t + (lane & 15);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = mt * 16 + 4 * (lane >> 4) + i;
-            if (m < M && n < N) out[(size_t)m * N + n] = acc[mt][i];
-        }
-}
-
+// X operand: fp16 rows [M][K] (hl = 0), or split fp32 activations (hl = 1):
+// rows [2M][K], the high parts of rows 0..M-1 then their low parts (split_hl).
+// In split mode an MFMA covers 8 output rows: A-operand slots 0-7 take the
+// high parts of 8 rows, slots 8-15 the low parts of the same rows, and the
+// two halves of the result are added in the epilogue (hi + lo * 2^-11), so
+// M <= 8 per 16-column tile.
 struct GemmArgs {
     const uint8_t* w;
     uint32_t w_bytes;
@@ -428,167 +422,32 @@ struct GemmArgs {
     float* out;  // Y when ks_count == 1, else partials [ks_count][M][N]
     int M, N, K, n_tiles, n_chunks, ks_count;
     int ks_q, ks_r;  // n_chunks = ks_q * ks_count + ks_r; slice s starts at s * ks_q + min(s, ks_r)
-    GemmFuse f;      // whole-X kernels only
+    int hl;          // split X (see above)
+    int xrows;       // rows of X: M, or 2M when split
+    GemmFuse f;      // epilogue (and the whole-X kernels' prologue)
 };
+
+// Row of X that A-operand slot r (0..15) of column tile mt reads; slots past
+// the last row repeat it (their outputs are never stored).
+__device__ __forceinline__ int xslot_row(const GemmArgs& a, int mt, int r)
+{
+    if (!a.hl) return min(16 * mt + r, a.M - 1);
+    const int m = min(8 * mt + (r & 7), a.M - 1);
+    return r < 8 ? m : a.M + m;
+}
+
+// Output row of accumulator element i of lane `lane` in column tile mt, or
+// -1 where the element is a low-part slot of split X.
+__device__ __forceinline__ int acc_row(const GemmArgs& a, int mt, int lane, int i)
+{
+    if (!a.hl) return 16 * mt + 4 * (lane >> 4) + i;
+    return lane < 32 ? 8 * mt + 4 * (lane >> 4) + i : -1;
+}
 
 __device__ __forceinline__ void slice_range(const GemmArgs& a, int ks, int& lo, int& hi)
 {
     lo = ks * a.ks_q + min(ks, a.ks_r);
     hi = lo + a.ks_q + (ks < a.ks_r ? 1 : 0);
-}
-
-template <int MT, int CMAX>
-__global__ __launch_bounds__(kWaves * 64) void gemm_q4_0_kernel(GemmArgs a)
-{
-    __shared__ uint4 xs[16 * MT * XStage<MT>::kUnitsPerRow];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int t = blockIdx.x * kWaves + wave;
-    const bool tile_live = t < a.n_tiles;
-    const int ks = blockIdx.y;
-    int qa, qb;
-    slice_range(a, ks, qa, qb);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + lane * 16;
-    const uint32_t s_lane = (uint32_t)t * a.n_chunks * kQ40Chunk + 1024 + r * 8;
-    int xrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + r, a.M - 1) * XStage<MT>::kUnitsPerRow;
-    const NibbleConsts nk = nibble_consts();
-    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-    float4_t acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = zero4;
-
-    for (int c0 = qa; c0 < qb; c0 += CMAX) {
-        const int nc = min(CMAX, qb - c0);
-        uint4 xv[XStage<MT>::kXU];
-        x_stage_load<MT>(xr, xv, a.M, a.K, c0 * 128, 16 * nc);
-        pin_loads();
-        uint4 wq[CMAX];
-        uint2 sc[CMAX];
-#pragma unroll
-        for (int i = 0; i < CMAX; ++i) {
-            const bool ok = tile_live && i < nc;
-            const uint32_t o = (uint32_t)(c0 + i) * kQ40Chunk;
-            wq[i] = buf_load16(wr, ok ? w_lane + o : kOOB);
-            sc[i] = buf_load8(wr, ok ? s_lane + o : kOOB);
-        }
-        pin_loads();
-        if (c0 != qa) __syncthreads();  // previous batch done reading xs
-        x_stage_store<MT>(xs, xv, a.M, 16 * nc);
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < CMAX; ++i) {
-            if (i < nc) {
-                const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
-                const uint32_t sw[2] = {sc[i].x, sc[i].y};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const half8_t B = dequant_q4_0(words[j], nk);
-                    const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 16 * i + 4 * j + g]);
-                        const float4_t pr = mfma16x16x32(A, B, zero4);
-                        acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
-                    }
-                }
-            }
-        }
-    }
-    if (tile_live) store_tile<MT>(acc, a.out + (size_t)ks * a.M * a.N, a.M, a.N, t);
-}
-
-template <int MT, int CMAX>
-__global__ __launch_bounds__(kWaves * 64) void gemm_q4_k_kernel(GemmArgs a)
-{
-    __shared__ uint4 xs[16 * MT * XStage<MT>::kUnitsPerRow];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int t = blockIdx.x * kWaves + wave;
-    const bool tile_live = t < a.n_tiles;
-    const int ks = blockIdx.y;
-    int sa, sb;
-    slice_range(a, ks, sa, sb);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u);
-    const uint32_t w_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + lane * 16;
-    const uint32_t h_lane = (uint32_t)t * a.n_chunks * kQ4KChunk + 2048 + r * 16;
-    int xrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xrow[mt] = min(mt * 16 + r, a.M - 1) * XStage<MT>::kUnitsPerRow + 8 * g;
-    const NibbleConsts nk = nibble_consts();
-    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-    float4_t acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = zero4;
-
-    for (int s0 = sa; s0 < sb; s0 += CMAX) {
-        const int nc = min(CMAX, sb - s0);
-        uint4 xv[XStage<MT>::kXU];
-        x_stage_load<MT>(xr, xv, a.M, a.K, s0 * 256, 32 * nc);
-        pin_loads();
-        uint4 w0[CMAX], w1[CMAX], hd[CMAX];
-#pragma unroll
-        for (int i = 0; i < CMAX; ++i) {
-            const bool ok = tile_live && i < nc;
-            const uint32_t o = (uint32_t)(s0 + i) * kQ4KChunk;
-            w0[i] = buf_load16(wr, ok ? w_lane + o : kOOB);
-            w1[i] = buf_load16(wr, ok ? w_lane + o + 1024 : kOOB);
-            hd[i] = buf_load16(wr, ok ? h_lane + o : kOOB);
-        }
-        pin_loads();
-        if (s0 != sa) __syncthreads();
-        x_stage_store<MT>(xs, xv, a.M, 32 * nc);
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < CMAX; ++i) {
-            if (i < nc) {
-                const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
-                const uint4 h = hd[i];
-                const float d = half_bits_to_float(h.x & 0xffffu);
-                const float dmin = half_bits_to_float(h.x >> 16);
-                SubScale ss[2];
-                half8_t mins[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    uint32_t scv, mn;
-                    q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
-                    const float fs = (float)scv;
-                    ss[e].sc = splat2(fs);
-                    ss[e].nsc1024 = splat2(-1024.0f * fs);
-                    ss[e].sc16 = splat2(fs * 0.0625f);
-                    ss[e].nsc64 = splat2(-64.0f * fs);
-                    const _Float16 hm = (_Float16)(float)mn;
-                    mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
-                }
-                float4_t P1[MT], P2[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    P1[mt] = zero4;
-                    P2[mt] = zero4;
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 32 * i + j]);
-                        P1[mt] = mfma16x16x32(A, B, P1[mt]);
-                        P2[mt] = mfma16x16x32(A, mins[j >> 2], P2[mt]);
-                    }
-                }
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
-                    acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
-                }
-            }
-        }
-    }
-    if (tile_live) store_tile<MT>(acc, a.out + (size_t)ks * a.M * a.N, a.M, a.N, t);
 }
 
 // ---- whole-X streaming kernels (small M) --------------------------------------
@@ -611,7 +470,7 @@ __host__ __device__ constexpr uint32_t wide_pitch(uint32_t K)
     return ((2u * K + 1023u) / 1024u) * 1024u + 16u;
 }
 
-// This wave's own part of X: rows 0..M-1, chunks [ca, cb) (16-byte units
+// This wave's own part of X: rows 0..xrows-1, chunks [ca, cb) (16-byte units
 // [ua, ub) of each row); element (m, k) goes to LDS byte m * wide_pitch(K) +
 // 2 k.  A wave reads X only inside its own part, so it waits for its own
 // copies (vmcnt) and no other wave's: no barrier before the first multiply.
@@ -629,7 +488,7 @@ __device__ __forceinline__ void x_copy_own(const GemmArgs& a, __amdgpu_buffer_rs
     const int ua = ca * UPC, ub = cb * UPC;
     const int np = ub > ua ? (ub - ua + 63) / 64 : 0;
     const uint32_t pitch = wide_pitch(a.K);
-    for (int m = 0; m < a.M; ++m) {
+    for (int m = 0; m < a.xrows; ++m) {
         for (int q = 0; q < np; ++q) {
             int s0 = ua + 64 * q;
             if (s0 + 64 > ub) s0 = max(ub - 64, 0);
@@ -656,10 +515,12 @@ __device__ __forceinline__ void q4_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint3
     }
 }
 
-// acc += the batch's chunks; A rows come from LDS (unit index xrow + 4 * block).
-template <int CMAX>
-__device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&wq)[CMAX],
-                                               const uint2 (&sc)[CMAX], const NibbleConsts& nk, float4_t& acc)
+// acc[mt] += the batch's chunks; A rows of column tile mt come from LDS (unit
+// index xrow[mt] + 4 * block).
+template <int CMAX, int MT>
+__device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
+                                               const uint4 (&wq)[CMAX], const uint2 (&sc)[CMAX],
+                                               const NibbleConsts& nk, float4_t (&acc)[MT])
 {
     const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -671,9 +532,12 @@ __device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, int xrow, int c0
             for (int j = 0; j < 4; ++j) {
                 const half8_t B = dequant_q4_0(words[j], nk);
                 const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]);
-                const float4_t pr = mfma16x16x32(A, B, zero4);
-                acc = __builtin_elementwise_fma((float4_t)d, pr, acc);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]);
+                    const float4_t pr = mfma16x16x32(A, B, zero4);
+                    acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
+                }
             }
         }
     }
@@ -704,10 +568,11 @@ __device__ __forceinline__ half8_t dequant_q8_0(uint32_t lo, uint32_t hi)
     return __builtin_bit_cast(half8_t, u) - (half8_t)(_Float16)1152.0f;
 }
 
-// acc += d_block * (A . q) per block, as for Q4_0.
-template <int CMAX>
-__device__ __forceinline__ void q8_0_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&w0)[CMAX],
-                                               const uint4 (&w1)[CMAX], const uint2 (&sc)[CMAX], float4_t& acc)
+// acc[mt] += d_block * (A . q) per block, as for Q4_0.
+template <int CMAX, int MT>
+__device__ __forceinline__ void q8_0_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
+                                               const uint4 (&w0)[CMAX], const uint4 (&w1)[CMAX],
+                                               const uint2 (&sc)[CMAX], float4_t (&acc)[MT])
 {
     const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -719,9 +584,12 @@ __device__ __forceinline__ void q8_0_mma_batch(const uint4* xs, int xrow, int c0
             for (int j = 0; j < 4; ++j) {
                 const half8_t B = dequant_q8_0(words[2 * j], words[2 * j + 1]);
                 const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]);
-                const float4_t pr = mfma16x16x32(A, B, zero4);
-                acc = __builtin_elementwise_fma((float4_t)d, pr, acc);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]);
+                    const float4_t pr = mfma16x16x32(A, B, zero4);
+                    acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
+                }
             }
         }
     }
@@ -792,7 +660,7 @@ __device__ __forceinline__ int epi_nloads(const GemmArgs& a)
 //          K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim], pos = pos0 + m
 //          (y0 = x0 c - x1 s, y1 = x0 s + x1 c; src/shaders/rope.glsl:50-73)
 //   silu:  rows interleaved (2i = gate i, 2i+1 = up i):
-//          act[m][i] = fp16(g * (1 / (1 + e^-g)) * u)
+//          a = g * (1 / (1 + e^-g)) * u, split: act[m][i] = hi, act[M + m][i] = lo
 //   resid: h[m][n] += s (in place); pss[m][t] = sum over the tile's 16 columns
 //          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m
 __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l, float2 pre, int pos0)
@@ -828,7 +696,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
         const float u = __shfl_xor(s, 1);
         if (ok && !(n & 1)) {
             const float sg = s * (1.0f / (1.0f + det_expf(-s)));
-            f.act[(size_t)m * (a.N / 2) + n / 2] = (_Float16)(sg * u);
+            _Float16 hi, lo;
+            split_hl(sg * u, hi, lo);
+            f.act[(size_t)m * (a.N / 2) + n / 2] = hi;
+            f.act[(size_t)(a.M + m) * (a.N / 2) + n / 2] = lo;
         }
         break;
     }
@@ -851,7 +722,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
     }
 }
 
-// X[m][k] = fp16((v[m][k] * r_m) * w[k]) into the LDS rows, r_m = 1 /
+// X[m][k] = (v[m][k] * r_m) * w[k] into the LDS rows (fp16, or split into
+// rows m and M + m when a.hl), r_m = 1 /
 // sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
 // Two phases so that the weight loads overlap the norm: norm_issue loads the
 // partial sums (rows wave and wave + NW, P <= 256, one 16-byte load per row),
@@ -953,12 +825,18 @@ __device__ __forceinline__ void norm_finish(const GemmArgs& a, NormRegs<NW>& n, 
                     const int m = m0 + i;
                     if (m < a.M) {
                         const float r = rs[m];
-                        half4_t x;
-                        x[0] = (_Float16)((n.vv[i][j].x * r) * n.w[j].x);
-                        x[1] = (_Float16)((n.vv[i][j].y * r) * n.w[j].y);
-                        x[2] = (_Float16)((n.vv[i][j].z * r) * n.w[j].z);
-                        x[3] = (_Float16)((n.vv[i][j].w * r) * n.w[j].w);
+                        const float v[4] = {(n.vv[i][j].x * r) * n.w[j].x, (n.vv[i][j].y * r) * n.w[j].y,
+                                            (n.vv[i][j].z * r) * n.w[j].z, (n.vv[i][j].w * r) * n.w[j].w};
+                        half4_t x, xl;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            _Float16 hi, lo;
+                            split_hl(v[e], hi, lo);
+                            x[e] = hi;
+                            xl[e] = lo;
+                        }
                         *(half4_t*)(xs + m * pitch + 8 * c) = x;
+                        if (a.hl) *(half4_t*)(xs + (a.M + m) * pitch + 8 * c) = xl;
                     }
                 }
             }
@@ -979,11 +857,12 @@ __device__ __forceinline__ void q4_k_load_batch(__amdgpu_buffer_rsrc_t wr, uint3
     }
 }
 
-// acc += the batch's super-blocks; A rows from LDS (unit xrow + 32 * sb + j).
-template <int CMAX>
-__device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, int xrow, int s0, int nc, const uint4 (&w0)[CMAX],
-                                               const uint4 (&w1)[CMAX], const uint4 (&hd)[CMAX], int g,
-                                               const NibbleConsts& nk, float4_t& acc)
+// acc[mt] += the batch's super-blocks; A rows from LDS (unit xrow[mt] + 32 * sb + j).
+template <int CMAX, int MT>
+__device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, const int (&xrow)[MT], int s0, int nc,
+                                               const uint4 (&w0)[CMAX], const uint4 (&w1)[CMAX],
+                                               const uint4 (&hd)[CMAX], int g, const NibbleConsts& nk,
+                                               float4_t (&acc)[MT])
 {
     const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1007,16 +886,27 @@ __device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, int xrow, int s0
                 const _Float16 hm = (_Float16)(float)mn;
                 mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
             }
-            float4_t P1 = zero4, P2 = zero4;
+            float4_t P1[MT], P2[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                P1[mt] = zero4;
+                P2[mt] = zero4;
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
-                const half8_t A = __builtin_bit_cast(half8_t, xs[xrow + 32 * (s0 + i) + j]);
-                P1 = mfma16x16x32(A, B, P1);
-                P2 = mfma16x16x32(A, mins[j >> 2], P2);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 32 * (s0 + i) + j]);
+                    P1[mt] = mfma16x16x32(A, B, P1[mt]);
+                    P2[mt] = mfma16x16x32(A, mins[j >> 2], P2[mt]);
+                }
             }
-            acc = __builtin_elementwise_fma((float4_t)d, P1, acc);
-            acc = __builtin_elementwise_fma((float4_t)(-dmin), P2, acc);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
+                acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
+            }
         }
     }
 }
@@ -1060,18 +950,20 @@ __device__ __forceinline__ void f16_load_batch(__amdgpu_buffer_rsrc_t wr, uint32
             w[i][j] = buf_load16(wr, i < nc ? w_lane + (uint32_t)(c0 + i) * kF16Chunk + 1024u * j : kOOB);
 }
 
-// acc += the batch's chunks: four MFMAs of 32 K per chunk, no dequantization
-template <int CMAX>
-__device__ __forceinline__ void f16_mma_batch(const uint4* xs, int xrow, int c0, int nc, const uint4 (&w)[CMAX][4],
-                                              float4_t& acc)
+// acc[mt] += the batch's chunks: four MFMAs of 32 K per chunk, no dequantization
+template <int CMAX, int MT>
+__device__ __forceinline__ void f16_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
+                                              const uint4 (&w)[CMAX][4], float4_t (&acc)[MT])
 {
 #pragma unroll
     for (int i = 0; i < CMAX; ++i)
         if (i < nc)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                acc = mfma16x16x32(__builtin_bit_cast(half8_t, xs[xrow + 4 * (4 * (c0 + i) + j)]),
-                                   __builtin_bit_cast(half8_t, w[i][j]), acc);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt] = mfma16x16x32(__builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]),
+                                           __builtin_bit_cast(half8_t, w[i][j]), acc[mt]);
 }
 
 template <int TYPE, int CMAX>
@@ -1093,18 +985,52 @@ __device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_r
                               b.hd);
 }
 
+template <int TYPE, int CMAX, int MT>
+__device__ __forceinline__ void stream_mma_mt(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
+                                              const WBatch<TYPE, CMAX>& b, const NibbleConsts& nk,
+                                              float4_t (&acc)[MT])
+{
+    if constexpr (TYPE == ULSPEC_GGML_F16)
+        f16_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
+        q8_0_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w0, b.w1, b.sc, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+        q4_0_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
+    else
+        q4_k_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w0, b.w1, b.hd, (threadIdx.x & 63) >> 4, nk, acc);
+}
+
 template <int TYPE, int CMAX>
 __device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, int nc, const WBatch<TYPE, CMAX>& b,
                                            const NibbleConsts& nk, float4_t& acc)
 {
-    if constexpr (TYPE == ULSPEC_GGML_F16)
-        f16_mma_batch<CMAX>(xs, xrow, c0, nc, b.w, acc);
-    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
-        q8_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.w0, b.w1, b.sc, acc);
-    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
-        q4_0_mma_batch<CMAX>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
-    else
-        q4_k_mma_batch<CMAX>(xs, xrow, c0, nc, b.w0, b.w1, b.hd, (threadIdx.x & 63) >> 4, nk, acc);
+    const int xr[1] = {xrow};
+    float4_t ac[1] = {acc};
+    stream_mma_mt<TYPE, CMAX, 1>(xs, xr, c0, nc, b, nk, ac);
+    acc = ac[0];
+}
+
+// Output row the epilogue thread (lane l, accumulator row `row`) of a
+// whole-X kernel handles: row 4 (l / 16) + row; with split X the lanes 32-63
+// (the low-part slots) handle none (M).
+__device__ __forceinline__ int epi_row(const GemmArgs& a, int l, int row)
+{
+    return a.hl && l >= 32 ? a.M : 4 * (l >> 4) + row;
+}
+
+// Sum of the P part sums of tile slot j in LDS, in part order; with split X
+// the high-part sum (lane l) plus 2^-11 times the low-part sum (lane l + 32).
+__device__ __forceinline__ float red_sum(const GemmArgs& a, const float* red, int j, int P, int row, int l)
+{
+    float s = red[((j * P) * 4 + row) * 64 + l];
+    for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
+    if (a.hl) {
+        const int lo_lane = l ^ 32;
+        float t = red[((j * P) * 4 + row) * 64 + lo_lane];
+        for (int p = 1; p < P; ++p) t += red[((j * P + p) * 4 + row) * 64 + lo_lane];
+        s = s + t * kLoUnscale;
+    }
+    return s;
 }
 
 // Multiply this wave's part of tile slot tw of iteration `it` (first batch
@@ -1132,10 +1058,9 @@ __device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_r
     // 256 threads per tile slot, NW / 4 slots per pass
     const int row = (threadIdx.x >> 6) & 3, l = lane;
     for (int j = threadIdx.x >> 8; j < tpi; j += NW / 4) {
-        float s = red[((j * P) * 4 + row) * 64 + l];
-        for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
+        const float s = red_sum(a, red, j, P, row, l);
         const int tt = it * tpi + j;
-        const int m = 4 * (l >> 4) + row, n = 16 * tt + (l & 15);
+        const int m = epi_row(a, l, row), n = 16 * tt + (l & 15);
         epilogue(a, s, m, n, tt, l, pre0 ? *pre0 : epi_load(a, m, n, pos0), pos0);
     }
 }
@@ -1164,7 +1089,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int n_iter = (a.n_tiles + tpi - 1) / tpi;
     const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const int xrow = xslot_row(a, 0, r) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
     const NibbleConsts nk = nibble_consts();
     const int pos0 = epi_pos0(a);
 
@@ -1172,7 +1097,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     if constexpr (NORM)
         norm_issue<NW>(a, nr);
     else
-        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
+        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
                                          min(cb, a.n_chunks));
     pin_loads();
     WBatch<TYPE, CMAX> A;
@@ -1182,7 +1107,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     // (tile slot 0 is the only one, tpi = 1) load with the weights
     float2 pre0 = {0.f, 0.f};
     if constexpr (!PIPE)
-        pre0 = epi_load(a, (threadIdx.x >> 8) == 0 ? 4 * (lane >> 4) + ((threadIdx.x >> 6) & 3) : a.M,
+        pre0 = epi_load(a, (threadIdx.x >> 8) == 0 ? epi_row(a, lane, (threadIdx.x >> 6) & 3) : a.M,
                         16 * it + (lane & 15), pos0);
     pin_loads();
     if constexpr (NORM) {
@@ -1240,10 +1165,9 @@ __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc
     lds_barrier();
     const int row = (threadIdx.x >> 6) & 3, l = lane, j = threadIdx.x >> 8;
     if (j < tpi) {
-        float s = red[((j * P) * 4 + row) * 64 + l];
-        for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
+        const float s = red_sum(a, red, j, P, row, l);
         const int tt = it * tpi + j;
-        epilogue(a, s, 4 * (l >> 4) + row, 16 * tt + (l & 15), tt, l, pre, pos0);
+        epilogue(a, s, epi_row(a, l, row), 16 * tt + (l & 15), tt, l, pre, pos0);
     }
 }
 
@@ -1252,7 +1176,7 @@ __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc
 __device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, int pos0)
 {
     const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = threadIdx.x >> 8;
-    const int m = j < tpi ? 4 * (l >> 4) + row : a.M;
+    const int m = j < tpi ? epi_row(a, l, row) : a.M;
     return epi_load(a, m, 16 * (it * tpi + j) + (l & 15), pos0);
 }
 
@@ -1273,7 +1197,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const uint32_t pitch = wide_pitch(a.K);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = min(r, a.M - 1) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const int xrow = xslot_row(a, 0, r) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
@@ -1285,7 +1209,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     if constexpr (NORM)
         norm_issue<NW>(a, nr);
     else
-        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.M * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
+        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
                                          ca + nc);
     pin_loads();
     WBatch<TYPE, C> ring[D];
@@ -1319,38 +1243,153 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     }
 }
 
-// Y[i] = sum over slices in slice order (deterministic); all loads issued
-// before the first add.
+// ---- split-K kernels (any M) --------------------------------------------------
+// Grid (row groups of kWaves 16-row tiles, K slices).  Wave w of a workgroup
+// owns tile blockIdx.x * kWaves + w over the slice's chunks.  Per batch of
+// CMAX chunks: the batch's X units to registers, every weight load of the
+// batch, X to LDS (XStage rows), barrier, dequantize + MFMA for the MT column
+// tiles.  Out-of-range chunks (past the slice or the last tile) load from an
+// offset past the buffer, which returns 0 and moves no data.  Each wave
+// accumulates its chunks in K order and stores the slice's partial Y (high
+// plus 2^-11 low part for split X) to out[ks][M][N]; gemm_reduce_kernel sums
+// the slices in slice order, so every output row is bitwise independent of M.
 constexpr int kMaxSlices = 32;
 
-__global__ __launch_bounds__(256) void reduce_slices_kernel(const float* __restrict__ part, float* __restrict__ Y,
-                                                            int MN, int ks_count)
+template <int TYPE, int MT, int CMAX>
+__global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
+{
+    constexpr int UPC = kUnitsPerChunk<TYPE>;
+    constexpr int UB = UPC * CMAX;
+    using XS = XStage<MT, UB>;
+    __shared__ uint4 xs[16 * MT * XS::kUnitsPerRow];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x * kWaves + wave;
+    const bool live = t < a.n_tiles;
+    const int ks = blockIdx.y;
+    int ca, cb;
+    slice_range(a, ks, ca, cb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u);
+    int xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const NibbleConsts nk = nibble_consts();
+    float4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = ca; c0 < cb; c0 += CMAX) {
+        const int nc = min(CMAX, cb - c0);
+        uint4 xv[XS::kXU];
+        x_stage_load<MT, UB>(xr, xv, a.xrows, a.K, c0 * UPC * 8, UPC * nc);
+        pin_loads();
+        WBatch<TYPE, CMAX> b;
+        stream_load<TYPE, CMAX>(a, wr, live ? t : a.n_tiles, c0, nc, b);
+        pin_loads();
+        if (c0 != ca) __syncthreads();  // the previous batch is done reading xs
+        x_stage_store<MT, UB>(xs, xv, a.xrows, UPC * nc);
+        __syncthreads();
+        stream_mma_mt<TYPE, CMAX, MT>(xs, xrow, 0, live ? nc : 0, b, nk, acc);
+    }
+    if (!live) return;  // wave-uniform
+    float* out = a.out + (size_t)ks * a.M * a.N;
+    const int n = 16 * t + r;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v = acc[mt][i];
+            if (a.hl) v = v + __shfl_xor(v, 32) * kLoUnscale;  // lanes 0-31: + their low-part slot
+            const int m = acc_row(a, mt, lane, i);
+            if (m >= 0 && m < a.M && n < a.N) out[(size_t)m * a.N + n] = v;
+        }
+}
+
+// Y[m][n] = the sum of the ks_count slices of part in slice order, then the
+// epilogue of output (m, n) (a.out is Y for the store epilogue).  One thread
+// per element of the padded [M][16 n_tiles] grid, n fastest, so a 16-lane
+// group is one row of one tile (the epilogue's lane pairs and xor tree).
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const float* __restrict__ part)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= MN) return;
+    const int NP = 16 * a.n_tiles;
+    const int m = i / NP, n = i - m * NP;
+    const int pos0 = epi_pos0(a);
+    const bool ok = m < a.M && n < a.N;
+    const size_t MN = (size_t)a.M * a.N;
     float v[kMaxSlices];
 #pragma unroll
-    for (int k = 0; k < kMaxSlices; ++k) v[k] = k < ks_count ? part[(size_t)k * MN + i] : 0.0f;
+    for (int k = 0; k < kMaxSlices; ++k) v[k] = ok && k < a.ks_count ? part[k * MN + (size_t)m * a.N + n] : 0.0f;
+    const float2 pre = epi_load(a, m < a.M ? m : a.M, n, pos0);
     float s = v[0];
 #pragma unroll
     for (int k = 1; k < kMaxSlices; ++k)
-        if (k < ks_count) s += v[k];
-    Y[i] = s;
+        if (k < a.ks_count) s += v[k];
+    epilogue(a, s, m, n, n >> 4, threadIdx.x & 63, pre, pos0);
 }
 
-constexpr int kQ40CMax = 8;
-constexpr int kQ4KCMax = 4;
+// Split X of the RMSNorm for the split-K path: x[m][k] = (v[m][k] * r_m) *
+// w[k] split into rows m (hi) and M + m (lo), r_m = 1 / sqrt(sum_p pss[m][p] /
+// K + eps), the partial sums reduced as the whole-X prologue reduces them.
+// One 256-thread workgroup per row.
+__global__ __launch_bounds__(256) void norm_split_kernel(GemmFuse f, int M, int K, _Float16* __restrict__ x)
+{
+    __shared__ float rs;
+    const int m = blockIdx.x, lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {
+        const int p0 = 4 * lane;
+        float pv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pv[e] = p0 + e < f.P ? f.pss[(size_t)m * f.P + p0 + e] : 0.0f;
+        float ss = (pv[0] + pv[1]) + (pv[2] + pv[3]);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) rs = 1.0f / __builtin_sqrtf(ss / (float)K + f.eps);
+    }
+    __syncthreads();
+    const float r = rs;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        _Float16 hi, lo;
+        split_hl((f.v[(size_t)m * K + k] * r) * f.norm_w[k], hi, lo);
+        x[(size_t)m * K + k] = hi;
+        x[(size_t)(M + m) * K + k] = lo;
+    }
+}
+
 constexpr int kQ40Stream = 12;
 constexpr int kQ4KStream = 6;
 
-template <int MT>
-void launch_mt(const Weight& w, const GemmArgs& a, hipStream_t st)
+// Chunks per batch of the split-K kernel: about 32 weight registers per lane
+// (Q4_0 6 per chunk, Q4_K 12, Q8_0 10, F16 16) up to two column tiles, half
+// that beyond (Q4_K: one super-block past four tiles, whose two partial sums
+// per tile take 8 registers each); a batch covers at most 1024 K (128 X units).
+template <int TYPE, int MT>
+constexpr int slice_cmax()
 {
-    const dim3 grid((w.n_tiles + kWaves - 1) / kWaves, w.ksplit);
-    if (w.type == ULSPEC_GGML_Q4_0)
-        hipLaunchKernelGGL((gemm_q4_0_kernel<MT, kQ40CMax>), grid, dim3(kWaves * 64), 0, st, a);
-    else
-        hipLaunchKernelGGL((gemm_q4_k_kernel<MT, (MT >= 3 ? 2 : kQ4KCMax)>), grid, dim3(kWaves * 64), 0, st, a);
+    return TYPE == ULSPEC_GGML_Q4_0 ? (MT <= 2 ? 8 : 4)
+           : TYPE == ULSPEC_GGML_Q4_K ? (MT <= 2 ? 4 : MT <= 4 ? 2 : 1)
+           : TYPE == ULSPEC_GGML_Q8_0 ? (MT <= 2 ? 4 : 2)
+                                       : (MT <= 2 ? 2 : 1);
+}
+
+template <int TYPE, int MT>
+void slice_launch_mt(const GemmArgs& a, hipStream_t st)
+{
+    const dim3 grid((a.n_tiles + kWaves - 1) / kWaves, a.ks_count);
+    hipLaunchKernelGGL((gemm_slice_kernel<TYPE, MT, slice_cmax<TYPE, MT>()>), grid, dim3(kWaves * 64), 0, st, a);
+}
+
+template <int TYPE>
+void slice_launch_t(const GemmArgs& a, int mt, hipStream_t st)
+{
+    switch (mt) {
+    case 1: slice_launch_mt<TYPE, 1>(a, st); break;
+    case 2: slice_launch_mt<TYPE, 2>(a, st); break;
+    case 3: slice_launch_mt<TYPE, 3>(a, st); break;
+    case 4: slice_launch_mt<TYPE, 4>(a, st); break;
+    default: slice_launch_mt<TYPE, 6>(a, st); break;
+    }
 }
 
 }  // namespace
@@ -1362,9 +1401,9 @@ namespace ulspec {
 constexpr size_t kWideLdsMax = 160 * 1024;
 constexpr size_t kStreamStatic = kWideWaves * 4 * 64 * sizeof(float) + 512;
 
-bool wide_fits(int M, uint32_t K)
+bool wide_fits(int rows, uint32_t K)
 {
-    return M <= 16 && (size_t)M * wide_pitch(K) <= kWideLdsMax - kStreamStatic;
+    return rows <= 16 && (size_t)rows * wide_pitch(K) <= kWideLdsMax - kStreamStatic;
 }
 
 // Opt the whole-X kernels in to the LDS they need for X.
@@ -1490,7 +1529,7 @@ void stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     const int n_cu = std::max(1, ctx->n_cu);
     const bool pipe = (int)w.n_tiles > n_cu;
-    const size_t lds = (size_t)a.M * wide_pitch(w.k);
+    const size_t lds = (size_t)a.xrows * wide_pitch(w.k);
     const bool norm = a.f.pro == kProNorm;
     hipStream_t st = ctx->stream;
     auto split = [&](int P) {
@@ -1561,74 +1600,104 @@ uint32_t choose_ksplit(uint32_t n_tiles, uint32_t n_chunks, int n_cu)
 
 size_t gemm_workspace_bytes(const Weight& w)
 {
-    return w.ksplit > 1 ? (size_t)w.ksplit * 64 * w.n * sizeof(float) : 0;
+    return w.ksplit > 1 ? (size_t)w.ksplit * kGemmRowsH16 * w.n * sizeof(float) : 0;
 }
 
-// Launch the GEMM for one weight; rows of X beyond 64 go in further launches.
-// Never allocates (the slice workspace is sized at upload).
-ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y)
-{
-    const _Float16* X = reinterpret_cast<const _Float16*>(x);
-    if (gemm_workspace_bytes(w) > ctx->ws_bytes)
-        return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
-    // fp16 and Q8_0 weights have no split-K kernel: rows go in groups that fit in LDS
-    uint32_t group = 64;
-    if (w.type == ULSPEC_GGML_F16 || w.type == ULSPEC_GGML_Q8_0)
-        while (group > 1 && !wide_fits((int)group, w.k)) --group;
-    for (uint32_t m0 = 0; m0 < M; m0 += group) {
-        const int mc = (int)std::min<uint32_t>(group, M - m0);
-        GemmArgs a;
-        a.w = w.dev;
-        a.w_bytes = (uint32_t)w.bytes;
-        a.x = X + (size_t)m0 * w.k;
-        a.out = w.ksplit > 1 ? (float*)ctx->ws : y + (size_t)m0 * w.n;
-        a.M = mc;
-        a.N = (int)w.n;
-        a.K = (int)w.k;
-        a.n_tiles = (int)w.n_tiles;
-        a.n_chunks = (int)w.n_chunks;
-        a.ks_count = (int)w.ksplit;
-        a.ks_q = (int)(w.n_chunks / w.ksplit);
-        a.ks_r = (int)(w.n_chunks % w.ksplit);
-        a.f = GemmFuse();
-        if (wide_fits(mc, w.k)) {  // whole X in LDS, parts summed in the kernel
-            a.out = y + (size_t)m0 * w.n;
-            stream_launch(ctx, w, a);
-            continue;
-        }
-        switch ((mc + 15) / 16) {
-        case 1: launch_mt<1>(w, a, ctx->stream); break;
-        case 2: launch_mt<2>(w, a, ctx->stream); break;
-        case 3: launch_mt<3>(w, a, ctx->stream); break;
-        default: launch_mt<4>(w, a, ctx->stream); break;
-        }
-        if (w.ksplit > 1) {
-            const int MN = mc * (int)w.n;
-            hipLaunchKernelGGL(reduce_slices_kernel, dim3((MN + 255) / 256), dim3(256), 0, ctx->stream,
-                               (const float*)ctx->ws, y + (size_t)m0 * w.n, MN, (int)w.ksplit);
-        }
-    }
-    return check_launch(ctx, "verify_gemm launch");
-}
+namespace {
 
-ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y)
+GemmArgs make_args(const Weight& w, const _Float16* x, uint32_t M, bool hl, float* out)
 {
-    if (M == 0 || !wide_fits((int)M, w.k)) return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows of K=%u do not fit", M, w.k);
-    if (f.pro == kProNorm && (M > (uint32_t)kNormMaxRows || w.k > 4096 || w.k % 4 || f.P < 1 || f.P > kNormMaxPartials))
-        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs M <= 16, K <= 4096 and 1..%d partial sums",
-                    kNormMaxPartials);
     GemmArgs a;
     a.w = w.dev;
     a.w_bytes = (uint32_t)w.bytes;
-    a.x = reinterpret_cast<const _Float16*>(x);
-    a.out = y;
+    a.x = x;
+    a.out = out;
     a.M = (int)M;
     a.N = (int)w.n;
     a.K = (int)w.k;
     a.n_tiles = (int)w.n_tiles;
     a.n_chunks = (int)w.n_chunks;
+    a.ks_count = 1;
+    a.ks_q = (int)w.n_chunks;
+    a.ks_r = 0;
+    a.hl = hl ? 1 : 0;
+    a.xrows = hl ? 2 * (int)M : (int)M;
+    a.f = GemmFuse();
+    return a;
+}
+
+// The split-K kernel over a.M rows into part[ks][M][N], then the slice sum and
+// a.f's epilogue into y (one slice and a plain store: straight into y).
+void split_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs a, float* part, float* y)
+{
+    a.ks_count = (int)w.ksplit;
+    a.ks_q = (int)(w.n_chunks / w.ksplit);
+    a.ks_r = (int)(w.n_chunks % w.ksplit);
+    const bool direct = w.ksplit == 1 && a.f.epi == kEpiStore;
+    a.out = direct ? y : part;
+    const int mt = a.hl ? (a.M + 7) / 8 : (a.M + 15) / 16;
+    if (w.type == ULSPEC_GGML_Q4_0) slice_launch_t<ULSPEC_GGML_Q4_0>(a, mt, ctx->stream);
+    else if (w.type == ULSPEC_GGML_Q4_K) slice_launch_t<ULSPEC_GGML_Q4_K>(a, mt, ctx->stream);
+    else if (w.type == ULSPEC_GGML_Q8_0) slice_launch_t<ULSPEC_GGML_Q8_0>(a, mt, ctx->stream);
+    else slice_launch_t<ULSPEC_GGML_F16>(a, mt, ctx->stream);
+    if (direct) return;
+    a.out = y;
+    const int threads = a.M * 16 * a.n_tiles;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a,
+                       (const float*)part);
+}
+
+}  // namespace
+
+// Launch the GEMM for one weight (fp16 X); rows beyond kGemmRowsH16 go in
+// further launches.  Never allocates (the slice workspace is sized at upload).
+ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, uint32_t M, float* y)
+{
+    const _Float16* X = reinterpret_cast<const _Float16*>(x);
+    if (gemm_workspace_bytes(w) > ctx->ws_bytes)
+        return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
+    for (uint32_t m0 = 0; m0 < M; m0 += kGemmRowsH16) {
+        const uint32_t mc = std::min<uint32_t>(kGemmRowsH16, M - m0);
+        GemmArgs a = make_args(w, X + (size_t)m0 * w.k, mc, false, y + (size_t)m0 * w.n);
+        if (wide_fits((int)mc, w.k)) {  // whole X in LDS, parts summed in the kernel
+            stream_launch(ctx, w, a);
+            continue;
+        }
+        split_launch(ctx, w, a, (float*)ctx->ws, y + (size_t)m0 * w.n);
+    }
+    return check_launch(ctx, "verify_gemm launch");
+}
+
+size_t gemm_split_part_bytes(const Weight& w, uint32_t M)
+{
+    return (size_t)w.ksplit * M * w.n * sizeof(float);
+}
+
+ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y)
+{
+    if (M == 0 || M > (uint32_t)kGemmRowsSplit)
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows (1..%d)", M, kGemmRowsSplit);
+    if (f.pro == kProNorm && (w.k > 4096 || w.k % 4 || f.P < 1 || f.P > kNormMaxPartials))
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs K <= 4096 and 1..%d partial sums",
+                    kNormMaxPartials);
+    GemmArgs a = make_args(w, reinterpret_cast<const _Float16*>(x), M, true, y);
     a.f = f;
-    stream_launch(ctx, w, a);
+    if (M <= 8 && wide_fits(2 * (int)M, w.k)) {  // whole split X in LDS
+        stream_launch(ctx, w, a);
+        return check_launch(ctx, "fused gemm launch");
+    }
+    float* part = f.part ? f.part : (float*)ctx->ws;
+    const size_t room = f.part ? f.part_bytes : ctx->ws_bytes;
+    if (gemm_split_part_bytes(w, M) > room)
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: %zu bytes of slice partials, %zu available",
+                    gemm_split_part_bytes(w, M), room);
+    if (f.pro == kProNorm) {
+        if (!f.x_scratch) return fail(ctx, ULSPEC_EINVAL, "fused gemm: the split path needs an X scratch buffer");
+        hipLaunchKernelGGL(norm_split_kernel, dim3(M), dim3(256), 0, ctx->stream, f, (int)M, (int)w.k, f.x_scratch);
+        a.x = f.x_scratch;
+        a.f.pro = kProCopy;
+    }
+    split_launch(ctx, w, a, part, y);
     return check_launch(ctx, "fused gemm launch");
 }
 
@@ -1678,7 +1747,7 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
     w.bytes = (size_t)w.n_tiles * w.n_chunks *
               (f16 ? kF16Chunk : q80 ? kQ80Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
     if (w.bytes >= kOOB) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes exceeds the 2 GiB per-weight limit", w.bytes);
-    w.ksplit = f16 || q80 ? 1 : choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
+    w.ksplit = choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipMalloc(&w.dev, w.bytes);
     if (e != hipSuccess) return hip_fail(ctx, e, "weight_upload hipMalloc");

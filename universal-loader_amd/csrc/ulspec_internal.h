@@ -73,6 +73,9 @@ ulspec_status gemm_init(ulspec_ctx* ctx);
 enum { kProCopy = 0, kProNorm = 1 };
 enum { kEpiStore = 0, kEpiRope = 1, kEpiSilu = 2, kEpiResid = 3 };
 constexpr int kNormMaxRows = 16;
+// Rows per launch: fp16 X through the ABI GEMM, split X through the fused GEMM.
+constexpr int kGemmRowsH16 = 64;
+constexpr int kGemmRowsSplit = 48;
 struct GemmFuse {
     int pro = kProCopy, epi = kEpiStore;
     // kProNorm: X = fp16(v * rsqrt(sum_p pss[m][p] / K + eps) * norm_w), K <= 4096
@@ -93,11 +96,17 @@ struct GemmFuse {
     _Float16* kc = nullptr;
     _Float16* vc = nullptr;
     int qdim = 0, kvdim = 0, hd = 0;
-    // kEpiSilu: rows interleaved gate / up -> act [M][N / 2]
+    // kEpiSilu: rows interleaved gate / up -> act, split fp16 pairs [2M][N / 2] (hi rows, then lo rows)
     _Float16* act = nullptr;
     // kEpiResid: h [M][N] += Y; pss_out [M][n_tiles] = per-tile sums of h^2
     float* h = nullptr;
     float* pss_out = nullptr;
+    // split-K path (rows or K beyond what the whole-X kernels hold): slice
+    // partials (NULL = the context workspace) and, for kProNorm, the split X
+    // [2M][K] the norm kernel writes
+    float* part = nullptr;
+    size_t part_bytes = 0;
+    _Float16* x_scratch = nullptr;
 };
 
 // Kernel launchers shared by the C ABI and the host engine (no validation of
@@ -106,10 +115,14 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
 // Rows of GGUF blocks (device) to fp16 rows out[out_row0 + r * out_row_step][K].
 ulspec_status rows_to_f16(ulspec_ctx* ctx, uint32_t type, const void* raw, uint32_t rows, uint32_t K,
                           _Float16* out, uint32_t out_row0, uint32_t out_row_step);
-// The whole-X kernel with a fused prologue / epilogue (M rows must fit in LDS).
+// The dequant-GEMM with a fused prologue / epilogue over split X (the model
+// forward): the whole-X kernels for M <= 8 rows that fit in LDS, else the
+// split-K kernel (with the norm kernel for kProNorm) and the reducing epilogue.
 ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y);
-bool wide_fits(int M, uint32_t K);
+bool wide_fits(int rows, uint32_t K);
 size_t gemm_workspace_bytes(const Weight& w);
+uint32_t choose_ksplit(uint32_t n_tiles, uint32_t n_chunks, int n_cu);
+size_t gemm_split_part_bytes(const Weight& w, uint32_t M);
 ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, size_t nbytes, uint32_t N, uint32_t K,
                             bool on_device, uint32_t* out_id);
 struct AttnCall {
@@ -123,6 +136,7 @@ struct AttnCall {
     float scale = 0.0f;
     void* out = nullptr;
     bool out_f16 = false;
+    bool out_split = false;  // split fp16 pair [2][nq][H][D] (hi, lo) for the next GEMM's X
     const int32_t* dyn_prefix = nullptr;  // device int: prefix = *dyn_prefix + prefix_add
     int prefix_add = 0;
     void* part = nullptr;    // split partials; NULL = the context workspace
