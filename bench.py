@@ -328,6 +328,42 @@ def workload_accept(pkg, ctx, args):
     }
 
 
+def workload_read(pkg, ctx, args):
+    """Streaming-read ceiling: the plain 16-byte-load read kernel over the
+    byte counts of the verify GEMMs (the Q4_0 4096x11008 weight, the 7B Q4_K
+    QKV and gate/up weights), 24 rotated copies of each (> 512 MB, past the
+    MALL), every load variant; the fastest variant per size is the ceiling."""
+    sink = ctx.alloc(16)
+    rows, head = [], None
+    for nbytes in (25362432, 28311552, 50724864):
+        bufs = [ctx.alloc(nbytes) for _ in range(24)]  # contents do not matter (the XOR only feeds the sink test)
+        best = None
+        for variant in range(3):
+            it = iter(range(1 << 30))
+            us = _time_direct(ctx, lambda: ctx.stream_read(bufs[next(it) % 24], nbytes, variant, sink),
+                              24 * args.reps)
+            gbs = nbytes / us / 1e3
+            log(f"read {nbytes / 1e6:.1f} MB, {4 << variant} loads per thread: {us:.2f} us, {gbs:.0f} GB/s")
+            rows.append({"bytes": nbytes, "loads_per_thread": 4 << variant, "us": us, "GB/s": gbs})
+            if best is None or us < best[0]:
+                best = (us, gbs, variant)
+        if nbytes == 25362432:
+            head = best
+        for b in bufs:
+            b.free()
+    sink.free()
+    us, gbs, variant = head
+    return {
+        "metric": "streaming-read ceiling GB/s (25.4 MB, the Q4_0 4096x11008 weight)", "value": gbs, "unit": "GB/s",
+        "ms_per_step": us / 1e3, "dtype": "u8",
+        "config": {"workload": "plain 16-byte-load read of 25 / 28 / 51 MB buffers, 24 rotated copies", "table": rows,
+                   "best_loads_per_thread": 4 << variant},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "avg_us": us, "algorithmic_bytes": 25362432},
+        "cpu_baseline": None,
+    }
+
+
 def workload_copy(pkg, ctx, args):
     """Calibration: device-to-device copies of 25362432 bytes (the size of a
     4096 x 11008 Q4_0 weight), the reference point that scales the FETCH_SIZE /
@@ -356,10 +392,11 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy"),
+    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read"),
                     default="step",
                     help="step: the speculative step (default); roofline: only the step's verify-GEMM roofline "
-                         "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration")
+                         "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration; "
+                         "read: the streaming-read ceiling")
     ap.add_argument("--reps", type=int, default=50, help="launches per timing (kernel workloads)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch each step's kernels directly instead of replaying the captured graph")
@@ -388,7 +425,7 @@ def main():
         return 0
     if args.workload != "step":
         fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
-              "copy": workload_copy}[args.workload]
+              "copy": workload_copy, "read": workload_read}[args.workload]
         out = fn(pkg, ctx, args)
         base = {"n_gpus": 1, "steps": args.reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic, seeded"}

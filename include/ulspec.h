@@ -87,6 +87,14 @@ ulspec_status ulspec_graph_replay(ulspec_ctx* ctx, uint32_t graph_id, uint32_t t
 ulspec_status ulspec_graph_destroy(ulspec_ctx* ctx, uint32_t graph_id);
 ulspec_status ulspec_timer_mark(ulspec_ctx* ctx, uint32_t slot /* < 16 */);
 ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t slot_b, float* ms);
+/* Measurement kernel with no counterpart in the reference: reads every 16-byte
+ * unit of the device buffer `buf` (bytes a multiple of 16) once, 256 threads
+ * per workgroup and 4 << variant (variant 0..2) loads per thread, all issued
+ * before the first use.  *sink (device) is written only when the XOR of all
+ * words is 0x5eed5eed, so the loads cannot be elided.  Its duration for a
+ * given size is the streaming-read ceiling the verify kernels are compared
+ * with. */
+ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant, uint32_t* sink);
 
 /* ---- K1: verify dequant-GEMM ------------------------------------------------
  * Upload one linear weight given as GGUF blocks (host memory, rows of K
@@ -188,8 +196,9 @@ ulspec_status ulspec_synth_q4(ulspec_ctx* ctx, uint32_t ggml_type, uint64_t seed
  * activation buffers for up to 16 rows.  Block order of
  * InferenceEngine::forward_layer_gpu (src/inference/inference_engine.cpp:602-682):
  * RMSNorm -> QKV -> RoPE -> attention -> O -> +residual -> RMSNorm -> gate/up
- * -> SiLU(gate) * up -> down -> +residual; final RMSNorm and LM head.  GEMM
- * inputs are fp16, the residual stream and logits fp32.  Replaces Model /
+ * -> SiLU(gate) * up -> down -> +residual; final RMSNorm and LM head.
+ * Activations, the residual stream and logits are fp32 (GEMM inputs reach the
+ * fp16 MFMAs as split (hi, lo) pairs); Q and the K/V cache are fp16.  Replaces Model /
  * KVCache (src/inference/model.h:49-115) and forward_layer_gpu (:475-692). */
 typedef struct ulspec_model ulspec_model;
 typedef struct {

@@ -60,7 +60,9 @@ def test_model_forward_logits_and_cache(pkg, ctx, ora, weights, prompt):
         ko, vo = o.kv_io(l, 0, 0, 40)
         for a, b in ((kg, ko), (vg, vo)):
             a, b = ora.h2f_fast(a).astype(np.float64), ora.h2f_fast(b).astype(np.float64)
-            assert np.abs(a - b).max() <= LOGIT_TOL * np.sqrt((b ** 2).mean())
+            # fp16 cache entries: one ulp (2^-10 relative) where the fp32 values
+            # on either side of a rounding boundary differ in the last bits
+            assert (np.abs(a - b) <= np.abs(b) * 2.0 ** -10 + 1e-3 * np.sqrt((b ** 2).mean())).all()
     g.close()
 
 

@@ -96,6 +96,7 @@ ABI = [
     ("ulspec_graph_destroy", C.c_int, [P, U32]),
     ("ulspec_timer_mark", C.c_int, [P, U32]),
     ("ulspec_timer_elapsed_ms", C.c_int, [P, U32, U32, C.POINTER(C.c_float)]),
+    ("ulspec_stream_read", C.c_int, [P, P, C.c_size_t, U32, P]),
     ("ulspec_weight_upload", C.c_int, [P, U32, P, C.c_size_t, U32, U32, C.POINTER(U32)]),
     ("ulspec_weight_info", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32),
                                      C.POINTER(C.c_size_t)]),
@@ -246,6 +247,10 @@ class Context:
         ms = C.c_float()
         self._check(lib().ulspec_timer_elapsed_ms(self.handle, a, b, C.byref(ms)))
         return ms.value
+
+    def stream_read(self, buf, nbytes, variant, sink):
+        """The streaming-read measurement kernel over nbytes of device buffer buf."""
+        self._check(lib().ulspec_stream_read(self.handle, _ptr(buf), nbytes, variant, _ptr(sink)))
 
     # -- K1 ------------------------------------------------------------------
     def weight_upload(self, wtype, blocks, n_rows, k):

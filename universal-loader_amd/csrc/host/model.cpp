@@ -172,26 +172,27 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         }
     }
     const std::vector<Weight>& W = ctx->weights;
-    // every GEMM: split-K partials and the norm's split X when it takes the split-K path
+    // every GEMM: split-K partials when it takes that path
     auto fuse = [&]() {
         GemmFuse f;
         f.part = part;
         f.part_bytes = part_bytes;
-        f.x_scratch = xn;
         return f;
     };
-    launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss);
+    // X of a GEMM after an RMSNorm is split(h * w), written with h by its
+    // producer; the GEMM scales its rows by 1 / rms(h) from the partial sums
+    auto normed = [&](GemmFuse& f, const float* pss_rows, int P) {
+        f.rs_pss = pss_rows;
+        f.rs_P = P;
+        f.rs_eps = c.rms_eps;
+    };
+    launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss, layers[0].attn_norm, xn);
     int P = (int)embed_partials(c.dim);
     ulspec_status s = ULSPEC_OK;
     for (uint32_t l = 0; l < c.n_layers && s == ULSPEC_OK; ++l) {
         const Layer& L = layers[l];
         GemmFuse q = fuse();
-        q.pro = kProNorm;
-        q.v = h;
-        q.pss = pss;
-        q.P = P;
-        q.norm_w = L.attn_norm;
-        q.eps = c.rms_eps;
+        normed(q, pss, P);
         q.epi = kEpiRope;
         q.pos_dev = pos_dev;
         q.pos_add = pos_add;
@@ -204,7 +205,7 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         q.qdim = (int)(H * D);
         q.kvdim = (int)(Hkv * D);
         q.hd = (int)D;
-        s = gemm_fused(ctx, W[L.wqkv], q, nullptr, M, nullptr);
+        s = gemm_fused(ctx, W[L.wqkv], q, (const uint16_t*)xn, M, M, nullptr);
         if (s != ULSPEC_OK) break;
         AttnCall a;
         a.q = (const uint16_t*)q16;
@@ -228,37 +229,35 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         o.epi = kEpiResid;
         o.h = h;
         o.pss_out = pss;
-        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att, M, nullptr);
+        o.xn_w = L.ffn_norm;
+        o.xn = xn;
+        o.xn_lo = (int)M;
+        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att, M, M, nullptr);
         if (s != ULSPEC_OK) break;
         P = (int)W[L.wo].n_tiles;
         GemmFuse u = fuse();
-        u.pro = kProNorm;
-        u.v = h;
-        u.pss = pss;
-        u.P = P;
-        u.norm_w = L.ffn_norm;
-        u.eps = c.rms_eps;
+        normed(u, pss, P);
         u.epi = kEpiSilu;
         u.act = act;
-        s = gemm_fused(ctx, W[L.wgu], u, nullptr, M, nullptr);
+        s = gemm_fused(ctx, W[L.wgu], u, (const uint16_t*)xn, M, M, nullptr);
         if (s != ULSPEC_OK) break;
         GemmFuse d = fuse();
         d.epi = kEpiResid;
         d.h = h;
         d.pss_out = pss;
-        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act, M, nullptr);
+        d.xn_w = l + 1 < c.n_layers ? layers[l + 1].attn_norm : out_norm;
+        d.xn = xn;
+        d.xn_lo = (int)M;
+        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act, M, M, nullptr);
         P = (int)W[L.wdown].n_tiles;
     }
     if (s != ULSPEC_OK) return s;
     if (n_logits) {
+        // the last n_logits rows: their high parts from row M - n_logits, low parts M rows below
         GemmFuse z = fuse();
-        z.pro = kProNorm;
-        z.v = h + (size_t)(M - n_logits) * c.dim;
-        z.pss = pss + (size_t)(M - n_logits) * P;
-        z.P = P;
-        z.norm_w = out_norm;
-        z.eps = c.rms_eps;
-        s = gemm_fused(ctx, W[w_out], z, nullptr, n_logits, logits_dev);
+        normed(z, pss + (size_t)(M - n_logits) * P, P);
+        s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)(xn + (size_t)(M - n_logits) * c.dim), n_logits, M,
+                       logits_dev);
     }
     if (s != ULSPEC_OK) return s;
     return check_launch(ctx, "model forward launch");

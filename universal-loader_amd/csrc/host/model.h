@@ -54,7 +54,7 @@ struct ulspec_model {
     _Float16* q16 = nullptr;   // [kRows][H D] (attention queries, fp16)
     _Float16* att = nullptr;   // split [2 kRows][H D]
     _Float16* act = nullptr;   // split [2 kRows][F]
-    _Float16* xn = nullptr;    // split [2 kRows][dim]: RMSNorm output of the split-K path
+    _Float16* xn = nullptr;    // split [2 kRows][dim]: h times the next RMSNorm's weights (the next GEMM's X)
     float* part = nullptr;     // split-K slice partials
     size_t part_bytes = 0;
     int32_t* tok = nullptr;    // [kRows]

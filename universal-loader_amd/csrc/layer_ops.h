@@ -10,9 +10,10 @@ namespace ulspec {
 
 // h[m][:] = dequantized row tokens[m] of the raw GGUF [V][dim] tensor (ids
 // out of range read row 0); pss[m][b] = sum of squares of h[m][256 b ..
-// 256 b + 255], b < embed_partials(dim).
+// 256 b + 255], b < embed_partials(dim); with xn, the split fp16 pairs of
+// h * xn_w (rows m, then rows M + m).
 uint32_t embed_partials(uint32_t dim);
 void launch_embed(hipStream_t st, const uint8_t* w, uint32_t type, uint32_t dim, const int32_t* tokens, uint32_t M,
-                  uint32_t V, float* h, float* pss);
+                  uint32_t V, float* h, float* pss, const float* xn_w, _Float16* xn);
 
 }  // namespace ulspec

@@ -1,9 +1,11 @@
 // layer_ops.hip -- token embedding of the model forward: dequantized rows of
 // the raw GGUF token_embd tensor start the fp32 residual stream, with the
-// per-block sums of squares its first RMSNorm consumes.  (The other Llama
-// block steps of src/inference/inference_engine.cpp:602-682 -- RMSNorm, RoPE
-// and the KV append, SiLU * up, the residual adds -- run fused into the
-// dequant-GEMM's prologue and epilogues.)
+// per-block sums of squares its first RMSNorm consumes and the split X of the
+// first GEMM (h times the norm's weights; the GEMM applies the norm's row
+// factor to its outputs).  (The other Llama block steps of
+// src/inference/inference_engine.cpp:602-682 -- RMSNorm, RoPE and the KV
+// append, SiLU * up, the residual adds -- run fused into the dequant-GEMM's
+// row scale and epilogues.)
 #include "detmath.h"
 #include "hip_common.h"
 #include "layer_ops.h"
@@ -19,9 +21,12 @@ __device__ __forceinline__ float h2f_bits(uint32_t b) { return (float)__builtin_
 // Q8_0 and Q6_K as ggml defines them (the types Q4_K_M files mix in).
 // Grid (ceil(dim / 256), M); block b of row m also writes pss[m][b], the sum
 // of its 256 values squared (xor tree in each wave, the 4 waves in order).
+// With xn, also the first GEMM's split X: rows m (hi) and xn_lo + m (lo) of h * xn_w.
 __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ w, uint32_t type, uint32_t dim,
                                                     const int32_t* __restrict__ tokens, uint32_t V,
-                                                    float* __restrict__ h, float* __restrict__ pss)
+                                                    float* __restrict__ h, float* __restrict__ pss,
+                                                    const float* __restrict__ xn_w, _Float16* __restrict__ xn,
+                                                    uint32_t xn_lo)
 {
     __shared__ float part[4];
     const uint32_t m = blockIdx.y;
@@ -67,6 +72,12 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
             v = (d * (float)sc) * (float)q - dmin * (float)mn;
         }
         h[(size_t)m * dim + e] = v;
+        if (xn) {
+            _Float16 hi, lo;
+            split_hl(v * xn_w[e], hi, lo);
+            xn[(size_t)m * dim + e] = hi;
+            xn[(size_t)(xn_lo + m) * dim + e] = lo;
+        }
     }
     float sq = v * v;
 #pragma unroll
@@ -81,9 +92,10 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
 uint32_t embed_partials(uint32_t dim) { return (dim + 255) / 256; }
 
 void launch_embed(hipStream_t st, const uint8_t* w, uint32_t type, uint32_t dim, const int32_t* tokens, uint32_t M,
-                  uint32_t V, float* h, float* pss)
+                  uint32_t V, float* h, float* pss, const float* xn_w, _Float16* xn)
 {
-    hipLaunchKernelGGL(embed_kernel, dim3(embed_partials(dim), M), dim3(256), 0, st, w, type, dim, tokens, V, h, pss);
+    hipLaunchKernelGGL(embed_kernel, dim3(embed_partials(dim), M), dim3(256), 0, st, w, type, dim, tokens, V, h, pss,
+                       xn_w, xn, M);
 }
 
 }  // namespace ulspec

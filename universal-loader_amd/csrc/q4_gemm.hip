@@ -236,21 +236,24 @@ __device__ __forceinline__ void vm_wait()
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int... Ns>
-__device__ __forceinline__ void vm_wait_sel(int n, std::integer_sequence<int, Ns...>)
-{
-    ((n == Ns ? vm_wait<Ns>() : void()), ...);
-}
+#define ULSPEC_VM_CASE(n) \
+    case n: vm_wait<n>(); break;
+#define ULSPEC_VM_CASE8(n) \
+    ULSPEC_VM_CASE(n) ULSPEC_VM_CASE(n + 1) ULSPEC_VM_CASE(n + 2) ULSPEC_VM_CASE(n + 3) \
+    ULSPEC_VM_CASE(n + 4) ULSPEC_VM_CASE(n + 5) ULSPEC_VM_CASE(n + 6) ULSPEC_VM_CASE(n + 7)
 
-// vm_wait with a wave-uniform count n known only at run time; counts outside
-// 1..63 wait for everything.
+// vm_wait with a wave-uniform count n known only at run time (a jump table);
+// counts outside 0..63 wait for everything.
 __device__ __forceinline__ void vm_wait_dyn(int n)
 {
-    if (n <= 0 || n >= 64)
-        vm_wait<0>();
-    else
-        vm_wait_sel(n, std::make_integer_sequence<int, 64>{});
+    switch (n) {
+        ULSPEC_VM_CASE8(0) ULSPEC_VM_CASE8(8) ULSPEC_VM_CASE8(16) ULSPEC_VM_CASE8(24)
+        ULSPEC_VM_CASE8(32) ULSPEC_VM_CASE8(40) ULSPEC_VM_CASE8(48) ULSPEC_VM_CASE8(56)
+    default: vm_wait<0>();
+    }
 }
+#undef ULSPEC_VM_CASE8
+#undef ULSPEC_VM_CASE
 
 // Raw buffer loads: 32-bit offsets from a base held in scalar registers, and
 // the hardware returns 0 for offsets at or past num_records instead of
@@ -356,78 +359,42 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w
     m = lo ? m_lo : m_hi;
 }
 
-// ---- split-K kernels -------------------------------------------------------
-// Grid (row groups, K slices).  A workgroup of kWaves waves covers kWaves
-// 16-row tiles (one per wave) and one K slice of the weight.  Per batch of up
-// to CMAX chunks (Q4_0 block quads / Q4_K super-blocks) it
-//   1. issues the loads of its X slice (16-byte units, registers),
-//   2. issues every weight load of the batch (all waves, all chunks at once,
-//      so the CU holds its whole share of the weight stream in flight),
-//   3. writes X to LDS (waiting only for the older X loads), barrier,
-//   4. dequantizes in registers and runs the MFMAs, X read back from LDS.
-// Out-of-range chunks (past the slice or the last tile) use an offset past
-// the buffer: the load returns 0 and makes no memory request.  Each wave's
-// chunks are accumulated in K order; slices are summed in slice order by the
-// reduction kernel, so every output row is bitwise independent of M.
+// ---- X operand and common pieces -------------------------------------------
+// X is fp16 rows [M][K] (hl = 0), or split fp32 activations (hl = 1): the
+// high parts (split_hl) of rows 0..M-1, and the low part of row m at row
+// lo_rows + m.  In split mode an MFMA covers 8 output rows: A-operand slots
+// 0-7 take the high parts of 8 rows, slots 8-15 the low parts of the same
+// rows, and the two halves of the result are added in the epilogue (hi + lo *
+// 2^-11), so M <= 8 per 16-column tile.
 constexpr int kWaves = 16;
 constexpr uint32_t kOOB = 0x80000000u;  // >= any buffer's num_records
 
-// X slice of one split-K batch in LDS: 16 MT rows of UB units (16 bytes =
-// 8 halves) plus one pad unit (bank spread); UB is a power of two <= 128.
-// Thread tid stages unit tid % UB of rows tid / UB + pass * (1024 / UB).
-template <int MT, int UB>
-struct XStage {
-    static constexpr int kUnitsPerRow = UB + 1;
-    static constexpr int kRowsPerPass = kWaves * 64 / UB;
-    static constexpr int kXU = (16 * MT + kRowsPerPass - 1) / kRowsPerPass;  // passes = units per thread
-};
-
-// Load this batch's X slice (rows < M, units [0, U) starting at element k0,
-// U <= UB) into registers.  Units past K load 0.
-template <int MT, int UB>
-__device__ __forceinline__ void x_stage_load(__amdgpu_buffer_rsrc_t xr, uint4 (&xv)[XStage<MT, UB>::kXU], int M,
-                                             int K, int k0, int U)
-{
-    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
-    const int k = k0 + 8 * uu;
-#pragma unroll
-    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
-        const int m = m0 + u * XStage<MT, UB>::kRowsPerPass;
-        const bool ok = m < M && uu < U && k < K;
-        xv[u] = buf_load16(xr, ok ? (uint32_t)(m * K + k) * 2u : kOOB);
-    }
-}
-
-template <int MT, int UB>
-__device__ __forceinline__ void x_stage_store(uint4* xs, const uint4 (&xv)[XStage<MT, UB>::kXU], int M, int U)
-{
-    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
-#pragma unroll
-    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
-        const int m = m0 + u * XStage<MT, UB>::kRowsPerPass;
-        if (m < M && uu < U) xs[m * XStage<MT, UB>::kUnitsPerRow + uu] = xv[u];
-    }
-}
-
-// X operand: fp16 rows [M][K] (hl = 0), or split fp32 activations (hl = 1):
-// rows [2M][K], the high parts of rows 0..M-1 then their low parts (split_hl).
-// In split mode an MFMA covers 8 output rows: A-operand slots 0-7 take the
-// high parts of 8 rows, slots 8-15 the low parts of the same rows, and the
-// two halves of the result are added in the epilogue (hi + lo * 2^-11), so
-// M <= 8 per 16-column tile.
 struct GemmArgs {
     const uint8_t* w;
     uint32_t w_bytes;
     const _Float16* x;
-    float* out;  // Y when ks_count == 1, else partials [ks_count][M][N]
+    float* out;  // Y, or the slice partials [ks_count][M][N] of the split-K kernel
     int M, N, K, n_tiles, n_chunks, ks_count;
     int ks_q, ks_r;  // n_chunks = ks_q * ks_count + ks_r; slice s starts at s * ks_q + min(s, ks_r)
     int hl;          // split X (see above)
-    int xrows;       // rows of X: M, or 2M when split
-    GemmFuse f;      // epilogue (and the whole-X kernels' prologue)
+    int lo_rows;     // split X: row of X holding the low part of row 0
+    int xrows;       // rows of X staged: M, or 2M when split
+    GemmFuse f;      // row scale and epilogue
 };
 
-// Row of X that A-operand slot r (0..15) of column tile mt reads; slots past
+// X row behind staged row rho (0 .. xrows-1).
+__device__ __forceinline__ int x_row(const GemmArgs& a, int rho)
+{
+    return a.hl && rho >= a.M ? a.lo_rows + rho - a.M : rho;
+}
+
+// Bytes of X the kernels may read.
+__device__ __forceinline__ uint32_t x_bytes(const GemmArgs& a)
+{
+    return (uint32_t)(a.hl ? a.lo_rows + a.M : a.M) * (uint32_t)a.K * 2u;
+}
+
+// Staged row that A-operand slot r (0..15) of column tile mt reads; slots past
 // the last row repeat it (their outputs are never stored).
 __device__ __forceinline__ int xslot_row(const GemmArgs& a, int mt, int r)
 {
@@ -450,109 +417,101 @@ __device__ __forceinline__ void slice_range(const GemmArgs& a, int ks, int& lo, 
     hi = lo + a.ks_q + (ks < a.ks_r ? 1 : 0);
 }
 
-// ---- whole-X streaming kernels (small M) --------------------------------------
-// The whole X (M rows) sits in LDS, copied once per workgroup with direct
-// buffer->LDS loads (no registers; row pitch rounded up to 1 KB plus 16 B so a
-// partial last load of a row only touches its own padding, and rows fall on
-// different banks) or built there by the RMSNorm prologue.  Per iteration the
-// NW waves of a workgroup cover tpi = NW / P tiles x P parts of K (P a power of
-// two, at most NW and at most the chunks per row).  When there are more
-// iterations than CUs, a grid of one 8-wave workgroup per CU walks them and
-// loads the first batch of the next iteration's weights while the current one
-// is multiplied, so each CU keeps a continuous stream of weight loads in
-// flight; otherwise 16-wave workgroups run one iteration each.  Parts are
-// summed in part order in LDS, then the epilogue runs.
-constexpr int kStreamWaves = 8;
-constexpr int kWideWaves = 16;
-
-__host__ __device__ constexpr uint32_t wide_pitch(uint32_t K)
-{
-    return ((2u * K + 1023u) / 1024u) * 1024u + 16u;
-}
-
-// This wave's own part of X: rows 0..xrows-1, chunks [ca, cb) (16-byte units
-// [ua, ub) of each row); element (m, k) goes to LDS byte m * wide_pitch(K) +
-// 2 k.  A wave reads X only inside its own part, so it waits for its own
-// copies (vmcnt) and no other wave's: no barrier before the first multiply.
-// Each copy moves 64 consecutive units; a part that is not a multiple of 64
-// units ends with a copy shifted back to end at ub, and a row shorter than 64
-// units copies units 0..63, the ones past the row end reading as zero into
-// the row's padding.  Units of a neighbouring part written this way receive
-// the same X values that part's own wave writes there.
-template <int UPC>
-__device__ __forceinline__ void x_copy_own(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes, int ca,
-                                           int cb)
-{
-    const int lane = threadIdx.x & 63;
-    const int KU = a.K / 8;
-    const int ua = ca * UPC, ub = cb * UPC;
-    const int np = ub > ua ? (ub - ua + 63) / 64 : 0;
-    const uint32_t pitch = wide_pitch(a.K);
-    for (int m = 0; m < a.xrows; ++m) {
-        for (int q = 0; q < np; ++q) {
-            int s0 = ua + 64 * q;
-            if (s0 + 64 > ub) s0 = max(ub - 64, 0);
-            const int u = s0 + lane;
-            const uint32_t off = u < KU ? (uint32_t)(m * KU + u) * 16u : kOOB;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void*)(xs_bytes + m * pitch + s0 * 16), 16, off, 0, 0, 0);
-        }
-    }
-}
-
+// ---- weights: one batch of up to CMAX chunks of one tile, in registers ------
+template <int TYPE, int CMAX>
+struct WBatch;
 template <int CMAX>
-__device__ __forceinline__ void q4_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t s_lane, int c0,
-                                                int nc, uint4 (&wq)[CMAX], uint2 (&sc)[CMAX])
+struct WBatch<ULSPEC_GGML_Q4_0, CMAX> {
+    static constexpr int kLoadsPerChunk = 2;
+    uint4 wq[CMAX];
+    uint2 sc[CMAX];
+};
+template <int CMAX>
+struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
+    static constexpr int kLoadsPerChunk = 3;
+    uint4 w0[CMAX], w1[CMAX], hd[CMAX];
+};
+template <int CMAX>
+struct WBatch<ULSPEC_GGML_Q8_0, CMAX> {
+    static constexpr int kLoadsPerChunk = 3;
+    uint4 w0[CMAX], w1[CMAX];
+    uint2 sc[CMAX];
+};
+template <int CMAX>
+struct WBatch<ULSPEC_GGML_F16, CMAX> {
+    static constexpr int kLoadsPerChunk = 4;
+    uint4 w[CMAX][4];
+};
+
+// Chunk c of tile t into slot i of b.  Every slot's loads are issued (out of
+// range when !ok or t is past the last tile: the load returns 0 and moves no
+// data), so the loads in flight are a compile-time count and each chunk
+// waits for exactly its own.
+template <int TYPE, int CMAX>
+__device__ __forceinline__ void load_slot(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, int t, int c, bool ok, int i,
+                                          WBatch<TYPE, CMAX>& b)
 {
-    // every slot is issued (past nc out of range, which moves no data), so
-    // the number of loads in flight is a compile-time constant and each
-    // chunk waits for exactly its own loads; launches pick CMAX to fit
+    const int lane = threadIdx.x & 63, r = lane & 15;
+    ok = ok && t < a.n_tiles;
+    const uint32_t ch = (uint32_t)(t < a.n_tiles ? t : 0) * (uint32_t)a.n_chunks + (uint32_t)c;
+    if constexpr (TYPE == ULSPEC_GGML_F16) {
+        const uint32_t o = ch * kF16Chunk + lane * 16;
 #pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
-        const uint32_t o = (uint32_t)(c0 + i) * kQ40Chunk;
-        wq[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
-        sc[i] = buf_load8(wr, i < nc ? s_lane + o : kOOB);
+        for (int j = 0; j < 4; ++j) b.w[i][j] = buf_load16(wr, ok ? o + 1024u * j : kOOB);
+    } else if constexpr (TYPE == ULSPEC_GGML_Q8_0) {
+        const uint32_t o = ch * kQ80Chunk;
+        b.w0[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
+        b.w1[i] = buf_load16(wr, ok ? o + 1024 + lane * 16 : kOOB);
+        b.sc[i] = buf_load8(wr, ok ? o + 2048 + r * 8 : kOOB);
+    } else if constexpr (TYPE == ULSPEC_GGML_Q4_0) {
+        const uint32_t o = ch * kQ40Chunk;
+        b.wq[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
+        b.sc[i] = buf_load8(wr, ok ? o + 1024 + r * 8 : kOOB);
+    } else {
+        const uint32_t o = ch * kQ4KChunk;
+        b.w0[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
+        b.w1[i] = buf_load16(wr, ok ? o + 1024 + lane * 16 : kOOB);
+        b.hd[i] = buf_load16(wr, ok ? o + 2048 + r * 16 : kOOB);
     }
 }
 
-// acc[mt] += the batch's chunks; A rows of column tile mt come from LDS (unit
-// index xrow[mt] + 4 * block).
+// Chunks c0 .. c0 + nc - 1 of tile t into slots 0 .. nc - 1 (the rest out of range).
+template <int TYPE, int CMAX>
+__device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, int t, int c0, int nc,
+                                            WBatch<TYPE, CMAX>& b)
+{
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) load_slot<TYPE, CMAX>(a, wr, t, c0 + i, i < nc, i, b);
+}
+
+// ---- dequantize + MFMA -------------------------------------------------------
+// acc[mt] += slots i0 <= i < min(i1, nc) of the batch, chunk c0 + i.  The A
+// operand of slot i, K step j comes from LDS unit xrow[mt] + cs * (c0 + i) + 4 j
+// (Q4_0 / Q8_0 / F16: 32-element blocks of 4 units) or + j (Q4_K: 8 steps of
+// one unit in each lane group's 64-element run); cs = units per chunk stride.
 template <int CMAX, int MT>
-__device__ __forceinline__ void q4_0_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
-                                               const uint4 (&wq)[CMAX], const uint2 (&sc)[CMAX],
-                                               const NibbleConsts& nk, float4_t (&acc)[MT])
+__device__ __forceinline__ void q4_0_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                         int i1, const WBatch<ULSPEC_GGML_Q4_0, CMAX>& b, const NibbleConsts& nk,
+                                         float4_t (&acc)[MT])
 {
     const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
+    for (int i = i0; i < i1; ++i) {
         if (i < nc) {
-            const uint32_t words[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
-            const uint32_t sw[2] = {sc[i].x, sc[i].y};
+            const uint32_t words[4] = {b.wq[i].x, b.wq[i].y, b.wq[i].z, b.wq[i].w};
+            const uint32_t sw[2] = {b.sc[i].x, b.sc[i].y};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const half8_t B = dequant_q4_0(words[j], nk);
                 const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]);
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + 4 * j]);
                     const float4_t pr = mfma16x16x32(A, B, zero4);
                     acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
                 }
             }
         }
-    }
-}
-
-template <int CMAX>
-__device__ __forceinline__ void q8_0_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t s_lane, int c0,
-                                                int nc, uint4 (&w0)[CMAX], uint4 (&w1)[CMAX], uint2 (&sc)[CMAX])
-{
-#pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
-        const uint32_t o = (uint32_t)(c0 + i) * kQ80Chunk;
-        w0[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
-        w1[i] = buf_load16(wr, i < nc ? w_lane + o + 1024 : kOOB);
-        sc[i] = buf_load8(wr, i < nc ? s_lane + o : kOOB);
     }
 }
 
@@ -570,29 +529,141 @@ __device__ __forceinline__ half8_t dequant_q8_0(uint32_t lo, uint32_t hi)
 
 // acc[mt] += d_block * (A . q) per block, as for Q4_0.
 template <int CMAX, int MT>
-__device__ __forceinline__ void q8_0_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
-                                               const uint4 (&w0)[CMAX], const uint4 (&w1)[CMAX],
-                                               const uint2 (&sc)[CMAX], float4_t (&acc)[MT])
+__device__ __forceinline__ void q8_0_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                         int i1, const WBatch<ULSPEC_GGML_Q8_0, CMAX>& b, float4_t (&acc)[MT])
 {
     const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
+    for (int i = i0; i < i1; ++i) {
         if (i < nc) {
-            const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
-            const uint32_t sw[2] = {sc[i].x, sc[i].y};
+            const uint32_t words[8] = {b.w0[i].x, b.w0[i].y, b.w0[i].z, b.w0[i].w,
+                                       b.w1[i].x, b.w1[i].y, b.w1[i].z, b.w1[i].w};
+            const uint32_t sw[2] = {b.sc[i].x, b.sc[i].y};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const half8_t B = dequant_q8_0(words[2 * j], words[2 * j + 1]);
                 const float d = half_bits_to_float((sw[j >> 1] >> (16 * (j & 1))) & 0xffffu);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
-                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]);
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + 4 * j]);
                     const float4_t pr = mfma16x16x32(A, B, zero4);
                     acc[mt] = __builtin_elementwise_fma((float4_t)d, pr, acc[mt]);
                 }
             }
         }
     }
+}
+
+// Q4_K: B = q * sc exactly, one MFMA chain per super-block scaled by d, and the
+// min term as a second chain with the 6-bit mins as the B operand, scaled by
+// -dmin.
+template <int CMAX, int MT>
+__device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                         int i1, const WBatch<ULSPEC_GGML_Q4_K, CMAX>& b, int g,
+                                         const NibbleConsts& nk, float4_t (&acc)[MT])
+{
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+        if (i < nc) {
+            const uint32_t words[8] = {b.w0[i].x, b.w0[i].y, b.w0[i].z, b.w0[i].w,
+                                       b.w1[i].x, b.w1[i].y, b.w1[i].z, b.w1[i].w};
+            const uint4 h = b.hd[i];
+            const float d = half_bits_to_float(h.x & 0xffffu);
+            const float dmin = half_bits_to_float(h.x >> 16);
+            SubScale ss[2];
+            half8_t mins[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                uint32_t scv, mn;
+                q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
+                const float fs = (float)scv;
+                ss[e].sc = splat2(fs);
+                ss[e].nsc1024 = splat2(-1024.0f * fs);
+                ss[e].sc16 = splat2(fs * 0.0625f);
+                ss[e].nsc64 = splat2(-64.0f * fs);
+                const _Float16 hm = (_Float16)(float)mn;
+                mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
+            }
+            float4_t P1[MT], P2[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                P1[mt] = zero4;
+                P2[mt] = zero4;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + j]);
+                    P1[mt] = mfma16x16x32(A, B, P1[mt]);
+                    P2[mt] = mfma16x16x32(A, mins[j >> 2], P2[mt]);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
+                acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
+            }
+        }
+    }
+}
+
+// F16: four MFMAs of 32 K per chunk, no dequantization.
+template <int CMAX, int MT>
+__device__ __forceinline__ void f16_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                        int i1, const WBatch<ULSPEC_GGML_F16, CMAX>& b, float4_t (&acc)[MT])
+{
+#pragma unroll
+    for (int i = i0; i < i1; ++i)
+        if (i < nc)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt] = mfma16x16x32(__builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + 4 * j]),
+                                           __builtin_bit_cast(half8_t, b.w[i][j]), acc[mt]);
+}
+
+template <int TYPE, int CMAX, int MT>
+__device__ __forceinline__ void stream_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                           int i1, const WBatch<TYPE, CMAX>& b, const NibbleConsts& nk,
+                                           float4_t (&acc)[MT])
+{
+    if constexpr (TYPE == ULSPEC_GGML_F16)
+        f16_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
+        q8_0_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
+        q4_0_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, nk, acc);
+    else
+        q4_k_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, (threadIdx.x & 63) >> 4, nk, acc);
+}
+
+// ---- row scale and epilogue --------------------------------------------------
+// Row scale r_m = 1 / sqrt(sum_p pss[m][p] / K + eps) (RMSNorm,
+// src/shaders/ffn/ffn_fused.glsl:23-33).  The GEMMs that follow a norm take X
+// = split(h * w) from the producer of h and apply r_m to each output, which
+// is x * W^T for x = (h * r) * w.  Lane l holds partials 4 l .. 4 l + 3 of the
+// row (P <= 256); rs_reduce sums them ((a + b) + (c + d), then an xor tree).
+constexpr int kMaxPartials = 256;
+
+__device__ __forceinline__ float4 rs_load(const GemmArgs& a, int m)
+{
+    const GemmFuse& f = a.f;
+    const __amdgpu_buffer_rsrc_t pr = make_rsrc(f.rs_pss, (uint32_t)a.M * (uint32_t)f.rs_P * 4u);
+    const int p0 = 4 * (threadIdx.x & 63);
+    return __builtin_bit_cast(float4, buf_load16(pr, m < a.M && p0 < f.rs_P ? (uint32_t)(m * f.rs_P + p0) * 4u : kOOB));
+}
+
+__device__ __forceinline__ float rs_reduce(const GemmArgs& a, float4 v)
+{
+    const int p0 = 4 * (threadIdx.x & 63), P = a.f.rs_P;
+    float ss = ((p0 < P ? v.x : 0.0f) + (p0 + 1 < P ? v.y : 0.0f)) + ((p0 + 2 < P ? v.z : 0.0f) + (p0 + 3 < P ? v.w : 0.0f));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    return 1.0f / __builtin_sqrtf(ss / (float)a.K + a.f.rs_eps);
 }
 
 // Position of row 0 for the RoPE epilogue: a scalar load through the
@@ -612,35 +683,40 @@ __device__ __forceinline__ int rope_row(const GemmFuse& f, int m)
 }
 
 // The memory operands of the epilogue of output (m, n), loaded ahead of it
-// with the weights of the same tile so that the epilogue reads no memory
-// (vmcnt retires in issue order: a load issued in the epilogue would wait for
-// every weight load in flight).  Two 4-byte loads for the resid and rope
-// epilogues (out of range where a thread has no output), none otherwise:
-//   resid: (h[m][n], -)      rope: (cos, sin) of the pair at position pos0 + m
-//                            (pos0 + depth(m) for a tree)
+// with the weights so that the epilogue reads no memory (vmcnt retires in
+// issue order: a load issued in the epilogue would wait for every weight load
+// in flight).  Two 4-byte loads for the resid and rope epilogues (out of range
+// where a thread has no output), none otherwise:
+//   resid: (h[m][n], xn_w[n])   rope: (cos, sin) of the pair at position
+//                               pos0 + m (pos0 + depth(m) for a tree)
 __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int pos0)
 {
     const GemmFuse& f = a.f;
     const bool ok = m < a.M && n < a.N;
-    __amdgpu_buffer_rsrc_t r;
+    __amdgpu_buffer_rsrc_t r0, r1;
     uint32_t o0 = kOOB, o1 = kOOB;
     if (f.epi == kEpiResid) {
-        r = make_rsrc(f.h, (uint32_t)a.M * (uint32_t)a.N * 4u);
-        if (ok) o0 = (uint32_t)(m * a.N + n) * 4u;
+        r0 = make_rsrc(f.h, (uint32_t)a.M * (uint32_t)a.N * 4u);
+        r1 = make_rsrc(f.xn_w, f.xn ? (uint32_t)a.N * 4u : 0u);
+        if (ok) {
+            o0 = (uint32_t)(m * a.N + n) * 4u;
+            o1 = (uint32_t)n * 4u;
+        }
     } else if (f.epi == kEpiRope) {
-        r = make_rsrc(f.rope, (uint32_t)(pos0 + a.M) * (uint32_t)(f.hd / 2) * 8u);
+        r0 = make_rsrc(f.rope, (uint32_t)(pos0 + a.M) * (uint32_t)(f.hd / 2) * 8u);
+        r1 = r0;
         if (ok && n < f.qdim + f.kvdim) {
             const int nn = n < f.qdim ? n : n - f.qdim;
             o0 = (uint32_t)((pos0 + rope_row(f, m)) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
             o1 = o0 + 4u;
         }
     } else {
-        r = make_rsrc(a.out, 0u);
+        r0 = r1 = make_rsrc(a.out, 0u);
     }
     float2 v = {0.f, 0.f};
     if (f.epi == kEpiResid || f.epi == kEpiRope) {
-        v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o0, 0, 0));
-        v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o1, 0, 0));
+        v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r0, o0, 0, 0));
+        v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r1, o1, 0, 0));
     }
     return v;
 }
@@ -651,18 +727,21 @@ __device__ __forceinline__ int epi_nloads(const GemmArgs& a)
     return a.f.epi == kEpiResid || a.f.epi == kEpiRope ? 2 : 0;
 }
 
-// Epilogue of output (m, n) of tile t, value s; pre from epi_load, pos0 from
-// epi_pos0.  Thread lanes l and l ^ 1 hold columns n and n ^ 1 of the same
-// row m (whole waves call this).
+// Epilogue of output (m, n) of tile t, value s (already row-scaled); pre from
+// epi_load, pos0 from epi_pos0.  Lanes l and l ^ 1 hold columns n and n ^ 1
+// of the same row m, and 16-lane groups one row of one tile (whole waves call
+// this).
 //   store: Y[m][n] = s
 //   rope:  RoPE pair (n, n+1) at position pos0 + m, or pos0 + depth(m) for a
 //          tree (Q and K rows, angles from epi_load), then fp16 Q -> q16[m][n],
 //          K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim], pos = pos0 + m
 //          (y0 = x0 c - x1 s, y1 = x0 s + x1 c; src/shaders/rope.glsl:50-73)
-//   silu:  rows interleaved (2i = gate i, 2i+1 = up i):
-//          a = g * (1 / (1 + e^-g)) * u, split: act[m][i] = hi, act[M + m][i] = lo
+//   silu:  rows interleaved (2i = gate i, 2i+1 = up i): a = g * (1 / (1 +
+//          e^-g)) * u, split: act[m][i] = hi, act[M + m][i] = lo
 //   resid: h[m][n] += s (in place); pss[m][t] = sum over the tile's 16 columns
-//          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m
+//          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m;
+//          with xn, the next GEMM's split X: xn[m][n] = hi, xn[xn_lo + m][n] =
+//          lo of h * xn_w[n] (the next norm's weights)
 __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l, float2 pre, int pos0)
 {
     const bool ok = m < a.M && n < a.N;
@@ -708,6 +787,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
         if (ok) {
             v = pre.x + s;
             f.h[(size_t)m * a.N + n] = v;
+            if (f.xn) {
+                _Float16 hi, lo;
+                split_hl(v * pre.y, hi, lo);
+                f.xn[(size_t)m * a.N + n] = hi;
+                f.xn[(size_t)(f.xn_lo + m) * a.N + n] = lo;
+            }
         }
         float sq = v * v;
         sq += __shfl_xor(sq, 1);
@@ -722,297 +807,189 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
     }
 }
 
-// X[m][k] = (v[m][k] * r_m) * w[k] into the LDS rows (fp16, or split into
-// rows m and M + m when a.hl), r_m = 1 /
-// sqrt(sum_p pss[m][p] / K + eps) (RMSNorm, src/shaders/ffn/ffn_fused.glsl:23-33).
-// Two phases so that the weight loads overlap the norm: norm_issue loads the
-// partial sums (rows wave and wave + NW, P <= 256, one 16-byte load per row),
-// the norm weights and the first kNormGroup rows of v into registers before
-// the weights' first batch is issued; norm_finish reduces the partials (four
-// per lane, then an xor tree), then converts float4 column groups
-// tid + 64 NW j (K <= 4096).  Rows past the first group (M > kNormGroup) are
-// loaded in norm_finish.  Rows past M and waves past K issue no loads: an
-// out-of-range buffer load still takes its turn in the texture unit.
-constexpr int kNormGroup = 8;
-constexpr int kNormMaxPartials = 256;
+// ---- split-K kernels (any M) --------------------------------------------------
+// Grid (row groups of kWaves 16-row tiles, K slices).  Wave w of a workgroup
+// owns tile blockIdx.x * kWaves + w over the slice's chunks.  Per batch of
+// CMAX chunks: the batch's X units to registers, every weight load of the
+// batch, X to LDS (XStage rows), barrier, dequantize + MFMA for the MT column
+// tiles.  Each wave accumulates its chunks in K order and stores the slice's
+// partial Y (high plus 2^-11 low part for split X) to out[ks][M][N];
+// gemm_reduce_kernel sums the slices in slice order, so every output row is
+// bitwise independent of M.
+constexpr int kMaxSlices = 32;
 
-template <int NW>
-struct NormRegs {
-    static constexpr int JN = 4096 / (NW * 64 * 4);  // float4 column groups per thread
-    float4 vv[kNormGroup][JN];
-    float4 w[JN];
-    float4 ps[2];
+// X slice of one batch in LDS: 16 MT rows of UB units (16 bytes = 8 halves)
+// plus one pad unit (bank spread); UB is a power of two <= 128.  Thread tid
+// stages unit tid % UB of rows tid / UB + pass * (1024 / UB).
+template <int MT, int UB>
+struct XStage {
+    static constexpr int kUnitsPerRow = UB + 1;
+    static constexpr int kRowsPerPass = kWaves * 64 / UB;
+    static constexpr int kXU = (16 * MT + kRowsPerPass - 1) / kRowsPerPass;  // passes = units per thread
 };
 
-template <int NW>
-__device__ __forceinline__ void norm_rows_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t vr, int m0,
-                                               NormRegs<NW>& n)
+// Load this batch's X slice (staged rows < xrows, units [0, U) starting at
+// element k0, U <= UB) into registers.  Units past K load 0.
+template <int MT, int UB>
+__device__ __forceinline__ void x_stage_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr,
+                                             uint4 (&xv)[XStage<MT, UB>::kXU], int k0, int U)
 {
-    const int K4 = a.K >> 2;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
+    const int k = k0 + 8 * uu;
 #pragma unroll
-    for (int j = 0; j < NormRegs<NW>::JN; ++j) {
-        const int c = (int)threadIdx.x + NW * 64 * j;
-        const bool wave_in = 64 * (wave + NW * j) < K4;  // wave-uniform
-#pragma unroll
-        for (int i = 0; i < kNormGroup; ++i) {
-            // rows past M and waves past K issue no load at all (an out-of-range
-            // buffer load still takes its turn in the texture unit)
-            if (m0 + i < a.M && wave_in)  // else left unset: norm_finish reads rows < M of waves in K
-                n.vv[i][j] = __builtin_bit_cast(
-                    float4, buf_load16(vr, c < K4 ? (uint32_t)((m0 + i) * K4 + c) * 16u : kOOB));
-        }
+    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
+        const int rho = m0 + u * XStage<MT, UB>::kRowsPerPass;
+        const bool ok = rho < a.xrows && uu < U && k < a.K;
+        xv[u] = buf_load16(xr, ok ? (uint32_t)(x_row(a, rho) * a.K + k) * 2u : kOOB);
     }
 }
 
-template <int NW>
-__device__ __forceinline__ void norm_issue(const GemmArgs& a, NormRegs<NW>& n)
+template <int MT, int UB>
+__device__ __forceinline__ void x_stage_store(const GemmArgs& a, uint4* xs, const uint4 (&xv)[XStage<MT, UB>::kXU],
+                                              int U)
 {
-    const GemmFuse& f = a.f;
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K4 = a.K >> 2;
-    const __amdgpu_buffer_rsrc_t pr = make_rsrc(f.pss, (uint32_t)a.M * (uint32_t)f.P * 4u);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(f.norm_w, (uint32_t)a.K * 4u);
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
-    // partial sums of rows wave and wave + NW (loads only where the row and
-    // the group of 64 partials exist: the conditions are wave-uniform)
-    // (lane holds partials 4 lane .. 4 lane + 3; those past P belong to the
-    // next row and are dropped in norm_finish)
+    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = wave + NW * i;
-        if (m < a.M)  // else left unset: norm_finish uses rows < M only
-            n.ps[i] = __builtin_bit_cast(float4, buf_load16(pr, 4 * lane < f.P ? (uint32_t)(m * f.P + 4 * lane) * 4u
-                                                                               : kOOB));
+    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
+        const int rho = m0 + u * XStage<MT, UB>::kRowsPerPass;
+        if (rho < a.xrows && uu < U) xs[rho * XStage<MT, UB>::kUnitsPerRow + uu] = xv[u];
     }
-#pragma unroll
-    for (int j = 0; j < NormRegs<NW>::JN; ++j) {
-        const int c = (int)threadIdx.x + NW * 64 * j;
-        if (64 * (wave + NW * j) < K4)
-            n.w[j] = __builtin_bit_cast(float4, buf_load16(wr, c < K4 ? (uint32_t)c * 16u : kOOB));
-    }
-    norm_rows_load<NW>(a, vr, 0, n);
 }
 
-template <int NW>
-__device__ __forceinline__ void norm_finish(const GemmArgs& a, NormRegs<NW>& n, uint8_t* xs, uint32_t pitch, float* rs)
+template <int TYPE, int MT, int CMAX>
+__global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
 {
+    constexpr int UPC = kUnitsPerChunk<TYPE>;
+    constexpr int UB = UPC * CMAX;
+    using XS = XStage<MT, UB>;
+    __shared__ uint4 xs[16 * MT * XS::kUnitsPerRow];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const GemmFuse& f = a.f;
-    const int K4 = a.K >> 2;
+    const int r = lane & 15, g = lane >> 4;
+    const int t = blockIdx.x * kWaves + wave;
+    const bool live = t < a.n_tiles;
+    const int ks = blockIdx.y;
+    int ca, cb;
+    slice_range(a, ks, ca, cb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
+    int xrow[MT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int m = wave + NW * i;
-        if (m >= a.M) continue;  // wave-uniform
-        const int p0 = 4 * lane;
-        const float4 v = n.ps[i];
-        float ss = ((p0 < f.P ? v.x : 0.0f) + (p0 + 1 < f.P ? v.y : 0.0f)) +
-                   ((p0 + 2 < f.P ? v.z : 0.0f) + (p0 + 3 < f.P ? v.w : 0.0f));
+    for (int mt = 0; mt < MT; ++mt)
+        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const NibbleConsts nk = nibble_consts();
+    float4_t acc[MT];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) rs[m] = 1.0f / __builtin_sqrtf(ss / (float)a.K + f.eps);
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c0 = ca; c0 < cb; c0 += CMAX) {
+        const int nc = min(CMAX, cb - c0);
+        uint4 xv[XS::kXU];
+        x_stage_load<MT, UB>(a, xr, xv, c0 * UPC * 8, UPC * nc);
+        pin_loads();
+        WBatch<TYPE, CMAX> b;
+        stream_load<TYPE, CMAX>(a, wr, live ? t : a.n_tiles, c0, nc, b);
+        pin_loads();
+        if (c0 != ca) __syncthreads();  // the previous batch is done reading xs
+        x_stage_store<MT, UB>(a, xs, xv, UPC * nc);
+        __syncthreads();
+        stream_mma<TYPE, CMAX, MT>(xs, xrow, UPC, 0, live ? nc : 0, 0, CMAX, b, nk, acc);
     }
-    lds_barrier();
-    const __amdgpu_buffer_rsrc_t vr = make_rsrc(f.v, (uint32_t)a.M * (uint32_t)a.K * 4u);
-    for (int m0 = 0; m0 < a.M; m0 += kNormGroup) {
-        if (m0) norm_rows_load<NW>(a, vr, m0, n);
+    if (!live) return;  // wave-uniform
+    float* out = a.out + (size_t)ks * a.M * a.N;
+    const int n = 16 * t + r;
 #pragma unroll
-        for (int j = 0; j < NormRegs<NW>::JN; ++j) {
-            const int c = (int)threadIdx.x + NW * 64 * j;
-            if (c < K4) {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int i = 0; i < kNormGroup; ++i) {
-                    const int m = m0 + i;
-                    if (m < a.M) {
-                        const float r = rs[m];
-                        const float v[4] = {(n.vv[i][j].x * r) * n.w[j].x, (n.vv[i][j].y * r) * n.w[j].y,
-                                            (n.vv[i][j].z * r) * n.w[j].z, (n.vv[i][j].w * r) * n.w[j].w};
-                        half4_t x, xl;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            _Float16 hi, lo;
-                            split_hl(v[e], hi, lo);
-                            x[e] = hi;
-                            xl[e] = lo;
-                        }
-                        *(half4_t*)(xs + m * pitch + 8 * c) = x;
-                        if (a.hl) *(half4_t*)(xs + (a.M + m) * pitch + 8 * c) = xl;
-                    }
-                }
-            }
+        for (int i = 0; i < 4; ++i) {
+            float v = acc[mt][i];
+            if (a.hl) v = v + __shfl_xor(v, 32) * kLoUnscale;  // lanes 0-31: + their low-part slot
+            const int m = acc_row(a, mt, lane, i);
+            if (m >= 0 && m < a.M && n < a.N) out[(size_t)m * a.N + n] = v;
         }
-    }
 }
 
-template <int CMAX>
-__device__ __forceinline__ void q4_k_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, uint32_t h_lane, int s0,
-                                                int nc, uint4 (&w0)[CMAX], uint4 (&w1)[CMAX], uint4 (&hd)[CMAX])
+// Y[m][n] = the sum of the ks_count slices of part in slice order, times the
+// row scale (if any), then the epilogue of output (m, n) (a.out is Y for the
+// store epilogue).  One thread per element of the padded [M][16 n_tiles]
+// grid, n fastest, so a 16-lane group is one row of one tile (the epilogue's
+// lane pairs and xor tree); the workgroup's rows get their scales first, one
+// wave per row.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const float* __restrict__ part)
 {
+    __shared__ float rs[256 / 16 + 2];
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int NP = 16 * a.n_tiles;
+    const int m = i / NP, n = i - m * NP;
+    const int m_first = (blockIdx.x * 256) / NP;
+    const int n_rows = min((blockIdx.x * 256 + 255) / NP - m_first + 1, 256 / 16 + 2);
+    const int pos0 = epi_pos0(a);
+    const bool ok = m < a.M && n < a.N;
+    const size_t MN = (size_t)a.M * a.N;
+    float v[kMaxSlices];
 #pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
-        const uint32_t o = (uint32_t)(s0 + i) * kQ4KChunk;
-        w0[i] = buf_load16(wr, i < nc ? w_lane + o : kOOB);
-        w1[i] = buf_load16(wr, i < nc ? w_lane + o + 1024 : kOOB);
-        hd[i] = buf_load16(wr, i < nc ? h_lane + o : kOOB);
-    }
-}
-
-// acc[mt] += the batch's super-blocks; A rows from LDS (unit xrow[mt] + 32 * sb + j).
-template <int CMAX, int MT>
-__device__ __forceinline__ void q4_k_mma_batch(const uint4* xs, const int (&xrow)[MT], int s0, int nc,
-                                               const uint4 (&w0)[CMAX], const uint4 (&w1)[CMAX],
-                                               const uint4 (&hd)[CMAX], int g, const NibbleConsts& nk,
-                                               float4_t (&acc)[MT])
-{
-    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < CMAX; ++i) {
-        if (i < nc) {
-            const uint32_t words[8] = {w0[i].x, w0[i].y, w0[i].z, w0[i].w, w1[i].x, w1[i].y, w1[i].z, w1[i].w};
-            const uint4 h = hd[i];
-            const float d = half_bits_to_float(h.x & 0xffffu);
-            const float dmin = half_bits_to_float(h.x >> 16);
-            SubScale ss[2];
-            half8_t mins[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                uint32_t scv, mn;
-                q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
-                const float fs = (float)scv;
-                ss[e].sc = splat2(fs);
-                ss[e].nsc1024 = splat2(-1024.0f * fs);
-                ss[e].sc16 = splat2(fs * 0.0625f);
-                ss[e].nsc64 = splat2(-64.0f * fs);
-                const _Float16 hm = (_Float16)(float)mn;
-                mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
-            }
-            float4_t P1[MT], P2[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                P1[mt] = zero4;
-                P2[mt] = zero4;
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + 32 * (s0 + i) + j]);
-                    P1[mt] = mfma16x16x32(A, B, P1[mt]);
-                    P2[mt] = mfma16x16x32(A, mins[j >> 2], P2[mt]);
-                }
-            }
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
-                acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
-            }
+    for (int k = 0; k < kMaxSlices; ++k) v[k] = ok && k < a.ks_count ? part[k * MN + (size_t)m * a.N + n] : 0.0f;
+    const float2 pre = epi_load(a, m < a.M ? m : a.M, n, pos0);
+    if (a.f.rs_pss) {
+        for (int j = threadIdx.x >> 6; j < n_rows; j += 4) {  // wave-uniform
+            const float r = rs_reduce(a, rs_load(a, m_first + j));
+            if ((threadIdx.x & 63) == 0) rs[j] = r;
         }
+        __syncthreads();
     }
+    float s = v[0];
+#pragma unroll
+    for (int k = 1; k < kMaxSlices; ++k)
+        if (k < a.ks_count) s += v[k];
+    if (a.f.rs_pss) s *= rs[min(m - m_first, 256 / 16 + 1)];
+    epilogue(a, s, m, n, n >> 4, threadIdx.x & 63, pre, pos0);
 }
 
-// One batch of up to CMAX chunks of one tile, in registers.
-template <int TYPE, int CMAX>
-struct WBatch;
-template <int CMAX>
-struct WBatch<ULSPEC_GGML_Q4_0, CMAX> {
-    static constexpr int kLoads = 2 * CMAX;  // buffer loads per batch
-    uint4 wq[CMAX];
-    uint2 sc[CMAX];
-};
-template <int CMAX>
-struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
-    static constexpr int kLoads = 3 * CMAX;
-    uint4 w0[CMAX], w1[CMAX], hd[CMAX];
-};
+// ---- whole-X kernels (small M) ------------------------------------------------
+// The whole X sits in LDS for the workgroup's lifetime.  Per iteration the NW
+// waves cover tpi = NW / P tiles x P parts of K (P a power of two, at most NW
+// and at most the chunks per row); wave p owns chunks [ca, cb) of its tiles
+// and the X of those chunks, which only it reads.  LDS layout, chunk-major:
+// unit c * CS + rho * RS + j holds X[x_row(rho)][8 (UPC c + j) .. + 7], RS =
+// UPC + 1 units per staged row and chunk (the pad unit spreads the rows over
+// the banks), CS = xrows * RS per chunk.  Each wave copies the X of its own
+// chunks (one contiguous LDS run) with direct buffer->LDS loads before its
+// weight loads and waits for those copies only (loads complete in issue
+// order): no barrier before the first multiply.  Parts are summed in part
+// order in LDS, then the row scale and the epilogue run.
+constexpr int kWideWaves = 16;
 
-template <int CMAX>
-struct WBatch<ULSPEC_GGML_Q8_0, CMAX> {
-    static constexpr int kLoads = 3 * CMAX;
-    uint4 w0[CMAX], w1[CMAX];
-    uint2 sc[CMAX];
-};
+template <int TYPE>
+constexpr int kRowStride = kUnitsPerChunk<TYPE> + 1;
 
-template <int CMAX>
-struct WBatch<ULSPEC_GGML_F16, CMAX> {
-    static constexpr int kLoads = 4 * CMAX;
-    uint4 w[CMAX][4];
-};
-
-template <int CMAX>
-__device__ __forceinline__ void f16_load_batch(__amdgpu_buffer_rsrc_t wr, uint32_t w_lane, int c0, int nc,
-                                               uint4 (&w)[CMAX][4])
+// This wave's X: chunks [ca, cb), all staged rows, into their LDS blocks --
+// one contiguous run of (cb - ca) * CS units, ceil((cb - ca) * CS / 64)
+// loads of 64 units (the pad units and units past K read as 0).
+template <int TYPE>
+__device__ __forceinline__ void x_copy_region(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes, int ca,
+                                              int cb, int CS)
 {
-#pragma unroll
-    for (int i = 0; i < CMAX; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            w[i][j] = buf_load16(wr, i < nc ? w_lane + (uint32_t)(c0 + i) * kF16Chunk + 1024u * j : kOOB);
-}
-
-// acc[mt] += the batch's chunks: four MFMAs of 32 K per chunk, no dequantization
-template <int CMAX, int MT>
-__device__ __forceinline__ void f16_mma_batch(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
-                                              const uint4 (&w)[CMAX][4], float4_t (&acc)[MT])
-{
-#pragma unroll
-    for (int i = 0; i < CMAX; ++i)
-        if (i < nc)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    acc[mt] = mfma16x16x32(__builtin_bit_cast(half8_t, xs[xrow[mt] + 4 * (4 * (c0 + i) + j)]),
-                                           __builtin_bit_cast(half8_t, w[i][j]), acc[mt]);
-}
-
-template <int TYPE, int CMAX>
-__device__ __forceinline__ void stream_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, int t, int c0, int nc,
-                                            WBatch<TYPE, CMAX>& b)
-{
-    const int lane = threadIdx.x & 63, r = lane & 15;
-    if (t >= a.n_tiles) nc = 0;
-    const uint32_t tile = (uint32_t)(t < a.n_tiles ? t : 0) * a.n_chunks;
-    if constexpr (TYPE == ULSPEC_GGML_F16)
-        f16_load_batch<CMAX>(wr, tile * kF16Chunk + lane * 16, c0, nc, b.w);
-    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
-        q8_0_load_batch<CMAX>(wr, tile * kQ80Chunk + lane * 16, tile * kQ80Chunk + 2048 + r * 8, c0, nc, b.w0, b.w1,
-                              b.sc);
-    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
-        q4_0_load_batch<CMAX>(wr, tile * kQ40Chunk + lane * 16, tile * kQ40Chunk + 1024 + r * 8, c0, nc, b.wq, b.sc);
-    else
-        q4_k_load_batch<CMAX>(wr, tile * kQ4KChunk + lane * 16, tile * kQ4KChunk + 2048 + r * 16, c0, nc, b.w0, b.w1,
-                              b.hd);
-}
-
-template <int TYPE, int CMAX, int MT>
-__device__ __forceinline__ void stream_mma_mt(const uint4* xs, const int (&xrow)[MT], int c0, int nc,
-                                              const WBatch<TYPE, CMAX>& b, const NibbleConsts& nk,
-                                              float4_t (&acc)[MT])
-{
-    if constexpr (TYPE == ULSPEC_GGML_F16)
-        f16_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w, acc);
-    else if constexpr (TYPE == ULSPEC_GGML_Q8_0)
-        q8_0_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w0, b.w1, b.sc, acc);
-    else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
-        q4_0_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.wq, b.sc, nk, acc);
-    else
-        q4_k_mma_batch<CMAX, MT>(xs, xrow, c0, nc, b.w0, b.w1, b.hd, (threadIdx.x & 63) >> 4, nk, acc);
-}
-
-template <int TYPE, int CMAX>
-__device__ __forceinline__ void stream_mma(const uint4* xs, int xrow, int c0, int nc, const WBatch<TYPE, CMAX>& b,
-                                           const NibbleConsts& nk, float4_t& acc)
-{
-    const int xr[1] = {xrow};
-    float4_t ac[1] = {acc};
-    stream_mma_mt<TYPE, CMAX, 1>(xs, xr, c0, nc, b, nk, ac);
-    acc = ac[0];
+    constexpr int UPC = kUnitsPerChunk<TYPE>, RS = kRowStride<TYPE>;
+    const int lane = threadIdx.x & 63;
+    const int KU = a.K / 8;
+    const int u0 = ca * CS, u1 = cb * CS;
+    const float inv_cs = 1.0f / (float)CS;
+    for (int q = u0; q < u1; q += 64) {
+        const int u = q + lane;
+        int c = (int)((float)u * inv_cs);  // u / CS, corrected below (u < 2^22)
+        if (c * CS > u) --c;
+        if ((c + 1) * CS <= u) ++c;
+        const int rem = u - c * CS;
+        const int rho = rem / RS, j = rem - rho * RS;
+        const int ku = c * UPC + j;
+        const uint32_t off = j < UPC && ku < KU && rho < a.xrows ? (uint32_t)(x_row(a, rho) * KU + ku) * 16u : kOOB;
+        if (u < u1)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                xr, (__attribute__((address_space(3))) void*)(xs_bytes + (size_t)q * 16), 16, off, 0, 0, 0);
+    }
 }
 
 // Output row the epilogue thread (lane l, accumulator row `row`) of a
-// whole-X kernel handles: row 4 (l / 16) + row; with split X the lanes 32-63
-// (the low-part slots) handle none (M).
+// whole-X kernel handles: 4 (l / 16) + row; with split X the lanes 32-63 (the
+// low-part slots) handle none (M).
 __device__ __forceinline__ int epi_row(const GemmArgs& a, int l, int row)
 {
     return a.hl && l >= 32 ? a.M : 4 * (l >> 4) + row;
@@ -1033,51 +1010,39 @@ __device__ __forceinline__ float red_sum(const GemmArgs& a, const float* red, in
     return s;
 }
 
-// Multiply this wave's part of tile slot tw of iteration `it` (first batch
-// already in `cur`), sum the parts in LDS, run the epilogue.
-template <int TYPE, int CMAX, int NW>
-__device__ __forceinline__ void stream_tile(const GemmArgs& a, __amdgpu_buffer_rsrc_t wr, const uint4* xs, float* red,
-                                            int xrow, int it, int tw, int P, int tpi, int ca, int cb,
-                                            WBatch<TYPE, CMAX>& cur, const NibbleConsts& nk, int pos0,
-                                            const float2* pre0 = nullptr)
+// Row scales of rows wave and wave + NW into rs (LDS), from loads issued by
+// the same wave before its X and weights.
+template <int NW>
+__device__ __forceinline__ void rs_finish(const GemmArgs& a, const float4 (&ps)[2], float* rs)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t = it * tpi + tw;
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    stream_mma<TYPE, CMAX>(xs, xrow, ca, t < a.n_tiles ? min(CMAX, cb - ca) : 0, cur, nk, acc);
-    for (int c0 = ca + CMAX; c0 < cb; c0 += CMAX) {  // the rest of a long part (not prefetched)
-        const int nc = min(CMAX, cb - c0);
-        stream_load<TYPE, CMAX>(a, wr, t, c0, nc, cur);
-        pin_loads();
-        stream_mma<TYPE, CMAX>(xs, xrow, c0, t < a.n_tiles ? nc : 0, cur, nk, acc);
-    }
-    __syncthreads();  // the previous iteration's epilogue is done with red
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
-    __syncthreads();
-    // 256 threads per tile slot, NW / 4 slots per pass
-    const int row = (threadIdx.x >> 6) & 3, l = lane;
-    for (int j = threadIdx.x >> 8; j < tpi; j += NW / 4) {
-        const float s = red_sum(a, red, j, P, row, l);
-        const int tt = it * tpi + j;
-        const int m = epi_row(a, l, row), n = 16 * tt + (l & 15);
-        epilogue(a, s, m, n, tt, l, pre0 ? *pre0 : epi_load(a, m, n, pos0), pos0);
+    for (int i = 0; i < (NW < 16 ? 2 : 1); ++i) {
+        const int m = wave + NW * i;
+        if (m < a.M) {  // wave-uniform
+            const float r = rs_reduce(a, ps[i]);
+            if (lane == 0) rs[m] = r;
+        }
     }
 }
 
-// NW waves per workgroup.  PIPE: the grid is smaller than the iteration count
-// and the next iteration's first batch is prefetched (two register sets);
-// otherwise every workgroup runs exactly one iteration.  NORM: X is built by
-// the RMSNorm prologue, else copied.  Issue order: X (copies or the norm's
-// register loads), then the first weight batch.  A copied X is waited for per
-// wave (vmcnt of its own copies, weights still in flight); the norm's X needs
-// every wave's rows, so it ends in a barrier.
-template <int TYPE, int CMAX, int NW, bool PIPE, bool NORM>
+template <int NW>
+__device__ __forceinline__ void rs_issue(const GemmArgs& a, float4 (&ps)[2])
+{
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int i = 0; i < (NW < 16 ? 2 : 1); ++i)
+        if (wave + NW * i < a.M) ps[i] = rs_load(a, wave + NW * i);
+}
+
+// One iteration per workgroup (tiles <= what the grid holds at once).
+template <int TYPE, int CMAX, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
     __shared__ float red[NW * 4 * 64];
-    __shared__ float rs[kNormMaxRows];
+    __shared__ float rs[16];
+    constexpr int RS = kRowStride<TYPE>, NWL = WBatch<TYPE, CMAX>::kLoadsPerChunk;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -1086,78 +1051,68 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int ca = p * a.ks_q + min(p, a.ks_r);
     const int cb = ca + a.ks_q + (p < a.ks_r ? 1 : 0);
     const int nc0 = max(0, min(CMAX, cb - ca));
-    const int n_iter = (a.n_tiles + tpi - 1) / tpi;
-    const uint32_t pitch = wide_pitch(a.K);
+    const int CS = a.xrows * RS;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = xslot_row(a, 0, r) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
+    const int xrow[1] = {xslot_row(a, 0, r) * RS + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     const int pos0 = epi_pos0(a);
+    const int it = blockIdx.x, t = it * tpi + tw;
 
-    NormRegs<NW> nr;
-    if constexpr (NORM)
-        norm_issue<NW>(a, nr);
-    else
-        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
-                                         min(cb, a.n_chunks));
+    // issue order: row-scale partials, this wave's X (its whole part), the
+    // first batch of weights, the epilogue operands
+    float4 ps[2];
+    if (a.f.rs_pss) rs_issue<NW>(a, ps);
+    x_copy_region<TYPE>(a, xr, (uint8_t*)xs, ca, cb, CS);
     pin_loads();
     WBatch<TYPE, CMAX> A;
-    int it = blockIdx.x;
-    stream_load<TYPE, CMAX>(a, wr, it * tpi + tw, ca, nc0, A);
-    // one tile per workgroup: the epilogue operands of this thread's output
-    // (tile slot 0 is the only one, tpi = 1) load with the weights
-    float2 pre0 = {0.f, 0.f};
-    if constexpr (!PIPE)
-        pre0 = epi_load(a, (threadIdx.x >> 8) == 0 ? epi_row(a, lane, (threadIdx.x >> 6) & 3) : a.M,
-                        16 * it + (lane & 15), pos0);
+    stream_load<TYPE, CMAX>(a, wr, t, ca, nc0, A);
+    // the epilogue operands of this thread's output (tile slot j = tid / 256)
+    const int j_epi = threadIdx.x >> 8;
+    const float2 pre = epi_load(a, j_epi < tpi ? epi_row(a, lane, (threadIdx.x >> 6) & 3) : a.M,
+                                16 * (it * tpi + j_epi) + (lane & 15), pos0);
     pin_loads();
-    if constexpr (NORM) {
-        norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
-        lds_barrier();
-    } else {
-        // this wave's copies: issued before its weight loads and the epilogue's
-        vm_wait_dyn(WBatch<TYPE, CMAX>::kLoads + (PIPE ? 0 : epi_nloads(a)));
+    if (a.f.rs_pss) rs_finish<NW>(a, ps, rs);
+    vm_wait_dyn(CMAX * NWL + epi_nloads(a));  // this wave's X copies, issued before its weights
+    float4_t acc[1] = {{0.f, 0.f, 0.f, 0.f}};
+    stream_mma<TYPE, CMAX, 1>(xs, xrow, CS, ca, t < a.n_tiles ? nc0 : 0, 0, CMAX, A, nk, acc);
+    for (int c0 = ca + CMAX; c0 < cb; c0 += CMAX) {  // the rest of a long part (not prefetched)
+        const int nc = min(CMAX, cb - c0);
+        stream_load<TYPE, CMAX>(a, wr, t, c0, nc, A);
+        pin_loads();
+        stream_mma<TYPE, CMAX, 1>(xs, xrow, CS, c0, t < a.n_tiles ? nc : 0, 0, CMAX, A, nk, acc);
     }
-    if constexpr (!PIPE) {
-        stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0, &pre0);
-    } else {
-        WBatch<TYPE, CMAX> B;
-        while (true) {
-            int nxt = it + gridDim.x;
-            stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, B);
-            pin_loads();
-            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, A, nk, pos0);
-            it = nxt;
-            if (it >= n_iter) break;
-            nxt = it + gridDim.x;
-            stream_load<TYPE, CMAX>(a, wr, nxt * tpi + tw, ca, nxt < n_iter ? nc0 : 0, A);
-            pin_loads();
-            stream_tile<TYPE, CMAX, NW>(a, wr, xs, red, xrow, it, tw, P, tpi, ca, cb, B, nk, pos0);
-            it = nxt;
-            if (it >= n_iter) break;
-        }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[0][i];
+    __syncthreads();
+    // 256 threads per tile slot, NW / 4 slots per pass
+    const int row = (threadIdx.x >> 6) & 3, l = lane;
+    for (int j = j_epi; j < tpi; j += NW / 4) {
+        float s = red_sum(a, red, j, P, row, l);
+        const int tt = it * tpi + j;
+        const int m = epi_row(a, l, row), n = 16 * tt + (l & 15);
+        if (a.f.rs_pss && m < a.M) s *= rs[m];
+        epilogue(a, s, m, n, tt, l, j == j_epi ? pre : epi_load(a, m, n, pos0), pos0);
     }
 }
 
-// ---- ring-buffered whole-X kernel (more tiles than CUs) ----------------------
-// One 8-wave workgroup per CU walks its iterations (tpi = 8 / P tiles x P
+// ---- ring kernel (more tiles than CUs) ----------------------------------------
+// One 16-wave workgroup per CU walks its iterations (tpi = 16 / P tiles x P
 // parts each, as above) with a ring of D register batches: the first D
-// iterations' weights are issued before X is finished, and each iteration
-// refills the batch it has just multiplied with the weights of the iteration
-// D ahead.  So D iterations of weight loads stay in flight behind the
-// arithmetic (one iteration of 16-row tiles over K = 4096 is 36 KB of Q4_K
-// per CU), and a wave never waits to issue before it multiplies.  Part sums
-// go through two alternating LDS buffers, so one barrier per iteration
-// suffices: iteration i + 2 writes the buffer iteration i read, and every
-// wave has finished reading it before the barrier of iteration i + 1.
+// iterations' weights are issued (after the wave's X copies) before the first
+// multiply, and each iteration refills the batch it has
+// just multiplied with the weights of the iteration D ahead, so D iterations
+// of weight loads stay in flight behind the arithmetic.  Part sums go through
+// two alternating LDS buffers, so one barrier per iteration suffices.
 constexpr int kRingWaves = 16;
 constexpr int kRingDepth = 2;
 
-// Sum the P part sums of the tpi (<= NW / 4) tiles of global iteration `it` and
-// run their epilogue (threads 256 j .. 256 j + 255 take tile slot j); pre is
-// this thread's epi_load of the same output.
+// Sum the P part sums of the tpi (<= NW / 4) tiles of global iteration `it`,
+// scale and run their epilogue (threads 256 j .. 256 j + 255 take tile slot
+// j); pre is this thread's epi_load of the same output.
 template <int NW>
-__device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc, float* red, int it, int P, int tpi,
-                                          float2 pre, int pos0)
+__device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc, float* red, const float* rs, int it,
+                                          int P, int tpi, float2 pre, int pos0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -1165,9 +1120,11 @@ __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc
     lds_barrier();
     const int row = (threadIdx.x >> 6) & 3, l = lane, j = threadIdx.x >> 8;
     if (j < tpi) {
-        const float s = red_sum(a, red, j, P, row, l);
+        float s = red_sum(a, red, j, P, row, l);
         const int tt = it * tpi + j;
-        epilogue(a, s, epi_row(a, l, row), 16 * tt + (l & 15), tt, l, pre, pos0);
+        const int m = epi_row(a, l, row);
+        if (a.f.rs_pss && m < a.M) s *= rs[m];
+        epilogue(a, s, m, 16 * tt + (l & 15), tt, l, pre, pos0);
     }
 }
 
@@ -1180,12 +1137,13 @@ __device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int t
     return epi_load(a, m, 16 * (it * tpi + j) + (l & 15), pos0);
 }
 
-template <int TYPE, int C, int D, int NW, bool NORM>
+template <int TYPE, int C, int D, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
     __shared__ float red[2][NW * 4 * 64];
-    __shared__ float rs[kNormMaxRows];
+    __shared__ float rs[16];
+    constexpr int RS = kRowStride<TYPE>, NWL = WBatch<TYPE, C>::kLoadsPerChunk;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -1195,22 +1153,21 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int nc = a.ks_q + (p < a.ks_r ? 1 : 0);  // <= C (checked by the host)
     const int n_iter = (a.n_tiles + tpi - 1) / tpi;
     const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const uint32_t pitch = wide_pitch(a.K);
+    const int CS = a.xrows * RS;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const int xrow = xslot_row(a, 0, r) * (int)(pitch / 16) + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
+    const int xrow[1] = {xslot_row(a, 0, r) * RS + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
-
     const int pos0 = epi_pos0(a);
     auto git = [&](int li) { return (int)blockIdx.x + li * (int)gridDim.x; };  // global iteration
 
-    NormRegs<NW> nr;
-    if constexpr (NORM)
-        norm_issue<NW>(a, nr);
-    else
-        x_copy_own<kUnitsPerChunk<TYPE>>(a, make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u), (uint8_t*)xs, ca,
-                                         ca + nc);
+    // issue order: row-scale partials, this wave's X, D batches of weights
+    // (each followed by its epilogue operands)
+    float4 ps[2];
+    if (a.f.rs_pss) rs_issue<NW>(a, ps);
+    x_copy_region<TYPE>(a, xr, (uint8_t*)xs, ca, ca + nc, CS);
     pin_loads();
     WBatch<TYPE, C> ring[D];
     float2 pre[D];
@@ -1220,145 +1177,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
         pre[k] = ring_epi_load(a, git(k), tpi, pos0);
     }
     pin_loads();
-    if constexpr (NORM) {
-        norm_finish<NW>(a, nr, (uint8_t*)xs, pitch, rs);
-        lds_barrier();
-    } else {
-        vm_wait_dyn(D * (WBatch<TYPE, C>::kLoads + epi_nloads(a)));  // this wave's copies
-    }
+    if (a.f.rs_pss) rs_finish<NW>(a, ps, rs);
+    vm_wait_dyn(D * (C * NWL + epi_nloads(a)));  // this wave's X copies
     for (int base = 0; base < n_loc; base += D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             const int li = base + k;
             if (li >= n_loc) break;
             const int t = tile_of(li);
-            float4_t acc = {0.f, 0.f, 0.f, 0.f};
-            stream_mma<TYPE, C>(xs, xrow, ca, t < a.n_tiles ? nc : 0, ring[k], nk, acc);
+            float4_t acc[1] = {{0.f, 0.f, 0.f, 0.f}};
+            stream_mma<TYPE, C, 1>(xs, xrow, CS, ca, t < a.n_tiles ? nc : 0, 0, C, ring[k], nk, acc);
             const float2 pk = pre[k];
             stream_load<TYPE, C>(a, wr, tile_of(li + D), ca, nc, ring[k]);
             pre[k] = ring_epi_load(a, git(li + D), tpi, pos0);
             pin_loads();
-            tile_sums<NW>(a, acc, red[li & 1], git(li), P, tpi, pk, pos0);
+            tile_sums<NW>(a, acc[0], red[li & 1], rs, git(li), P, tpi, pk, pos0);
         }
     }
 }
-
-// ---- split-K kernels (any M) --------------------------------------------------
-// Grid (row groups of kWaves 16-row tiles, K slices).  Wave w of a workgroup
-// owns tile blockIdx.x * kWaves + w over the slice's chunks.  Per batch of
-// CMAX chunks: the batch's X units to registers, every weight load of the
-// batch, X to LDS (XStage rows), barrier, dequantize + MFMA for the MT column
-// tiles.  Out-of-range chunks (past the slice or the last tile) load from an
-// offset past the buffer, which returns 0 and moves no data.  Each wave
-// accumulates its chunks in K order and stores the slice's partial Y (high
-// plus 2^-11 low part for split X) to out[ks][M][N]; gemm_reduce_kernel sums
-// the slices in slice order, so every output row is bitwise independent of M.
-constexpr int kMaxSlices = 32;
-
-template <int TYPE, int MT, int CMAX>
-__global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
-{
-    constexpr int UPC = kUnitsPerChunk<TYPE>;
-    constexpr int UB = UPC * CMAX;
-    using XS = XStage<MT, UB>;
-    __shared__ uint4 xs[16 * MT * XS::kUnitsPerRow];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int t = blockIdx.x * kWaves + wave;
-    const bool live = t < a.n_tiles;
-    const int ks = blockIdx.y;
-    int ca, cb;
-    slice_range(a, ks, ca, cb);
-    const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)a.xrows * (uint32_t)a.K * 2u);
-    int xrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
-    const NibbleConsts nk = nibble_consts();
-    float4_t acc[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = ca; c0 < cb; c0 += CMAX) {
-        const int nc = min(CMAX, cb - c0);
-        uint4 xv[XS::kXU];
-        x_stage_load<MT, UB>(xr, xv, a.xrows, a.K, c0 * UPC * 8, UPC * nc);
-        pin_loads();
-        WBatch<TYPE, CMAX> b;
-        stream_load<TYPE, CMAX>(a, wr, live ? t : a.n_tiles, c0, nc, b);
-        pin_loads();
-        if (c0 != ca) __syncthreads();  // the previous batch is done reading xs
-        x_stage_store<MT, UB>(xs, xv, a.xrows, UPC * nc);
-        __syncthreads();
-        stream_mma_mt<TYPE, CMAX, MT>(xs, xrow, 0, live ? nc : 0, b, nk, acc);
-    }
-    if (!live) return;  // wave-uniform
-    float* out = a.out + (size_t)ks * a.M * a.N;
-    const int n = 16 * t + r;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float v = acc[mt][i];
-            if (a.hl) v = v + __shfl_xor(v, 32) * kLoUnscale;  // lanes 0-31: + their low-part slot
-            const int m = acc_row(a, mt, lane, i);
-            if (m >= 0 && m < a.M && n < a.N) out[(size_t)m * a.N + n] = v;
-        }
-}
-
-// Y[m][n] = the sum of the ks_count slices of part in slice order, then the
-// epilogue of output (m, n) (a.out is Y for the store epilogue).  One thread
-// per element of the padded [M][16 n_tiles] grid, n fastest, so a 16-lane
-// group is one row of one tile (the epilogue's lane pairs and xor tree).
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const float* __restrict__ part)
-{
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int NP = 16 * a.n_tiles;
-    const int m = i / NP, n = i - m * NP;
-    const int pos0 = epi_pos0(a);
-    const bool ok = m < a.M && n < a.N;
-    const size_t MN = (size_t)a.M * a.N;
-    float v[kMaxSlices];
-#pragma unroll
-    for (int k = 0; k < kMaxSlices; ++k) v[k] = ok && k < a.ks_count ? part[k * MN + (size_t)m * a.N + n] : 0.0f;
-    const float2 pre = epi_load(a, m < a.M ? m : a.M, n, pos0);
-    float s = v[0];
-#pragma unroll
-    for (int k = 1; k < kMaxSlices; ++k)
-        if (k < a.ks_count) s += v[k];
-    epilogue(a, s, m, n, n >> 4, threadIdx.x & 63, pre, pos0);
-}
-
-// Split X of the RMSNorm for the split-K path: x[m][k] = (v[m][k] * r_m) *
-// w[k] split into rows m (hi) and M + m (lo), r_m = 1 / sqrt(sum_p pss[m][p] /
-// K + eps), the partial sums reduced as the whole-X prologue reduces them.
-// One 256-thread workgroup per row.
-__global__ __launch_bounds__(256) void norm_split_kernel(GemmFuse f, int M, int K, _Float16* __restrict__ x)
-{
-    __shared__ float rs;
-    const int m = blockIdx.x, lane = threadIdx.x & 63;
-    if (threadIdx.x < 64) {
-        const int p0 = 4 * lane;
-        float pv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pv[e] = p0 + e < f.P ? f.pss[(size_t)m * f.P + p0 + e] : 0.0f;
-        float ss = (pv[0] + pv[1]) + (pv[2] + pv[3]);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        if (lane == 0) rs = 1.0f / __builtin_sqrtf(ss / (float)K + f.eps);
-    }
-    __syncthreads();
-    const float r = rs;
-    for (int k = threadIdx.x; k < K; k += 256) {
-        _Float16 hi, lo;
-        split_hl((f.v[(size_t)m * K + k] * r) * f.norm_w[k], hi, lo);
-        x[(size_t)m * K + k] = hi;
-        x[(size_t)(M + m) * K + k] = lo;
-    }
-}
-
-constexpr int kQ40Stream = 12;
-constexpr int kQ4KStream = 6;
 
 // Chunks per batch of the split-K kernel: about 32 weight registers per lane
 // (Q4_0 6 per chunk, Q4_K 12, Q8_0 10, F16 16) up to two column tiles, half
@@ -1396,17 +1232,25 @@ void slice_launch_t(const GemmArgs& a, int mt, hipStream_t st)
 
 namespace ulspec {
 
-// LDS available to one workgroup on gfx950, and what the streaming kernel
-// keeps besides X (part sums, norm factors, margin).
+// LDS available to one workgroup on gfx950, and what each whole-X kernel
+// keeps besides X (part sums and row scales).
 constexpr size_t kWideLdsMax = 160 * 1024;
-constexpr size_t kStreamStatic = kWideWaves * 4 * 64 * sizeof(float) + 512;
+constexpr size_t kStaticWide = (size_t)kWideWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+constexpr size_t kStaticSmall = (size_t)8 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+constexpr size_t kStaticRing = (size_t)2 * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
 
-bool wide_fits(int rows, uint32_t K)
+// LDS bytes of the whole X of `rows` staged rows in the chunk-major layout.
+size_t x_lds_bytes(const Weight& w, int rows)
 {
-    return rows <= 16 && (size_t)rows * wide_pitch(K) <= kWideLdsMax - kStreamStatic;
+    const size_t rs = (w.type == ULSPEC_GGML_Q4_K ? 32 : 16) + 1;
+    return (size_t)w.n_chunks * rows * rs * 16;
 }
 
-// Opt the whole-X kernels in to the LDS they need for X.
+bool wide_fits(const Weight& w, int rows)
+{
+    return rows <= 16 && x_lds_bytes(w, rows) + kStaticWide <= kWideLdsMax;
+}
+
 // Batch sizes (chunks per wave) the one-tile-per-workgroup kernel is built
 // for: a launch takes the smallest that holds a whole part, so no load slot
 // is wasted on chunks past the part (longer parts loop over batches).
@@ -1417,50 +1261,43 @@ using WideQ4K = CList<1, 2, 3, 4>;
 using WideF16 = CList<1, 2>;  // 16 VGPRs of weights per chunk
 using WideQ80 = CList<1, 2, 3, 4, 6>;  // 10 VGPRs of weights per chunk
 
-// Per type: the one-tile batch sizes and the pipelined kernel's batch.
 template <int TYPE>
 struct GemmCfg;
 template <>
 struct GemmCfg<ULSPEC_GGML_Q4_0> {
     using Wide = WideQ40;
-    static constexpr int kStream = kQ40Stream;
 };
 template <>
 struct GemmCfg<ULSPEC_GGML_Q4_K> {
     using Wide = WideQ4K;
-    static constexpr int kStream = kQ4KStream;
 };
 template <>
 struct GemmCfg<ULSPEC_GGML_Q8_0> {
     using Wide = WideQ80;
-    static constexpr int kStream = 8;
 };
 template <>
 struct GemmCfg<ULSPEC_GGML_F16> {
     using Wide = WideF16;
-    static constexpr int kStream = 2;
 };
 
 template <int TYPE, int... C>
 void wide_kernels(CList<C...>, std::vector<const void*>& out)
 {
-    (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves, false, false>), ...);
-    (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves, false, true>), ...);
+    (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves>), ...);
 }
 
 // One tile per 8-wave workgroup, one chunk per wave: weights of at most 8
-// chunks per row (Q4_K K <= 2048) with 1-2 tiles per CU.  The workgroups of
-// one launch are all resident at once, so every CU works, where the ring
-// kernel's 16-wave workgroups would leave CUs idle (384 tiles of 8 chunks: 192
-// of them).  With more tiles per CU the ring kernel, which normalizes X once
+// chunks per row (Q4_K K <= 2048) with up to 4 tiles per CU.  The workgroups
+// of one launch are all resident at once, so every CU works, where the ring
+// kernel's 16-wave workgroups would leave CUs idle (384 tiles of 8 chunks:
+// 192 of them).  With more tiles per CU the ring kernel, which copies X once
 // per CU instead of once per tile, is faster.
 constexpr int kSmallWaves = 8;
-constexpr int kSmallTilesPerCu = 4;      // copied X
-constexpr int kSmallTilesPerCuNorm = 2;  // RMSNorm prologue: each workgroup normalises the whole of X
+constexpr int kSmallTilesPerCu = 4;
 
 // Launch the one-tile kernel with the smallest batch >= cpp (the largest when none is).
 template <int TYPE, int... C>
-void wide_launch(CList<C...>, int cpp, bool norm, dim3 grid, dim3 block, size_t lds, hipStream_t st, GemmArgs& a)
+void wide_launch(CList<C...>, int cpp, dim3 grid, dim3 block, size_t lds, hipStream_t st, GemmArgs& a)
 {
     constexpr int cs[] = {C...};
     int pick = cs[sizeof...(C) - 1];
@@ -1474,117 +1311,92 @@ void wide_launch(CList<C...>, int cpp, bool norm, dim3 grid, dim3 block, size_t 
         constexpr int CM = decltype(cmax)::value;
         if (done || CM != pick) return;
         done = true;
-        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CM, kWideWaves, false, true>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CM, kWideWaves, false, false>), grid, block, lds, st, a);
+        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CM, kWideWaves>), grid, block, lds, st, a);
     };
     (one(std::integral_constant<int, C>{}), ...);
 }
 
-// Static LDS of the ring kernel: two part-sum buffers and the norm factors.
-constexpr size_t kRingStatic = 2 * kRingWaves * 4 * 64 * sizeof(float) + 512;
-
 template <int TYPE>
-void type_kernels(std::vector<const void*>& fns, std::vector<const void*>& rings)
+void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& small, std::vector<const void*>& rings)
 {
-    fns.push_back((const void*)gemm_stream_kernel<TYPE, GemmCfg<TYPE>::kStream, kStreamWaves, true, false>);
-    fns.push_back((const void*)gemm_stream_kernel<TYPE, GemmCfg<TYPE>::kStream, kStreamWaves, true, true>);
-    wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, fns);
-    fns.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves, false, false>);
-    fns.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves, false, true>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, false>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, true>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, false>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, true>);
+    wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, wide);
+    small.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves>);
+    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves>);
 }
 
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
-    std::vector<const void*> fns, rings;
-    type_kernels<ULSPEC_GGML_Q4_0>(fns, rings);
-    type_kernels<ULSPEC_GGML_Q4_K>(fns, rings);
-    type_kernels<ULSPEC_GGML_F16>(fns, rings);
-    type_kernels<ULSPEC_GGML_Q8_0>(fns, rings);
-    const int dyn = (int)(kWideLdsMax - kStreamStatic);
-    for (const void* f : fns) {
-        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
-        if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
-    }
-    const int dyn_ring = (int)(kWideLdsMax - kRingStatic);
-    for (const void* f : rings) {
-        hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, dyn_ring);
-        if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
-    }
+    std::vector<const void*> wide, small, rings;
+    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings);
+    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings);
+    type_kernels<ULSPEC_GGML_F16>(wide, small, rings);
+    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings);
+    const struct {
+        const std::vector<const void*>* fns;
+        size_t fixed;
+    } groups[] = {{&wide, kStaticWide}, {&small, kStaticSmall}, {&rings, kStaticRing}};
+    for (const auto& gr : groups)
+        for (const void* f : *gr.fns) {
+            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)(kWideLdsMax - gr.fixed));
+            if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
+        }
     return ULSPEC_OK;
 }
 
-// Launch the whole-X kernel.  1-2 tiles per CU and at most 8 chunks per row:
-// the 8-wave one-tile kernel.  More tiles than CUs and at most two chunks per
-// part: the ring kernel, one 16-wave workgroup per CU, P parts per tile (the
-// largest power of two <= min(16, chunks per row), P >= 4), 16 / P tiles per
-// iteration.  Otherwise the older pipelined 8-wave kernel for more tiles than
-// CUs, else one 16-wave workgroup per tile with 16 parts (waves with an empty
-// part idle).
+// Launch a whole-X kernel if one fits; false when the split-K path must run.
+// At most 8 chunks per row and 1-4 tiles per CU: the 8-wave one-tile kernel.
+// More tiles than CUs and at most two chunks per part: the ring kernel, one
+// 16-wave workgroup per CU, P parts per tile (the largest power of two <=
+// min(16, chunks per row), P >= 4), 16 / P tiles per iteration.  At most one
+// tile per CU: one 16-wave workgroup per tile with 16 parts (waves with an
+// empty part idle).
 template <int TYPE>
-void stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
+bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     const int n_cu = std::max(1, ctx->n_cu);
     const bool pipe = (int)w.n_tiles > n_cu;
-    const size_t lds = (size_t)a.xrows * wide_pitch(w.k);
-    const bool norm = a.f.pro == kProNorm;
+    const size_t lds = x_lds_bytes(w, a.xrows);
     hipStream_t st = ctx->stream;
+    if (a.xrows > 16) return false;
     auto split = [&](int P) {
         a.ks_count = P;
         a.ks_q = (int)(w.n_chunks / P);
         a.ks_r = (int)(w.n_chunks % P);
     };
-    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves &&
-        (int)w.n_tiles <= (norm ? kSmallTilesPerCuNorm : kSmallTilesPerCu) * n_cu) {
+    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves && (int)w.n_tiles <= kSmallTilesPerCu * n_cu &&
+        lds + kStaticSmall <= kWideLdsMax) {
         split(kSmallWaves);  // one chunk (or none) per wave
-        const dim3 grid(w.n_tiles), block(kSmallWaves * 64);
-        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves, false, true>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves, false, false>), grid, block, lds, st, a);
-        return;
+        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves>), dim3(w.n_tiles), dim3(kSmallWaves * 64), lds,
+                           st, a);
+        return true;
     }
     if (pipe) {
         int P = kRingWaves;
         while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
         const int cpp = (int)((w.n_chunks + P - 1) / P);
-        if (P >= 4 && cpp <= 2 && lds + kRingStatic <= kWideLdsMax) {
-            split(P);
-            const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
-            const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
-            if (cpp <= 1) {
-                if (norm) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, true>), grid, block, lds, st, a);
-                else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves, false>), grid, block, lds, st, a);
-            } else {
-                if (norm) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, true>), grid, block, lds, st, a);
-                else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves, false>), grid, block, lds, st, a);
-            }
-            return;
-        }
+        if (P < 4 || cpp > 2 || lds + kStaticRing > kWideLdsMax) return false;
+        split(P);
+        const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
+        const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
+        if (cpp <= 1) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves>), grid, block, lds, st, a);
+        else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves>), grid, block, lds, st, a);
+        return true;
     }
-    int P = pipe ? kStreamWaves : kWideWaves;
-    if (pipe)
-        while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
-    split(P);
-    const int n_iter = ((int)w.n_tiles + (pipe ? kStreamWaves / P : 1) - 1) / (pipe ? kStreamWaves / P : 1);
-    const dim3 grid(pipe ? std::min(n_iter, n_cu) : n_iter), block((pipe ? kStreamWaves : kWideWaves) * 64);
-    if (pipe) {
-        constexpr int CS = GemmCfg<TYPE>::kStream;
-        if (norm) hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CS, kStreamWaves, true, true>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((gemm_stream_kernel<TYPE, CS, kStreamWaves, true, false>), grid, block, lds, st, a);
-    } else {
-        const int cpp = a.ks_q + (a.ks_r ? 1 : 0);
-        wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, cpp, norm, grid, block, lds, st, a);
-    }
+    if (lds + kStaticWide > kWideLdsMax) return false;
+    split(kWideWaves);
+    const int cpp = a.ks_q + (a.ks_r ? 1 : 0);
+    wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, cpp, dim3(w.n_tiles), dim3(kWideWaves * 64), lds, st, a);
+    return true;
 }
 
-void stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
+bool stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
-    if (w.type == ULSPEC_GGML_Q4_0) stream_launch_t<ULSPEC_GGML_Q4_0>(ctx, w, a);
-    else if (w.type == ULSPEC_GGML_Q4_K) stream_launch_t<ULSPEC_GGML_Q4_K>(ctx, w, a);
-    else if (w.type == ULSPEC_GGML_Q8_0) stream_launch_t<ULSPEC_GGML_Q8_0>(ctx, w, a);
-    else stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
+    if (w.type == ULSPEC_GGML_Q4_0) return stream_launch_t<ULSPEC_GGML_Q4_0>(ctx, w, a);
+    if (w.type == ULSPEC_GGML_Q4_K) return stream_launch_t<ULSPEC_GGML_Q4_K>(ctx, w, a);
+    if (w.type == ULSPEC_GGML_Q8_0) return stream_launch_t<ULSPEC_GGML_Q8_0>(ctx, w, a);
+    return stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
 }
 
 // K slices per weight: about one workgroup per CU in total.
@@ -1605,7 +1417,7 @@ size_t gemm_workspace_bytes(const Weight& w)
 
 namespace {
 
-GemmArgs make_args(const Weight& w, const _Float16* x, uint32_t M, bool hl, float* out)
+GemmArgs make_args(const Weight& w, const _Float16* x, uint32_t M, bool hl, uint32_t lo_rows, float* out)
 {
     GemmArgs a;
     a.w = w.dev;
@@ -1621,19 +1433,21 @@ GemmArgs make_args(const Weight& w, const _Float16* x, uint32_t M, bool hl, floa
     a.ks_q = (int)w.n_chunks;
     a.ks_r = 0;
     a.hl = hl ? 1 : 0;
+    a.lo_rows = hl ? (int)lo_rows : 0;
     a.xrows = hl ? 2 * (int)M : (int)M;
     a.f = GemmFuse();
     return a;
 }
 
-// The split-K kernel over a.M rows into part[ks][M][N], then the slice sum and
-// a.f's epilogue into y (one slice and a plain store: straight into y).
+// The split-K kernel over a.M rows into part[ks][M][N], then the slice sum, row
+// scale and a.f's epilogue into y (one slice, no row scale and a plain store:
+// straight into y).
 void split_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs a, float* part, float* y)
 {
     a.ks_count = (int)w.ksplit;
     a.ks_q = (int)(w.n_chunks / w.ksplit);
     a.ks_r = (int)(w.n_chunks % w.ksplit);
-    const bool direct = w.ksplit == 1 && a.f.epi == kEpiStore;
+    const bool direct = w.ksplit == 1 && a.f.epi == kEpiStore && !a.f.rs_pss;
     a.out = direct ? y : part;
     const int mt = a.hl ? (a.M + 7) / 8 : (a.M + 15) / 16;
     if (w.type == ULSPEC_GGML_Q4_0) slice_launch_t<ULSPEC_GGML_Q4_0>(a, mt, ctx->stream);
@@ -1658,11 +1472,8 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
         return fail(ctx, ULSPEC_EINVAL, "verify_gemm: workspace smaller than the weight needs");
     for (uint32_t m0 = 0; m0 < M; m0 += kGemmRowsH16) {
         const uint32_t mc = std::min<uint32_t>(kGemmRowsH16, M - m0);
-        GemmArgs a = make_args(w, X + (size_t)m0 * w.k, mc, false, y + (size_t)m0 * w.n);
-        if (wide_fits((int)mc, w.k)) {  // whole X in LDS, parts summed in the kernel
-            stream_launch(ctx, w, a);
-            continue;
-        }
+        GemmArgs a = make_args(w, X + (size_t)m0 * w.k, mc, false, 0, y + (size_t)m0 * w.n);
+        if (stream_launch(ctx, w, a)) continue;  // whole X in LDS, parts summed in the kernel
         split_launch(ctx, w, a, (float*)ctx->ws, y + (size_t)m0 * w.n);
     }
     return check_launch(ctx, "verify_gemm launch");
@@ -1673,30 +1484,22 @@ size_t gemm_split_part_bytes(const Weight& w, uint32_t M)
     return (size_t)w.ksplit * M * w.n * sizeof(float);
 }
 
-ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y)
+ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M,
+                         uint32_t lo_rows, float* y)
 {
-    if (M == 0 || M > (uint32_t)kGemmRowsSplit)
-        return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows (1..%d)", M, kGemmRowsSplit);
-    if (f.pro == kProNorm && (w.k > 4096 || w.k % 4 || f.P < 1 || f.P > kNormMaxPartials))
-        return fail(ctx, ULSPEC_EINVAL, "fused gemm: RMSNorm prologue needs K <= 4096 and 1..%d partial sums",
-                    kNormMaxPartials);
-    GemmArgs a = make_args(w, reinterpret_cast<const _Float16*>(x), M, true, y);
+    if (M == 0 || M > (uint32_t)kGemmRowsSplit || lo_rows < M)
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: %u rows (1..%d), low parts at row %u", M, kGemmRowsSplit,
+                    lo_rows);
+    if (f.rs_pss && (f.rs_P < 1 || f.rs_P > kMaxPartials))
+        return fail(ctx, ULSPEC_EINVAL, "fused gemm: the row scale needs 1..%d partial sums", kMaxPartials);
+    GemmArgs a = make_args(w, reinterpret_cast<const _Float16*>(x), M, true, lo_rows, y);
     a.f = f;
-    if (M <= 8 && wide_fits(2 * (int)M, w.k)) {  // whole split X in LDS
-        stream_launch(ctx, w, a);
-        return check_launch(ctx, "fused gemm launch");
-    }
+    if (M <= 8 && stream_launch(ctx, w, a)) return check_launch(ctx, "fused gemm launch");
     float* part = f.part ? f.part : (float*)ctx->ws;
     const size_t room = f.part ? f.part_bytes : ctx->ws_bytes;
     if (gemm_split_part_bytes(w, M) > room)
         return fail(ctx, ULSPEC_EINVAL, "fused gemm: %zu bytes of slice partials, %zu available",
                     gemm_split_part_bytes(w, M), room);
-    if (f.pro == kProNorm) {
-        if (!f.x_scratch) return fail(ctx, ULSPEC_EINVAL, "fused gemm: the split path needs an X scratch buffer");
-        hipLaunchKernelGGL(norm_split_kernel, dim3(M), dim3(256), 0, ctx->stream, f, (int)M, (int)w.k, f.x_scratch);
-        a.x = f.x_scratch;
-        a.f.pro = kProCopy;
-    }
     split_launch(ctx, w, a, part, y);
     return check_launch(ctx, "fused gemm launch");
 }

@@ -246,6 +246,47 @@ extern "C" ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t a, ui
     return ULSPEC_OK;
 }
 
+namespace {
+
+// Streaming read: thread t of workgroup b reads units (b * 256 * U + t + 256 u),
+// u < U, every load issued before the XOR that consumes them.
+template <int U>
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, size_t n16,
+                                                          uint32_t* __restrict__ sink)
+{
+    const size_t i = (size_t)blockIdx.x * 256 * U + threadIdx.x;
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const size_t k = i + (size_t)u * 256;
+        v[u] = k < n16 ? p[k] : uint4{0u, 0u, 0u, 0u};
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == 0x5eed5eedu) *sink = acc;
+}
+
+}  // namespace
+
+extern "C" ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant,
+                                            uint32_t* sink)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!buf || !sink || bytes == 0 || bytes % 16 || variant > 2)
+        return fail(ctx, ULSPEC_EINVAL, "stream_read: buffer, sink, bytes %% 16 == 0 and variant 0..2 required");
+    (void)hipSetDevice(ctx->device);
+    const size_t n16 = bytes / 16;
+    const int U = 4 << variant;
+    const size_t grid = (n16 + 256 * (size_t)U - 1) / (256 * (size_t)U);
+    if (grid > 0x7fffffffu) return fail(ctx, ULSPEC_EINVAL, "stream_read: %zu bytes is too large", bytes);
+    const uint4* p = (const uint4*)buf;
+    if (U == 4) hipLaunchKernelGGL(stream_read_kernel<4>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    else if (U == 8) hipLaunchKernelGGL(stream_read_kernel<8>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    else hipLaunchKernelGGL(stream_read_kernel<16>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    return check_launch(ctx, "stream_read launch");
+}
+
 namespace ulspec {
 
 ulspec_status workspace(ulspec_ctx* ctx, size_t bytes, void** out)

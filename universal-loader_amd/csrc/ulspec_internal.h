@@ -69,21 +69,19 @@ inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
 // One-time kernel attributes of the dequant-GEMM (called by ulspec_create).
 ulspec_status gemm_init(ulspec_ctx* ctx);
 
-// Fusions of the whole-X dequant-GEMM used by the model forward.
-enum { kProCopy = 0, kProNorm = 1 };
+// Row scale and epilogues of the dequant-GEMM in the model forward.
 enum { kEpiStore = 0, kEpiRope = 1, kEpiSilu = 2, kEpiResid = 3 };
-constexpr int kNormMaxRows = 16;
 // Rows per launch: fp16 X through the ABI GEMM, split X through the fused GEMM.
 constexpr int kGemmRowsH16 = 64;
 constexpr int kGemmRowsSplit = 48;
 struct GemmFuse {
-    int pro = kProCopy, epi = kEpiStore;
-    // kProNorm: X = fp16(v * rsqrt(sum_p pss[m][p] / K + eps) * norm_w), K <= 4096
-    const float* v = nullptr;
-    const float* pss = nullptr;
-    int P = 0;
-    const float* norm_w = nullptr;
-    float eps = 0.0f;
+    int epi = kEpiStore;
+    // row scale (the RMSNorm before this GEMM): Y[m][:] *= 1 / sqrt(sum_p
+    // rs_pss[m][p] / K + rs_eps), p < rs_P <= 256; X is then split(h * w),
+    // written by the producer of h (the resid epilogue's xn, the embedding)
+    const float* rs_pss = nullptr;
+    int rs_P = 0;
+    float rs_eps = 0.0f;
     // kEpiRope: Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc at slot *pos_dev + pos_add + m;
     // the RoPE position of row m is *pos_dev + pos_add + m, or with tree != 0
     // *pos_dev + pos_add + depth(m), depth(m) = bits 4m .. 4m+3 of row_depth
@@ -98,15 +96,17 @@ struct GemmFuse {
     int qdim = 0, kvdim = 0, hd = 0;
     // kEpiSilu: rows interleaved gate / up -> act, split fp16 pairs [2M][N / 2] (hi rows, then lo rows)
     _Float16* act = nullptr;
-    // kEpiResid: h [M][N] += Y; pss_out [M][n_tiles] = per-tile sums of h^2
+    // kEpiResid: h [M][N] += Y; pss_out [M][n_tiles] = per-tile sums of h^2;
+    // with xn the next GEMM's split X: rows m (hi) and xn_lo + m (lo) of h * xn_w
     float* h = nullptr;
     float* pss_out = nullptr;
+    const float* xn_w = nullptr;
+    _Float16* xn = nullptr;
+    int xn_lo = 0;
     // split-K path (rows or K beyond what the whole-X kernels hold): slice
-    // partials (NULL = the context workspace) and, for kProNorm, the split X
-    // [2M][K] the norm kernel writes
+    // partials (NULL = the context workspace)
     float* part = nullptr;
     size_t part_bytes = 0;
-    _Float16* x_scratch = nullptr;
 };
 
 // Kernel launchers shared by the C ABI and the host engine (no validation of
@@ -115,11 +115,12 @@ ulspec_status gemm_launch(ulspec_ctx* ctx, const Weight& w, const uint16_t* x, u
 // Rows of GGUF blocks (device) to fp16 rows out[out_row0 + r * out_row_step][K].
 ulspec_status rows_to_f16(ulspec_ctx* ctx, uint32_t type, const void* raw, uint32_t rows, uint32_t K,
                           _Float16* out, uint32_t out_row0, uint32_t out_row_step);
-// The dequant-GEMM with a fused prologue / epilogue over split X (the model
-// forward): the whole-X kernels for M <= 8 rows that fit in LDS, else the
-// split-K kernel (with the norm kernel for kProNorm) and the reducing epilogue.
-ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M, float* y);
-bool wide_fits(int rows, uint32_t K);
+// The dequant-GEMM with a fused row scale / epilogue over split X (the model
+// forward; the low part of row m at row lo_rows + m): the whole-X kernels for
+// M <= 8 rows that fit in LDS, else the split-K kernel and the reducing
+// epilogue.
+ulspec_status gemm_fused(ulspec_ctx* ctx, const Weight& w, const GemmFuse& f, const uint16_t* x, uint32_t M,
+                         uint32_t lo_rows, float* y);
 size_t gemm_workspace_bytes(const Weight& w);
 uint32_t choose_ksplit(uint32_t n_tiles, uint32_t n_chunks, int n_cu);
 size_t gemm_split_part_bytes(const Weight& w, uint32_t M);
