@@ -153,6 +153,21 @@ ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
                             uint32_t V, const float* target_logits, const float* draft_logits,
                             const int32_t* draft_tokens, const float* uniforms,
                             int32_t* out_tokens, int32_t* out_n_accepted);
+/* ulspec_accept that allocates nothing: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, rule and
+ * results as ulspec_accept; its kernels keep their intermediate sums in a
+ * static device scratch array of ULSPEC_ACCEPT_NOALLOC_SCRATCH bytes per GPU
+ * (held until the process ends) instead of the context workspace.  Calls
+ * whose scratch would exceed it (B (2k+1) logit rows; e.g. B = 16, k = 8 with
+ * top-k fits) fail with ULSPEC_EUNSUPPORTED before any launch.  Every call on
+ * one GPU shares the array: calls that overlap on one GPU (other streams or
+ * contexts) race. */
+#define ULSPEC_ACCEPT_NOALLOC_SCRATCH (32u << 20)
+ulspec_status ulspec_accept_noalloc(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
+                                    uint32_t V, const float* target_logits, const float* draft_logits,
+                                    const int32_t* draft_tokens, const float* uniforms,
+                                    int32_t* out_tokens, int32_t* out_n_accepted);
 /* Tree verification, B trees of one shape: nodes 0 .. n-1 (n <= 16), node 0
  * the root (the last committed token), parent (HOST int32 [n]) with
  * parent[0] = -1 and parent[i] in [0, i).  target_logits [B][n][V]: row v is

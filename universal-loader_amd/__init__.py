@@ -103,6 +103,7 @@ ABI = [
     ("ulspec_verify_gemm", C.c_int, [P, U32, P, U32, P]),
     ("ulspec_verify_attention", C.c_int, [P, P, P, P, U32, U32, P, U32, U32, U32, C.c_float, P]),
     ("ulspec_accept", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P]),
+    ("ulspec_accept_noalloc", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P]),
     ("ulspec_accept_tree", C.c_int, [P, C.POINTER(Sampling), U32, U32, U32, P, P, P, P, P, P, P, P]),
     ("ulspec_sample", C.c_int, [P, C.POINTER(Sampling), U32, U32, P, P, P]),
     ("ulspec_uniforms", C.c_int, [P, C.c_uint64, C.c_uint64, U32, P]),
@@ -282,6 +283,12 @@ class Context:
     def accept(self, s, B, k, V, target, draft, draft_tokens, uniforms, out_tokens, out_nacc):
         self._check(lib().ulspec_accept(self.handle, C.byref(s), B, k, V, _ptr(target), _ptr(draft),
                                         _ptr(draft_tokens), _ptr(uniforms), _ptr(out_tokens), _ptr(out_nacc)))
+
+    def accept_noalloc(self, s, B, k, V, target, draft, draft_tokens, uniforms, out_tokens, out_nacc):
+        """accept() on the library's static scratch: allocates nothing."""
+        self._check(lib().ulspec_accept_noalloc(self.handle, C.byref(s), B, k, V, _ptr(target), _ptr(draft),
+                                                _ptr(draft_tokens), _ptr(uniforms), _ptr(out_tokens),
+                                                _ptr(out_nacc)))
 
     def accept_tree(self, s, B, n, V, parent, target, draft, tokens, uniforms, out_tokens, out_path, out_nacc):
         """Tree verification; parent is a host array [n], the rest device buffers."""

@@ -1622,6 +1622,41 @@ extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s
                          out_n_accepted, nullptr);
 }
 
+// Scratch of the no-allocation entry point, one copy per GPU.  In host code
+// `noalloc_scratch` names a host-side stand-in, not device memory: kernels
+// get the address hipGetSymbolAddress returns for the context's device
+// (accept_init, at context creation).
+static __device__ __align__(256) uint8_t noalloc_scratch[ULSPEC_ACCEPT_NOALLOC_SCRATCH];
+
+namespace ulspec {
+ulspec_status accept_init(ulspec_ctx* ctx)
+{
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+    if (e != hipSuccess || !p) return hip_fail(ctx, e, "hipGetSymbolAddress(accept scratch)");
+    ctx->noalloc_scratch = p;
+    return ULSPEC_OK;
+}
+}  // namespace ulspec
+
+extern "C" ulspec_status ulspec_accept_noalloc(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,
+                                               uint32_t V, const float* target_logits, const float* draft_logits,
+                                               const int32_t* draft_tokens, const float* uniforms,
+                                               int32_t* out_tokens, int32_t* out_n_accepted)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (!ctx->noalloc_scratch) return fail(ctx, ULSPEC_EDEVICE, "accept_noalloc: scratch address not set");
+    if (B == 0 || k == 0 || k > 16)
+        return fail(ctx, ULSPEC_EINVAL, "accept_noalloc: need B >= 1, 1 <= k <= 16 (B=%u k=%u)", B, k);
+    const size_t need = accept_workspace_bytes(B, k);
+    if (need > ULSPEC_ACCEPT_NOALLOC_SCRATCH)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "accept_noalloc: %zu bytes of scratch needed, %u available", need,
+                    ULSPEC_ACCEPT_NOALLOC_SCRATCH);
+    (void)hipSetDevice(ctx->device);
+    return accept_launch(ctx, s, B, k, V, target_logits, draft_logits, draft_tokens, uniforms, out_tokens,
+                         out_n_accepted, ctx->noalloc_scratch);
+}
+
 extern "C" ulspec_status ulspec_accept_tree(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t n,
                                             uint32_t V, const int32_t* parent, const float* target_logits,
                                             const float* draft_logits, const int32_t* tokens, const float* uniforms,

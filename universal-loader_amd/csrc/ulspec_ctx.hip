@@ -94,7 +94,7 @@ extern "C" ulspec_status ulspec_create(int hip_device, ulspec_ctx** out)
         delete ctx;
         return ULSPEC_EDEVICE;
     }
-    if (gemm_init(ctx) != ULSPEC_OK) {
+    if (gemm_init(ctx) != ULSPEC_OK || accept_init(ctx) != ULSPEC_OK) {
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
         return ULSPEC_EDEVICE;

@@ -39,6 +39,8 @@ struct ulspec_ctx {
     // Host staging for weight uploads.
     void* staging = nullptr;
     size_t staging_bytes = 0;
+    // Device address of the no-allocation scratch on this context's device.
+    void* noalloc_scratch = nullptr;
     // Captured graphs and timing events.
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;
@@ -66,8 +68,10 @@ inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
                 hipGetErrorString(e));
 }
 
-// One-time kernel attributes of the dequant-GEMM (called by ulspec_create).
+// One-time kernel attributes of the dequant-GEMM and the no-allocation
+// scratch address (called by ulspec_create, with the context's device current).
 ulspec_status gemm_init(ulspec_ctx* ctx);
+ulspec_status accept_init(ulspec_ctx* ctx);
 
 // Row scale and epilogues of the dequant-GEMM in the model forward.
 enum { kEpiStore = 0, kEpiRope = 1, kEpiSilu = 2, kEpiResid = 3 };
