@@ -126,12 +126,9 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
     steps = tokens = 0
     draws_exact = accept_exact = own_agree = True
     worst = 0.0
-    for n, r in recorded:
-        if busy > args.cpu_seconds:
-            break
+    def cpu_step(n, r, threads):
+        """The CPU path's own step on the GPU's committed and draft tokens."""
         d, u = r["draft_tokens"], r["uniforms"]
-        t0 = time.perf_counter()
-        # the CPU path's own step on the GPU's committed tokens and draft tokens
         dl = [od.forward(seq[n - 2:n], n - 2, n_logits=1)[0]]
         own_d = [ora.sample(s, dl[0][None], u[0:1])[0]]
         for j in range(1, k):
@@ -139,7 +136,15 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
             own_d.append(ora.sample(s, dl[j][None], u[j:j + 1])[0])
         dl = np.array(dl)
         tl = ot.forward(np.concatenate([[seq[n - 1]], d]).astype(np.int32), n - 1, n_logits=k + 1)
-        out_c, nacc_c = ora.accept(s, tl[None], dl[None], d[None], u[k:][None])
+        out_c, nacc_c = ora.accept(s, tl[None], dl[None], d[None], u[k:][None], nthreads=threads)
+        return dl, own_d, tl, nacc_c
+
+    for n, r in recorded:
+        if busy > args.cpu_seconds:
+            break
+        d, u = r["draft_tokens"], r["uniforms"]
+        t0 = time.perf_counter()
+        dl, own_d, tl, nacc_c = cpu_step(n, r, nt)
         busy += time.perf_counter() - t0
         steps += 1
         tokens += int(nacc_c[0]) + 1
@@ -152,22 +157,53 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
         for a, b in ((r["draft_logits"], dl), (r["target_logits"], tl)):
             b64 = b.astype(np.float64)
             worst = max(worst, float(np.abs(a - b64).max() / np.sqrt((b64 ** 2).mean())))
+    # the same steps on one thread (a bounded sample: at least one step)
+    for m in models:
+        m.set_threads(1)
+    busy1, tokens1, steps1 = 0.0, 0, 0
+    for n, r in recorded[:steps]:
+        if steps1 and busy1 > args.cpu_seconds / 2:
+            break
+        t0 = time.perf_counter()
+        _, _, _, nacc1 = cpu_step(n, r, 1)
+        busy1 += time.perf_counter() - t0
+        tokens1 += int(nacc1[0]) + 1
+        steps1 += 1
     for m in models:
         m.close()
     mode = "greedy" if args.greedy else f"T={args.temperature}"
     return {
         "value": tokens / busy if busy else None, "unit": "tokens/s", "cores": nt, "kind": "port",
+        "value_1thread": tokens1 / busy1 if busy1 else None, "steps_1thread": steps1, "cpu_model": _cpu_model(),
         "sample": f"{steps} speculative steps (k=5, {mode}) of the 7B-shape Q4_K target/draft pair at context "
-                  f"{n0}, from the GPU's post-prefill KV cache; oracle/ C restatement, AVX2 f32 GEMM, {nt} threads",
+                  f"{n0}, from the GPU's post-prefill KV cache; oracle/ C restatement, AVX2 f32 GEMM, {nt} threads "
+                  f"(value), the first {steps1} of them on 1 thread (value_1thread)",
         "parity": {"steps": steps, "draft_draws_bit_exact": draws_exact, "accept_bit_exact": accept_exact,
                    "cpu_decisions_equal_gpu": own_agree, "logits_max_err_over_rms": worst},
     }
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def _ora():
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle
     return oracle
+
+
+def _copies(nbytes, total=600e6):
+    """Copies of an input of nbytes that rotate through more than the 256 MB
+    last-level cache (at least 2)."""
+    return max(2, int(np.ceil(total / nbytes)))
 
 
 def _time_direct(ctx, fn, reps):
@@ -247,15 +283,24 @@ def workload_attention(pkg, ctx, args):
         q = rng.standard_normal((nq, H, D)).astype(np.float16).view(np.uint16)
         k = rng.standard_normal((L, H, D)).astype(np.float16).view(np.uint16)
         v = rng.standard_normal((L, H, D)).astype(np.float16).view(np.uint16)
-        bq, bk, bv, bo = ctx.upload(q), ctx.upload(k), ctx.upload(v), ctx.alloc(nq * H * D * 4)
-        scale = 1.0 / np.sqrt(D)
-        us = _time_direct(ctx, lambda: ctx.verify_attention(bq, bk, bv, P, nq, parent, H, H, D, scale, bo), args.reps)
         alg = 2 * L * H * D * 2 + nq * H * D * (2 + 4)
+        nc = _copies(alg)
+        bq, bo = ctx.upload(q), ctx.alloc(nq * H * D * 4)
+        kv = [(ctx.upload(k), ctx.upload(v)) for _ in range(nc)]
+        bk, bv = kv[0]
+        scale = 1.0 / np.sqrt(D)
+        it = iter(range(1 << 30))
+
+        def call():
+            ck, cv = kv[next(it) % nc]
+            ctx.verify_attention(bq, ck, cv, P, nq, parent, H, H, D, scale, bo)
+        us = _time_direct(ctx, call, nc * args.reps)
+        ctx.verify_attention(bq, bk, bv, P, nq, parent, H, H, D, scale, bo)
         gbs = alg / us / 1e3
         o = ctx.download(bo, np.float32, (nq, H, D))
         ref = ora.attention_f64(q, k, v, P, parent, H, H, D, scale)
         err = float(np.abs(o - ref).max())
-        out.append({"case": name, "us": us, "GB/s": gbs, "max_abs_err_vs_f64": err})
+        out.append({"case": name, "us": us, "GB/s": gbs, "max_abs_err_vs_f64": err, "rotated_copies": nc})
         log(f"attention {name}: {us:.2f} us, {gbs:.0f} GB/s, max err {err:.1e}")
         if name == "causal5":
             head = (us, alg, gbs)
@@ -264,13 +309,14 @@ def workload_attention(pkg, ctx, args):
                 ora.attention_f32(q, k, v, P, None, H, H, D, scale)
                 n += 1
             cpu_gbs = alg * n / (time.perf_counter() - t0) / 1e9
-        for b in (bq, bk, bv, bo):
+        for b in (bq, bo, *[x for pair in kv for x in pair]):
             b.free()
     us, alg, gbs = head
     return {
         "metric": "verify-attention HBM GB/s (32x128, prefix 4096, 5 causal queries)", "value": gbs, "unit": "GB/s",
         "ms_per_step": us / 1e3, "dtype": "fp16 K/V, fp32 softmax",
-        "config": {"workload": "verify attention H=32 D=128 prefix 4096, causal nq=5 (and tree nq=16)", "cases": out},
+        "config": {"workload": "verify attention H=32 D=128 prefix 4096, causal nq=5 (and tree nq=16), K/V rotated "
+                               "over copies totalling > 512 MB", "cases": out},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
         "cpu_baseline": {"value": cpu_gbs, "unit": "GB/s", "cores": ora.nthreads_default(), "kind": "port",
@@ -295,17 +341,27 @@ def workload_accept(pkg, ctx, args):
         s_ora = ora.sampling(temperature=0.8, top_k=40, top_p=0.9)
         dt = np.stack([ora.sample(s_ora, dl[b], ora.uniforms(args.seed + 1, b * k, k)) for b in range(B)])
         u = np.stack([ora.uniforms(args.seed + 2, b * (k + 1), k + 1) for b in range(B)])
-        btl, bdl, bdt, bu = ctx.upload(tl), ctx.upload(dl), ctx.upload(dt), ctx.upload(u)
+        nc = _copies(tl.nbytes + dl.nbytes)
+        logit_bufs = [(ctx.upload(tl), ctx.upload(dl)) for _ in range(nc)]
+        btl, bdl = logit_bufs[0]
+        bdt, bu = ctx.upload(dt), ctx.upload(u)
         bo, bn = ctx.alloc(B * (k + 1) * 4), ctx.alloc(B * 4)
         for greedy in (False, True):
             s = pkg.sampling(greedy=True) if greedy else pkg.sampling(temperature=0.8, top_k=40, top_p=0.9)
-            us = _time_direct(ctx, lambda: ctx.accept(s, B, k, V, btl, bdl, bdt, bu, bo, bn), args.reps)
+            it = iter(range(1 << 30))
+
+            def call():
+                ct, cd = logit_bufs[next(it) % nc]
+                ctx.accept(s, B, k, V, ct, cd, bdt, bu, bo, bn)
+            us = _time_direct(ctx, call, nc * args.reps)
+            ctx.accept(s, B, k, V, btl, bdl, bdt, bu, bo, bn)
             alg = 4 * B * (2 * k + 1) * V if not greedy else 4 * B * (k + 1) * V
             gbs = alg / us / 1e3
             got = ctx.download(bo, np.int32, (B, k + 1))
             want, _ = ora.accept(ora.sampling(greedy=True) if greedy else s_ora, tl, dl, dt, u)
             exact = bool(np.array_equal(got, want))
-            cases.append({"k": k, "V": V, "greedy": greedy, "us": us, "GB/s": gbs, "bit_exact": exact})
+            cases.append({"k": k, "V": V, "greedy": greedy, "us": us, "GB/s": gbs, "bit_exact": exact,
+                          "rotated_copies": nc})
             log(f"accept k={k} V={V} greedy={greedy}: {us:.2f} us, {gbs:.0f} GB/s, bit-exact {exact}")
             if (k, V, greedy) == (4, 32000, False):
                 head = (us, alg, gbs)
@@ -314,13 +370,14 @@ def workload_accept(pkg, ctx, args):
                     ora.accept(s_ora, tl, dl, dt, u)
                     n += 1
                 cpu_gbs = alg * n / (time.perf_counter() - t0) / 1e9
-        for b in (btl, bdl, bdt, bu, bo, bn):
+        for b in (bdt, bu, bo, bn, *[x for pair in logit_bufs for x in pair]):
             b.free()
     us, alg, gbs = head
     return {
         "metric": "acceptance-sampling HBM GB/s (B=16, k=4, V=32000)", "value": gbs, "unit": "GB/s",
         "ms_per_step": us / 1e3, "dtype": "fp32 logits, exact u64 fixed point",
-        "config": {"workload": "acceptance sampling B=16 k=4 V=32000, T 0.8 top-k 40 top-p 0.9", "cases": cases},
+        "config": {"workload": "acceptance sampling B=16 k=4 V=32000, T 0.8 top-k 40 top-p 0.9, logits rotated over "
+                               "copies totalling > 512 MB", "cases": cases},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
         "cpu_baseline": {"value": cpu_gbs, "unit": "GB/s", "cores": ora.nthreads_default(), "kind": "port",

@@ -321,13 +321,18 @@ ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint
  * u(seed, s*(2k+1) + k + j) emits n_accepted + 1 tokens, which are committed
  * (stale K/V rows past them are overwritten by the next step).  Replaces
  * SpeculativeDecoder::generate_with_speculation
- * (src/inference/speculative_decoder.cpp:25-71). */
+ * (src/inference/speculative_decoder.cpp:25-71).
+ * k = 0 (draft may be NULL): plain decoding of the target, the reference's
+ * path with speculation off -- a step forwards t_{n-1} and samples t_n from
+ * warp(target logits) with u(seed, s).  k <= 16. */
 typedef struct ulspec_spec ulspec_spec;
 ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
                                  uint64_t seed, ulspec_spec** out);
 void          ulspec_spec_destroy(ulspec_spec* sp);
-/* Commit the prompt (n >= 2): both models process tokens 0 .. n-2; token n-1
- * is pending.  Resets the counters.  Synchronous. */
+/* Commit the prompt (n >= 1): both models process tokens 0 .. n-2; token n-1
+ * is pending.  Resets the counters.  With n = 1 and k > 0 the first step is a
+ * plain step (u(seed, 0)): the draft's catch-up pair needs two tokens.
+ * Synchronous. */
 ulspec_status ulspec_spec_prefill(ulspec_spec* sp, const int32_t* prompt, uint32_t n);
 /* Enqueue n_steps steps (asynchronous); EINVAL if they could overrun the
  * context (each step commits at most k+1 tokens). */

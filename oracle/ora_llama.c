@@ -35,6 +35,11 @@ struct ora_llama {
     float* rope; /* [max_ctx][D/2][2] */
 };
 
+void ora_llama_set_threads(ora_llama* m, int nthreads)
+{
+    if (m) m->nthreads = nthreads > 0 ? nthreads : 1;
+}
+
 ora_llama* ora_llama_create(const ora_llama_cfg* cfg, int nthreads)
 {
     if (!cfg || cfg->n_heads <= 0 || cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads ||
@@ -221,8 +226,9 @@ int ora_llama_kv_io(ora_llama* m, int64_t layer, int dir, int64_t pos0, int64_t 
 int ora_spec_prefill(ora_llama* t, ora_llama* d, const int32_t* prompt, int64_t n, int32_t* seq, int64_t cap,
                      ora_spec_state* st)
 {
-    if (n < 2 || n > cap) return -1;
-    if (ora_llama_forward(t, prompt, n - 1, 0, NULL, 0) || ora_llama_forward(d, prompt, n - 1, 0, NULL, 0)) return -1;
+    if (n < 1 || n > cap) return -1;
+    if (n > 1 && (ora_llama_forward(t, prompt, n - 1, 0, NULL, 0) || (d && ora_llama_forward(d, prompt, n - 1, 0, NULL, 0))))
+        return -1;
     memcpy(seq, prompt, sizeof(int32_t) * (size_t)n);
     st->n = n;
     st->step = st->accepted = st->proposed = 0;
@@ -233,7 +239,21 @@ int ora_spec_step(ora_llama* t, ora_llama* d, const ora_sampling* s, int64_t k, 
                   int64_t cap, ora_spec_state* st)
 {
     int64_t V = t->c.vocab, n = st->n;
-    if (k < 1 || k > 15 || n < 2 || n + k + 1 > cap || d->c.vocab != V) return -1;
+    if (k < 0 || k > 15 || n < 1 || n + k + 1 > cap || (k > 0 && (!d || d->c.vocab != V))) return -1;
+    if (k == 0 || n == 1) {
+        /* plain step: t_n from warp(target logits of t_{n-1}) with counter step (2k+1) */
+        float u0 = ora_uniform(seed, (uint64_t)(st->step * (2 * k + 1)));
+        float* tl = (float*)malloc(sizeof(float) * (size_t)V);
+        int32_t last = seq[n - 1], tok = 0;
+        int rc = ora_llama_forward(t, &last, 1, n - 1, tl, 1);
+        if (!rc) rc = ora_sample(s, 1, V, tl, &u0, &tok);
+        free(tl);
+        if (rc) return -1;
+        seq[n] = tok;
+        st->n = n + 1;
+        st->step += 1;
+        return 0;
+    }
     float u[33];
     for (int64_t j = 0; j <= 2 * k; ++j) u[j] = ora_uniform(seed, (uint64_t)(st->step * (2 * k + 1) + j));
     float* dl = (float*)malloc(sizeof(float) * (size_t)(k * V));

@@ -161,6 +161,9 @@ typedef struct {
 typedef struct ora_llama ora_llama;
 ora_llama* ora_llama_create(const ora_llama_cfg* cfg, int nthreads);
 void       ora_llama_free(ora_llama* m);
+/* Worker threads of the forward's GEMMs and attention (the results do not
+ * depend on it). */
+void       ora_llama_set_threads(ora_llama* m, int nthreads);
 /* GGUF tensor by name (token_embd / output_norm / output / blk.<i>.{attn_norm,
  * attn_q, attn_k, attn_v, attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down}
  * .weight); norms F32 (type 0), the rest Q4_0 / Q4_K; bytes are copied. */
@@ -180,11 +183,14 @@ int        ora_llama_kv_io(ora_llama* m, int64_t layer, int dir, int64_t pos0, i
  *   draft forward [seq[n-2], seq[n-1]] at n-2 -> d_1 = sample(row n-1, u_0);
  *   draft forward [d_j] at n-1+j -> d_{j+1} = sample(.., u_j), j = 1 .. k-1
  *   target forward [seq[n-1], d_1 .. d_k] at n-1 .. n-1+k
- *   ora_accept(.., uniforms u_k .. u_2k) -> n_acc + 1 tokens appended. */
+ *   ora_accept(.., uniforms u_k .. u_2k) -> n_acc + 1 tokens appended.
+ * A plain step (k = 0, draft NULL: decoding of the target alone; or n = 1,
+ * before the draft has the two tokens of its catch-up pair): target forward
+ * [seq[n-1]] at n-1 -> seq[n] = sample(.., u_0); proposed unchanged. */
 typedef struct {
     int64_t n, step, accepted, proposed;
 } ora_spec_state;
-/* Both models process prompt[0 .. n-2]; seq = prompt; counters zero. */
+/* Both models process prompt[0 .. n-2] (n >= 1); seq = prompt; counters zero. */
 int     ora_spec_prefill(ora_llama* target, ora_llama* draft, const int32_t* prompt, int64_t n, int32_t* seq,
                          int64_t cap, ora_spec_state* st);
 int     ora_spec_step(ora_llama* target, ora_llama* draft, const ora_sampling* s, int64_t k, uint64_t seed,

@@ -10,7 +10,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
+# ORACLE_LIB selects another build of the same sources (the sanitizer build,
+# oracle/_build/liboracle_san.so, under a preloaded ASan runtime).
+LIB_PATH = os.environ.get("ORACLE_LIB") or os.path.join(_HERE, "_build", "liboracle.so")
 
 F16, Q4_0, Q8_0, Q4_K, Q6_K = 1, 2, 8, 12, 14
 
@@ -82,6 +84,7 @@ def _declare(L):
     d("ora_accept", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, C.c_int)
     d("ora_accept_tree", C.c_int, P, I64, I64, I64, P, P, P, P, P, P, P, P, C.c_int)
     d("ora_llama_create", P, P, C.c_int)
+    d("ora_llama_set_threads", None, P, C.c_int)
     d("ora_llama_free", None, P)
     d("ora_llama_set_tensor", C.c_int, P, C.c_char_p, C.c_int, P, C.c_size_t, I64, I64)
     d("ora_llama_forward", C.c_int, P, P, I64, I64, P, I64)
@@ -273,6 +276,9 @@ class Llama:
         if not self.handle:
             raise ValueError("ora_llama_create rejected the configuration")
 
+    def set_threads(self, nthreads):
+        lib().ora_llama_set_threads(self.handle, nthreads)
+
     def close(self):
         if self.handle:
             lib().ora_llama_free(self.handle)
@@ -313,23 +319,26 @@ class Speculative:
 
     def __init__(self, target, draft, k, s, seed, cap=None):
         self.target, self.draft, self.k, self.s, self.seed = target, draft, k, s, seed
-        self.cap = cap or min(target.cfg.max_ctx, draft.cfg.max_ctx)
+        self.cap = cap or (min(target.cfg.max_ctx, draft.cfg.max_ctx) if draft is not None else target.cfg.max_ctx)
         self.seq = np.zeros(self.cap, np.int32)
         self.st = SpecState()
 
+    def _dh(self):
+        return self.draft.handle if self.draft is not None else None
+
     def prefill(self, prompt):
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)
-        if lib().ora_spec_prefill(self.target.handle, self.draft.handle, prompt.ctypes.data_as(P), len(prompt),
+        if lib().ora_spec_prefill(self.target.handle, self._dh(), prompt.ctypes.data_as(P), len(prompt),
                                   self.seq.ctypes.data_as(P), self.cap, C.byref(self.st)):
             raise ValueError("ora_spec_prefill failed")
 
     def step(self):
-        if lib().ora_spec_step(self.target.handle, self.draft.handle, C.byref(self.s), self.k, self.seed,
+        if lib().ora_spec_step(self.target.handle, self._dh(), C.byref(self.s), self.k, self.seed,
                                self.seq.ctypes.data_as(P), self.cap, C.byref(self.st)):
             raise ValueError("ora_spec_step failed")
 
     def generate(self, n_new):
-        n = lib().ora_spec_generate(self.target.handle, self.draft.handle, C.byref(self.s), self.k, self.seed, n_new,
+        n = lib().ora_spec_generate(self.target.handle, self._dh(), C.byref(self.s), self.k, self.seed, n_new,
                                     self.seq.ctypes.data_as(P), self.cap, C.byref(self.st))
         if n < 0:
             raise ValueError("ora_spec_generate failed")

@@ -1,9 +1,15 @@
 // Drives the C++ host classes of include/ulspec_inference.hpp on a small
-// random model: greedy speculative generation must equal greedy generation
-// with k = 1 (both are the target's argmax chain), the acceptance rate starts
-// at 0.5, and a step reports n_accepted + 1 committed tokens.
+// random model: greedy speculative generation must equal greedy plain
+// decoding (speculation off; both are the target's argmax chain), the
+// acceptance rate starts at 0.5, a step reports n_accepted + 1 committed
+// tokens, and the reference's generate_with_speculation(context_token, n)
+// shape, started from one token, follows the argmax chain.  With two GGUF
+// paths (target, draft; vocabulary strings "▁w<i>") it also loads them
+// through InferenceAPI::load_model / load_draft_model and generates text.
 // Prints "OK" and exits 0 on success.
+#include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -56,7 +62,57 @@ static void load(Model& m, uint64_t seed)
     }
 }
 
-int main()
+// The target's greedy continuation of seq by n tokens (full re-forward each token).
+static std::vector<uint32_t> argmax_chain(Model& m, std::vector<uint32_t> seq, size_t n)
+{
+    for (size_t i = 0; i < n; ++i) {
+        std::vector<float> lg = m.token_logits(seq);
+        seq.push_back((uint32_t)(std::max_element(lg.begin(), lg.end()) - lg.begin()));
+    }
+    return seq;
+}
+
+static int files_part(Context& ctx, const char* target_path, const char* draft_path)
+{
+    InferenceAPI api(ctx, 128, 4, 3);
+    if (api.generate("w1", GenerationConfig{}) != "Error: No model loaded") {
+        std::printf("no-model message\n");
+        return 1;
+    }
+    if (api.load_model("/nonexistent/model.gguf") || api.last_error().empty()) {
+        std::printf("load_model of a missing file\n");
+        return 1;
+    }
+    if (!api.load_model(target_path) || !api.load_draft_model(draft_path)) {
+        std::printf("load_model: %s\n", api.last_error().c_str());
+        return 1;
+    }
+    api.register_custom_tokenizer([](const std::string& text) {
+        std::vector<uint32_t> ids;
+        for (size_t i = 0; (i = text.find('w', i)) != std::string::npos; ++i) ids.push_back((uint32_t)std::atoi(&text[i + 1]));
+        return ids;
+    });
+    GenerationConfig c;
+    c.max_tokens = 16;
+    c.do_sample = false;
+    api.enable_speculative_decoding(true);
+    const std::string spec = api.generate("w1 w2 w3 w4", c);
+    api.enable_speculative_decoding(false);
+    const std::string plain = api.generate("w1 w2 w3 w4", c);
+    GenerationResult r = api.generate_tokens(std::vector<uint32_t>{1, 2, 3, 4}, c);
+    if (spec != plain || r.text != plain || r.num_tokens != 16 || std::count(plain.begin(), plain.end(), ' ') != 16) {
+        std::printf("text generation: '%s' vs '%s'\n", spec.c_str(), plain.c_str());
+        return 1;
+    }
+    const float rate = api.get_acceptance_rate();
+    if (!(rate >= 0.0f && rate <= 1.0f)) {
+        std::printf("acceptance rate %f\n", rate);
+        return 1;
+    }
+    return 0;
+}
+
+int main(int argc, char** argv)
 {
     try {
         Context ctx(0);
@@ -89,6 +145,29 @@ int main()
             std::printf("step result sizes\n");
             return 1;
         }
+        // the reference's call shape from a single context token: a plain
+        // first step, then speculative steps on the committed sequence
+        SpeculativeDecoder d2(tc.vocab, 3, 0.0f);
+        d2.attach(target, draft, ulspec_sampling{1.0f, 0, 1.0f, 1}, 5);
+        SpeculationResult a = d2.generate_with_speculation(prompt[0], 4);
+        if (a.accepted_tokens.size() != 1 || a.num_accepted != 0 || !a.rejected_tokens.empty()) {
+            std::printf("first step from one token\n");
+            return 1;
+        }
+        std::vector<uint32_t> chain{prompt[0], a.accepted_tokens[0]};
+        for (int i = 0; i < 6; ++i) {
+            SpeculationResult b = d2.generate_with_speculation(chain.back());
+            if (b.accepted_tokens.size() != b.num_accepted + 1) {
+                std::printf("overload step sizes\n");
+                return 1;
+            }
+            chain.insert(chain.end(), b.accepted_tokens.begin(), b.accepted_tokens.end());
+        }
+        if (chain != argmax_chain(target, {prompt[0]}, chain.size() - 1)) {
+            std::printf("overload chain != argmax chain\n");
+            return 1;
+        }
+        if (argc >= 3 && files_part(ctx, argv[1], argv[2])) return 1;
         std::printf("OK rate %.3f\n", dec.get_acceptance_rate());
         return 0;
     } catch (const Error& e) {

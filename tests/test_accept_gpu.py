@@ -225,8 +225,8 @@ def test_accept_argument_errors(ctx, pkg):
         ctx.accept(pkg.sampling(1.0, top_k=300), 1, 1, 1000, b, b, b, b, b, b)
     assert e.value.status == pkg.EUNSUPPORTED
     with pytest.raises(pkg.UlspecError) as e:
-        ctx.accept(pkg.sampling(1.0, top_p=0.9), 1, 1, 1000, b, b, b, b, b, b)
-    assert e.value.status == pkg.EUNSUPPORTED
+        ctx.accept(pkg.sampling(1.0, top_p=float("nan")), 1, 1, 1000, b, b, b, b, b, b)
+    assert e.value.status == pkg.EINVAL
     # rows of one call: B (2k+1) and R at most 65535 (checked before any launch)
     with pytest.raises(pkg.UlspecError) as e:
         ctx.accept(pkg.sampling(1.0), 5000, 8, 1000, b, b, b, b, b, b)

@@ -291,6 +291,32 @@ def test_warp_top_k_top_p_against_sort(ora, rng):
     assert E[123] == E[456] and Z == int(E.sum())
 
 
+@pytest.mark.parametrize("kind", ["normal", "ties", "flat", "signed_zeros"])
+def test_warp_top_p_without_top_k_is_the_shortest_prefix(ora, rng, kind):
+    """Full-vocabulary top-p: the kept tokens are a prefix of (logit desc,
+    index asc) order, their mass reaches top_p * Z (as doubles) and the prefix
+    one shorter does not; kept tokens keep their full-warp weight."""
+    V = 3000
+    logits = (rng.standard_normal(V) * 3).astype(np.float32)
+    if kind == "ties":
+        logits = (np.round(logits * 2) / 2).astype(np.float32)
+    elif kind == "flat":
+        logits[:] = 0.75
+    elif kind == "signed_zeros":
+        logits[::2], logits[1::2] = 0.0, -0.0
+        logits[17] = 0.5
+    full, Zf, _ = ora.warp_row(ora.sampling(0.8), logits)
+    order = sorted(range(V), key=lambda i: (-float(logits[i]), i))
+    for tp in (0.0, 1e-6, 0.3, 0.9, 0.97):
+        E, Z, nk = ora.warp_row(ora.sampling(0.8, top_p=tp), logits)
+        kept = order[:nk]
+        assert all(E[i] == full[i] for i in kept) and all(E[i] == 0 for i in order[nk:])
+        mass = sum(int(full[i]) for i in kept)
+        thr = float(np.float32(tp)) * float(Zf)
+        assert Z == mass and float(mass) >= thr
+        assert nk == 1 or float(mass - int(full[kept[-1]])) < thr
+
+
 def test_cdf_pick_convention(ora):
     W = np.array([0, 3, 0, 5, 2], np.uint64)  # Z = 10
     # T = floor(u * 10); first i with T < cumsum -> [1,1,1,3,3,3,3,3,4,4]
@@ -315,6 +341,7 @@ def test_accept_first_token_distribution_is_exactly_p(ora, rng):
     n = 64
     grid = (np.arange(n) + 0.5) / n
     counts = np.zeros(V)
+    accepted = 0.0
     for x in range(V):  # draft token drawn from q: weight each x by q(x)
         for u0 in grid:
             us = np.stack([np.full(n, u0), grid], 1).astype(np.float32)
@@ -323,11 +350,13 @@ def test_accept_first_token_distribution_is_exactly_p(ora, rng):
             out, nacc = ora.accept(s, T, D, np.full((n, 1), x, np.int32), us)
             for t in out[:, 0]:
                 counts[t] += float(q[x]) / (n * n)
+            accepted += float(q[x]) * float((nacc == 1).sum()) / (n * n)
     assert np.allclose(counts, [float(v) for v in p], atol=3.0 / n)
-    # P(accept) = sum min(p, q)
+    # the accepted fraction for x ~ q is sum_x q(x) min(1, p(x)/q(x)) = sum min(p, q);
+    # the u_0 grid quantises each x's acceptance to 1/n
     acc = sum(min(a, b) for a, b in zip(p, q))
-    # accept probability for x ~ q is sum_x q(x) * min(1, p/q) = sum min(p, q)
-    assert 0.0 < float(acc) <= 1.0
+    assert 0.05 < float(acc) < 0.95  # a case where both outcomes occur
+    assert abs(accepted - float(acc)) <= 1.0 / n
 
 
 def test_accept_equal_distributions_always_accept(ora, rng):

@@ -99,8 +99,10 @@ def test_greedy_tokens_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
         m.close()
 
 
-def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
-    """Temperature 0.8 over the full vocabulary, step by step: the oracle runs
+@pytest.mark.parametrize("top_p", [1.0, 0.9])
+def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt, top_p):
+    """Temperature 0.8 over the full vocabulary (and with top_p 0.9 alone, the
+    kept prefix selected on the device), step by step: the oracle runs
     the same step on the GPU's committed sequence and draft tokens (teacher
     forcing).  Every draft draw and every accept decision is bit-exact with the
     oracle's rule on the step's logits; the oracle's own logits for the same
@@ -108,8 +110,8 @@ def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
     compared token for token: an inverse-CDF draw over 32000 tokens moves when
     the logits move by 1e-4, so fp32 order differences change some draws.)"""
     tw, dw = weights
-    k, n_new, seed = 4, 128, 2024
-    s_gpu, s_ora = pkg.sampling(temperature=0.8), ora.sampling(temperature=0.8)
+    k, n_new, seed = 4, 128 if top_p == 1.0 else 48, 2024
+    s_gpu, s_ora = pkg.sampling(temperature=0.8, top_p=top_p), ora.sampling(temperature=0.8, top_p=top_p)
     gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
     sp = pkg.Speculative(gt, gd, k, s_gpu, seed)
     sp.prefill(prompt)
@@ -147,7 +149,7 @@ def test_sampling_steps_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
     st = sp.state()
     assert np.array_equal(sp.tokens(), np.array(seq, np.int32))
     assert st["steps"] == steps and st["accepted"] == accepted and st["proposed"] == k * steps
-    print(f"  t0.8: {len(seq) - len(prompt)} tokens in {steps} steps, accepted {accepted}/{k * steps}, "
+    print(f"  t0.8 top_p {top_p}: {len(seq) - len(prompt)} tokens in {steps} steps, accepted {accepted}/{k * steps}, "
           f"logits max err / rms {worst:.2e}")
     assert worst <= LOGIT_TOL
     for m in (sp, gt, gd):
@@ -201,6 +203,56 @@ def test_greedy_speculation_equals_autoregressive_argmax(pkg, ctx, weights, prom
         seq.append(int(np.argmax(lg)))
     assert list(got) == seq
     for m in (sp, gt, gd, ref):
+        m.close()
+
+
+def test_plain_decoding_bit_exact_with_oracle(pkg, ctx, ora, weights, prompt):
+    """k = 0 (no draft): one target row and one draw per token.  Greedy:
+    the oracle's own plain loop, free-running, token for token.  T = 0.8:
+    every draw is the oracle's rule on the step's logits with u(seed, step)."""
+    tw, _ = weights
+    gt = _gpu_model(pkg, ctx, TARGET, tw)
+    ot = _ora_model(ora, TARGET, tw)
+    sp = pkg.Speculative(gt, None, 0, pkg.sampling(greedy=True), 5)
+    sp.prefill(prompt[:30])
+    sp.generate(20)
+    osp = ora.Speculative(ot, None, 0, ora.sampling(greedy=True), 5)
+    osp.prefill(prompt[:30])
+    osp.generate(20)
+    assert np.array_equal(sp.tokens(), osp.tokens())
+    assert sp.state() == dict(osp.state(), proposed=0, accepted=0) and sp.state()["steps"] == 20
+    sp.close()
+    s, so, seed = pkg.sampling(temperature=0.8), ora.sampling(temperature=0.8), 11
+    sp = pkg.Speculative(gt, None, 0, s, seed)
+    sp.prefill(prompt[:30])
+    for step in range(12):
+        n = sp.state()["n"]
+        sp.steps(1)
+        r = sp.last_step()
+        u = ora.uniforms(seed, step, 1)
+        assert r["uniforms"][0].view(np.uint32) == u[0].view(np.uint32)
+        assert sp.tokens(n, 1)[0] == ora.sample(so, r["target_logits"], u)[0], step
+    sp.close()
+    gt.close()
+    ot.close()
+
+
+def test_one_token_prompt_starts_with_a_plain_step(pkg, ctx, ora, weights, prompt):
+    """A prompt of one token: the first step is plain (the draft's catch-up
+    pair needs two tokens), then speculative steps; greedy, bit-exact with the
+    oracle's loop, which does the same."""
+    tw, dw = weights
+    gt, gd = _gpu_model(pkg, ctx, TARGET, tw), _gpu_model(pkg, ctx, DRAFT, dw)
+    ot, od = _ora_model(ora, TARGET, tw), _ora_model(ora, DRAFT, dw)
+    sp = pkg.Speculative(gt, gd, 4, pkg.sampling(greedy=True), 3)
+    sp.prefill(prompt[:1])
+    sp.generate(30)
+    osp = ora.Speculative(ot, od, 4, ora.sampling(greedy=True), 3)
+    osp.prefill(prompt[:1])
+    osp.generate(30)
+    assert np.array_equal(sp.tokens(), osp.tokens())
+    assert sp.state() == osp.state()
+    for m in (sp, gt, gd, ot, od):
         m.close()
 
 

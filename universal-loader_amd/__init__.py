@@ -501,13 +501,15 @@ def load_gguf_model(ctx, gguf, max_ctx=0):
 
 
 class Speculative:
-    """ulspec_spec: the device speculative-decoding loop over a target and a draft model."""
+    """ulspec_spec: the device speculative-decoding loop over a target and a
+    draft model; k = 0 (draft None) decodes with the target alone."""
 
     def __init__(self, target, draft, k, s, seed):
         self.ctx = target.ctx
         self.target, self.draft, self.k = target, draft, k
         h = P()
-        self.ctx._check(lib().ulspec_spec_create(target.handle, draft.handle, k, C.byref(s), seed, C.byref(h)))
+        self.ctx._check(lib().ulspec_spec_create(target.handle, draft.handle if draft is not None else None, k,
+                                                 C.byref(s), seed, C.byref(h)))
         self.handle = h.value
 
     def close(self):

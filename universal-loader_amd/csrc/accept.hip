@@ -48,6 +48,7 @@ constexpr int kMaxRounds = 256;   // rounds of the CDF draw: V <= 256 * 4 * kSeq
 
 struct RowStat {
     uint64_t Z;
+    uint64_t kmin;  // top-p bound in full-vocabulary mode: tokens with a smaller order_key weigh 0
     float lmax;
     int32_t argmax;
     int32_t nk;  // kept tokens; == V in full-vocabulary mode (list unused)
@@ -121,6 +122,13 @@ __device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t& excl, uint64_
     }
     excl = before + incl - v;
     return total;
+}
+
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t x)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
 }
 
 // Bitonic sort of n (power of two) u64 keys in LDS, descending.  Strides of
@@ -215,6 +223,20 @@ struct W4 {
 __device__ __forceinline__ W4 fixed_e4(float4 l, float lmax, const WarpParams& p)
 {
     return W4{fixed_e(l.x, lmax, p), fixed_e(l.y, lmax, p), fixed_e(l.z, lmax, p), fixed_e(l.w, lmax, p)};
+}
+
+// Weight of token i in a full-vocabulary warp whose top-p prefix is the
+// tokens with order_key >= kmin (kmin = 0 keeps every token).
+__device__ __forceinline__ uint64_t kept_e(float l, uint32_t i, float lmax, uint64_t kmin, const WarpParams& p)
+{
+    return order_key(float_key(l), i) >= kmin ? fixed_e(l, lmax, p) : 0;
+}
+
+__device__ __forceinline__ W4 kept_e4(float4 l, uint32_t q, float lmax, uint64_t kmin, const WarpParams& p)
+{
+    const uint32_t i = 4 * q;
+    return W4{kept_e(l.x, i, lmax, kmin, p), kept_e(l.y, i + 1, lmax, kmin, p), kept_e(l.z, i + 2, lmax, kmin, p),
+              kept_e(l.w, i + 3, lmax, kmin, p)};
 }
 
 // Kept tokens of a row from buf[0..k) (order keys by (logit desc, index asc)):
@@ -324,6 +346,143 @@ __device__ void topk_tie_fallback(const float* __restrict__ row, uint32_t V, uin
     bitonic_desc(buf, kKMax);
 }
 
+// ---- top-p over the whole vocabulary -----------------------------------------
+// The kept set of top_p < 1 without top_k is the shortest prefix of the row in
+// (logit desc, index asc) order whose fixed-point sum c has (double)c >=
+// (double)top_p * (double)Z.  With S(K) = sum of E over order keys >= K
+// (non-increasing in K, and (double) is monotone) that prefix ends at the
+// largest key K* with (double)S(K*) >= thr, so the kept tokens are those with
+// order_key >= K*.  K* is found by a radix select on mass: four passes over
+// the 8-bit digits of the 32-bit logit key, each histogramming (mass, count)
+// of the tokens that share the digits chosen so far and taking the largest
+// digit whose suffix sum (plus the mass of every larger key) reaches thr
+// (with a nonempty bin: for thr <= 0 the first token alone).  The tokens of
+// the chosen logit all weigh the same E*; the first j of them (index order)
+// complete the prefix, j the least with (double)(above + j E*) >= thr, and
+// only when j is short of all of them is the j-th index located.
+struct ToppLds {
+    uint64_t mass[256];
+    uint32_t count[256];
+    uint32_t digit, count_sel, tie_idx;
+    uint64_t excl_sel, mass_sel;
+};
+
+// (mass, count) of the wave's active tokens into their digit bins: one LDS
+// atomic per distinct digit (all lanes of the wave call it).
+__device__ __forceinline__ void wave_bin_add(bool act, uint32_t d, uint64_t w, ToppLds& s)
+{
+    const int lane = threadIdx.x & 63;
+    uint64_t pend = __ballot(act);
+    while (pend) {  // wave-uniform
+        const int leader = __builtin_ctzll(pend);
+        const uint32_t dl = (uint32_t)__shfl((int)d, leader);
+        const bool mine = act && d == dl;
+        const uint64_t m = __ballot(mine);
+        const uint64_t x = wave_sum_u64(mine ? w : 0);
+        if (lane == leader) {
+            atomicAdd((unsigned long long*)&s.mass[dl], (unsigned long long)x);
+            atomicAdd(&s.count[dl], (uint32_t)__popcll(m));
+        }
+        pend &= ~m;
+    }
+}
+
+// kmin (the order key K*) and the kept sum of a row; all kRowThreads threads
+// call it and get both.
+__device__ void topp_select(const float* __restrict__ row, uint32_t V, float lmax, const WarpParams& p, ToppLds& s,
+                            uint64_t* red, uint64_t& kmin, uint64_t& zkept)
+{
+    constexpr int NT = kRowThreads;
+    constexpr int kBatch = 4;  // float4 groups in flight per thread
+    const int tid = threadIdx.x;
+    const uint32_t V4 = (V + 3) / 4;
+    uint32_t prefix = 0;
+    uint64_t above = 0;
+    double thr = 0.0;
+    if (tid == 0) {
+        s.digit = 0;
+        s.count_sel = 1;
+        s.tie_idx = 0;
+        s.excl_sel = s.mass_sel = 0;
+    }
+    for (int lvl = 0; lvl < 4; ++lvl) {
+        const int sh = 24 - 8 * lvl;
+        for (int t = tid; t < 256; t += NT) {
+            s.mass[t] = 0;
+            s.count[t] = 0;
+        }
+        __syncthreads();
+        for (uint32_t q0 = 0; q0 < V4; q0 += kBatch * NT) {  // uniform
+            float4 v[kBatch];
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r) v[r] = load4(row, V, min(q0 + (uint32_t)(r * NT + tid), V4 - 1));
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r) {
+                const uint32_t q = q0 + (uint32_t)(r * NT + tid);
+                const float e[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t key = float_key(e[c]);
+                    const bool act = q < V4 && 4 * q + c < V && (lvl == 0 || (key >> (sh + 8)) == prefix);
+                    const uint64_t w = act ? fixed_e(e[c], lmax, p) : 0;
+                    wave_bin_add(act, (key >> sh) & 255u, w, s);
+                }
+            }
+        }
+        __syncthreads();
+        // thread t < 256 holds bin 255 - t: thread order is descending digit order
+        const uint64_t mv = tid < 256 ? s.mass[255 - tid] : 0;
+        const uint32_t cv = tid < 256 ? s.count[255 - tid] : 0;
+        uint64_t excl = 0;
+        const uint64_t total = block_exclusive_scan_u64<NT>(mv, excl, red);
+        if (lvl == 0) thr = (double)p.top_p * (double)total;
+        const bool ok = cv > 0 && (double)(above + excl + mv) >= thr;
+        const uint64_t first = block_max_u64<NT>(ok ? (uint64_t)(NT - tid) : 0, red);  // > 0: see above
+        if (tid == NT - (int)first) {
+            s.digit = 255u - (uint32_t)tid;
+            s.excl_sel = excl;
+            s.mass_sel = mv;
+            s.count_sel = cv;
+        }
+        __syncthreads();
+        prefix = (prefix << 8) | s.digit;
+        above += s.excl_sel;
+    }
+    // prefix is the logit key of K*; its n_t tokens weigh e_star each
+    const uint32_t n_t = s.count_sel;
+    const uint64_t e_star = s.mass_sel / n_t;
+    uint32_t j = n_t;
+    {
+        const double need = (thr - (double)above) / (double)e_star;
+        if (need < (double)n_t) j = need <= 1.0 ? 1u : (uint32_t)__builtin_ceil(need);
+        j = j < 1 ? 1 : (j > n_t ? n_t : j);
+        while (j > 1 && (double)(above + (uint64_t)(j - 1) * e_star) >= thr) --j;
+        while (j < n_t && (double)(above + (uint64_t)j * e_star) < thr) ++j;
+    }
+    zkept = above + (uint64_t)j * e_star;
+    if (j == n_t) {
+        kmin = (uint64_t)prefix << 32;
+        return;
+    }
+    // the j-th token of that logit in index order: thread t owns [t C, (t+1) C)
+    const uint32_t C = (V + NT - 1) / NT;
+    const uint32_t c0 = min(V, tid * C), c1 = min(V, c0 + C);
+    uint64_t mine = 0;
+    for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == prefix;
+    uint64_t rank = 0;
+    block_exclusive_scan_u64<NT>(mine, rank, red);
+    if (mine && rank < j && j <= rank + mine) {
+        uint64_t r = rank;
+        for (uint32_t i = c0; i < c1; ++i)
+            if (float_key(row[i]) == prefix && ++r == j) {
+                s.tie_idx = i;
+                break;
+            }
+    }
+    __syncthreads();
+    kmin = order_key(prefix, s.tie_idx);
+}
+
 __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __restrict__ logits, uint32_t V,
                                                                 WarpParams p, RowStat* __restrict__ stats,
                                                                 RowSel sel)
@@ -350,10 +509,22 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
     if (tid == 0) {
         st->lmax = lmax;
         st->argmax = (int32_t)(0xffffffffu - (uint32_t)top);
+        st->kmin = 0;
     }
     if (p.greedy) return;
 
     const bool topk = p.top_k > 0 && p.top_k < V;
+    if (!topk && p.top_p < 1.0f) {  // full-vocabulary top-p: the kept prefix and its sum
+        __shared__ ToppLds tps;
+        uint64_t kmin, z;
+        topp_select(row, V, lmax, p, tps, red, kmin, z);
+        if (tid == 0) {
+            st->Z = z;
+            st->kmin = kmin;
+            st->nk = (int32_t)V;
+        }
+        return;
+    }
     if (!topk) {  // full vocabulary: Z over every token
         uint64_t z = 0;
         scan_row<kRowThreads>(row, V, [&](uint32_t, float l) { z += fixed_e(l, lmax, p); });
@@ -401,7 +572,7 @@ __device__ uint64_t weight_of(const RowStat& st, const float* row, uint32_t V, b
                               const WarpParams& p)
 {
     if (x < 0 || (uint32_t)x >= V) return 0;
-    if (!topk) return fixed_e(row[x], st.lmax, p);
+    if (!topk) return kept_e(row[x], (uint32_t)x, st.lmax, st.kmin, p);
     int lo = 0, hi = st.nk - 1;
     while (lo <= hi) {
         const int mid = (lo + hi) >> 1;
@@ -420,13 +591,6 @@ __device__ uint64_t weight_of(const RowStat& st, const float* row, uint32_t V, b
 // Round totals first (kRound rounds per pass, wave xor trees, then LDS), the
 // round holding T, one block scan inside it, then the 4 elements of the
 // owning thread.
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t x)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
-
 template <typename F4>
 __device__ int32_t block_cdf_pick(uint32_t V, float u, F4 w4, uint64_t* scratch, int32_t* pick)
 {
@@ -544,7 +708,9 @@ __device__ int32_t draw_row(const RowStat& st, const float* row, uint32_t V, boo
 {
     if (topk) return list_cdf_pick(st.idx, st.E, st.nk, st.Z, u, V);
     const float lmax = st.lmax;
-    return block_cdf_pick(V, u, [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); }, scratch, pick);
+    const uint64_t kmin = st.kmin;
+    return block_cdf_pick(V, u, [&](uint32_t q) { return kept_e4(load4(row, V, q), q, lmax, kmin, p); }, scratch,
+                          pick);
 }
 
 __device__ __forceinline__ uint64_t residual_weight(uint64_t P, uint64_t Q, uint64_t Zp, uint64_t Zq, int sh)
@@ -716,14 +882,15 @@ __global__ __launch_bounds__(kSeqThreads) void decide_tree_kernel(const RowStat*
         } else {
             const float* drow = dl + ((size_t)b * n + v) * V;
             const float lpm = ts[v].lmax, lqm = ds[v].lmax;
+            const uint64_t kpm = ts[v].kmin, kqm = ds[v].kmin;
             uint64_t Zc = ts[v].Z;
             const uint64_t Zq = ds[v].Z;  // read only when v has children (draft stats exist then)
             int L = 0;                     // levels of the residual chain (full vocabulary)
             bool have_list = false;
             // weights of elements 4q..4q+3 at the current level (full vocabulary), and the draft's
             auto level4 = [&](uint32_t q, W4& qw) {
-                W4 a = fixed_e4(load4(trow, V, q), lpm, p);
-                qw = fixed_e4(load4(drow, V, q), lqm, p);
+                W4 a = kept_e4(load4(trow, V, q), q, lpm, kpm, p);
+                qw = kept_e4(load4(drow, V, q), q, lqm, kqm, p);
                 for (int l = 0; l < L; ++l) {
                     a.a = residual_weight(a.a, qw.a, lvZ[l], Zq, lvSh[l]);
                     a.b = residual_weight(a.b, qw.b, lvZ[l], Zq, lvSh[l]);
@@ -925,6 +1092,7 @@ __device__ __forceinline__ uint64_t row_top(const ChunkPart* part, ChunkPlan cp,
 
 // Sum and last nonzero index of the chunk's weights fixed_e(l - lmax).
 __global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, WarpParams p,
+                                                                  const uint64_t* __restrict__ kmin,
                                                                   ChunkPart* __restrict__ part)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
@@ -935,10 +1103,11 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_sum_kernel(RowSrc rs, uin
     // this thread's first group is loaded before the chunk maxima are read
     const float4 v0 = load4(row, V, min(q0, V4 - 1));
     const float lmax = key_float((uint32_t)(row_top(rp, cp, scratch) >> 32));
+    const uint64_t km = kmin ? kmin[r] : 0;
     uint64_t sum = 0;
     int32_t last = -1;
     for (uint32_t q = q0; q < q1; q += kChunkThreads) {
-        const W4 w = fixed_e4(q == q0 ? v0 : load4(row, V, q), lmax, p);
+        const W4 w = kept_e4(q == q0 ? v0 : load4(row, V, q), q, lmax, km, p);
         const uint64_t e[4] = {w.a, w.b, w.c, w.d};
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -1026,6 +1195,7 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* 
                                                                    const float* __restrict__ uniforms, uint32_t V,
                                                                    ChunkPlan cp, WarpParams p,
                                                                    const ChunkPart* __restrict__ part,
+                                                                   const uint64_t* __restrict__ kmin,
                                                                    int32_t* __restrict__ out)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
@@ -1038,9 +1208,26 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* 
     }
     const float* row = logits + (size_t)r * V;
     const float lmax = key_float((uint32_t)(top >> 32));
-    const int32_t t = chunk_draw(V, cp, uniforms[r], [&](uint32_t q) { return fixed_e4(load4(row, V, q), lmax, p); },
-                                 rp, scratch);
+    const uint64_t km = kmin ? kmin[r] : 0;
+    const int32_t t = chunk_draw(V, cp, uniforms[r],
+                                 [&](uint32_t q) { return kept_e4(load4(row, V, q), q, lmax, km, p); }, rp, scratch);
     if (threadIdx.x == 0) out[r] = t;
+}
+
+// Top-p bound (kmin) of every row of a chunk launch, one workgroup per row;
+// lmax from the row's chunk maxima.
+__global__ __launch_bounds__(kRowThreads) void topp_rows_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, WarpParams p,
+                                                                const ChunkPart* __restrict__ part,
+                                                                uint64_t* __restrict__ kmin)
+{
+    __shared__ uint64_t red[kRowThreads / 64];
+    __shared__ ToppLds tps;
+    const uint32_t r = blockIdx.x;
+    const ChunkPart* rp = part + (size_t)r * cp.G;
+    const uint64_t top = block_max_u64<kRowThreads>(threadIdx.x < cp.G ? rp[threadIdx.x].top : 0, red);
+    uint64_t km, z;
+    topp_select(rs.row(r, V), V, key_float((uint32_t)(top >> 32)), p, tps, red, km, z);
+    if (threadIdx.x == 0) kmin[r] = km;
 }
 
 // ---- acceptance, full vocabulary or greedy -------------------------------------
@@ -1052,6 +1239,7 @@ enum { kPlanDone = 0, kPlanResidual = 1, kPlanBonus = 2 };
 struct AcceptPlan {
     int32_t mode, row, sh, pad;
     uint64_t Zp, Zq;
+    uint64_t kp, kq;  // top-p bounds of the two rows (0: every token kept)
     float lpm, lqm;
 };
 
@@ -1078,6 +1266,7 @@ __global__ __launch_bounds__(64) void accept_walk_kernel(const float* __restrict
                                                          const float* __restrict__ uniforms, uint32_t k, uint32_t V,
                                                          ChunkPlan cp, WarpParams p,
                                                          const ChunkPart* __restrict__ part,
+                                                         const uint64_t* __restrict__ kmin,
                                                          AcceptPlan* __restrict__ plan, int32_t* __restrict__ out,
                                                          int32_t* __restrict__ nacc)
 {
@@ -1105,8 +1294,9 @@ __global__ __launch_bounds__(64) void accept_walk_kernel(const float* __restrict
         row_totals(dp + (size_t)i * cp.G, cp, true, topQ, Zq);
         const float lpm = key_float((uint32_t)(topT >> 32)), lqm = key_float((uint32_t)(topQ >> 32));
         const bool in = xi >= 0 && (uint32_t)xi < V;
-        const uint64_t Px = in ? fixed_e(tl[((size_t)b * (k + 1) + i) * V + xi], lpm, p) : 0;
-        const uint64_t Qx = in ? fixed_e(dl[((size_t)b * k + i) * V + xi], lqm, p) : 0;
+        const size_t rt = (size_t)b * (k + 1) + i, rd = (size_t)B * (k + 1) + (size_t)b * k + i;
+        const uint64_t Px = in ? kept_e(tl[rt * V + xi], (uint32_t)xi, lpm, kmin ? kmin[rt] : 0, p) : 0;
+        const uint64_t Qx = in ? kept_e(dl[((size_t)b * k + i) * V + xi], (uint32_t)xi, lqm, kmin ? kmin[rd] : 0, p) : 0;
         const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
         const double rhs = (double)Px * (double)Zq;
         if (lhs < rhs) {
@@ -1118,6 +1308,8 @@ __global__ __launch_bounds__(64) void accept_walk_kernel(const float* __restrict
         pl.sh = 62 - bitlen64(Zp) - bitlen64(Zq);
         pl.Zp = Zp;
         pl.Zq = Zq;
+        pl.kp = kmin ? kmin[rt] : 0;
+        pl.kq = kmin ? kmin[rd] : 0;
         pl.lpm = lpm;
         pl.lqm = lqm;
         break;
@@ -1143,7 +1335,7 @@ __global__ __launch_bounds__(64) void accept_walk_kernel(const float* __restrict
 __device__ __forceinline__ W4 residual4(const float* trow, const float* drow, uint32_t V, uint32_t q,
                                         const AcceptPlan& pl, const WarpParams& p)
 {
-    const W4 a = fixed_e4(load4(trow, V, q), pl.lpm, p), b = fixed_e4(load4(drow, V, q), pl.lqm, p);
+    const W4 a = kept_e4(load4(trow, V, q), q, pl.lpm, pl.kp, p), b = kept_e4(load4(drow, V, q), q, pl.lqm, pl.kq, p);
     return W4{residual_weight(a.a, b.a, pl.Zp, pl.Zq, pl.sh), residual_weight(a.b, b.b, pl.Zp, pl.Zq, pl.sh),
               residual_weight(a.c, b.c, pl.Zp, pl.Zq, pl.sh), residual_weight(a.d, b.d, pl.Zp, pl.Zq, pl.sh)};
 }
@@ -1190,6 +1382,7 @@ __global__ __launch_bounds__(kChunkThreads) void accept_pick_kernel(const float*
                                                                     const ChunkPart* __restrict__ part,
                                                                     const ChunkPart* __restrict__ rpart,
                                                                     const AcceptPlan* __restrict__ plan,
+                                                                    const uint64_t* __restrict__ kmin,
                                                                     int32_t* __restrict__ out)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
@@ -1209,7 +1402,8 @@ __global__ __launch_bounds__(kChunkThreads) void accept_pick_kernel(const float*
     } else {  // the bonus, or an all-zero residual: draw from the target row
         const ChunkPart* tp = part + ((size_t)b * (k + 1) + pl.row) * cp.G;
         const float lmax = key_float((uint32_t)(row_top(tp, cp, scratch) >> 32));
-        t = chunk_draw(V, cp, u, [&](uint32_t q) { return fixed_e4(load4(trow, V, q), lmax, p); }, tp, scratch);
+        const uint64_t km = kmin ? kmin[(size_t)b * (k + 1) + pl.row] : 0;
+        t = chunk_draw(V, cp, u, [&](uint32_t q) { return kept_e4(load4(trow, V, q), q, lmax, km, p); }, tp, scratch);
     }
     if (threadIdx.x == 0) out[(size_t)b * (k + 1) + pl.row] = t;
 }
@@ -1457,8 +1651,6 @@ ulspec_status make_params(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t V,
     if (!(s->top_p == s->top_p)) return fail(ctx, ULSPEC_EINVAL, "top_p is NaN");
     if (s->top_k > (uint32_t)kKMax && s->top_k < V)
         return fail(ctx, ULSPEC_EUNSUPPORTED, "top_k %u > %d", s->top_k, kKMax);
-    if ((s->top_k == 0 || s->top_k >= V) && s->top_p < 1.0f)
-        return fail(ctx, ULSPEC_EUNSUPPORTED, "top_p without top_k (a sort of the whole vocabulary)");
     p.invT = 1.0f / s->temperature;
     return ULSPEC_OK;
 }
@@ -1470,13 +1662,14 @@ namespace ulspec {
 size_t accept_workspace_bytes(uint32_t B, uint32_t k)
 {
     const size_t stats = topk_ws_bytes(B * (k + 1) + B * k);
-    const size_t chunks = (size_t)(B * (k + 1) + B * k + B) * kMaxChunks * sizeof(ChunkPart) + B * sizeof(AcceptPlan);
+    const size_t chunks = (size_t)(B * (k + 1) + B * k + B) * kMaxChunks * sizeof(ChunkPart) +
+                          B * sizeof(AcceptPlan) + (size_t)(B * (k + 1) + B * k) * sizeof(uint64_t);
     return std::max(stats, chunks);
 }
 
 size_t sample_workspace_bytes(uint32_t R)
 {
-    return std::max((size_t)R * kMaxChunks * sizeof(ChunkPart), topk_ws_bytes(R));
+    return std::max((size_t)R * (kMaxChunks * sizeof(ChunkPart) + sizeof(uint64_t)), topk_ws_bytes(R));
 }
 
 ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,
@@ -1505,19 +1698,25 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         ChunkPart* part = (ChunkPart*)ws;  // [rows_t + rows_d][G]
         ChunkPart* rpart = part + (size_t)(rows_t + rows_d) * cp.G;  // [B][G]
         AcceptPlan* plan = (AcceptPlan*)(rpart + (size_t)B * cp.G);
+        const bool topp = !p.greedy && p.top_p < 1.0f;
+        uint64_t* kmin = topp ? (uint64_t*)(plan + B) : nullptr;  // [rows_t + rows_d]
         const RowSrc rs{target_logits, rows_t, draft_logits};
         const dim3 grid(cp.G, rows_t + rows_d), blk(kChunkThreads);
         hipLaunchKernelGGL(chunk_max_kernel, grid, blk, 0, ctx->stream, rs, V, cp, part);
-        if (!p.greedy) hipLaunchKernelGGL(chunk_sum_kernel, grid, blk, 0, ctx->stream, rs, V, cp, p, part);
+        if (topp)
+            hipLaunchKernelGGL(topp_rows_kernel, dim3(rows_t + rows_d), dim3(kRowThreads), 0, ctx->stream, rs, V, cp,
+                               p, (const ChunkPart*)part, kmin);
+        if (!p.greedy)
+            hipLaunchKernelGGL(chunk_sum_kernel, grid, blk, 0, ctx->stream, rs, V, cp, p, (const uint64_t*)kmin, part);
         hipLaunchKernelGGL(accept_walk_kernel, dim3(B), dim3(64), 0, ctx->stream, target_logits, draft_logits,
-                           draft_tokens, uniforms, k, V, cp, p, (const ChunkPart*)part, plan, out_tokens,
-                           out_n_accepted);
+                           draft_tokens, uniforms, k, V, cp, p, (const ChunkPart*)part, (const uint64_t*)kmin, plan,
+                           out_tokens, out_n_accepted);
         if (!p.greedy) {
             hipLaunchKernelGGL(residual_sum_kernel, dim3(cp.G, B), blk, 0, ctx->stream, target_logits, draft_logits, k,
                                V, cp, p, (const AcceptPlan*)plan, rpart);
             hipLaunchKernelGGL(accept_pick_kernel, dim3(B), blk, 0, ctx->stream, target_logits, draft_logits, uniforms,
                                k, V, cp, p, (const ChunkPart*)part, (const ChunkPart*)rpart, (const AcceptPlan*)plan,
-                               out_tokens);
+                               (const uint64_t*)kmin, out_tokens);
         }
         return check_launch(ctx, "accept launch");
     }
@@ -1593,13 +1792,18 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     if (p.greedy || p.top_k == 0 || p.top_k >= V) {
         const ChunkPlan cp = chunk_plan(V);
         ChunkPart* part = (ChunkPart*)ws;
+        const bool topp = !p.greedy && p.top_p < 1.0f;
+        uint64_t* kmin = topp ? (uint64_t*)(part + (size_t)R * cp.G) : nullptr;  // [R]
         const RowSrc rs{logits, R, nullptr};
         hipLaunchKernelGGL(chunk_max_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, part);
+        if (topp)
+            hipLaunchKernelGGL(topp_rows_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, rs, V, cp, p,
+                               (const ChunkPart*)part, kmin);
         if (!p.greedy)
             hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, p,
-                               part);
+                               (const uint64_t*)kmin, part);
         hipLaunchKernelGGL(chunk_pick_kernel, dim3(R), dim3(kChunkThreads), 0, ctx->stream, logits, uniforms, V, cp,
-                           p, (const ChunkPart*)part, out_tokens);
+                           p, (const ChunkPart*)part, (const uint64_t*)kmin, out_tokens);
         return check_launch(ctx, "sample launch");
     }
     const TopkWs tw = topk_ws(ws, R);

@@ -14,6 +14,12 @@
 // fixed kernel sequence: it is captured once into a HIP graph and replayed,
 // with no host synchronisation inside or between steps.  Uniforms of step s:
 // draft j uses counter s*(2k+1) + j, the accept rule s*(2k+1) + k + j.
+//
+// k = 0 is plain decoding of the target (no draft model): a step forwards
+// t_{n-1} at n-1 and samples t_n from its logits with counter s.  A prompt of
+// one token starts the same way for k > 0: the first step is such a plain
+// step (the draft's catch-up pair needs two committed tokens), after which
+// the draft catches up on [t_0, t_1].
 #include <algorithm>
 
 #include "../detmath.h"
@@ -41,6 +47,16 @@ __global__ void spec_begin_kernel(const SpecState* __restrict__ st, const int32_
         tok_d[0] = seq[st->n - 2];
         tok_d[1] = seq[st->n - 1];
     }
+}
+
+// Plain (target-only) step: the uniform of counter step (2k+1) and the last token.
+__global__ void spec_plain_begin_kernel(const SpecState* __restrict__ st, const int32_t* __restrict__ seq,
+                                        uint64_t seed, uint32_t k, float* __restrict__ unif,
+                                        int32_t* __restrict__ tok_t)
+{
+    if (threadIdx.x != 0) return;
+    unif[0] = counter_uniform(seed, st->step * (2 * k + 1));
+    tok_t[0] = seq[st->n - 1];
 }
 
 __global__ void spec_verify_tokens_kernel(const SpecState* __restrict__ st, const int32_t* __restrict__ seq,
@@ -89,6 +105,7 @@ struct ulspec_spec {
     int32_t* tok_t = nullptr;
     int32_t* out_tok = nullptr;
     int32_t* nacc = nullptr;
+    int32_t* zero = nullptr;  // 0: the accepted count of a plain step
     float* unif = nullptr;
     float* dlogits = nullptr;  // [k][V]
     float* tlogits = nullptr;  // [k+1][V]
@@ -97,17 +114,31 @@ struct ulspec_spec {
     SpecState* host_st = nullptr;  // pinned
     std::vector<void*> allocs;
     bool prefilled = false;
+    bool plain_first = false;  // one-token prompt: the next step is a plain step
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
     void* graph_ws = nullptr;       // context workspace the graph was captured with
     uint32_t n_hi = 0;              // upper bound of the committed count
     ulspec_status enqueue_step();
     ulspec_status launch_step();
+    ulspec_status launch_plain_step();
     ulspec_status sync_state();
 };
 
+ulspec_status ulspec_spec::launch_plain_step()
+{
+    hipStream_t stream = ctx->stream;
+    hipLaunchKernelGGL(spec_plain_begin_kernel, dim3(1), dim3(64), 0, stream, st, seq, seed, k, unif, tok_t);
+    ulspec_status r = t->forward(tok_t, 1, &st->n, -1, tlogits, 1);
+    if (r == ULSPEC_OK) r = sample_launch(ctx, &s, 1, V, tlogits, unif, out_tok, ws_sample);
+    if (r != ULSPEC_OK) return r;
+    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, seq, out_tok, (const int32_t*)zero, 0u);
+    return check_launch(ctx, "plain step launch");
+}
+
 ulspec_status ulspec_spec::launch_step()
 {
+    if (k == 0) return launch_plain_step();
     hipStream_t stream = ctx->stream;
     hipLaunchKernelGGL(spec_begin_kernel, dim3(1), dim3(64), 0, stream, st, seq, seed, k, unif, tok_d);
     // draft: catch-up pair, then single tokens
@@ -169,22 +200,25 @@ ulspec_status ulspec_spec::sync_state()
 extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k,
                                             const ulspec_sampling* s, uint64_t seed, ulspec_spec** out)
 {
-    if (!target || !draft) return ULSPEC_EINVAL;
+    if (!target || (!draft && k > 0)) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = target->ctx;
-    if (draft->ctx != ctx) return fail(ctx, ULSPEC_EINVAL, "spec_create: models on different contexts");
+    if (k == 0) draft = nullptr;  // plain decoding of the target: no draft model
+    if (draft && draft->ctx != ctx) return fail(ctx, ULSPEC_EINVAL, "spec_create: models on different contexts");
     if (!s || !out) return fail(ctx, ULSPEC_EINVAL, "spec_create: null pointer");
-    if (k == 0 || k + 1 > target->rows_max || draft->rows_max < 2)
-        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u (k + 1 <= %u rows of the target)", k, target->rows_max);
-    if (target->cfg.vocab != draft->cfg.vocab) return fail(ctx, ULSPEC_EINVAL, "spec_create: vocabularies differ");
-    if (!target->complete() || !draft->complete()) return fail(ctx, ULSPEC_EINVAL, "spec_create: model tensors missing");
+    if (k > 16 || k + 1 > target->rows_max || (draft && draft->rows_max < 2))
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u (k <= 16, k + 1 <= %u rows of the target)", k,
+                    target->rows_max);
+    if (draft && target->cfg.vocab != draft->cfg.vocab)
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: vocabularies differ");
+    if (!target->complete() || (draft && !draft->complete()))
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: model tensors missing");
     const uint32_t V = target->cfg.vocab;
     // the sampling parameters are validated by a dry check of the accept rule's limits
     if (!s->greedy) {
         if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
             return fail(ctx, ULSPEC_EINVAL, "spec_create: temperature must be positive and finite");
         if (s->top_k > 256 && s->top_k < V) return fail(ctx, ULSPEC_EUNSUPPORTED, "spec_create: top_k > 256");
-        if ((s->top_k == 0 || s->top_k >= V) && s->top_p < 1.0f)
-            return fail(ctx, ULSPEC_EUNSUPPORTED, "spec_create: top_p without top_k");
+        if (!(s->top_p == s->top_p)) return fail(ctx, ULSPEC_EINVAL, "spec_create: top_p is NaN");
     }
     (void)hipSetDevice(ctx->device);
     ulspec_spec* sp = new ulspec_spec;
@@ -195,7 +229,7 @@ extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* 
     sp->V = V;
     sp->s = *s;
     sp->seed = seed;
-    sp->cap = std::min(target->cfg.max_ctx, draft->cfg.max_ctx);
+    sp->cap = draft ? std::min(target->cfg.max_ctx, draft->cfg.max_ctx) : target->cfg.max_ctx;
     struct Want {
         void** p;
         size_t bytes;
@@ -207,21 +241,26 @@ extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* 
         {(void**)&sp->tok_t, 64},
         {(void**)&sp->out_tok, 64},
         {(void**)&sp->nacc, 16},
+        {(void**)&sp->zero, 16},
         {(void**)&sp->unif, 4 * (2 * 16 + 1)},
         {(void**)&sp->dlogits, (size_t)k * V * 4},
         {(void**)&sp->tlogits, (size_t)(k + 1) * V * 4},
-        {(void**)&sp->ws_accept, accept_workspace_bytes(1, k)},
+        {(void**)&sp->ws_accept, k ? accept_workspace_bytes(1, k) : 0},
         {(void**)&sp->ws_sample, sample_workspace_bytes(1)},
     };
     ulspec_status st = ULSPEC_OK;
     for (const Want& w : wants) {
         if (st != ULSPEC_OK) break;
+        if (!w.bytes) continue;  // k = 0: no draft rows, no acceptance
         hipError_t e = hipMalloc(w.p, w.bytes);
         if (e != hipSuccess) st = hip_fail(ctx, e, "spec_create hipMalloc");
         else sp->allocs.push_back(*w.p);
     }
     if (st == ULSPEC_OK) {
-        hipError_t e = hipHostMalloc((void**)&sp->host_st, sizeof(SpecState), hipHostMallocDefault);
+        hipError_t e = hipMemset(sp->zero, 0, 16);
+        if (e == hipSuccess) e = hipMemset(sp->nacc, 0, 16);
+        if (e == hipSuccess) e = hipMemset(sp->st, 0, sizeof(SpecState));  // no tokens before the prefill
+        if (e == hipSuccess) e = hipHostMalloc((void**)&sp->host_st, sizeof(SpecState), hipHostMallocDefault);
         if (e != hipSuccess) st = hip_fail(ctx, e, "spec_create hipHostMalloc");
     }
     if (st != ULSPEC_OK) {
@@ -247,21 +286,26 @@ extern "C" ulspec_status ulspec_spec_prefill(ulspec_spec* sp, const int32_t* pro
 {
     if (!sp) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = sp->ctx;
-    if (!prompt || n < 2) return fail(ctx, ULSPEC_EINVAL, "spec_prefill: need at least 2 prompt tokens");
+    if (!prompt || n < 1) return fail(ctx, ULSPEC_EINVAL, "spec_prefill: need at least 1 prompt token");
     if ((uint64_t)n + sp->k + 1 > sp->cap) return fail(ctx, ULSPEC_EINVAL, "spec_prefill: %u tokens leave no room", n);
     for (uint32_t i = 0; i < n; ++i)
         if (prompt[i] < 0 || (uint32_t)prompt[i] >= sp->V)
             return fail(ctx, ULSPEC_EINVAL, "spec_prefill: token %d out of range", prompt[i]);
     (void)hipSetDevice(ctx->device);
-    ulspec_status st = ulspec_model_forward(sp->t, prompt, n - 1, 0, nullptr, 0);
-    if (st == ULSPEC_OK) st = ulspec_model_forward(sp->d, prompt, n - 1, 0, nullptr, 0);
-    if (st != ULSPEC_OK) return st;
+    ulspec_status st = ULSPEC_OK;
+    if (hipMemset(sp->nacc, 0, 16) != hipSuccess) return fail(ctx, ULSPEC_EDEVICE, "spec_prefill: reset");
+    if (n > 1) {
+        st = ulspec_model_forward(sp->t, prompt, n - 1, 0, nullptr, 0);
+        if (st == ULSPEC_OK && sp->d) st = ulspec_model_forward(sp->d, prompt, n - 1, 0, nullptr, 0);
+        if (st != ULSPEC_OK) return st;
+    }
     hipError_t e = hipMemcpy(sp->seq, prompt, (size_t)n * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_fail(ctx, e, "spec_prefill copy");
     hipLaunchKernelGGL(spec_reset_kernel, dim3(1), dim3(1), 0, ctx->stream, sp->st, (int32_t)n);
     st = check_launch(ctx, "spec_prefill launch");
     if (st != ULSPEC_OK) return st;
     sp->prefilled = true;
+    sp->plain_first = n == 1 && sp->k > 0;
     return sp->sync_state();
 }
 
@@ -279,7 +323,13 @@ extern "C" ulspec_status ulspec_spec_steps(ulspec_spec* sp, uint32_t n_steps)
                         sp->cap, sp->n_hi);
     }
     for (uint32_t i = 0; i < n_steps; ++i) {
-        ulspec_status st = sp->enqueue_step();
+        ulspec_status st;
+        if (sp->plain_first) {  // direct launches: the graph holds the speculative step
+            st = sp->launch_plain_step();
+            sp->plain_first = false;
+        } else {
+            st = sp->enqueue_step();
+        }
         if (st != ULSPEC_OK) return st;
         sp->n_hi += sp->k + 1;
     }
@@ -353,7 +403,7 @@ extern "C" ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_lo
         {out_tokens, sp->out_tok, (k + 1) * 4},         {n_accepted, sp->nacc, 4},
     };
     for (const Copy& c : copies)
-        if (e == hipSuccess && c.dst) e = hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost);
+        if (e == hipSuccess && c.dst && c.bytes) e = hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost);
     return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_last_step copy");
 }
 

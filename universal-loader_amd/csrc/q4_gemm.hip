@@ -1336,10 +1336,19 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
         const std::vector<const void*>* fns;
         size_t fixed;
     } groups[] = {{&wide, kStaticWide}, {&small, kStaticSmall}, {&rings, kStaticRing}};
+    // The launch checks add each group's static LDS to the dynamic size; the
+    // opt-in must not let static + dynamic exceed the CU's 160 KB, so both
+    // come from the compiled kernel's own static size.
     for (const auto& gr : groups)
         for (const void* f : *gr.fns) {
-            hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)(kWideLdsMax - gr.fixed));
+            hipFuncAttributes at{};
+            hipError_t e = hipFuncGetAttributes(&at, f);
+            if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncGetAttributes(GEMM kernel)");
+            if (at.sharedSizeBytes != gr.fixed)
+                return fail(ctx, ULSPEC_EDEVICE, "GEMM kernel static LDS %zu B, launch checks assume %zu B",
+                            (size_t)at.sharedSizeBytes, gr.fixed);
+            e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)(kWideLdsMax - at.sharedSizeBytes));
             if (e != hipSuccess) return hip_fail(ctx, e, "hipFuncSetAttribute(max dynamic LDS)");
         }
     return ULSPEC_OK;

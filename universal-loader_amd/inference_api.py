@@ -194,16 +194,16 @@ class InferenceAPI:
 
     def generate_tokens(self, prompt_ids, config=None):
         """max_tokens new token ids after prompt_ids: speculative steps with the
-        draft model when enabled, otherwise k = 1 steps of the same device loop
-        with the target as its own draft."""
+        draft model when enabled, otherwise plain decoding of the target (the
+        device loop with k = 0: one target row and one draw per token)."""
         with self._lock:
             if self._target is None:
                 raise UlspecError(EUNSUPPORTED, "no model loaded")
             config = config or self._config
             s = self._sampling(config)
             spec = self._spec and self._draft is not None
-            k = self.SPEC_LENGTH if spec else 1
-            loop = Speculative(self._target, self._draft if spec else self._target, k, s, self._seed)
+            k = self.SPEC_LENGTH if spec else 0
+            loop = Speculative(self._target, self._draft if spec else None, k, s, self._seed)
             try:
                 t0 = time.perf_counter()
                 loop.prefill(np.asarray(prompt_ids, np.int32))
