@@ -5,10 +5,11 @@ Workload: random-init (synthetic) Llama target -- dim 4096, 32 layers, 32
 heads, FFN 11008, vocab 32000 -- and draft -- dim 2048, 16 layers, 16 heads,
 FFN 5632 -- all linear layers, the embedding and the LM head GGUF Q4_K; a
 seeded prompt of 2048 tokens (prefill untimed); k = 5 draft tokens per step;
-batch 1; temperature 0.8 over the full vocabulary (--greedy: argmax rule).
-One step = 5 draft forwards + one target forward over 6 rows + acceptance +
-commit, replayed from a captured HIP graph.  Inputs live in HBM before the
-timed region starts.
+batch 1 (--batch B: B sequences of their own 2048-token prompts stepped
+together, the target verifying 6 B rows per step); temperature 0.8 over the
+full vocabulary (--greedy: argmax rule).  One step = 5 draft forwards + one
+target forward over 6 rows per sequence + acceptance + commit, replayed from a
+captured HIP graph.  Inputs live in HBM before the timed region starts.
 
 Printed (one JSON line): value = committed tokens / wall seconds over exactly
 --steps steps, bracketed by stream synchronisations; "roofline" for the verify
@@ -444,6 +445,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--greedy", action="store_true")
+    ap.add_argument("--batch", type=int, default=1, help="sequences stepped together (1 .. 8)")
     ap.add_argument("--temperature", type=float, default=0.8)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
@@ -492,28 +494,36 @@ def main():
     use_cpu = not args.no_cpu
     cpu_steps = args.cpu_steps if use_cpu else 0
     cap = CONTEXT + (cpu_steps + args.warmup + args.steps) * (K_SPEC + 1) + 32
+    B = args.batch
+    if not 1 <= B <= 8:
+        print(f"bench.py: --batch {B} (1 .. 8 sequences)", file=sys.stderr)
+        return 2
     t0 = time.perf_counter()
-    target, th = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=cap), pkg.Q4_K, seed=1, keep_host=use_cpu)
+    target, th = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=cap, n_seq=B), pkg.Q4_K, seed=1, keep_host=use_cpu)
     n_target_w = len(weight_ids(pkg, ctx))
-    draft, dh = synthetic_llama(pkg, ctx, dict(DRAFT, max_ctx=cap), pkg.Q4_K, seed=2, keep_host=use_cpu)
+    draft, dh = synthetic_llama(pkg, ctx, dict(DRAFT, max_ctx=cap, n_seq=B), pkg.Q4_K, seed=2, keep_host=use_cpu)
     t_synth = time.perf_counter() - t0
     log(f"weights synthesized and uploaded in {t_synth:.1f} s")
-    prompt = np.random.default_rng(args.seed).integers(0, TARGET["vocab"], CONTEXT).astype(np.int32)
+    rng = np.random.default_rng(args.seed)
+    prompts = [rng.integers(0, TARGET["vocab"], CONTEXT).astype(np.int32) for _ in range(B)]
     s = pkg.sampling(greedy=True) if args.greedy else pkg.sampling(temperature=args.temperature)
-    sp = pkg.Speculative(target, draft, K_SPEC, s, args.seed)
+    sp = pkg.Speculative(target, draft, K_SPEC, s, args.seed, n_seq=B)
     sp.set_graph(not args.no_graph)
     t0 = time.perf_counter()
-    sp.prefill(prompt)
+    sp.prefill(prompts[0] if B == 1 else prompts)
     t_prefill = time.perf_counter() - t0
-    log(f"prefill of {CONTEXT} tokens in {t_prefill:.1f} s")
+    log(f"prefill of {B} x {CONTEXT} tokens in {t_prefill:.1f} s")
     recorded, kv_t, kv_d = [], None, None
-    if use_cpu:
+    if use_cpu:  # the CPU path on sequence 0
         kv_t = [target.kv_io(l, 0, 0, CONTEXT - 1) for l in range(TARGET["n_layers"])]
         kv_d = [draft.kv_io(l, 0, 0, CONTEXT - 1) for l in range(DRAFT["n_layers"])]
         for _ in range(cpu_steps):
-            n = sp.state()["n"]
+            n = sp.seq_state(0)["n"]
             sp.steps(1)
-            recorded.append((n, sp.last_step()))
+            r = sp.last_step()
+            if B > 1:
+                r = {name: (a[0] if name != "n_accepted" else int(a[0])) for name, a in r.items()}
+            recorded.append((n, r))
     sp.steps(args.warmup)
     st0 = sp.state()
     ctx.sync()
@@ -531,11 +541,12 @@ def main():
     log(f"{args.steps} steps: {tokens} tokens in {wall * 1e3:.1f} ms (events {ev_ms:.1f} ms), "
         f"accepted {accepted}/{proposed}")
     ids = [(i, info) for i, info in weight_ids(pkg, ctx)[:n_target_w]]
-    us, alg = gemm_roofline(pkg, ctx, ids, K_SPEC + 1)
+    Mv = (K_SPEC + 1) * B  # the target's verify rows per step
+    us, alg = gemm_roofline(pkg, ctx, ids, Mv)
     achieved = alg / (us * 1e-6) / 1e9
-    log(f"verify GEMM (target, M=6): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
+    log(f"verify GEMM (target, M={Mv}): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
         f"{achieved:.0f} GB/s")
-    seq = sp.tokens() if use_cpu else None
+    seq = sp.tokens(seq=0) if use_cpu else None
     sp.close()
     cpu = None
     if use_cpu:
@@ -543,18 +554,21 @@ def main():
         log(f"cpu baseline: {cpu}")
     mode = "greedy" if args.greedy else f"temperature {args.temperature}, full vocabulary"
     out = {
-        "metric": METRIC, "value": tokens / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC if B == 1 else METRIC.replace("bs=1", f"bs={B}"), "value": tokens / wall, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": wall * 1e3 / args.steps, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q4_k weights x fp32 activations (split fp16 MFMA operands), fp32 accumulate",
         "data": "synthetic: random-init N(0, 0.02^2) weights quantized to Q4_K on the device, seeded prompt",
         "config": {"workload": f"speculative decoding step, 7B-shape Q4_K target (dim 4096, 32 layers, 32 heads, "
                                f"FFN 11008, vocab 32000) + draft (dim 2048, 16 layers, 16 heads, FFN 5632), k=5, "
-                               f"bs=1, context {CONTEXT}, {mode}",
-                   "k": K_SPEC, "batch": 1, "context": CONTEXT, "acceptance": accepted / max(1, proposed),
+                               f"bs={B}, context {CONTEXT}, {mode}",
+                   "k": K_SPEC, "batch": B, "context": CONTEXT, "acceptance": accepted / max(1, proposed),
                    "tokens": tokens, "event_ms": ev_ms},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(),
-                     "kernel": "verify dequant-GEMM (gemm_ring_kernel for QKV, gate/up, LM head; gemm_stream_kernel for O, down), the 129 target weights, M=6",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic() if B == 1 else None,
+                     "kernel": ("verify dequant-GEMM (gemm_ring_kernel for QKV, gate/up, LM head; gemm_stream_kernel "
+                                "for O, down), the 129 target weights, M=6") if B == 1 else
+                               f"verify dequant-GEMM (split-K gemm_slice_kernel + gemm_reduce_kernel), the 129 target "
+                               f"weights, M={Mv}",
                      "avg_us": us, "algorithmic_bytes": alg},
         "cpu_baseline": cpu,
     }

@@ -223,6 +223,13 @@ typedef struct {
     float    rope_base;  /* RoPE theta base (10000 in src/shaders/rope.glsl) */
 } ulspec_model_cfg;
 ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, ulspec_model** out);
+/* A model with n_seq <= 8 sequence slots, each with its own K/V cache of
+ * max_ctx positions (one set of weights): the batch of the reference's
+ * generate_batch (src/api/inference_api.h:63) for the device loop of
+ * ulspec_spec_create_batch.  ulspec_model_create is n_seq = 1; the other
+ * model entry points work on slot 0. */
+ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, uint32_t n_seq,
+                                        ulspec_model** out);
 void          ulspec_model_destroy(ulspec_model* m);
 /* One GGUF tensor by its GGUF name (token_embd.weight, output_norm.weight,
  * output.weight, blk.<i>.{attn_norm,attn_q,attn_k,attn_v,attn_output,ffn_norm,
@@ -240,6 +247,9 @@ ulspec_status ulspec_model_set_tensor(ulspec_model* m, const char* name, uint32_
  * (src/api/inference_api.cpp:277-280) and prefill. */
 ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* tokens, uint32_t M, uint32_t pos,
                                    float* logits, uint32_t n_logits);
+/* ulspec_model_forward on sequence slot seq (its own K/V cache). */
+ulspec_status ulspec_model_forward_seq(ulspec_model* m, uint32_t seq, const int32_t* tokens, uint32_t M,
+                                       uint32_t pos, float* logits, uint32_t n_logits);
 /* Forward a draft tree of M nodes (host ids; M <= 16 and at most the model's
  * row limit) whose K/V go to slots pos .. pos+M-1: node i (parent[i] in [-1,
  * i), host array; -1 = child of the prefix) takes RoPE position pos +
@@ -262,6 +272,9 @@ ulspec_status ulspec_model_kv_compact(ulspec_model* m, uint32_t pos, const int32
  * host arrays [n][n_kv_heads][head_dim] of fp16 bits.  Synchronous. */
 ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n, uint16_t* k,
                                  uint16_t* v);
+/* ulspec_model_kv_io on sequence slot seq. */
+ulspec_status ulspec_model_kv_io_seq(ulspec_model* m, uint32_t seq, uint32_t layer, int dir, uint32_t pos0,
+                                     uint32_t n, uint16_t* k, uint16_t* v);
 
 /* ---- GGUF files -------------------------------------------------------------
  * Read-only memory map of a GGUF v2/v3 file: header, metadata and tensor
@@ -328,28 +341,47 @@ ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint
 typedef struct ulspec_spec ulspec_spec;
 ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
                                  uint64_t seed, ulspec_spec** out);
+/* The same loop over n_seq <= 8 sequences at once (models created with at
+ * least n_seq slots, (k+1) n_seq <= 48): every forward takes one group of
+ * rows per sequence (M = (k+1) n_seq verify rows through the target), each
+ * sequence on its own cache slot and positions; the accept rule runs over
+ * the n_seq sequences.  Sequence b of step s uses uniforms
+ * u(seed, (s n_seq + b)(2k+1) + j) (n_seq = 1: the counters above).  The
+ * batch of the reference's generate_batch (src/api/inference_api.h:63). */
+ulspec_status ulspec_spec_create_batch(ulspec_model* target, ulspec_model* draft, uint32_t k,
+                                       const ulspec_sampling* s, uint64_t seed, uint32_t n_seq, ulspec_spec** out);
 void          ulspec_spec_destroy(ulspec_spec* sp);
 /* Commit the prompt (n >= 1): both models process tokens 0 .. n-2; token n-1
  * is pending.  Resets the counters.  With n = 1 and k > 0 the first step is a
  * plain step (u(seed, 0)): the draft's catch-up pair needs two tokens.
  * Synchronous. */
 ulspec_status ulspec_spec_prefill(ulspec_spec* sp, const int32_t* prompt, uint32_t n);
+/* Prefill of a batch loop: the n_seq prompts concatenated, lens[b] >= 2
+ * tokens each (>= 1 for k = 0). */
+ulspec_status ulspec_spec_prefill_batch(ulspec_spec* sp, const int32_t* prompts, const uint32_t* lens);
 /* Enqueue n_steps steps (asynchronous); EINVAL if they could overrun the
  * context (each step commits at most k+1 tokens). */
 ulspec_status ulspec_spec_steps(ulspec_spec* sp, uint32_t n_steps);
-/* Steps until at least n_new tokens were committed by this call; *n_out = the
- * number committed (up to n_new + k).  Synchronous. */
+/* Steps until at least n_new tokens were committed by this call (by every
+ * sequence); *n_out = the number committed (the fewest of any sequence, up to
+ * n_new + k).  Synchronous. */
 ulspec_status ulspec_spec_generate(ulspec_spec* sp, uint32_t n_new, uint32_t* n_out);
 /* Synchronises, then reports committed tokens (prompt included), steps,
- * accepted draft tokens and proposed draft tokens since the prefill. */
+ * accepted draft tokens and proposed draft tokens since the prefill (sums
+ * over the sequences of a batch). */
 ulspec_status ulspec_spec_state(ulspec_spec* sp, uint32_t* n_tokens, uint64_t* steps, uint64_t* accepted,
                                 uint64_t* proposed);
-/* Committed tokens start .. start+n-1 to host memory.  Synchronous. */
+/* The same for sequence seq of a batch. */
+ulspec_status ulspec_spec_seq_state(ulspec_spec* sp, uint32_t seq, uint32_t* n_tokens, uint64_t* accepted,
+                                    uint64_t* proposed);
+/* Committed tokens start .. start+n-1 (of sequence 0) to host memory.  Synchronous. */
 ulspec_status ulspec_spec_tokens(ulspec_spec* sp, uint32_t start, uint32_t n, int32_t* out);
+ulspec_status ulspec_spec_seq_tokens(ulspec_spec* sp, uint32_t seq, uint32_t start, uint32_t n, int32_t* out);
 /* Inputs and outputs of the last step, copied to host arrays (any may be
- * NULL): target logits [k+1][V], draft logits [k][V], draft tokens [k],
- * uniforms [2k+1], emitted tokens [k+1] (-1 padded), n_accepted.
- * Synchronous.  For checking a step against a CPU restatement. */
+ * NULL), sequence-major for a batch of B: target logits [B][k+1][V], draft
+ * logits [B][k][V], draft tokens [B][k], uniforms [B][2k+1], emitted tokens
+ * [B][k+1] (-1 padded), n_accepted [B].  Synchronous.  For checking a step
+ * against a CPU restatement. */
 ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
                                     int32_t* draft_tokens, float* uniforms, int32_t* out_tokens,
                                     int32_t* n_accepted);

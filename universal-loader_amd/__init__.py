@@ -109,6 +109,9 @@ ABI = [
     ("ulspec_uniforms", C.c_int, [P, C.c_uint64, C.c_uint64, U32, P]),
     ("ulspec_synth_q4", C.c_int, [P, U32, C.c_uint64, C.c_uint64, U32, U32, C.c_float, P]),
     ("ulspec_model_create", C.c_int, [P, C.POINTER(ModelCfg), C.POINTER(P)]),
+    ("ulspec_model_create_batch", C.c_int, [P, C.POINTER(ModelCfg), U32, C.POINTER(P)]),
+    ("ulspec_model_forward_seq", C.c_int, [P, U32, P, U32, U32, P, U32]),
+    ("ulspec_model_kv_io_seq", C.c_int, [P, U32, U32, C.c_int, U32, U32, P, P]),
     ("ulspec_model_destroy", None, [P]),
     ("ulspec_model_set_tensor", C.c_int, [P, C.c_char_p, U32, P, C.c_size_t, C.c_uint64, C.c_uint64, C.c_int]),
     ("ulspec_model_forward", C.c_int, [P, P, U32, U32, P, U32]),
@@ -124,6 +127,10 @@ ABI = [
                                     C.POINTER(C.c_uint64)]),
     ("ulspec_spec_tokens", C.c_int, [P, U32, U32, P]),
     ("ulspec_spec_last_step", C.c_int, [P, P, P, P, P, P, P]),
+    ("ulspec_spec_create_batch", C.c_int, [P, P, U32, C.POINTER(Sampling), C.c_uint64, U32, C.POINTER(P)]),
+    ("ulspec_spec_prefill_batch", C.c_int, [P, P, P]),
+    ("ulspec_spec_seq_state", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    ("ulspec_spec_seq_tokens", C.c_int, [P, U32, U32, U32, P]),
     ("ulspec_spec_set_graph", C.c_int, [P, C.c_int]),
     ("ulspec_gguf_open", C.c_int, [C.c_char_p, C.POINTER(P), C.c_char_p, C.c_size_t]),
     ("ulspec_gguf_close", None, [P]),
@@ -317,11 +324,13 @@ class Model:
     """ulspec_model: a Llama-shaped target or draft model on one context."""
 
     def __init__(self, ctx, dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps=1e-5,
-                 rope_base=10000.0):
+                 rope_base=10000.0, n_seq=1):
+        """n_seq > 1: that many sequence slots (K/V caches) for a batch loop."""
         self.ctx = ctx
+        self.n_seq = n_seq
         self.cfg = ModelCfg(dim, n_layers, n_heads, n_kv_heads, ffn, vocab, max_ctx, rms_eps, rope_base)
         h = P()
-        ctx._check(lib().ulspec_model_create(ctx.handle, C.byref(self.cfg), C.byref(h)))
+        ctx._check(lib().ulspec_model_create_batch(ctx.handle, C.byref(self.cfg), n_seq, C.byref(h)))
         self.handle = h.value
 
     def close(self):
@@ -338,11 +347,11 @@ class Model:
             ptr, nbytes, dev = data.ctypes.data, data.nbytes, 0
         self.ctx._check(lib().ulspec_model_set_tensor(self.handle, name.encode(), wtype, ptr, nbytes, ne0, ne1, dev))
 
-    def forward(self, tokens, pos, n_logits=0):
+    def forward(self, tokens, pos, n_logits=0, seq=0):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         out = np.empty((n_logits, self.cfg.vocab), np.float32) if n_logits else None
-        self.ctx._check(lib().ulspec_model_forward(self.handle, tokens.ctypes.data_as(P), len(tokens), pos,
-                                                   out.ctypes.data_as(P) if out is not None else None, n_logits))
+        self.ctx._check(lib().ulspec_model_forward_seq(self.handle, seq, tokens.ctypes.data_as(P), len(tokens), pos,
+                                                       out.ctypes.data_as(P) if out is not None else None, n_logits))
         return out
 
     def forward_tree(self, tokens, parent, pos):
@@ -359,7 +368,7 @@ class Model:
         """Keep the accepted path's K/V rows (path, n_accepted: device buffers)."""
         self.ctx._check(lib().ulspec_model_kv_compact(self.handle, pos, _ptr(path), _ptr(n_accepted), n_max))
 
-    def kv_io(self, layer, dir, pos0, n, k=None, v=None):
+    def kv_io(self, layer, dir, pos0, n, k=None, v=None, seq=0):
         row = self.cfg.n_kv_heads * (self.cfg.dim // self.cfg.n_heads)
         if dir == 0:
             k = np.empty((n, row), np.uint16)
@@ -367,8 +376,8 @@ class Model:
         else:
             k = np.ascontiguousarray(k, dtype=np.uint16)
             v = np.ascontiguousarray(v, dtype=np.uint16)
-        self.ctx._check(lib().ulspec_model_kv_io(self.handle, layer, dir, pos0, n, k.ctypes.data_as(P),
-                                                 v.ctypes.data_as(P)))
+        self.ctx._check(lib().ulspec_model_kv_io_seq(self.handle, seq, layer, dir, pos0, n, k.ctypes.data_as(P),
+                                                     v.ctypes.data_as(P)))
         return k, v
 
 
@@ -504,12 +513,13 @@ class Speculative:
     """ulspec_spec: the device speculative-decoding loop over a target and a
     draft model; k = 0 (draft None) decodes with the target alone."""
 
-    def __init__(self, target, draft, k, s, seed):
+    def __init__(self, target, draft, k, s, seed, n_seq=1):
+        """n_seq > 1: a batch of that many sequences (models with as many slots)."""
         self.ctx = target.ctx
-        self.target, self.draft, self.k = target, draft, k
+        self.target, self.draft, self.k, self.n_seq = target, draft, k, n_seq
         h = P()
-        self.ctx._check(lib().ulspec_spec_create(target.handle, draft.handle if draft is not None else None, k,
-                                                 C.byref(s), seed, C.byref(h)))
+        self.ctx._check(lib().ulspec_spec_create_batch(target.handle, draft.handle if draft is not None else None, k,
+                                                       C.byref(s), seed, n_seq, C.byref(h)))
         self.handle = h.value
 
     def close(self):
@@ -518,8 +528,14 @@ class Speculative:
             self.handle = None
 
     def prefill(self, prompt):
-        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
-        self.ctx._check(lib().ulspec_spec_prefill(self.handle, prompt.ctypes.data_as(P), len(prompt)))
+        """One prompt, or a list of n_seq prompts for a batch."""
+        if self.n_seq == 1 and not isinstance(prompt, (list, tuple)):
+            prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+            self.ctx._check(lib().ulspec_spec_prefill(self.handle, prompt.ctypes.data_as(P), len(prompt)))
+            return
+        lens = np.array([len(p) for p in prompt], np.uint32)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompt]), dtype=np.int32)
+        self.ctx._check(lib().ulspec_spec_prefill_batch(self.handle, flat.ctypes.data_as(P), lens.ctypes.data_as(P)))
 
     def steps(self, n):
         self.ctx._check(lib().ulspec_spec_steps(self.handle, n))
@@ -535,21 +551,29 @@ class Speculative:
                                                 C.byref(prop)))
         return {"n": n.value, "steps": steps.value, "accepted": acc.value, "proposed": prop.value}
 
-    def tokens(self, start=0, n=None):
+    def seq_state(self, seq):
+        n, acc, prop = U32(), C.c_uint64(), C.c_uint64()
+        self.ctx._check(lib().ulspec_spec_seq_state(self.handle, seq, C.byref(n), C.byref(acc), C.byref(prop)))
+        return {"n": n.value, "accepted": acc.value, "proposed": prop.value}
+
+    def tokens(self, start=0, n=None, seq=0):
         if n is None:
-            n = self.state()["n"] - start
+            n = self.seq_state(seq)["n"] - start
         out = np.empty(n, np.int32)
-        self.ctx._check(lib().ulspec_spec_tokens(self.handle, start, n, out.ctypes.data_as(P)))
+        self.ctx._check(lib().ulspec_spec_seq_tokens(self.handle, seq, start, n, out.ctypes.data_as(P)))
         return out
 
     def last_step(self):
-        """Inputs and outputs of the last step (host copies)."""
-        k, V = self.k, self.target.cfg.vocab
-        r = {"target_logits": np.empty((k + 1, V), np.float32), "draft_logits": np.empty((k, V), np.float32),
-             "draft_tokens": np.empty(k, np.int32), "uniforms": np.empty(2 * k + 1, np.float32),
-             "out_tokens": np.empty(k + 1, np.int32), "n_accepted": np.empty(1, np.int32)}
+        """Inputs and outputs of the last step (host copies); for a batch, every
+        array has a leading sequence axis and n_accepted is an array."""
+        k, V, B = self.k, self.target.cfg.vocab, self.n_seq
+        r = {"target_logits": np.empty((B, k + 1, V), np.float32), "draft_logits": np.empty((B, k, V), np.float32),
+             "draft_tokens": np.empty((B, k), np.int32), "uniforms": np.empty((B, 2 * k + 1), np.float32),
+             "out_tokens": np.empty((B, k + 1), np.int32), "n_accepted": np.empty(B, np.int32)}
         self.ctx._check(lib().ulspec_spec_last_step(self.handle, *[a.ctypes.data_as(P) for a in r.values()]))
-        r["n_accepted"] = int(r["n_accepted"][0])
+        if B == 1:
+            r = {name: a[0] for name, a in r.items()}
+            r["n_accepted"] = int(r["n_accepted"])
         return r
 
     def set_graph(self, use_graph):

@@ -42,13 +42,16 @@ constexpr int kAttnWaves = 4;
 constexpr int kMaxQ = 16;
 constexpr int kAttnMaxSplits = 64;
 
+// nseq sequences (grid z), each with its own queries, cache and prefix.
 struct AttnArgs {
-    const _Float16* q;  // [nq][H][D]
-    const _Float16* k;  // [L][Hkv][D]
+    const _Float16* q;  // [nseq][nq][H][D]
+    const _Float16* k;  // [nseq][kv_seq / (Hkv D)][Hkv][D]: sequence b's cache from k + b kv_seq
     const _Float16* v;
-    void* out;          // [nq][H][D]: fp32, fp16 (out_mode 1) or split fp16 [2][nq][H][D] (2)
-    float* part;        // [H][splits][nq][D + 2]: O (unnormalised), m, l
-    const int32_t* dyn_prefix;  // if set, n_prefix = *dyn_prefix + prefix_add (read on the device)
+    void* out;          // [nseq nq][H][D]: fp32, fp16 (out_mode 1) or split fp16 [2][nseq nq][H][D] (2)
+    float* part;        // [nseq][H][splits][nq][D + 2]: O (unnormalised), m, l
+    const int32_t* dyn_prefix;  // if set, n_prefix of sequence b = dyn_prefix[b] + prefix_add (read on the device)
+    size_t kv_seq;      // elements between two sequences' caches
+    int nseq;
     int prefix_add;
     int n_prefix, nq, L, H, Hkv, splits, keys_per_split;
     float scale_log2;   // scale * log2(e)
@@ -65,7 +68,7 @@ __device__ __forceinline__ void store_out(const AttnArgs& a, size_t i, float v)
         _Float16 hi, lo;
         split_hl(v, hi, lo);
         ((_Float16*)a.out)[i] = hi;
-        ((_Float16*)a.out)[(size_t)a.nq * a.H * D + i] = lo;
+        ((_Float16*)a.out)[(size_t)a.nseq * a.nq * a.H * D + i] = lo;
     } else {
         ((float*)a.out)[i] = v;
     }
@@ -73,11 +76,11 @@ __device__ __forceinline__ void store_out(const AttnArgs& a, size_t i, float v)
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Prefix length and total keys of this call (the split plan covers a.L keys;
-// a device-side prefix may make the actual length shorter).
-__device__ __forceinline__ void attn_len(const AttnArgs& a, int& n_prefix, int& L)
+// Prefix length and total keys of sequence b (the split plan covers a.L
+// keys; a device-side prefix may make the actual length shorter).
+__device__ __forceinline__ void attn_len(const AttnArgs& a, int b, int& n_prefix, int& L)
 {
-    n_prefix = a.dyn_prefix ? *a.dyn_prefix + a.prefix_add : a.n_prefix;
+    n_prefix = a.dyn_prefix ? a.dyn_prefix[b] + a.prefix_add : a.n_prefix;
     L = n_prefix + a.nq;
 }
 
@@ -89,14 +92,17 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
     __shared__ float red_o[kAttnWaves][kMaxQ][D + 1];  // odd pitch: the MFMA-layout writes spread over banks
     __shared__ float red_m[kAttnWaves][kMaxQ], red_l[kAttnWaves][kMaxQ];
 
-    const int h = blockIdx.x, s = blockIdx.y;
+    const int h = blockIdx.x, s = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;  // c: query (S^T, O^T columns) / key / d column
     const int hk = h / (a.H / a.Hkv);
     const size_t row_stride = (size_t)a.Hkv * D;
+    const _Float16* qs = a.q + (size_t)b * a.nq * a.H * D;
+    const _Float16* ks = a.k + (size_t)b * a.kv_seq;
+    const _Float16* vs = a.v + (size_t)b * a.kv_seq;
 
     int n_prefix, L;
-    attn_len(a, n_prefix, L);
+    attn_len(a, b, n_prefix, L);
     const int j0 = s * a.keys_per_split;
     if (j0 >= L) return;  // only when the prefix is read on the device
     const int j1 = min(L, j0 + a.keys_per_split);
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
     const bool qvalid = c < a.nq;
 #pragma unroll
     for (int st = 0; st < D / 32; ++st)
-        qb[st] = qvalid ? *(const half8_t*)(a.q + ((size_t)c * a.H + h) * D + 32 * st + 8 * g) : half8_t{};
+        qb[st] = qvalid ? *(const half8_t*)(qs + ((size_t)c * a.H + h) * D + 32 * st + 8 * g) : half8_t{};
     uint32_t mask = 0;
 #pragma unroll
     for (int i = 0; i < kMaxQ; ++i)
@@ -128,8 +134,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
             const size_t kbase = (size_t)(key < j1 ? key : j0) * row_stride + (size_t)hk * D + 8 * g;
 #pragma unroll
             for (int st = 0; st < D / 32; ++st) {
-                ka[i][st] = *(const half8_t*)(a.k + kbase + 32 * st);
-                va[i][st] = *(const half8_t*)(a.v + kbase + 32 * st);
+                ka[i][st] = *(const half8_t*)(ks + kbase + 32 * st);
+                va[i][st] = *(const half8_t*)(vs + kbase + 32 * st);
             }
         }
         asm volatile("" ::: "memory");  // keep every load of the round ahead of the first use
@@ -214,7 +220,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
         red_l[wave][c] = l;
     }
     __syncthreads();
-    float* pp = a.part + ((size_t)h * a.splits + s) * a.nq * (D + 2);
+    float* pp = a.part + (((size_t)b * a.H + h) * a.splits + s) * a.nq * (D + 2);
     // the nq * D outputs only, d fastest (coalesced stores, conflict-free reads)
     for (int idx = threadIdx.x; idx < a.nq * D; idx += kAttnWaves * 64) {
         const int qi = idx / D, d = idx - qi * D;
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
             Lw += red_l[w][qi] * f;
         }
         if (a.splits == 1) {
-            store_out<D>(a, ((size_t)qi * a.H + h) * D + d, o / Lw);
+            store_out<D>(a, (((size_t)b * a.nq + qi) * a.H + h) * D + d, o / Lw);
         } else {
             pp[qi * (D + 2) + d] = o;
             if (d == 0) {
@@ -253,17 +259,17 @@ template <int D>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
 {
     __shared__ float sm[kAttnMaxSplits], sl[kAttnMaxSplits];
-    const int h = blockIdx.x, qi = blockIdx.y, d = threadIdx.x;
+    const int h = blockIdx.x, qi = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
     const int S = a.splits;
     const size_t stride = (size_t)a.nq * (D + 2);
-    const float* q0 = a.part + (size_t)h * S * stride + qi * (D + 2);
+    const float* q0 = a.part + ((size_t)b * a.H + h) * S * stride + qi * (D + 2);
     float first[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) first[u] = q0[min(u, S - 1) * stride + d];
     const int ds = min(d, S - 1);
     const float mv = q0[ds * stride + D], lv = q0[ds * stride + D + 1];
     int n_prefix, L;
-    attn_len(a, n_prefix, L);
+    attn_len(a, b, n_prefix, L);
     const int ns = min(S, (L + a.keys_per_split - 1) / a.keys_per_split);
     if (d < S) {
         sm[d] = mv;
@@ -286,19 +292,19 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
                 Ls += sl[s0 + u] * f;
             }
     }
-    store_out<D>(a, ((size_t)qi * a.H + h) * D + d, o / Ls);
+    store_out<D>(a, (((size_t)b * a.nq + qi) * a.H + h) * D + d, o / Ls);
 }
 
 template <int D>
 void launch_attn(const AttnArgs& a, int T, hipStream_t st)
 {
-    const dim3 grid(a.H, a.splits), block(kAttnWaves * 64);
+    const dim3 grid(a.H, a.splits, a.nseq), block(kAttnWaves * 64);
     switch (T) {
     case 1: hipLaunchKernelGGL((attn_kernel<D, 1>), grid, block, 0, st, a); break;
     case 2: hipLaunchKernelGGL((attn_kernel<D, 2>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((attn_kernel<D, 4>), grid, block, 0, st, a); break;
     }
-    if (a.splits > 1) hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.H, a.nq), dim3(D), 0, st, a);
+    if (a.splits > 1) hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.H, a.nq, a.nseq), dim3(D), 0, st, a);
 }
 
 }  // namespace
@@ -323,9 +329,9 @@ int attn_tiles(int kps)
     return kps % 256 == 0 ? 4 : (kps % 128 == 0 ? 2 : 1);
 }
 
-size_t attn_workspace_bytes(int splits, int H, int nq, int D)
+size_t attn_workspace_bytes(int splits, int H, int nq, int D, int nseq)
 {
-    return splits > 1 ? (size_t)splits * H * nq * (D + 2) * sizeof(float) : 0;
+    return splits > 1 ? (size_t)nseq * splits * H * nq * (D + 2) * sizeof(float) : 0;
 }
 
 }  // namespace ulspec
@@ -349,6 +355,8 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
     a.out_mode = c.out_split ? 2 : c.out_f16 ? 1 : 0;
     a.dyn_prefix = c.dyn_prefix;
     a.prefix_add = c.prefix_add;
+    a.nseq = (int)c.nseq;
+    a.kv_seq = c.kv_seq;
     a.n_prefix = (int)c.n_prefix;  // with dyn_prefix: the largest prefix the call may see
     a.nq = (int)c.nq;
     a.L = (int)(c.n_prefix + c.nq);
@@ -368,10 +376,12 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
         }
         a.mask[i] = mk;
     }
-    attn_plan(a.L, a.H, ctx->n_cu, a.splits, a.keys_per_split);
+    if (c.nseq < 1 || c.nseq > (uint32_t)kMaxSeqs || (c.nseq > 1 && !c.dyn_prefix))
+        return fail(ctx, ULSPEC_EINVAL, "verify_attention: %u sequences (1..%d, device prefixes)", c.nseq, kMaxSeqs);
+    attn_plan(a.L, a.H * a.nseq, ctx->n_cu, a.splits, a.keys_per_split);
     if (c.dyn_prefix && a.splits == 1) a.splits = 2;  // keep the merge: a split may return early
     void* ws = c.part;
-    const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D);
+    const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D, a.nseq);
     if (wsb && !ws) {
         ulspec_status st = workspace(ctx, wsb, &ws);
         if (st != ULSPEC_OK) return st;

@@ -156,11 +156,18 @@ bool ulspec_model::complete() const
 }
 
 ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
-                                    float* logits_dev, uint32_t n_logits, const int32_t* parent)
+                                    float* logits_dev, uint32_t n_logits, const int32_t* parent, uint32_t nseq,
+                                    uint32_t seq0)
 {
     const ulspec_model_cfg& c = cfg;
     const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, D = head_dim;
-    if (M == 0 || M > rows_max || n_logits > M) return fail(ctx, ULSPEC_EINVAL, "forward: %u rows (max %u)", M, rows_max);
+    if (nseq == 0 || nseq > (uint32_t)kMaxSeqs || seq0 + nseq > n_seq || M % nseq || (parent && nseq > 1))
+        return fail(ctx, ULSPEC_EINVAL, "forward: %u sequences from slot %u (of %u), M=%u", nseq, seq0, n_seq, M);
+    const uint32_t r = M / nseq;  // rows per sequence
+    if (M == 0 || r > rows_max || M > rows_cap || n_logits > r)
+        return fail(ctx, ULSPEC_EINVAL, "forward: %u rows of %u sequences (max %u each, %u in all)", M, nseq, rows_max,
+                    rows_cap);
+    const size_t kv_seq = (size_t)c.max_ctx * Hkv * D;
     uint64_t depth_bits = 0;  // 4-bit depth of each tree row (depth <= M - 1 <= 15)
     if (parent) {
         uint32_t depth[kRows];
@@ -196,6 +203,11 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         q.epi = kEpiRope;
         q.pos_dev = pos_dev;
         q.pos_add = pos_add;
+        q.nseq = (int)nseq;
+        q.seq_rows = (int)r;
+        q.seq0 = (int)seq0;
+        q.seq_slots = c.max_ctx;
+        q.rope_rows = c.max_ctx;
         q.tree = parent != nullptr;
         q.row_depth = depth_bits;
         q.rope = rope;
@@ -209,10 +221,12 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         if (s != ULSPEC_OK) break;
         AttnCall a;
         a.q = (const uint16_t*)q16;
-        a.k_cache = (const uint16_t*)L.kc;
-        a.v_cache = (const uint16_t*)L.vc;
-        a.n_prefix = c.max_ctx - M;
-        a.nq = M;
+        a.k_cache = (const uint16_t*)(L.kc + seq0 * kv_seq);
+        a.v_cache = (const uint16_t*)(L.vc + seq0 * kv_seq);
+        a.n_prefix = c.max_ctx - r;
+        a.nq = r;
+        a.nseq = nseq;
+        a.kv_seq = kv_seq;
         a.parent = parent;
         a.H = H;
         a.Hkv = Hkv;
@@ -252,12 +266,20 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         P = (int)W[L.wdown].n_tiles;
     }
     if (s != ULSPEC_OK) return s;
-    if (n_logits) {
-        // the last n_logits rows: their high parts from row M - n_logits, low parts M rows below
+    if (n_logits && (nseq == 1 || n_logits == r)) {
+        // the last n_logits rows (every row of every sequence when n_logits = r):
+        // their high parts from row M - nseq n_logits, low parts M rows below
+        const uint32_t nl = nseq * n_logits;
         GemmFuse z = fuse();
-        normed(z, pss + (size_t)(M - n_logits) * P, P);
-        s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)(xn + (size_t)(M - n_logits) * c.dim), n_logits, M,
-                       logits_dev);
+        normed(z, pss + (size_t)(M - nl) * P, P);
+        s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)(xn + (size_t)(M - nl) * c.dim), nl, M, logits_dev);
+    } else if (n_logits) {
+        // the last n_logits rows of each sequence, gathered first
+        const uint32_t nl = nseq * n_logits;
+        launch_gather_rows(ctx->stream, xn, pss, M, c.dim, (uint32_t)P, r, n_logits, nseq, xg, pg);
+        GemmFuse z = fuse();
+        normed(z, pg, P);
+        s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)xg, nl, nl, logits_dev);
     }
     if (s != ULSPEC_OK) return s;
     return check_launch(ctx, "model forward launch");
@@ -265,8 +287,16 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
 
 extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, ulspec_model** out)
 {
+    return ulspec_model_create_batch(ctx, cfg, 1, out);
+}
+
+extern "C" ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec_model_cfg* cfg, uint32_t n_seq,
+                                                   ulspec_model** out)
+{
     ULSPEC_CHECK_CTX(ctx);
     if (!cfg || !out) return fail(ctx, ULSPEC_EINVAL, "model_create: null pointer");
+    if (n_seq == 0 || n_seq > (uint32_t)kMaxSeqs)
+        return fail(ctx, ULSPEC_EINVAL, "model_create: %u sequences (1 .. %d)", n_seq, kMaxSeqs);
     const ulspec_model_cfg& c = *cfg;
     if (c.n_heads == 0 || c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads || c.dim % c.n_heads)
         return fail(ctx, ULSPEC_EINVAL, "model_create: dim=%u heads=%u kv_heads=%u", c.dim, c.n_heads, c.n_kv_heads);
@@ -280,13 +310,18 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
     if (!(c.rms_eps > 0.0f) || !(c.rope_base > 1.0f) || !std::isfinite(c.rope_base))
         return fail(ctx, ULSPEC_EINVAL, "model_create: rms_eps / rope_base");
     (void)hipSetDevice(ctx->device);
-    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn, R = ulspec_model::kRows;
+    const uint32_t H = c.n_heads, Hkv = c.n_kv_heads, F = c.ffn;
+    // rows of one forward: 16 for one sequence, 6 per sequence (k + 1 <= 6) up to 48 for a batch
+    const uint32_t R = n_seq == 1 ? ulspec_model::kRows
+                                  : std::max(ulspec_model::kRows, std::min(ulspec_model::kBatchRows, 6 * n_seq));
     ulspec_model* m = new ulspec_model;
     m->ctx = ctx;
     m->cfg = c;
     m->head_dim = D;
     m->layers.resize(c.n_layers);
-    m->rows_max = R;
+    m->rows_max = ulspec_model::kRows;
+    m->rows_cap = R;
+    m->n_seq = n_seq;
     // slice partials of the split-K path: the most any of the model's weights
     // needs at R rows (slices are chosen at upload from the tile and chunk
     // counts; ceil(K / 128) bounds the chunks of every weight type)
@@ -299,7 +334,7 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         }
     }
     m->pss_stride = std::max(embed_partials(c.dim), (c.dim + 15) / 16);
-    const size_t kv_bytes = (size_t)c.max_ctx * Hkv * D * sizeof(_Float16);
+    const size_t kv_bytes = (size_t)n_seq * c.max_ctx * Hkv * D * sizeof(_Float16);
     int splits = 0, kps = 0;
     attn_plan((int)c.max_ctx, (int)H, ctx->n_cu, splits, kps);
     if (splits < 2) splits = 2;
@@ -316,10 +351,12 @@ extern "C" ulspec_status ulspec_model_create(ulspec_ctx* ctx, const ulspec_model
         {(void**)&m->xn, (size_t)2 * R * c.dim * 2},
         {(void**)&m->part, m->part_bytes},
         {(void**)&m->tok, (size_t)R * 4},
-        {(void**)&m->pos, 16},
+        {(void**)&m->pos, 4 * kMaxSeqs},
         {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},
         {(void**)&m->rope, (size_t)c.max_ctx * (D / 2) * sizeof(float2)},
         {(void**)&m->kv_tab, (size_t)2 * c.n_layers * sizeof(_Float16*)},
+        {(void**)&m->xg, (size_t)2 * R * c.dim * 2},
+        {(void**)&m->pg, (size_t)R * m->pss_stride * 4},
     };
     ulspec_status st = ULSPEC_OK;
     for (const Want& w : wants)
@@ -511,7 +548,21 @@ extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* to
                                               float* logits, uint32_t n_logits)
 {
     if (!m) return ULSPEC_EINVAL;
-    ulspec_ctx* ctx = m->ctx;
+    return m->forward_host(tokens, M, pos, logits, n_logits, 0);
+}
+
+extern "C" ulspec_status ulspec_model_forward_seq(ulspec_model* m, uint32_t seq, const int32_t* tokens, uint32_t M,
+                                                  uint32_t pos, float* logits, uint32_t n_logits)
+{
+    if (!m) return ULSPEC_EINVAL;
+    if (seq >= m->n_seq) return fail(m->ctx, ULSPEC_EINVAL, "model_forward_seq: sequence %u of %u", seq, m->n_seq);
+    return m->forward_host(tokens, M, pos, logits, n_logits, seq);
+}
+
+ulspec_status ulspec_model::forward_host(const int32_t* tokens, uint32_t M, uint32_t pos, float* logits,
+                                         uint32_t n_logits, uint32_t seq)
+{
+    ulspec_model* m = this;
     if (!tokens || M == 0) return fail(ctx, ULSPEC_EINVAL, "model_forward: no tokens");
     if (n_logits > m->rows_max || n_logits > M || (n_logits && !logits))
         return fail(ctx, ULSPEC_EINVAL, "model_forward: n_logits=%u (<= %u and <= M, with an output)", n_logits,
@@ -533,7 +584,7 @@ extern "C" ulspec_status ulspec_model_forward(ulspec_model* m, const int32_t* to
         hipError_t e = hipMemcpyAsync(m->tok, tokens + m0, mc * sizeof(int32_t), hipMemcpyHostToDevice, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "model_forward tokens");
         launch_set_i32(ctx->stream, m->pos, (int32_t)(pos + m0));
-        ulspec_status st = m->forward(m->tok, mc, m->pos, 0, m->logits, final_chunk ? n_logits : 0);
+        ulspec_status st = m->forward(m->tok, mc, m->pos, 0, m->logits, final_chunk ? n_logits : 0, nullptr, 1, seq);
         if (st != ULSPEC_OK) return st;
         if (final_chunk) break;
         m0 += mc;
@@ -597,15 +648,23 @@ extern "C" ulspec_status ulspec_model_kv_compact(ulspec_model* m, uint32_t pos, 
 extern "C" ulspec_status ulspec_model_kv_io(ulspec_model* m, uint32_t layer, int dir, uint32_t pos0, uint32_t n,
                                             uint16_t* k, uint16_t* v)
 {
+    return ulspec_model_kv_io_seq(m, 0, layer, dir, pos0, n, k, v);
+}
+
+extern "C" ulspec_status ulspec_model_kv_io_seq(ulspec_model* m, uint32_t seq, uint32_t layer, int dir, uint32_t pos0,
+                                                uint32_t n, uint16_t* k, uint16_t* v)
+{
     if (!m) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = m->ctx;
-    if (layer >= m->cfg.n_layers || (uint64_t)pos0 + n > m->cfg.max_ctx || (dir != 0 && dir != 1) || (n && (!k || !v)))
-        return fail(ctx, ULSPEC_EINVAL, "model_kv_io: layer %u rows %u+%u dir %d", layer, pos0, n, dir);
+    if (seq >= m->n_seq || layer >= m->cfg.n_layers || (uint64_t)pos0 + n > m->cfg.max_ctx || (dir != 0 && dir != 1) ||
+        (n && (!k || !v)))
+        return fail(ctx, ULSPEC_EINVAL, "model_kv_io: sequence %u layer %u rows %u+%u dir %d", seq, layer, pos0, n, dir);
     (void)hipSetDevice(ctx->device);
     const size_t row = (size_t)m->cfg.n_kv_heads * m->head_dim;
     const size_t bytes = (size_t)n * row * sizeof(uint16_t);
-    _Float16* kc = m->layers[layer].kc + (size_t)pos0 * row;
-    _Float16* vc = m->layers[layer].vc + (size_t)pos0 * row;
+    const size_t base = ((size_t)seq * m->cfg.max_ctx + pos0) * row;
+    _Float16* kc = m->layers[layer].kc + base;
+    _Float16* vc = m->layers[layer].vc + base;
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e == hipSuccess && bytes) {
         if (dir == 0) {

@@ -26,7 +26,7 @@ struct ulspec_model {
         uint32_t wqkv = ~0u, wo = ~0u, wgu = ~0u, wdown = ~0u;  // context weight ids
         float* attn_norm = nullptr;
         float* ffn_norm = nullptr;
-        _Float16* kc = nullptr;  // [max_ctx][Hkv][D]
+        _Float16* kc = nullptr;  // [n_seq][max_ctx][Hkv][D]
         _Float16* vc = nullptr;
     };
 
@@ -42,11 +42,15 @@ struct ulspec_model {
     uint32_t w_out = ~0u;
     float2* rope = nullptr;    // [max_ctx][head_dim / 2] (cos, sin)
 
-    // activations, up to kRows rows per forward.  GEMM inputs are fp32
-    // activations held as split fp16 pairs [2 rows][width] (high parts, then
-    // low parts): the attention output and SiLU(gate) * up.
+    // activations, up to rows_cap rows per forward (kRows per sequence;
+    // n_seq sequence slots, each with its own K / V cache).  GEMM inputs are
+    // fp32 activations held as split fp16 pairs [2 rows][width] (high parts,
+    // then low parts): the attention output and SiLU(gate) * up.
     static constexpr uint32_t kRows = 16;
-    uint32_t rows_max = 0;
+    static constexpr uint32_t kBatchRows = 48;  // rows of a batched forward (8 sequences x 6)
+    uint32_t rows_max = 0;     // rows of one sequence per forward
+    uint32_t rows_cap = 0;     // rows of all sequences of one forward
+    uint32_t n_seq = 1;
     float* h = nullptr;        // [kRows][dim] residual stream (fp32)
     float* pss = nullptr;      // [kRows][pss_stride] RMSNorm partial sums of h^2
     uint32_t pss_stride = 0;
@@ -60,18 +64,27 @@ struct ulspec_model {
     int32_t* tok = nullptr;    // [kRows]
     int32_t* pos = nullptr;    // [1]
     float* attn_part = nullptr;
+    _Float16* xg = nullptr;    // split [2 rows_cap][dim]: the LM head's rows gathered from xn
+    float* pg = nullptr;       // [rows_cap][pss_stride]: their row-scale partials
     _Float16** kv_tab = nullptr;  // device [2][n_layers]: every layer's K cache, then every V cache
     std::vector<void*> allocs;
 
     bool complete() const;
-    // Forward M <= rows_max tokens read from device memory at positions
-    // *pos_dev + pos_add ...; logits of the last n_logits rows to `logits`
-    // (device).  With `parent` (host [M], parent[i] in [-1, i)) the rows are
-    // a tree: row i keeps its K/V slot (pos + i) but takes RoPE position pos +
-    // depth(i) and attends to the prefix and its ancestors only.
-    // Asynchronous, never allocates or synchronises.
+    // Forward M tokens read from device memory: nseq groups of r = M / nseq
+    // <= rows_max rows, group b on sequence slot seq0 + b at positions
+    // pos_dev[b] + pos_add ... (pos_dev: nseq device ints); logits of the
+    // last n_logits rows of every group to `logits` (device, [nseq][n_logits]
+    // [vocab]).  With `parent` (host [M], parent[i] in [-1, i); one sequence)
+    // the rows are a tree: row i keeps its K/V slot (pos + i) but takes RoPE
+    // position pos + depth(i) and attends to the prefix and its ancestors
+    // only.  Asynchronous, never allocates or synchronises.
     ulspec_status forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
-                          float* logits_dev, uint32_t n_logits, const int32_t* parent = nullptr);
+                          float* logits_dev, uint32_t n_logits, const int32_t* parent = nullptr, uint32_t nseq = 1,
+                          uint32_t seq0 = 0);
+    // Host tokens on sequence slot seq (chunks of rows_max rows), logits of the
+    // last n_logits rows to host memory.  Synchronous.
+    ulspec_status forward_host(const int32_t* tokens, uint32_t M, uint32_t pos, float* logits, uint32_t n_logits,
+                               uint32_t seq);
 };
 
 namespace ulspec {

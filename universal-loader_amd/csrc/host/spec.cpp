@@ -37,56 +37,99 @@ struct SpecState {
     uint64_t proposed;  // proposed draft tokens
 };
 
-__global__ void spec_begin_kernel(const SpecState* __restrict__ st, const int32_t* __restrict__ seq, uint64_t seed,
-                                  uint32_t k, float* __restrict__ unif, int32_t* __restrict__ tok_d)
+// Uniforms of step s for every sequence b: counter (s B + b)(2k+1) + j, j = 0
+// .. 2k, to unif [B][2k+1]; draft draws j < k also to udraft [k][B] (one
+// contiguous row of B per draft step), the accept rule's to uacc [B][k+1].
+// The draft's catch-up pair [t_{n-2}, t_{n-1}] of each sequence to tok_d [B][2].
+__global__ void spec_begin_kernel(const int32_t* __restrict__ npos, const int32_t* __restrict__ seq, uint32_t cap,
+                                  const SpecState* __restrict__ st, uint64_t seed, uint32_t k, uint32_t B,
+                                  float* __restrict__ unif, float* __restrict__ udraft, float* __restrict__ uacc,
+                                  int32_t* __restrict__ tok_d)
 {
-    const uint32_t i = threadIdx.x;
-    const uint64_t base = st->step * (2 * k + 1);
-    if (i < 2 * k + 1) unif[i] = counter_uniform(seed, base + i);
-    if (i == 0) {
-        tok_d[0] = seq[st->n - 2];
-        tok_d[1] = seq[st->n - 1];
+    const uint32_t per = 2 * k + 1;
+    const uint64_t step = st[0].step;
+    for (uint32_t i = threadIdx.x; i < B * per; i += blockDim.x) {
+        const uint32_t b = i / per, j = i - b * per;
+        const float u = counter_uniform(seed, (step * B + b) * per + j);
+        unif[i] = u;
+        if (j < k) udraft[j * B + b] = u;
+        else uacc[b * (k + 1) + (j - k)] = u;
+    }
+    for (uint32_t b = threadIdx.x; b < B; b += blockDim.x) {
+        tok_d[2 * b] = seq[(size_t)b * cap + npos[b] - 2];
+        tok_d[2 * b + 1] = seq[(size_t)b * cap + npos[b] - 1];
     }
 }
 
-// Plain (target-only) step: the uniform of counter step (2k+1) and the last token.
-__global__ void spec_plain_begin_kernel(const SpecState* __restrict__ st, const int32_t* __restrict__ seq,
-                                        uint64_t seed, uint32_t k, float* __restrict__ unif,
+// Plain (target-only) step: the uniform of counter (s B + b)(2k+1) and the
+// last token of every sequence.
+__global__ void spec_plain_begin_kernel(const int32_t* __restrict__ npos, const int32_t* __restrict__ seq,
+                                        uint32_t cap, const SpecState* __restrict__ st, uint64_t seed, uint32_t k,
+                                        uint32_t B, float* __restrict__ unif, float* __restrict__ uplain,
                                         int32_t* __restrict__ tok_t)
 {
-    if (threadIdx.x != 0) return;
-    unif[0] = counter_uniform(seed, st->step * (2 * k + 1));
-    tok_t[0] = seq[st->n - 1];
+    const uint64_t step = st[0].step;
+    for (uint32_t b = threadIdx.x; b < B; b += blockDim.x) {
+        const float u = counter_uniform(seed, (step * B + b) * (2 * k + 1));
+        unif[b * (2 * k + 1)] = u;
+        uplain[b] = u;
+        tok_t[b] = seq[(size_t)b * cap + npos[b] - 1];
+    }
 }
 
-__global__ void spec_verify_tokens_kernel(const SpecState* __restrict__ st, const int32_t* __restrict__ seq,
-                                          const int32_t* __restrict__ dtok, uint32_t k, int32_t* __restrict__ tok_t)
+// Target rows of every sequence: [t_{n-1}, d_1 .. d_k] from dtok_s [k][B].
+__global__ void spec_verify_tokens_kernel(const int32_t* __restrict__ npos, const int32_t* __restrict__ seq,
+                                          uint32_t cap, const int32_t* __restrict__ dtok_s, uint32_t k, uint32_t B,
+                                          int32_t* __restrict__ tok_t)
 {
-    const uint32_t i = threadIdx.x;
-    if (i == 0) tok_t[0] = seq[st->n - 1];
-    else if (i <= k) tok_t[i] = dtok[i - 1];
+    for (uint32_t i = threadIdx.x; i < B * (k + 1); i += blockDim.x) {
+        const uint32_t b = i / (k + 1), j = i - b * (k + 1);
+        tok_t[i] = j == 0 ? seq[(size_t)b * cap + npos[b] - 1] : dtok_s[(j - 1) * B + b];
+    }
 }
 
-__global__ void spec_commit_kernel(SpecState* __restrict__ st, int32_t* __restrict__ seq,
-                                   const int32_t* __restrict__ out_tok, const int32_t* __restrict__ nacc, uint32_t k)
+// Draft tokens and logits from step-major [k][B] to sequence-major [B][k]
+// (the accept rule's layout); float4 groups of the V-float rows (V % 4 == 0).
+__global__ __launch_bounds__(256) void spec_gather_draft_kernel(const int32_t* __restrict__ dtok_s,
+                                                                const float4* __restrict__ dl_s, uint32_t k,
+                                                                uint32_t B, uint32_t V4, int32_t* __restrict__ dtok,
+                                                                float4* __restrict__ dl)
 {
-    if (threadIdx.x != 0) return;
-    const int32_t a = *nacc;
-    const int32_t n = st->n;
-    for (int32_t i = 0; i <= a; ++i) seq[n + i] = out_tok[i];
-    st->n = n + a + 1;
-    st->step += 1;
-    st->accepted += (uint64_t)a;
-    st->proposed += k;
+    const uint32_t row = blockIdx.y;  // sequence-major row b k + j
+    const uint32_t b = row / k, j = row - b * k;
+    const float4* src = dl_s + (size_t)(j * B + b) * V4;
+    float4* dst = dl + (size_t)row * V4;
+    for (uint32_t q = blockIdx.x * 256 + threadIdx.x; q < V4; q += gridDim.x * 256) dst[q] = src[q];
+    if (blockIdx.x == 0 && threadIdx.x == 0) dtok[row] = dtok_s[j * B + b];
 }
 
-__global__ void spec_reset_kernel(SpecState* st, int32_t n)
+// One thread per sequence: append its n_acc + 1 tokens.
+__global__ void spec_commit_kernel(SpecState* __restrict__ st, int32_t* __restrict__ npos, int32_t* __restrict__ seq,
+                                   uint32_t cap, const int32_t* __restrict__ out_tok, const int32_t* __restrict__ nacc,
+                                   uint32_t k, uint32_t kout, uint32_t B)
 {
-    st->n = n;
-    st->pad = 0;
-    st->step = 0;
-    st->accepted = 0;
-    st->proposed = 0;
+    const uint32_t b = threadIdx.x;
+    if (b >= B) return;
+    const int32_t a = nacc[b];
+    const int32_t n = npos[b];
+    for (int32_t i = 0; i <= a; ++i) seq[(size_t)b * cap + n + i] = out_tok[b * (kout + 1) + i];
+    npos[b] = n + a + 1;
+    st[b].n = n + a + 1;
+    st[b].step += 1;
+    st[b].accepted += (uint64_t)a;
+    st[b].proposed += k;
+}
+
+__global__ void spec_reset_kernel(SpecState* st, int32_t* npos, const int32_t* __restrict__ n, uint32_t B)
+{
+    const uint32_t b = threadIdx.x;
+    if (b >= B) return;
+    st[b].n = n[b];
+    st[b].pad = 0;
+    st[b].step = 0;
+    st[b].accepted = 0;
+    st[b].proposed = 0;
+    npos[b] = n[b];
 }
 
 }  // namespace
@@ -95,44 +138,53 @@ struct ulspec_spec {
     ulspec_ctx* ctx = nullptr;
     ulspec_model* t = nullptr;
     ulspec_model* d = nullptr;
-    uint32_t k = 0, V = 0, cap = 0;
+    uint32_t k = 0, V = 0, cap = 0, B = 1;
     ulspec_sampling s{};
     uint64_t seed = 0;
-    SpecState* st = nullptr;
-    int32_t* seq = nullptr;
-    int32_t* tok_d = nullptr;
-    int32_t* dtok = nullptr;
-    int32_t* tok_t = nullptr;
-    int32_t* out_tok = nullptr;
-    int32_t* nacc = nullptr;
-    int32_t* zero = nullptr;  // 0: the accepted count of a plain step
-    float* unif = nullptr;
-    float* dlogits = nullptr;  // [k][V]
-    float* tlogits = nullptr;  // [k+1][V]
+    SpecState* st = nullptr;   // [B]
+    int32_t* npos = nullptr;   // [B] committed tokens (the forwards' positions)
+    int32_t* nset = nullptr;   // [B] prefill lengths
+    int32_t* seq = nullptr;    // [B][cap]
+    int32_t* tok_d = nullptr;  // [B][2]
+    int32_t* dtok_s = nullptr; // [k][B]
+    int32_t* dtok = nullptr;   // [B][k] (== dtok_s when B = 1)
+    int32_t* tok_t = nullptr;  // [B][k+1]
+    int32_t* out_tok = nullptr;  // [B][k+1]
+    int32_t* nacc = nullptr;   // [B]
+    int32_t* zero = nullptr;   // [B] zeros: the accepted counts of a plain step
+    float* unif = nullptr;     // [B][2k+1]
+    float* udraft = nullptr;   // [max(k, 1)][B]
+    float* uacc = nullptr;     // [B][k+1]
+    float* dl_s = nullptr;     // [k][B][V] (draft logits, step-major)
+    float* dlogits = nullptr;  // [B][k][V] (== dl_s when B = 1)
+    float* tlogits = nullptr;  // [B][k+1][V]
     void* ws_accept = nullptr;
     void* ws_sample = nullptr;
-    SpecState* host_st = nullptr;  // pinned
+    SpecState* host_st = nullptr;  // pinned [B]
     std::vector<void*> allocs;
     bool prefilled = false;
     bool plain_first = false;  // one-token prompt: the next step is a plain step
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
     void* graph_ws = nullptr;       // context workspace the graph was captured with
-    uint32_t n_hi = 0;              // upper bound of the committed count
+    uint32_t n_hi = 0;              // upper bound of the longest committed count
     ulspec_status enqueue_step();
     ulspec_status launch_step();
     ulspec_status launch_plain_step();
     ulspec_status sync_state();
+    ulspec_status prefill(const int32_t* prompts, const uint32_t* lens);
 };
 
 ulspec_status ulspec_spec::launch_plain_step()
 {
     hipStream_t stream = ctx->stream;
-    hipLaunchKernelGGL(spec_plain_begin_kernel, dim3(1), dim3(64), 0, stream, st, seq, seed, k, unif, tok_t);
-    ulspec_status r = t->forward(tok_t, 1, &st->n, -1, tlogits, 1);
-    if (r == ULSPEC_OK) r = sample_launch(ctx, &s, 1, V, tlogits, unif, out_tok, ws_sample);
+    hipLaunchKernelGGL(spec_plain_begin_kernel, dim3(1), dim3(64), 0, stream, (const int32_t*)npos,
+                       (const int32_t*)seq, cap, (const SpecState*)st, seed, k, B, unif, udraft, tok_t);
+    ulspec_status r = t->forward(tok_t, B, npos, -1, tlogits, 1, nullptr, B, 0);
+    if (r == ULSPEC_OK) r = sample_launch(ctx, &s, B, V, tlogits, udraft, out_tok, ws_sample);
     if (r != ULSPEC_OK) return r;
-    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, seq, out_tok, (const int32_t*)zero, 0u);
+    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, npos, seq, cap, (const int32_t*)out_tok,
+                       (const int32_t*)zero, 0u, 0u, B);
     return check_launch(ctx, "plain step launch");
 }
 
@@ -140,21 +192,28 @@ ulspec_status ulspec_spec::launch_step()
 {
     if (k == 0) return launch_plain_step();
     hipStream_t stream = ctx->stream;
-    hipLaunchKernelGGL(spec_begin_kernel, dim3(1), dim3(64), 0, stream, st, seq, seed, k, unif, tok_d);
-    // draft: catch-up pair, then single tokens
-    ulspec_status r = d->forward(tok_d, 2, &st->n, -2, dlogits, 1);
-    if (r == ULSPEC_OK) r = sample_launch(ctx, &s, 1, V, dlogits, unif, dtok, ws_sample);
+    hipLaunchKernelGGL(spec_begin_kernel, dim3(1), dim3(256), 0, stream, (const int32_t*)npos, (const int32_t*)seq,
+                       cap, (const SpecState*)st, seed, k, B, unif, udraft, uacc, tok_d);
+    // draft: catch-up pair, then single tokens (B rows per forward, one per sequence)
+    ulspec_status r = d->forward(tok_d, 2 * B, npos, -2, dl_s, 1, nullptr, B, 0);
+    if (r == ULSPEC_OK) r = sample_launch(ctx, &s, B, V, dl_s, udraft, dtok_s, ws_sample);
     for (uint32_t j = 1; j < k && r == ULSPEC_OK; ++j) {
-        r = d->forward(dtok + j - 1, 1, &st->n, (int32_t)j - 1, dlogits + (size_t)j * V, 1);
-        if (r == ULSPEC_OK) r = sample_launch(ctx, &s, 1, V, dlogits + (size_t)j * V, unif + j, dtok + j, ws_sample);
+        r = d->forward(dtok_s + (j - 1) * B, B, npos, (int32_t)j - 1, dl_s + (size_t)j * B * V, 1, nullptr, B, 0);
+        if (r == ULSPEC_OK)
+            r = sample_launch(ctx, &s, B, V, dl_s + (size_t)j * B * V, udraft + j * B, dtok_s + j * B, ws_sample);
     }
     if (r != ULSPEC_OK) return r;
-    hipLaunchKernelGGL(spec_verify_tokens_kernel, dim3(1), dim3(32), 0, stream, st, seq, dtok, k, tok_t);
-    r = t->forward(tok_t, k + 1, &st->n, -1, tlogits, k + 1);
-    if (r == ULSPEC_OK)
-        r = accept_launch(ctx, &s, 1, k, V, tlogits, dlogits, dtok, unif + k, out_tok, nacc, ws_accept);
+    hipLaunchKernelGGL(spec_verify_tokens_kernel, dim3(1), dim3(256), 0, stream, (const int32_t*)npos,
+                       (const int32_t*)seq, cap, (const int32_t*)dtok_s, k, B, tok_t);
+    r = t->forward(tok_t, (k + 1) * B, npos, -1, tlogits, k + 1, nullptr, B, 0);
     if (r != ULSPEC_OK) return r;
-    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, seq, out_tok, nacc, k);
+    if (B > 1)
+        hipLaunchKernelGGL(spec_gather_draft_kernel, dim3((V / 4 + 255) / 256, B * k), dim3(256), 0, stream,
+                           (const int32_t*)dtok_s, (const float4*)dl_s, k, B, V / 4, dtok, (float4*)dlogits);
+    r = accept_launch(ctx, &s, B, k, V, tlogits, dlogits, dtok, uacc, out_tok, nacc, ws_accept);
+    if (r != ULSPEC_OK) return r;
+    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, npos, seq, cap, (const int32_t*)out_tok,
+                       (const int32_t*)nacc, k, k, B);
     return check_launch(ctx, "spec step launch");
 }
 
@@ -190,29 +249,79 @@ ulspec_status ulspec_spec::enqueue_step()
 
 ulspec_status ulspec_spec::sync_state()
 {
-    hipError_t e = hipMemcpyAsync(host_st, st, sizeof(SpecState), hipMemcpyDeviceToHost, ctx->stream);
+    hipError_t e = hipMemcpyAsync(host_st, st, B * sizeof(SpecState), hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "spec state sync");
-    n_hi = (uint32_t)host_st->n;
+    n_hi = 0;
+    for (uint32_t b = 0; b < B; ++b) n_hi = std::max(n_hi, (uint32_t)host_st[b].n);
     return ULSPEC_OK;
 }
 
-extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k,
-                                            const ulspec_sampling* s, uint64_t seed, ulspec_spec** out)
+// Prompts of every sequence (concatenated, lens[b] tokens each): both models
+// process tokens 0 .. n_b - 2 on the sequence's slot; counters reset.
+ulspec_status ulspec_spec::prefill(const int32_t* prompts, const uint32_t* lens)
+{
+    const uint32_t min_len = k > 0 && B > 1 ? 2 : 1;
+    size_t off = 0;
+    for (uint32_t b = 0; b < B; ++b) {
+        if (lens[b] < min_len)
+            return fail(ctx, ULSPEC_EINVAL, "spec_prefill: sequence %u has %u tokens (at least %u)", b, lens[b],
+                        min_len);
+        if ((uint64_t)lens[b] + k + 1 > cap)
+            return fail(ctx, ULSPEC_EINVAL, "spec_prefill: %u tokens leave no room", lens[b]);
+        for (uint32_t i = 0; i < lens[b]; ++i)
+            if (prompts[off + i] < 0 || (uint32_t)prompts[off + i] >= V)
+                return fail(ctx, ULSPEC_EINVAL, "spec_prefill: token %d out of range", prompts[off + i]);
+        off += lens[b];
+    }
+    (void)hipSetDevice(ctx->device);
+    if (hipMemset(nacc, 0, 4 * B) != hipSuccess) return fail(ctx, ULSPEC_EDEVICE, "spec_prefill: reset");
+    std::vector<int32_t> n(B);
+    off = 0;
+    for (uint32_t b = 0; b < B; ++b) {
+        const uint32_t nb = lens[b];
+        ulspec_status st_ = ULSPEC_OK;
+        if (nb > 1) {
+            st_ = t->forward_host(prompts + off, nb - 1, 0, nullptr, 0, b);
+            if (st_ == ULSPEC_OK && d) st_ = d->forward_host(prompts + off, nb - 1, 0, nullptr, 0, b);
+            if (st_ != ULSPEC_OK) return st_;
+        }
+        hipError_t e = hipMemcpy(seq + (size_t)b * cap, prompts + off, (size_t)nb * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_fail(ctx, e, "spec_prefill copy");
+        n[b] = (int32_t)nb;
+        off += nb;
+    }
+    hipError_t e = hipMemcpy(nset, n.data(), B * sizeof(int32_t), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(ctx, e, "spec_prefill copy");
+    hipLaunchKernelGGL(spec_reset_kernel, dim3(1), dim3(64), 0, ctx->stream, st, npos, (const int32_t*)nset, B);
+    ulspec_status r = check_launch(ctx, "spec_prefill launch");
+    if (r != ULSPEC_OK) return r;
+    prefilled = true;
+    plain_first = B == 1 && lens[0] == 1 && k > 0;
+    return sync_state();
+}
+
+static ulspec_status spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
+                                 uint64_t seed, uint32_t B, ulspec_spec** out)
 {
     if (!target || (!draft && k > 0)) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = target->ctx;
     if (k == 0) draft = nullptr;  // plain decoding of the target: no draft model
     if (draft && draft->ctx != ctx) return fail(ctx, ULSPEC_EINVAL, "spec_create: models on different contexts");
     if (!s || !out) return fail(ctx, ULSPEC_EINVAL, "spec_create: null pointer");
-    if (k > 16 || k + 1 > target->rows_max || (draft && draft->rows_max < 2))
-        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u (k <= 16, k + 1 <= %u rows of the target)", k,
-                    target->rows_max);
+    if (B == 0 || B > (uint32_t)kMaxSeqs || target->n_seq < B || (draft && draft->n_seq < B))
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: %u sequences (1 .. %d, and at most the models' slots)", B,
+                    kMaxSeqs);
+    if (k > 16 || k + 1 > target->rows_max || (k + 1) * B > target->rows_cap ||
+        (draft && (draft->rows_max < 2 || 2 * B > draft->rows_cap)))
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u for %u sequences (k <= 16, (k + 1) B <= %u target rows)", k,
+                    B, target->rows_cap);
     if (draft && target->cfg.vocab != draft->cfg.vocab)
         return fail(ctx, ULSPEC_EINVAL, "spec_create: vocabularies differ");
     if (!target->complete() || (draft && !draft->complete()))
         return fail(ctx, ULSPEC_EINVAL, "spec_create: model tensors missing");
     const uint32_t V = target->cfg.vocab;
+    if (B > 1 && V % 4) return fail(ctx, ULSPEC_EUNSUPPORTED, "spec_create: batches need a vocabulary multiple of 4");
     // the sampling parameters are validated by a dry check of the accept rule's limits
     if (!s->greedy) {
         if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
@@ -227,40 +336,52 @@ extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* 
     sp->d = draft;
     sp->k = k;
     sp->V = V;
+    sp->B = B;
     sp->s = *s;
     sp->seed = seed;
     sp->cap = draft ? std::min(target->cfg.max_ctx, draft->cfg.max_ctx) : target->cfg.max_ctx;
+    const size_t kk = std::max<uint32_t>(k, 1);
     struct Want {
         void** p;
         size_t bytes;
     } wants[] = {
-        {(void**)&sp->st, sizeof(SpecState)},
-        {(void**)&sp->seq, (size_t)sp->cap * 4},
-        {(void**)&sp->tok_d, 16},
-        {(void**)&sp->dtok, 64},
-        {(void**)&sp->tok_t, 64},
-        {(void**)&sp->out_tok, 64},
-        {(void**)&sp->nacc, 16},
-        {(void**)&sp->zero, 16},
-        {(void**)&sp->unif, 4 * (2 * 16 + 1)},
-        {(void**)&sp->dlogits, (size_t)k * V * 4},
-        {(void**)&sp->tlogits, (size_t)(k + 1) * V * 4},
-        {(void**)&sp->ws_accept, k ? accept_workspace_bytes(1, k) : 0},
-        {(void**)&sp->ws_sample, sample_workspace_bytes(1)},
+        {(void**)&sp->st, B * sizeof(SpecState)},
+        {(void**)&sp->npos, 4 * B},
+        {(void**)&sp->nset, 4 * B},
+        {(void**)&sp->seq, (size_t)B * sp->cap * 4},
+        {(void**)&sp->tok_d, 8 * B},
+        {(void**)&sp->dtok_s, 4 * kk * B},
+        {(void**)&sp->dtok, B > 1 ? 4 * kk * B : 0},
+        {(void**)&sp->tok_t, 4 * (size_t)(k + 1) * B},
+        {(void**)&sp->out_tok, 4 * (size_t)(k + 1) * B},
+        {(void**)&sp->nacc, 4 * B},
+        {(void**)&sp->zero, 4 * B},
+        {(void**)&sp->unif, 4 * (size_t)(2 * k + 1) * B},
+        {(void**)&sp->udraft, 4 * kk * B},
+        {(void**)&sp->uacc, 4 * (size_t)(k + 1) * B},
+        {(void**)&sp->dl_s, (size_t)k * B * V * 4},
+        {(void**)&sp->dlogits, B > 1 ? (size_t)k * B * V * 4 : 0},
+        {(void**)&sp->tlogits, (size_t)(k + 1) * B * V * 4},
+        {(void**)&sp->ws_accept, k ? accept_workspace_bytes(B, k) : 0},
+        {(void**)&sp->ws_sample, sample_workspace_bytes(B)},
     };
     ulspec_status st = ULSPEC_OK;
     for (const Want& w : wants) {
         if (st != ULSPEC_OK) break;
-        if (!w.bytes) continue;  // k = 0: no draft rows, no acceptance
+        if (!w.bytes) continue;  // k = 0: no draft rows, no acceptance; B = 1: no re-layout
         hipError_t e = hipMalloc(w.p, w.bytes);
         if (e != hipSuccess) st = hip_fail(ctx, e, "spec_create hipMalloc");
         else sp->allocs.push_back(*w.p);
     }
+    if (st == ULSPEC_OK && B == 1) {  // the accept rule reads the step-major buffers directly
+        sp->dtok = sp->dtok_s;
+        sp->dlogits = sp->dl_s;
+    }
     if (st == ULSPEC_OK) {
-        hipError_t e = hipMemset(sp->zero, 0, 16);
-        if (e == hipSuccess) e = hipMemset(sp->nacc, 0, 16);
-        if (e == hipSuccess) e = hipMemset(sp->st, 0, sizeof(SpecState));  // no tokens before the prefill
-        if (e == hipSuccess) e = hipHostMalloc((void**)&sp->host_st, sizeof(SpecState), hipHostMallocDefault);
+        hipError_t e = hipMemset(sp->zero, 0, 4 * B);
+        if (e == hipSuccess) e = hipMemset(sp->nacc, 0, 4 * B);
+        if (e == hipSuccess) e = hipMemset(sp->st, 0, B * sizeof(SpecState));  // no tokens before the prefill
+        if (e == hipSuccess) e = hipHostMalloc((void**)&sp->host_st, B * sizeof(SpecState), hipHostMallocDefault);
         if (e != hipSuccess) st = hip_fail(ctx, e, "spec_create hipHostMalloc");
     }
     if (st != ULSPEC_OK) {
@@ -269,6 +390,19 @@ extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* 
     }
     *out = sp;
     return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k,
+                                            const ulspec_sampling* s, uint64_t seed, ulspec_spec** out)
+{
+    return spec_create(target, draft, k, s, seed, 1, out);
+}
+
+extern "C" ulspec_status ulspec_spec_create_batch(ulspec_model* target, ulspec_model* draft, uint32_t k,
+                                                  const ulspec_sampling* s, uint64_t seed, uint32_t n_seq,
+                                                  ulspec_spec** out)
+{
+    return spec_create(target, draft, k, s, seed, n_seq, out);
 }
 
 extern "C" void ulspec_spec_destroy(ulspec_spec* sp)
@@ -285,28 +419,16 @@ extern "C" void ulspec_spec_destroy(ulspec_spec* sp)
 extern "C" ulspec_status ulspec_spec_prefill(ulspec_spec* sp, const int32_t* prompt, uint32_t n)
 {
     if (!sp) return ULSPEC_EINVAL;
-    ulspec_ctx* ctx = sp->ctx;
-    if (!prompt || n < 1) return fail(ctx, ULSPEC_EINVAL, "spec_prefill: need at least 1 prompt token");
-    if ((uint64_t)n + sp->k + 1 > sp->cap) return fail(ctx, ULSPEC_EINVAL, "spec_prefill: %u tokens leave no room", n);
-    for (uint32_t i = 0; i < n; ++i)
-        if (prompt[i] < 0 || (uint32_t)prompt[i] >= sp->V)
-            return fail(ctx, ULSPEC_EINVAL, "spec_prefill: token %d out of range", prompt[i]);
-    (void)hipSetDevice(ctx->device);
-    ulspec_status st = ULSPEC_OK;
-    if (hipMemset(sp->nacc, 0, 16) != hipSuccess) return fail(ctx, ULSPEC_EDEVICE, "spec_prefill: reset");
-    if (n > 1) {
-        st = ulspec_model_forward(sp->t, prompt, n - 1, 0, nullptr, 0);
-        if (st == ULSPEC_OK && sp->d) st = ulspec_model_forward(sp->d, prompt, n - 1, 0, nullptr, 0);
-        if (st != ULSPEC_OK) return st;
-    }
-    hipError_t e = hipMemcpy(sp->seq, prompt, (size_t)n * 4, hipMemcpyHostToDevice);
-    if (e != hipSuccess) return hip_fail(ctx, e, "spec_prefill copy");
-    hipLaunchKernelGGL(spec_reset_kernel, dim3(1), dim3(1), 0, ctx->stream, sp->st, (int32_t)n);
-    st = check_launch(ctx, "spec_prefill launch");
-    if (st != ULSPEC_OK) return st;
-    sp->prefilled = true;
-    sp->plain_first = n == 1 && sp->k > 0;
-    return sp->sync_state();
+    if (sp->B != 1) return fail(sp->ctx, ULSPEC_EINVAL, "spec_prefill: %u sequences (ulspec_spec_prefill_batch)", sp->B);
+    if (!prompt || n < 1) return fail(sp->ctx, ULSPEC_EINVAL, "spec_prefill: need at least 1 prompt token");
+    return sp->prefill(prompt, &n);
+}
+
+extern "C" ulspec_status ulspec_spec_prefill_batch(ulspec_spec* sp, const int32_t* prompts, const uint32_t* lens)
+{
+    if (!sp) return ULSPEC_EINVAL;
+    if (!prompts || !lens) return fail(sp->ctx, ULSPEC_EINVAL, "spec_prefill_batch: null pointer");
+    return sp->prefill(prompts, lens);
 }
 
 extern "C" ulspec_status ulspec_spec_steps(ulspec_spec* sp, uint32_t n_steps)
@@ -343,8 +465,9 @@ extern "C" ulspec_status ulspec_spec_generate(ulspec_spec* sp, uint32_t n_new, u
     if (!sp->prefilled) return fail(ctx, ULSPEC_EINVAL, "spec_generate: no prefill");
     ulspec_status st = sp->sync_state();
     if (st != ULSPEC_OK) return st;
-    const uint32_t start = (uint32_t)sp->host_st->n;
-    uint32_t produced = 0;
+    std::vector<uint32_t> start(sp->B);
+    for (uint32_t b = 0; b < sp->B; ++b) start[b] = (uint32_t)sp->host_st[b].n;
+    uint32_t produced = 0;  // by the sequence that has produced the fewest
     while (produced < n_new) {
         // as many steps as cannot pass n_new (each commits <= k+1), at least one
         const uint32_t r = std::max<uint32_t>(1, (n_new - produced) / (sp->k + 1));
@@ -352,7 +475,8 @@ extern "C" ulspec_status ulspec_spec_generate(ulspec_spec* sp, uint32_t n_new, u
         if (st != ULSPEC_OK) return st;
         st = sp->sync_state();
         if (st != ULSPEC_OK) return st;
-        produced = (uint32_t)sp->host_st->n - start;
+        produced = ~0u;
+        for (uint32_t b = 0; b < sp->B; ++b) produced = std::min(produced, (uint32_t)sp->host_st[b].n - start[b]);
     }
     if (n_out) *n_out = produced;
     return ULSPEC_OK;
@@ -365,23 +489,51 @@ extern "C" ulspec_status ulspec_spec_state(ulspec_spec* sp, uint32_t* n_tokens, 
     (void)hipSetDevice(sp->ctx->device);
     ulspec_status st = sp->sync_state();
     if (st != ULSPEC_OK) return st;
-    if (n_tokens) *n_tokens = (uint32_t)sp->host_st->n;
-    if (steps) *steps = sp->host_st->step;
-    if (accepted) *accepted = sp->host_st->accepted;
-    if (proposed) *proposed = sp->host_st->proposed;
+    uint64_t n = 0, acc = 0, prop = 0;
+    for (uint32_t b = 0; b < sp->B; ++b) {
+        n += (uint64_t)sp->host_st[b].n;
+        acc += sp->host_st[b].accepted;
+        prop += sp->host_st[b].proposed;
+    }
+    if (n_tokens) *n_tokens = (uint32_t)n;
+    if (steps) *steps = sp->host_st[0].step;
+    if (accepted) *accepted = acc;
+    if (proposed) *proposed = prop;
     return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_spec_seq_state(ulspec_spec* sp, uint32_t seq, uint32_t* n_tokens, uint64_t* accepted,
+                                               uint64_t* proposed)
+{
+    if (!sp) return ULSPEC_EINVAL;
+    if (seq >= sp->B) return fail(sp->ctx, ULSPEC_EINVAL, "spec_seq_state: sequence %u of %u", seq, sp->B);
+    (void)hipSetDevice(sp->ctx->device);
+    ulspec_status st = sp->sync_state();
+    if (st != ULSPEC_OK) return st;
+    if (n_tokens) *n_tokens = (uint32_t)sp->host_st[seq].n;
+    if (accepted) *accepted = sp->host_st[seq].accepted;
+    if (proposed) *proposed = sp->host_st[seq].proposed;
+    return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_spec_seq_tokens(ulspec_spec* sp, uint32_t seq, uint32_t start, uint32_t n,
+                                                int32_t* out)
+{
+    if (!sp) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = sp->ctx;
+    if (seq >= sp->B) return fail(ctx, ULSPEC_EINVAL, "spec_tokens: sequence %u of %u", seq, sp->B);
+    ulspec_status st = sp->sync_state();
+    if (st != ULSPEC_OK) return st;
+    if (!out || (uint64_t)start + n > (uint64_t)sp->host_st[seq].n)
+        return fail(ctx, ULSPEC_EINVAL, "spec_tokens: %u+%u beyond %d committed", start, n, sp->host_st[seq].n);
+    hipError_t e = n ? hipMemcpy(out, sp->seq + (size_t)seq * sp->cap + start, (size_t)n * 4, hipMemcpyDeviceToHost)
+                     : hipSuccess;
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_tokens copy");
 }
 
 extern "C" ulspec_status ulspec_spec_tokens(ulspec_spec* sp, uint32_t start, uint32_t n, int32_t* out)
 {
-    if (!sp) return ULSPEC_EINVAL;
-    ulspec_ctx* ctx = sp->ctx;
-    ulspec_status st = sp->sync_state();
-    if (st != ULSPEC_OK) return st;
-    if (!out || (uint64_t)start + n > (uint64_t)sp->host_st->n)
-        return fail(ctx, ULSPEC_EINVAL, "spec_tokens: %u+%u beyond %d committed", start, n, sp->host_st->n);
-    hipError_t e = hipMemcpy(out, sp->seq + start, (size_t)n * 4, hipMemcpyDeviceToHost);
-    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_tokens copy");
+    return ulspec_spec_seq_tokens(sp, 0, start, n, out);
 }
 
 extern "C" ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
@@ -392,15 +544,15 @@ extern "C" ulspec_status ulspec_spec_last_step(ulspec_spec* sp, float* target_lo
     ulspec_ctx* ctx = sp->ctx;
     (void)hipSetDevice(ctx->device);
     hipError_t e = hipStreamSynchronize(ctx->stream);
-    const size_t k = sp->k, V = sp->V;
+    const size_t k = sp->k, V = sp->V, B = sp->B;
     struct Copy {
         void* dst;
         const void* src;
         size_t bytes;
     } copies[] = {
-        {target_logits, sp->tlogits, (k + 1) * V * 4}, {draft_logits, sp->dlogits, k * V * 4},
-        {draft_tokens, sp->dtok, k * 4},                {uniforms, sp->unif, (2 * k + 1) * 4},
-        {out_tokens, sp->out_tok, (k + 1) * 4},         {n_accepted, sp->nacc, 4},
+        {target_logits, sp->tlogits, B * (k + 1) * V * 4}, {draft_logits, sp->dlogits, B * k * V * 4},
+        {draft_tokens, sp->dtok, B * k * 4},                {uniforms, sp->unif, B * (2 * k + 1) * 4},
+        {out_tokens, sp->out_tok, B * (k + 1) * 4},         {n_accepted, sp->nacc, B * 4},
     };
     for (const Copy& c : copies)
         if (e == hipSuccess && c.dst && c.bytes) e = hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost);

@@ -16,4 +16,11 @@ uint32_t embed_partials(uint32_t dim);
 void launch_embed(hipStream_t st, const uint8_t* w, uint32_t type, uint32_t dim, const int32_t* tokens, uint32_t M,
                   uint32_t V, float* h, float* pss, const float* xn_w, _Float16* xn);
 
+// The last n of every group of r rows (nseq groups, M = nseq r rows): split
+// X rows (xn: hi rows 0 .. M-1, lo rows M ..; dim halves each) and their P
+// row-scale partials (pss [M][P]) -> xg (hi rows 0 .. nseq n - 1, lo rows
+// nseq n ..) and pg [nseq n][P].
+void launch_gather_rows(hipStream_t st, const _Float16* xn, const float* pss, uint32_t M, uint32_t dim, uint32_t P,
+                        uint32_t r, uint32_t n, uint32_t nseq, _Float16* xg, float* pg);
+
 }  // namespace ulspec

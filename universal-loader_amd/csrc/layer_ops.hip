@@ -87,9 +87,32 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
     if (threadIdx.x == 0) pss[(size_t)m * gridDim.x + blockIdx.x] = ((part[0] + part[1]) + part[2]) + part[3];
 }
 
+// One workgroup per gathered row i (blockIdx.x < nseq n): source row
+// (i / n) r + r - n + i % n.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const _Float16* __restrict__ xn,
+                                                          const float* __restrict__ pss, uint32_t M, uint32_t dim,
+                                                          uint32_t P, uint32_t r, uint32_t n, uint32_t G,
+                                                          _Float16* __restrict__ xg, float* __restrict__ pg)
+{
+    const uint32_t i = blockIdx.x;
+    const uint32_t src = (i / n) * r + (r - n) + i % n;
+    for (uint32_t c = threadIdx.x; c < dim; c += 256) {
+        xg[(size_t)i * dim + c] = xn[(size_t)src * dim + c];
+        xg[(size_t)(G + i) * dim + c] = xn[(size_t)(M + src) * dim + c];
+    }
+    for (uint32_t c = threadIdx.x; c < P; c += 256) pg[(size_t)i * P + c] = pss[(size_t)src * P + c];
+}
+
 }  // namespace
 
 uint32_t embed_partials(uint32_t dim) { return (dim + 255) / 256; }
+
+void launch_gather_rows(hipStream_t st, const _Float16* xn, const float* pss, uint32_t M, uint32_t dim, uint32_t P,
+                        uint32_t r, uint32_t n, uint32_t nseq, _Float16* xg, float* pg)
+{
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseq * n), dim3(256), 0, st, xn, pss, M, dim, P, r, n, nseq * n, xg,
+                       pg);
+}
 
 void launch_embed(hipStream_t st, const uint8_t* w, uint32_t type, uint32_t dim, const int32_t* tokens, uint32_t M,
                   uint32_t V, float* h, float* pss, const float* xn_w, _Float16* xn)

@@ -666,20 +666,71 @@ __device__ __forceinline__ float rs_reduce(const GemmArgs& a, float4 v)
     return 1.0f / __builtin_sqrtf(ss / (float)a.K + a.f.rs_eps);
 }
 
-// Position of row 0 for the RoPE epilogue: a scalar load through the
-// constant address space (the value is fixed for the whole kernel), so it
-// never waits behind the vector loads in flight.
-__device__ __forceinline__ int epi_pos0(const GemmArgs& a)
+// First position of each sequence's rows for the RoPE epilogue: scalar
+// loads through the constant address space (the values are fixed for the
+// whole kernel), so they never wait behind the vector loads in flight.
+// (Named fields, not an array: the positions stay in registers.)
+static_assert(kMaxSeqs == 8, "EpiPos holds 8 sequences");
+struct EpiPos {
+    int p0, p1, p2, p3, p4, p5, p6, p7;
+};
+
+__device__ __forceinline__ EpiPos epi_pos0(const GemmArgs& a)
 {
-    if (a.f.epi != kEpiRope) return 0;
+    EpiPos r{0, 0, 0, 0, 0, 0, 0, 0};
+    if (a.f.epi != kEpiRope) return r;
     const __attribute__((address_space(4))) int32_t* p = (const __attribute__((address_space(4))) int32_t*)a.f.pos_dev;
-    return *p + a.f.pos_add;
+    const int n = a.f.nseq, add = a.f.pos_add;
+    r.p0 = p[0] + add;
+    if (n > 1) {
+        r.p1 = p[1] + add;
+        r.p2 = n > 2 ? p[2] + add : 0;
+        r.p3 = n > 3 ? p[3] + add : 0;
+        r.p4 = n > 4 ? p[4] + add : 0;
+        r.p5 = n > 5 ? p[5] + add : 0;
+        r.p6 = n > 6 ? p[6] + add : 0;
+        r.p7 = n > 7 ? p[7] + add : 0;
+    }
+    return r;
 }
 
-// RoPE position of row m, relative to pos0: m, or the row's tree depth.
-__device__ __forceinline__ int rope_row(const GemmFuse& f, int m)
+// Sequence of row m (rows are grouped by sequence, seq_rows each) and the
+// row's index j within it.
+__device__ __forceinline__ int row_seq(const GemmFuse& f, int m, int& j)
 {
-    return f.tree ? (int)((f.row_depth >> (4 * (m & 15))) & 15u) : m;
+    const int b = f.nseq > 1 ? m / f.seq_rows : 0;
+    j = m - b * f.seq_rows;
+    return b;
+}
+
+__device__ __forceinline__ int seq_pos0(EpiPos ps, int b)
+{
+    int v = ps.p0;
+    v = b == 1 ? ps.p1 : v;
+    v = b == 2 ? ps.p2 : v;
+    v = b == 3 ? ps.p3 : v;
+    v = b == 4 ? ps.p4 : v;
+    v = b == 5 ? ps.p5 : v;
+    v = b == 6 ? ps.p6 : v;
+    v = b == 7 ? ps.p7 : v;
+    return v;
+}
+
+// RoPE position of row m: its sequence's first position plus j, or plus the
+// row's tree depth.
+__device__ __forceinline__ int rope_pos(const GemmFuse& f, EpiPos ps, int m)
+{
+    int j;
+    const int b = row_seq(f, m, j);
+    return seq_pos0(ps, b) + (f.tree ? (int)((f.row_depth >> (4 * (j & 15))) & 15u) : j);
+}
+
+// K / V cache row of row m: slot first position + j of its sequence's cache.
+__device__ __forceinline__ size_t kv_row(const GemmFuse& f, EpiPos ps, int m)
+{
+    int j;
+    const int b = row_seq(f, m, j);
+    return (size_t)(f.seq0 + b) * f.seq_slots + (size_t)(seq_pos0(ps, b) + j);
 }
 
 // The memory operands of the epilogue of output (m, n), loaded ahead of it
@@ -687,9 +738,9 @@ __device__ __forceinline__ int rope_row(const GemmFuse& f, int m)
 // issue order: a load issued in the epilogue would wait for every weight load
 // in flight).  Two 4-byte loads for the resid and rope epilogues (out of range
 // where a thread has no output), none otherwise:
-//   resid: (h[m][n], xn_w[n])   rope: (cos, sin) of the pair at position
-//                               pos0 + m (pos0 + depth(m) for a tree)
-__device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int pos0)
+//   resid: (h[m][n], xn_w[n])   rope: (cos, sin) of the pair at the row's
+//                               RoPE position (rope_pos)
+__device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, EpiPos pos0)
 {
     const GemmFuse& f = a.f;
     const bool ok = m < a.M && n < a.N;
@@ -703,11 +754,11 @@ __device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, int 
             o1 = (uint32_t)n * 4u;
         }
     } else if (f.epi == kEpiRope) {
-        r0 = make_rsrc(f.rope, (uint32_t)(pos0 + a.M) * (uint32_t)(f.hd / 2) * 8u);
+        r0 = make_rsrc(f.rope, (uint32_t)min((uint64_t)f.rope_rows * (uint64_t)(f.hd / 2) * 8u, (uint64_t)0xffffffffu));
         r1 = r0;
         if (ok && n < f.qdim + f.kvdim) {
             const int nn = n < f.qdim ? n : n - f.qdim;
-            o0 = (uint32_t)((pos0 + rope_row(f, m)) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
+            o0 = (uint32_t)(rope_pos(f, pos0, m) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
             o1 = o0 + 4u;
         }
     } else {
@@ -732,9 +783,10 @@ __device__ __forceinline__ int epi_nloads(const GemmArgs& a)
 // of the same row m, and 16-lane groups one row of one tile (whole waves call
 // this).
 //   store: Y[m][n] = s
-//   rope:  RoPE pair (n, n+1) at position pos0 + m, or pos0 + depth(m) for a
-//          tree (Q and K rows, angles from epi_load), then fp16 Q -> q16[m][n],
-//          K -> kc[pos][n - qdim], V -> vc[pos][n - qdim - kvdim], pos = pos0 + m
+//   rope:  RoPE pair (n, n+1) at the row's position (rope_pos: its sequence's
+//          first position + j, or + depth(j) for a tree; Q and K rows, angles
+//          from epi_load), then fp16 Q -> q16[m][n], K -> kc[row][n - qdim],
+//          V -> vc[row][n - qdim - kvdim], row = kv_row(m)
 //          (y0 = x0 c - x1 s, y1 = x0 s + x1 c; src/shaders/rope.glsl:50-73)
 //   silu:  rows interleaved (2i = gate i, 2i+1 = up i): a = g * (1 / (1 +
 //          e^-g)) * u, split: act[m][i] = hi, act[M + m][i] = lo
@@ -742,7 +794,8 @@ __device__ __forceinline__ int epi_nloads(const GemmArgs& a)
 //          of h^2 (xor tree over the 16 lanes), the RMSNorm partial of row m;
 //          with xn, the next GEMM's split X: xn[m][n] = hi, xn[xn_lo + m][n] =
 //          lo of h * xn_w[n] (the next norm's weights)
-__device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l, float2 pre, int pos0)
+__device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int n, int t, int l, float2 pre,
+                                         EpiPos pos0)
 {
     const bool ok = m < a.M && n < a.N;
     const GemmFuse& f = a.f;
@@ -751,7 +804,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
         const float other = __shfl_xor(s, 1);
         if (!ok) break;
         const bool odd = n & 1;
-        const int pos = pos0 + m;
+        const size_t pos = kv_row(f, pos0, m);
         if (n < f.qdim + f.kvdim) {
             const int nn = n < f.qdim ? n : n - f.qdim;
             const float2 cs = pre;
@@ -921,7 +974,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const floa
     const int m = i / NP, n = i - m * NP;
     const int m_first = (blockIdx.x * 256) / NP;
     const int n_rows = min((blockIdx.x * 256 + 255) / NP - m_first + 1, 256 / 16 + 2);
-    const int pos0 = epi_pos0(a);
+    const EpiPos pos0 = epi_pos0(a);
     const bool ok = m < a.M && n < a.N;
     const size_t MN = (size_t)a.M * a.N;
     float v[kMaxSlices];
@@ -1056,7 +1109,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
     const int xrow[1] = {xslot_row(a, 0, r) * RS + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
-    const int pos0 = epi_pos0(a);
+    const EpiPos pos0 = epi_pos0(a);
     const int it = blockIdx.x, t = it * tpi + tw;
 
     // issue order: row-scale partials, this wave's X (its whole part), the
@@ -1112,7 +1165,7 @@ constexpr int kRingDepth = 2;
 // j); pre is this thread's epi_load of the same output.
 template <int NW>
 __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc, float* red, const float* rs, int it,
-                                          int P, int tpi, float2 pre, int pos0)
+                                          int P, int tpi, float2 pre, EpiPos pos0)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -1130,7 +1183,7 @@ __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc
 
 // epi_load of this thread's output in global iteration `it` (nothing when its
 // tile slot is unused).
-__device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, int pos0)
+__device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, EpiPos pos0)
 {
     const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = threadIdx.x >> 8;
     const int m = j < tpi ? epi_row(a, l, row) : a.M;
@@ -1160,7 +1213,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
-    const int pos0 = epi_pos0(a);
+    const EpiPos pos0 = epi_pos0(a);
     auto git = [&](int li) { return (int)blockIdx.x + li * (int)gridDim.x; };  // global iteration
 
     // issue order: row-scale partials, this wave's X, D batches of weights

@@ -73,6 +73,9 @@ inline ulspec_status hip_fail(ulspec_ctx* ctx, hipError_t e, const char* what)
 ulspec_status gemm_init(ulspec_ctx* ctx);
 ulspec_status accept_init(ulspec_ctx* ctx);
 
+// Sequences of one batched forward (each with its own K / V cache slot).
+constexpr int kMaxSeqs = 8;
+
 // Row scale and epilogues of the dequant-GEMM in the model forward.
 enum { kEpiStore = 0, kEpiRope = 1, kEpiSilu = 2, kEpiResid = 3 };
 // Rows per launch: fp16 X through the ABI GEMM, split X through the fused GEMM.
@@ -86,11 +89,16 @@ struct GemmFuse {
     const float* rs_pss = nullptr;
     int rs_P = 0;
     float rs_eps = 0.0f;
-    // kEpiRope: Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc at slot *pos_dev + pos_add + m;
-    // the RoPE position of row m is *pos_dev + pos_add + m, or with tree != 0
-    // *pos_dev + pos_add + depth(m), depth(m) = bits 4m .. 4m+3 of row_depth
+    // kEpiRope: rows are nseq groups of seq_rows (one per sequence, sequence
+    // slots seq0 ..); row j of sequence b takes RoPE position pos_dev[b] +
+    // pos_add + j (with tree != 0: + depth(j), depth(j) = bits 4j .. 4j+3 of
+    // row_depth) and its K / V go to cache row (seq0 + b) seq_slots +
+    // pos_dev[b] + pos_add + j; Q rows [0, qdim) -> q16, K rows -> kc, V rows -> vc
     const int32_t* pos_dev = nullptr;
     int pos_add = 0;
+    int nseq = 1, seq_rows = 0, seq0 = 0;
+    uint32_t seq_slots = 0;  // cache rows per sequence (max_ctx)
+    uint32_t rope_rows = 0;  // positions of the rope table
     int tree = 0;
     uint64_t row_depth = 0;
     const float2* rope = nullptr;
@@ -142,13 +150,17 @@ struct AttnCall {
     void* out = nullptr;
     bool out_f16 = false;
     bool out_split = false;  // split fp16 pair [2][nq][H][D] (hi, lo) for the next GEMM's X
-    const int32_t* dyn_prefix = nullptr;  // device int: prefix = *dyn_prefix + prefix_add
+    const int32_t* dyn_prefix = nullptr;  // device int per sequence: prefix = dyn_prefix[b] + prefix_add
     int prefix_add = 0;
     void* part = nullptr;    // split partials; NULL = the context workspace
+    // nseq sequences: q and out hold nseq groups of nq rows, sequence b's
+    // cache starts kv_seq elements after sequence b-1's (needs dyn_prefix)
+    uint32_t nseq = 1;
+    size_t kv_seq = 0;
 };
 ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c);
 void attn_plan(int L, int H, int n_cu, int& splits, int& kps);
-size_t attn_workspace_bytes(int splits, int H, int nq, int D);
+size_t attn_workspace_bytes(int splits, int H, int nq, int D, int nseq = 1);
 size_t accept_workspace_bytes(uint32_t B, uint32_t k);
 size_t sample_workspace_bytes(uint32_t R);
 ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k, uint32_t V,

@@ -30,7 +30,9 @@ def norm_names(n_layers, **_):
 def synthetic_llama(pkg, ctx, cfg, wtype, seed, std=0.02, keep_host=False):
     """Create a Model with synthetic weights.  With keep_host, also return the
     raw GGUF bytes of every tensor as {name: (type, bytes, ne0, ne1)}."""
-    model = pkg.Model(ctx, **cfg)
+    cfg = dict(cfg)
+    n_seq = cfg.pop("n_seq", 1)
+    model = pkg.Model(ctx, **cfg, n_seq=n_seq)
     shapes = tensor_shapes(**cfg)
     biggest = max(ne1 * pkg.row_bytes(wtype, ne0) for _, ne0, ne1 in shapes)
     buf = ctx.alloc(biggest)
