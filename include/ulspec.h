@@ -350,6 +350,30 @@ ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint
  * batch of the reference's generate_batch (src/api/inference_api.h:63). */
 ulspec_status ulspec_spec_create_batch(ulspec_model* target, ulspec_model* draft, uint32_t k,
                                        const ulspec_sampling* s, uint64_t seed, uint32_t n_seq, ulspec_spec** out);
+/* Tree steps over a fixed draft tree (one sequence): n <= 16 nodes in
+ * breadth-first order (parent, HOST int32 [n]: parent[0] = -1, parent[i] in
+ * [0, i), depths non-decreasing, each node's children consecutive; node 0 is
+ * the last committed token).  Per step the draft runs one tree-masked forward
+ * per level over [t_{n-2}, root, nodes so far] and draws the children of each
+ * level from their parent's logits (sampling: i.i.d. with node i's uniform
+ * u(seed, s(2n-1) + i - 1); greedy: the parent's best tokens in order), the
+ * target scores the n nodes in one tree forward, ulspec_accept_tree's rule
+ * (uniforms u(seed, s(2n-1) + n - 1 + j)) picks the path, both K/V caches are
+ * compacted along it and path + final token are committed (a chain of k+1
+ * nodes is the chain loop, counters included).  Replaces
+ * TreeSpeculation::generate_tree_speculation / verify_tree
+ * (src/inference/speculative_decoder.h:62-87, .cpp:118-176).  Prompts need
+ * at least 2 tokens; ulspec_spec_state's `proposed` counts the tree depth per
+ * step. */
+ulspec_status ulspec_spec_create_tree(ulspec_model* target, ulspec_model* draft, uint32_t n, const int32_t* parent,
+                                      const ulspec_sampling* s, uint64_t seed, ulspec_spec** out);
+/* The last tree step's target logits [n][V], draft logits of nodes 0 .. n-2
+ * [n-1][V] (rows of leaf nodes are not written), node tokens [n], uniforms
+ * [2n-1], ulspec_accept_tree's tokens [n] and path [n], and n_accepted.
+ * Synchronous. */
+ulspec_status ulspec_spec_tree_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
+                                         int32_t* tokens, float* uniforms, int32_t* out_tokens, int32_t* path,
+                                         int32_t* n_accepted);
 void          ulspec_spec_destroy(ulspec_spec* sp);
 /* Commit the prompt (n >= 1): both models process tokens 0 .. n-2; token n-1
  * is pending.  Resets the counters.  With n = 1 and k > 0 the first step is a

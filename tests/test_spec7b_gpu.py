@@ -123,3 +123,25 @@ def test_7b_sampling_steps_bit_exact(pkg, ora, models, prompt):
     print(f"  T=0.8 7B: {len(seq) - CONTEXT} tokens, accepted {accepted}/{k * STEPS}, worst logits err {worst:.2e}")
     assert worst <= LOGIT_TOL
     sp.close()
+
+
+@pytest.mark.parametrize("mode", ["greedy", "sampling"])
+def test_7b_tree_steps_bit_exact(pkg, ora, models, prompt, mode):
+    """16-node tree steps (branching <= 3, depth 5) on the 7B pair: draws,
+    ulspec_accept_tree decisions, K/V compaction of both caches and commits
+    against the oracle, teacher-forced (tree_step_util.check_tree_steps); the
+    node logits against the oracle's path forwards within LOGIT_TOL."""
+    from tree_step_util import TREE16, check_tree_steps
+    gt, gd, ot, od = models
+    seed = 4242
+    args = dict(greedy=True) if mode == "greedy" else dict(temperature=0.8)
+    sp = pkg.Speculative(gt, gd, 0, pkg.sampling(**args), seed, parent=TREE16)
+    sp.prefill(prompt)
+    for g, o, cfg in ((gt, ot, TARGET), (gd, od, DRAFT)):
+        for l in range(cfg["n_layers"]):
+            k, v = g.kv_io(l, 0, 0, CONTEXT - 1)
+            o.kv_io(l, 1, 0, CONTEXT - 1, k, v)
+    seq, worst = check_tree_steps(ora, sp, ot, od, ora.sampling(**args), list(prompt), TREE16, seed, 3,
+                                  mode == "greedy", LOGIT_TOL)
+    print(f"  7B tree {mode}: {len(seq) - CONTEXT} tokens in 3 steps, worst logits err {worst:.2e}")
+    sp.close()

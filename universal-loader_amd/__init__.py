@@ -131,6 +131,8 @@ ABI = [
     ("ulspec_spec_prefill_batch", C.c_int, [P, P, P]),
     ("ulspec_spec_seq_state", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     ("ulspec_spec_seq_tokens", C.c_int, [P, U32, U32, U32, P]),
+    ("ulspec_spec_create_tree", C.c_int, [P, P, U32, P, C.POINTER(Sampling), C.c_uint64, C.POINTER(P)]),
+    ("ulspec_spec_tree_last_step", C.c_int, [P, P, P, P, P, P, P, P]),
     ("ulspec_spec_set_graph", C.c_int, [P, C.c_int]),
     ("ulspec_gguf_open", C.c_int, [C.c_char_p, C.POINTER(P), C.c_char_p, C.c_size_t]),
     ("ulspec_gguf_close", None, [P]),
@@ -513,13 +515,22 @@ class Speculative:
     """ulspec_spec: the device speculative-decoding loop over a target and a
     draft model; k = 0 (draft None) decodes with the target alone."""
 
-    def __init__(self, target, draft, k, s, seed, n_seq=1):
-        """n_seq > 1: a batch of that many sequences (models with as many slots)."""
+    def __init__(self, target, draft, k, s, seed, n_seq=1, parent=None):
+        """n_seq > 1: a batch of that many sequences (models with as many slots).
+        parent (a breadth-first tree of n nodes): tree steps; k is then n - 1."""
         self.ctx = target.ctx
-        self.target, self.draft, self.k, self.n_seq = target, draft, k, n_seq
+        self.target, self.draft, self.n_seq = target, draft, n_seq
         h = P()
-        self.ctx._check(lib().ulspec_spec_create_batch(target.handle, draft.handle if draft is not None else None, k,
-                                                       C.byref(s), seed, n_seq, C.byref(h)))
+        if parent is not None:
+            self.parent = np.ascontiguousarray(parent, dtype=np.int32)
+            self.k = len(self.parent) - 1
+            self.ctx._check(lib().ulspec_spec_create_tree(target.handle, draft.handle, len(self.parent),
+                                                          self.parent.ctypes.data_as(P), C.byref(s), seed,
+                                                          C.byref(h)))
+        else:
+            self.parent, self.k = None, k
+            self.ctx._check(lib().ulspec_spec_create_batch(target.handle, draft.handle if draft is not None else None,
+                                                           k, C.byref(s), seed, n_seq, C.byref(h)))
         self.handle = h.value
 
     def close(self):
@@ -567,6 +578,15 @@ class Speculative:
         """Inputs and outputs of the last step (host copies); for a batch, every
         array has a leading sequence axis and n_accepted is an array."""
         k, V, B = self.k, self.target.cfg.vocab, self.n_seq
+        if self.parent is not None:
+            n = k + 1
+            r = {"target_logits": np.empty((n, V), np.float32), "draft_logits": np.empty((n - 1, V), np.float32),
+                 "tokens": np.empty(n, np.int32), "uniforms": np.empty(2 * n - 1, np.float32),
+                 "out_tokens": np.empty(n, np.int32), "path": np.empty(n, np.int32),
+                 "n_accepted": np.empty(1, np.int32)}
+            self.ctx._check(lib().ulspec_spec_tree_last_step(self.handle, *[a.ctypes.data_as(P) for a in r.values()]))
+            r["n_accepted"] = int(r["n_accepted"][0])
+            return r
         r = {"target_logits": np.empty((B, k + 1, V), np.float32), "draft_logits": np.empty((B, k, V), np.float32),
              "draft_tokens": np.empty((B, k), np.int32), "uniforms": np.empty((B, 2 * k + 1), np.float32),
              "out_tokens": np.empty((B, k + 1), np.int32), "n_accepted": np.empty(B, np.int32)}

@@ -1006,16 +1006,43 @@ __global__ __launch_bounds__(kSeqThreads) void decide_tree_kernel(const RowStat*
 
 // Top-k / top-p draw of one row per workgroup from its kept list (greedy and
 // full-vocabulary draws run in the chunk kernels below).
+// Draw d (blockIdx.x) comes from row map[d] (row d without a map).
 __global__ __launch_bounds__(kSeqThreads) void sample_kernel(const RowStat* __restrict__ stats,
                                                              const float* __restrict__ uniforms, uint32_t V,
+                                                             const int32_t* __restrict__ map,
                                                              int32_t* __restrict__ out)
 {
     __shared__ int32_t sidx[kKMax];
     __shared__ uint64_t sE[kKMax];
-    const uint32_t r = blockIdx.x;
+    const uint32_t d = blockIdx.x, r = map ? (uint32_t)map[d] : d;
     const int n = stage_list(stats[r], sidx, sE);
     __syncthreads();
-    if (threadIdx.x == 0) out[r] = list_cdf_pick(sidx, sE, n, stats[r].Z, uniforms[r], V);
+    if (threadIdx.x == 0) out[d] = list_cdf_pick(sidx, sE, n, stats[r].Z, uniforms[d], V);
+}
+
+// Greedy tree drafting: workgroup i takes row i and writes its n_kids[i]
+// largest tokens by (logit desc, index asc), in that order, to
+// out[first_kid[i] ..]: pass r picks the largest order key below pick r-1.
+__global__ __launch_bounds__(kRowThreads) void topb_kernel(const float* __restrict__ logits, uint32_t V,
+                                                           const int32_t* __restrict__ first_kid,
+                                                           const int32_t* __restrict__ n_kids,
+                                                           int32_t* __restrict__ out)
+{
+    __shared__ uint64_t red[kRowThreads / 64];
+    const uint32_t i = blockIdx.x;
+    const float* row = logits + (size_t)i * V;
+    uint64_t prev = ~0ull;
+    const int nk = n_kids[i];
+    for (int r = 0; r < nk; ++r) {  // uniform
+        uint64_t best = 0;
+        scan_row<kRowThreads>(row, V, [&](uint32_t idx, float l) {
+            const uint64_t o = order_key(float_key(l), idx);
+            if (o < prev && o > best) best = o;
+        });
+        best = block_max_u64<kRowThreads>(best, red);
+        if (threadIdx.x == 0) out[first_kid[i] + r] = (int32_t)(0xffffffffu - (uint32_t)best);
+        prev = best;
+    }
 }
 
 // Full-vocabulary (or greedy) draw, each row split over up to kMaxChunks
@@ -1190,28 +1217,30 @@ __device__ int32_t chunk_draw(uint32_t V, ChunkPlan cp, float u, F4 w4, const Ch
     return t;
 }
 
-// One workgroup per row: the argmax (greedy) or the inverse-CDF draw.
+// One workgroup per draw d: the argmax (greedy) or the inverse-CDF draw from
+// row map[d] (row d without a map) with uniforms[d].
 __global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* __restrict__ logits,
                                                                    const float* __restrict__ uniforms, uint32_t V,
                                                                    ChunkPlan cp, WarpParams p,
                                                                    const ChunkPart* __restrict__ part,
                                                                    const uint64_t* __restrict__ kmin,
+                                                                   const int32_t* __restrict__ map,
                                                                    int32_t* __restrict__ out)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
-    const uint32_t r = blockIdx.x;
+    const uint32_t d = blockIdx.x, r = map ? (uint32_t)map[d] : d;
     const ChunkPart* rp = part + (size_t)r * cp.G;
     const uint64_t top = row_top(rp, cp, scratch);
     if (p.greedy) {
-        if (threadIdx.x == 0) out[r] = (int32_t)(0xffffffffu - (uint32_t)top);
+        if (threadIdx.x == 0) out[d] = (int32_t)(0xffffffffu - (uint32_t)top);
         return;
     }
     const float* row = logits + (size_t)r * V;
     const float lmax = key_float((uint32_t)(top >> 32));
     const uint64_t km = kmin ? kmin[r] : 0;
-    const int32_t t = chunk_draw(V, cp, uniforms[r],
+    const int32_t t = chunk_draw(V, cp, uniforms[d],
                                  [&](uint32_t q) { return kept_e4(load4(row, V, q), q, lmax, km, p); }, rp, scratch);
-    if (threadIdx.x == 0) out[r] = t;
+    if (threadIdx.x == 0) out[d] = t;
 }
 
 // Top-p bound (kmin) of every row of a chunk launch, one workgroup per row;
@@ -1779,11 +1808,20 @@ ulspec_status accept_tree_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint
 ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
                             const float* uniforms, int32_t* out_tokens, void* ws)
 {
+    return sample_mapped_launch(ctx, s, R, V, logits, R, nullptr, uniforms, out_tokens, ws);
+}
+
+ulspec_status sample_mapped_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
+                                   const float* logits, uint32_t D, const int32_t* map, const float* uniforms,
+                                   int32_t* out_tokens, void* ws)
+{
     WarpParams p;
     ulspec_status st = make_params(ctx, s, V, p);
     if (st != ULSPEC_OK) return st;
     if (R == 0 || V == 0) return fail(ctx, ULSPEC_EINVAL, "sample: need R >= 1 and V >= 1");
-    if (R > kMaxGridRows) return fail(ctx, ULSPEC_EUNSUPPORTED, "sample: R=%u rows (at most %u per call)", R, kMaxGridRows);
+    if (R > kMaxGridRows || D > kMaxGridRows)
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "sample: R=%u rows, %u draws (at most %u per call)", R, D, kMaxGridRows);
+    if (D == 0 || (!map && D != R)) return fail(ctx, ULSPEC_EINVAL, "sample: %u draws from %u rows", D, R);
     if (!logits || !out_tokens || (!p.greedy && !uniforms)) return fail(ctx, ULSPEC_EINVAL, "sample: null pointer");
     if (!ws) {
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
@@ -1802,17 +1840,26 @@ ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         if (!p.greedy)
             hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, p,
                                (const uint64_t*)kmin, part);
-        hipLaunchKernelGGL(chunk_pick_kernel, dim3(R), dim3(kChunkThreads), 0, ctx->stream, logits, uniforms, V, cp,
-                           p, (const ChunkPart*)part, (const uint64_t*)kmin, out_tokens);
+        hipLaunchKernelGGL(chunk_pick_kernel, dim3(D), dim3(kChunkThreads), 0, ctx->stream, logits, uniforms, V, cp,
+                           p, (const ChunkPart*)part, (const uint64_t*)kmin, map, out_tokens);
         return check_launch(ctx, "sample launch");
     }
     const TopkWs tw = topk_ws(ws, R);
     launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw);
-    hipLaunchKernelGGL(sample_kernel, dim3(R), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, uniforms,
-                       V, out_tokens);
+    hipLaunchKernelGGL(sample_kernel, dim3(D), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, uniforms,
+                       V, map, out_tokens);
     return check_launch(ctx, "sample launch");
 }
 
+}  // namespace ulspec
+
+namespace ulspec {
+void topb_launch(ulspec_ctx* ctx, const float* logits, uint32_t V, uint32_t rows, const int32_t* first_kid,
+                 const int32_t* n_kids, int32_t* out_tokens)
+{
+    hipLaunchKernelGGL(topb_kernel, dim3(rows), dim3(kRowThreads), 0, ctx->stream, logits, V, first_kid, n_kids,
+                       out_tokens);
+}
 }  // namespace ulspec
 
 extern "C" ulspec_status ulspec_accept(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t B, uint32_t k,

@@ -20,6 +20,19 @@
 // one token starts the same way for k > 0: the first step is such a plain
 // step (the draft's catch-up pair needs two committed tokens), after which
 // the draft catches up on [t_0, t_1].
+//
+// Tree steps (ulspec_spec_create_tree, one sequence): a fixed draft tree of n
+// <= 16 nodes in breadth-first order (node 0 the root t_{n-1}).  The draft
+// runs one tree-masked forward per level l < depth over [t_{n-2}, root, the
+// nodes of levels <= l] (row 0 re-computes t_{n-2}, as the chain's catch-up
+// pair does) and draws the children of level l from their parents' logits:
+// i.i.d. with the uniforms of the node (sampling; the multi-draft rule needs
+// children drawn from q), or the parent's best tokens in order (greedy).  The
+// target scores all n nodes in one tree forward, ulspec_accept_tree picks the
+// path, both caches are compacted along it, and the path plus the final
+// token are committed.  Uniforms of step s: node i's draw u(seed,
+// s(2n-1) + i - 1), the acceptance u(seed, s(2n-1) + n - 1 + j) -- the chain's
+// counters when the tree is a chain of k + 1 nodes.
 #include <algorithm>
 
 #include "../detmath.h"
@@ -103,6 +116,20 @@ __global__ __launch_bounds__(256) void spec_gather_draft_kernel(const int32_t* _
     if (blockIdx.x == 0 && threadIdx.x == 0) dtok[row] = dtok_s[j * B + b];
 }
 
+// Tree step: the 2n - 1 uniforms, the draft's first row t_{n-2} and the root t_{n-1}.
+__global__ void spec_tree_begin_kernel(const int32_t* __restrict__ npos, const int32_t* __restrict__ seq,
+                                       const SpecState* __restrict__ st, uint64_t seed, uint32_t n,
+                                       float* __restrict__ unif, int32_t* __restrict__ trow)
+{
+    const uint64_t step = st[0].step;
+    for (uint32_t j = threadIdx.x; j < 2 * n - 1; j += blockDim.x)
+        unif[j] = counter_uniform(seed, step * (2 * n - 1) + j);
+    if (threadIdx.x == 0) {
+        trow[0] = seq[npos[0] - 2];
+        trow[1] = seq[npos[0] - 1];
+    }
+}
+
 // One thread per sequence: append its n_acc + 1 tokens.
 __global__ void spec_commit_kernel(SpecState* __restrict__ st, int32_t* __restrict__ npos, int32_t* __restrict__ seq,
                                    uint32_t cap, const int32_t* __restrict__ out_tok, const int32_t* __restrict__ nacc,
@@ -168,9 +195,21 @@ struct ulspec_spec {
     hipGraphExec_t graph = nullptr;
     void* graph_ws = nullptr;       // context workspace the graph was captured with
     uint32_t n_hi = 0;              // upper bound of the longest committed count
+    // tree steps
+    bool tree = false;
+    uint32_t depth = 0;                 // levels below the root
+    std::vector<int32_t> parent_h;      // [n] the tree (target forward, acceptance)
+    std::vector<int32_t> dparent_h;     // [n + 1] the draft's rows: t_{n-2}, then the tree under it
+    std::vector<uint32_t> lv_first, lv_count;  // nodes of each level
+    int32_t* trow = nullptr;            // [n + 1]: t_{n-2}, then the n node tokens
+    int32_t* tmap = nullptr;            // [n] child -> its parent's row among its level's logits
+    int32_t* kid_first = nullptr;       // [n] first child of each node
+    int32_t* kid_count = nullptr;       // [n]
+    int32_t* path = nullptr;            // [n]
     ulspec_status enqueue_step();
     ulspec_status launch_step();
     ulspec_status launch_plain_step();
+    ulspec_status launch_tree_step();
     ulspec_status sync_state();
     ulspec_status prefill(const int32_t* prompts, const uint32_t* lens);
 };
@@ -188,8 +227,41 @@ ulspec_status ulspec_spec::launch_plain_step()
     return check_launch(ctx, "plain step launch");
 }
 
+ulspec_status ulspec_spec::launch_tree_step()
+{
+    hipStream_t stream = ctx->stream;
+    const uint32_t n = k + 1;
+    hipLaunchKernelGGL(spec_tree_begin_kernel, dim3(1), dim3(64), 0, stream, (const int32_t*)npos, (const int32_t*)seq,
+                       (const SpecState*)st, seed, n, unif, trow);
+    ulspec_status r = ULSPEC_OK;
+    for (uint32_t l = 0; l < depth && r == ULSPEC_OK; ++l) {
+        const uint32_t f = lv_first[l], c = lv_count[l], rows = 1 + f + c;
+        r = d->forward(trow, rows, npos, -2, dlogits + (size_t)f * V, c, dparent_h.data());
+        if (r != ULSPEC_OK) break;
+        const uint32_t f1 = lv_first[l + 1], c1 = lv_count[l + 1];
+        if (s.greedy)
+            topb_launch(ctx, dlogits + (size_t)f * V, V, c, kid_first + f, kid_count + f, trow + 1);
+        else
+            r = sample_mapped_launch(ctx, &s, c, V, dlogits + (size_t)f * V, c1, tmap + f1, unif + f1 - 1,
+                                     trow + 1 + f1, ws_sample);
+    }
+    if (r == ULSPEC_OK) r = t->forward(trow + 1, n, npos, -1, tlogits, n, parent_h.data());
+    if (r == ULSPEC_OK)
+        r = accept_tree_launch(ctx, &s, 1, n, V, parent_h.data(), tlogits, dlogits, trow + 1, unif + n - 1, out_tok,
+                               path, nacc, ws_accept);
+    if (r != ULSPEC_OK) return r;
+    launch_kv_compact(stream, t->kv_tab, t->cfg.n_layers, t->cfg.n_kv_heads * t->head_dim, t->cfg.max_ctx, npos, -1,
+                      path, nacc, n);
+    launch_kv_compact(stream, d->kv_tab, d->cfg.n_layers, d->cfg.n_kv_heads * d->head_dim, d->cfg.max_ctx, npos, -1,
+                      path, nacc, n);
+    hipLaunchKernelGGL(spec_commit_kernel, dim3(1), dim3(64), 0, stream, st, npos, seq, cap, (const int32_t*)out_tok,
+                       (const int32_t*)nacc, depth, n - 1, 1u);
+    return check_launch(ctx, "tree step launch");
+}
+
 ulspec_status ulspec_spec::launch_step()
 {
+    if (tree) return launch_tree_step();
     if (k == 0) return launch_plain_step();
     hipStream_t stream = ctx->stream;
     hipLaunchKernelGGL(spec_begin_kernel, dim3(1), dim3(256), 0, stream, (const int32_t*)npos, (const int32_t*)seq,
@@ -405,6 +477,110 @@ extern "C" ulspec_status ulspec_spec_create_batch(ulspec_model* target, ulspec_m
     return spec_create(target, draft, k, s, seed, n_seq, out);
 }
 
+extern "C" ulspec_status ulspec_spec_create_tree(ulspec_model* target, ulspec_model* draft, uint32_t n,
+                                                 const int32_t* parent, const ulspec_sampling* s, uint64_t seed,
+                                                 ulspec_spec** out)
+{
+    if (!target || !draft || !out) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = target->ctx;
+    if (!parent || n < 2 || n > ulspec_model::kRows)
+        return fail(ctx, ULSPEC_EINVAL, "spec_create_tree: %u nodes (2 .. %u) and a parent array", n,
+                    ulspec_model::kRows);
+    // breadth-first order: parents before children, depths non-decreasing,
+    // the children of a node consecutive
+    std::vector<int32_t> depth(n, 0), first(n, -1), count(n, 0);
+    if (parent[0] != -1) return fail(ctx, ULSPEC_EINVAL, "spec_create_tree: parent[0] must be -1");
+    for (uint32_t i = 1; i < n; ++i) {
+        const int32_t p = parent[i];
+        if (p < 0 || p >= (int32_t)i) return fail(ctx, ULSPEC_EINVAL, "spec_create_tree: parent[%u]=%d", i, p);
+        depth[i] = depth[p] + 1;
+        if (depth[i] < depth[i - 1] || (first[p] >= 0 && first[p] + count[p] != (int32_t)i) ||
+            (i > 1 && parent[i - 1] > p))
+            return fail(ctx, ULSPEC_EINVAL, "spec_create_tree: nodes must be in breadth-first order (node %u)", i);
+        if (first[p] < 0) first[p] = (int32_t)i;
+        ++count[p];
+    }
+    ulspec_status st = spec_create(target, draft, n - 1, s, seed, 1, out);
+    if (st != ULSPEC_OK) return st;
+    ulspec_spec* sp = *out;
+    sp->tree = true;
+    sp->depth = (uint32_t)depth[n - 1];
+    sp->parent_h.assign(parent, parent + n);
+    sp->dparent_h.resize(n + 1);
+    sp->dparent_h[0] = -1;
+    for (uint32_t i = 0; i < n; ++i) sp->dparent_h[1 + i] = (int32_t)(parent[i] + 1);
+    sp->lv_first.assign(sp->depth + 1, 0);
+    sp->lv_count.assign(sp->depth + 1, 0);
+    for (uint32_t i = 0; i < n; ++i) {
+        if (sp->lv_count[depth[i]]++ == 0) sp->lv_first[depth[i]] = i;
+    }
+    std::vector<int32_t> tmap(n, 0), kf(n, 0), kc(n, 0);
+    for (uint32_t i = 1; i < n; ++i) tmap[i] = parent[i] - (int32_t)sp->lv_first[depth[i] - 1];
+    for (uint32_t i = 0; i < n; ++i) {
+        kf[i] = first[i] < 0 ? 0 : first[i];
+        kc[i] = count[i];
+    }
+    struct Want {
+        void** p;
+        size_t bytes;
+        const void* init;
+    } wants[] = {
+        {(void**)&sp->trow, 4 * (size_t)(n + 1), nullptr}, {(void**)&sp->tmap, 4 * (size_t)n, tmap.data()},
+        {(void**)&sp->kid_first, 4 * (size_t)n, kf.data()}, {(void**)&sp->kid_count, 4 * (size_t)n, kc.data()},
+        {(void**)&sp->path, 4 * (size_t)n, nullptr},
+    };
+    for (const Want& w : wants) {
+        hipError_t e = hipMalloc(w.p, w.bytes);
+        if (e == hipSuccess) sp->allocs.push_back(*w.p);
+        if (e == hipSuccess && w.init) e = hipMemcpy(*w.p, w.init, w.bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "spec_create_tree");
+        if (st != ULSPEC_OK) break;
+    }
+    // workspaces: the tree rule's, and the draws' over up to n - 1 parent rows of one level
+    const size_t ws_bytes[2] = {accept_tree_workspace_bytes(1, n), sample_workspace_bytes(n)};
+    void** ws_ptr[2] = {&sp->ws_accept, &sp->ws_sample};
+    for (int i = 0; i < 2 && st == ULSPEC_OK; ++i) {
+        void* ws = nullptr;
+        hipError_t e = hipMalloc(&ws, ws_bytes[i]);
+        if (e == hipSuccess) {
+            sp->allocs.push_back(ws);
+            *ws_ptr[i] = ws;
+        } else {
+            st = hip_fail(ctx, e, "spec_create_tree");
+        }
+    }
+    if (st != ULSPEC_OK) {
+        ulspec_spec_destroy(sp);
+        *out = nullptr;
+    }
+    return st;
+}
+
+extern "C" ulspec_status ulspec_spec_tree_last_step(ulspec_spec* sp, float* target_logits, float* draft_logits,
+                                                    int32_t* tokens, float* uniforms, int32_t* out_tokens,
+                                                    int32_t* path, int32_t* n_accepted)
+{
+    if (!sp) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = sp->ctx;
+    if (!sp->tree) return fail(ctx, ULSPEC_EINVAL, "spec_tree_last_step: not a tree loop");
+    (void)hipSetDevice(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    const size_t n = sp->k + 1, V = sp->V;
+    struct Copy {
+        void* dst;
+        const void* src;
+        size_t bytes;
+    } copies[] = {
+        {target_logits, sp->tlogits, n * V * 4}, {draft_logits, sp->dlogits, (n - 1) * V * 4},
+        {tokens, sp->trow + 1, n * 4},           {uniforms, sp->unif, (2 * n - 1) * 4},
+        {out_tokens, sp->out_tok, n * 4},        {path, sp->path, n * 4},
+        {n_accepted, sp->nacc, 4},
+    };
+    for (const Copy& c : copies)
+        if (e == hipSuccess && c.dst && c.bytes) e = hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "spec_tree_last_step copy");
+}
+
 extern "C" void ulspec_spec_destroy(ulspec_spec* sp)
 {
     if (!sp) return;
@@ -436,6 +612,7 @@ extern "C" ulspec_status ulspec_spec_steps(ulspec_spec* sp, uint32_t n_steps)
     if (!sp) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = sp->ctx;
     if (!sp->prefilled) return fail(ctx, ULSPEC_EINVAL, "spec_steps: no prefill");
+    if (sp->tree && sp->plain_first) return fail(ctx, ULSPEC_EINVAL, "spec_steps: a tree loop needs 2 prompt tokens");
     (void)hipSetDevice(ctx->device);
     if ((uint64_t)sp->n_hi + (uint64_t)n_steps * (sp->k + 1) > sp->cap) {
         ulspec_status st = sp->sync_state();

@@ -173,6 +173,15 @@ ulspec_status accept_tree_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint
                                  int32_t* out_path, int32_t* out_n_accepted, void* ws);
 ulspec_status sample_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V, const float* logits,
                             const float* uniforms, int32_t* out_tokens, void* ws);
+// D draws, draw d from row map[d] of logits [R][V] with uniforms[d] (the
+// workspace of sample_workspace_bytes(R)).
+ulspec_status sample_mapped_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t R, uint32_t V,
+                                   const float* logits, uint32_t D, const int32_t* map, const float* uniforms,
+                                   int32_t* out_tokens, void* ws);
+// Greedy tree drafting: the n_kids[i] best tokens of row i (logit desc, index
+// asc) to out_tokens[first_kid[i] ..].
+void topb_launch(ulspec_ctx* ctx, const float* logits, uint32_t V, uint32_t rows, const int32_t* first_kid,
+                 const int32_t* n_kids, int32_t* out_tokens);
 
 // Grow the context workspace to at least `bytes` (stream-ordered reuse).
 ulspec_status workspace(ulspec_ctx* ctx, size_t bytes, void** out);
