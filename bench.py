@@ -386,6 +386,50 @@ def workload_accept(pkg, ctx, args):
     }
 
 
+def workload_q6k(pkg, ctx, args):
+    """The LM-head-shaped verify GEMM of Q4_K_M files, output.weight 32000 x
+    4096 in Q6_K at M = 6: the native Q6_K kernel (0.82 B per weight) against
+    the same shape held as fp16 (2 B per weight, how Q6_K was run before).
+    Random Q6_K blocks (every 6-bit value and int8 scale is valid; d = 2^-12)
+    and random fp16 weights; copies rotated past the last-level cache."""
+    N, K, M = 32000, 4096, 6
+    rng = np.random.default_rng(args.seed)
+    nsb = K // 256
+    X = rng.standard_normal((M, K)).astype(np.float16).view(np.uint16)
+    xb, yb = ctx.upload(X), ctx.alloc(M * N * 4)
+    rows, out = [], {}
+    for name, wtype, nbytes in (("q6_k", pkg.Q6_K, N * nsb * 210), ("f16", pkg.F16, N * K * 2)):
+        if wtype == pkg.Q6_K:
+            blocks = rng.integers(0, 256, (N, nsb, 210), dtype=np.uint8)
+            blocks[:, :, 208:210] = np.full((N, nsb, 1), 2.0 ** -12, np.float16).view(np.uint8)
+        else:
+            blocks = (rng.standard_normal((N, K)) * 0.02).astype(np.float16).view(np.uint8)
+        nc = _copies(nbytes)
+        ids = [ctx.weight_upload(wtype, blocks, N, K) for _ in range(nc)]
+        del blocks
+        it = iter(range(1 << 30))
+        us = _time_direct(ctx, lambda: ctx.verify_gemm(ids[next(it) % nc], xb, M, yb), nc * args.reps)
+        alg = nbytes + 2 * M * K + 4 * M * N
+        gbs = alg / us / 1e3
+        out[name] = (us, alg, gbs)
+        rows.append({"type": name, "bytes_per_weight": nbytes / (N * K), "us": us, "GB/s": gbs,
+                     "weights_per_us": N * K / us})
+        log(f"{name} N={N} K={K} M={M}: {us:.2f} us, {alg / 1e6:.1f} MB, {gbs:.0f} GB/s "
+            f"({100 * gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s), {N * K / us / 1e6:.2f} G weights/ms")
+    xb.free()
+    yb.free()
+    us, alg, gbs = out["q6_k"]
+    return {
+        "metric": "Q6_K verify-GEMM HBM GB/s (32000x4096, M=6)", "value": gbs, "unit": "GB/s", "ms_per_step": us / 1e3,
+        "dtype": "q6_k weights x fp16 activations, fp32 accumulate",
+        "config": {"workload": "Q6_K verify dequant-GEMM N=32000 K=4096 M=6 against the fp16-held weight",
+                   "table": rows, "speedup_vs_f16": out["f16"][0] / us},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                     "traffic": None, "avg_us": us, "algorithmic_bytes": alg},
+        "cpu_baseline": None,
+    }
+
+
 def workload_read(pkg, ctx, args):
     """Streaming-read ceiling: the plain 16-byte-load read kernel over the
     byte counts of the verify GEMMs (the Q4_0 4096x11008 weight, the 7B Q4_K
@@ -451,11 +495,11 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read"),
+    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read", "q6k"),
                     default="step",
                     help="step: the speculative step (default); roofline: only the step's verify-GEMM roofline "
                          "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration; "
-                         "read: the streaming-read ceiling")
+                         "read: the streaming-read ceiling; q6k: the native Q6_K GEMM against fp16 at 32000x4096")
     ap.add_argument("--reps", type=int, default=50, help="launches per timing (kernel workloads)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch each step's kernels directly instead of replaying the captured graph")
@@ -484,7 +528,7 @@ def main():
         return 0
     if args.workload != "step":
         fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
-              "copy": workload_copy, "read": workload_read}[args.workload]
+              "copy": workload_copy, "read": workload_read, "q6k": workload_q6k}[args.workload]
         out = fn(pkg, ctx, args)
         base = {"n_gpus": 1, "steps": args.reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic, seeded"}

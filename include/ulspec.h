@@ -99,11 +99,11 @@ ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes,
 /* ---- K1: verify dequant-GEMM ------------------------------------------------
  * Upload one linear weight given as GGUF blocks (host memory, rows of K
  * elements, ne[0] = K contiguous; src/core/tensor.h:17-65).  The context keeps
- * a device copy re-tiled for the kernel: Q4_0 / Q4_K / Q8_0 in their own
- * 18 / 144 / 34 bytes per block; F16 as is; Q6_K (which Q4_K_M files mix in)
- * dequantized once to fp16 (d * scale * q rounded to fp16: the only inexact
- * step of that type).  K is a multiple of the block size, and
- * of 32 for F16.  weight_info reports the uploaded type.
+ * a device copy re-tiled for the kernel: Q4_0 / Q4_K / Q6_K / Q8_0 in their
+ * own 18 / 144 / 210 / 34 bytes per block (Q6_K: (q - 32) * scale formed in
+ * fp16 in the kernel, rounded only where its magnitude exceeds 2048); F16 as
+ * is.  K is a multiple of the block size, and of 32 for F16.  weight_info
+ * reports the uploaded type.
  * Replaces the first-use repack + upload of run_linear_q4k
  * (src/inference/inference_engine.cpp:536-548, repack_q4k_tensor :891-927). */
 ulspec_status ulspec_weight_upload(ulspec_ctx* ctx, uint32_t ggml_type, const void* gguf_blocks,

@@ -1,5 +1,6 @@
 """The GGUF types Q4_K_M files mix in (Q6_K, Q8_0, F16) on the GPU: the
-dequant-GEMM against the oracle's float64 product, and a model whose
+dequant-GEMM against the oracle's float64 product (Q6_K natively, read back
+bit for bit through unit rows), and a model whose
 tensors mix all five types (one fused QKV weight mixing Q4_K and Q6_K) read
 from a GGUF file against the oracle model.
 
@@ -69,6 +70,51 @@ def test_f16_gemm_is_exact_in_the_weights(ctx, ora, rng):
     X[np.arange(len(ks)), ks] = 1
     y = _gemm(ctx, wid, X.view(np.uint16), N)
     assert np.array_equal(y, W[:, ks].T.astype(np.float32))
+
+
+def _q6_k_fields(W, N, K):
+    """q (0..63), int8 scale and fp16 d of every element of GGUF Q6_K rows
+    (ggml's block_q6_K: ql[128] low nibbles, qh[64] 2-bit pairs, scales[16],
+    d), as [N][K] arrays."""
+    blk = W.reshape(N, K // 256, 210)
+    i = np.arange(256)
+    h, p = i // 128, i % 128
+    quarter, l = p // 32, p % 32
+    lo = blk[:, :, 64 * h + l + 32 * (quarter & 1)]
+    lo = np.where(quarter < 2, lo & 15, lo >> 4).astype(np.int32)
+    hb = ((blk[:, :, 128 + 32 * h + l] >> (2 * quarter)) & 3).astype(np.int32)
+    sc = blk[:, :, 192 + i // 16].view(np.int8).astype(np.int32)
+    d = np.ascontiguousarray(blk[:, :, 208:210]).view(np.float16)[..., 0]
+    return (lo | (hb << 4)).reshape(N, K), sc.reshape(N, K), np.repeat(d, 256, axis=1).reshape(N, K)
+
+
+def test_q6_k_gemm_reads_back_the_weights(ctx, ora, rng):
+    """Native Q6_K: with X = e_k rows the product reads back each weight as
+    f32(d) * f16((q - 32) sc), bit for bit -- exact wherever |(q - 32) sc|
+    <= 2048, one fp16 rounding beyond -- on the whole-X path (M = 8) and the
+    split-K path (M = 16).  The numpy decode is checked against the oracle's
+    dequantization first."""
+    N, K = 40, 512
+    W = ora.synth_q4(14, 21, 3, N, K)
+    W = W.reshape(N, K // 256, 210).copy()
+    W[:5, :, 192:208] = rng.integers(-128, 128, (5, K // 256, 16)).astype(np.int8).view(np.uint8)  # large scales
+    W = W.ravel()
+    q, sc, d = _q6_k_fields(W, N, K)
+    want_w = d.astype(np.float64) * sc * (q - 32)
+    assert np.array_equal(ora.dequantize(14, W, N * K).reshape(N, K), want_w.astype(np.float32))
+    wid = ctx.weight_upload(14, W, N, K)
+    b16 = ((q - 32) * sc).astype(np.float16).astype(np.float32)
+    want = d.astype(np.float32) * b16
+    assert (np.abs((q - 32) * sc) > 2048).any()  # the rounded case is covered
+    ks = np.array([0, 1, 7, 8, 15, 16, 31, 32, 63, 64, 100, 127, 128, 200, 255, 256,
+                   257, 300, 383, 384, 400, 450, 500, 511])
+    for M in (8, 16):
+        for k0 in range(0, len(ks), M):
+            kk = ks[k0:k0 + M]
+            X = np.zeros((len(kk), K), np.float16)
+            X[np.arange(len(kk)), kk] = 1
+            y = _gemm(ctx, wid, X.view(np.uint16), N)
+            assert np.array_equal(y, want[:, kk].T), (M, kk)
 
 
 def test_f16_k_must_be_a_multiple_of_32(pkg, ctx):

@@ -22,6 +22,17 @@
 //                 group g covers qs bytes 32g..32g+31 (sub-blocks 2g, 2g+1);
 //                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
 //     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
+//   Q6_K chunk (tile t, super-block s) = 3360 B (16 x 210, ggml's block_q6_K
+//   with the 6-bit values split and re-tiled):
+//     [0,2048)    low 4 bits, placed as the Q4_K nibbles (step j of lane l at
+//                 (j/4)*1024 + l*16 + (j%4)*4; lane group g covers elements
+//                 64g..64g+63 of the super-block, step j elements 64g+8j..+7)
+//     [2048,3072) high 2 bits, word w of lane l at 2048 + l*16 + w*4 for steps
+//                 2w (bit pairs at 4,20 8,24 12,28 0,16 for e0,e1 e2,e3 e4,e5
+//                 e6,e7) and 2w+1 (the same positions + 2), so that masking
+//                 before / after an 8-bit shift lines them up with the nibbles
+//     [3072,3328) the int8 scales (one per 16 elements) of row r at r*16
+//     [3328,3360) fp16 d of row r at r*2
 #include <type_traits>
 #include <utility>
 #include <vector>
@@ -44,14 +55,20 @@ constexpr int kQ40Chunk = 1152;
 // in GGUF.
 constexpr int kQ80Chunk = 2176;
 constexpr int kQ4KChunk = 2304;
+constexpr int kQ6KChunk = 3360;
 // fp16 weights (GGUF F16, and Q6_K or mixed-type fused weights converted at
 // upload): a chunk is
 // one 16-row tile x 128 K, 4 KB; lane l reads 16 contiguous bytes at
 // 1024 j + 16 l for MFMA j (rows l & 15, K 32 j + 8 (l >> 4) ..).
 constexpr int kF16Chunk = 4096;
-// 16-byte X units (8 halves) per weight chunk: 128 K for Q4_0 and F16, 256 for Q4_K
+// Types whose chunk is one 256-element super-block (lane group g takes
+// elements 64 g .. 64 g + 63 of it); the others take 128 K per chunk.
 template <int TYPE>
-constexpr int kUnitsPerChunk = TYPE == ULSPEC_GGML_Q4_K ? 32 : 16;
+constexpr bool kSuperBlock = TYPE == ULSPEC_GGML_Q4_K || TYPE == ULSPEC_GGML_Q6_K;
+// 16-byte X units (8 halves) per weight chunk: 128 K for Q4_0, Q8_0 and F16,
+// 256 for Q4_K and Q6_K
+template <int TYPE>
+constexpr int kUnitsPerChunk = kSuperBlock<TYPE> ? 32 : 16;
 
 __device__ __forceinline__ uint32_t perm_nibbles(const uint32_t q[8])
 {
@@ -152,6 +169,66 @@ __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
     }
 }
 
+// Element i (0..255) of a ggml block_q6_K (ql[128] low nibbles, qh[64] 2-bit
+// pairs, int8 scales[16], fp16 d): its 4 low bits, 2 high bits and scale.
+__device__ __forceinline__ void q6k_element(const uint8_t* blk, uint32_t i, uint32_t& lo, uint32_t& hb, int& sc)
+{
+    const uint32_t h = i / 128, p = i % 128, quarter = p / 32, l = p % 32;
+    const uint8_t byte = blk[64 * h + l + (quarter & 1 ? 32 : 0)];
+    lo = quarter < 2 ? (byte & 15u) : (byte >> 4);
+    hb = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+    sc = (int8_t)blk[192 + i / 16];
+}
+
+// One thread per (tile, super-block, lane, step j): the lane's low-nibble
+// word of step j, for even j the high-bit word of steps j and j + 1, and for
+// lane 0-15 / step 0 the row's scales and d; zeros past N.
+__global__ void repack_q6_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
+                                   uint32_t nsb, uint64_t total)
+{
+    const uint64_t id = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const uint32_t j = id & 7;
+    const uint32_t L = (id >> 3) & 63;
+    const uint64_t ts = id >> 9;  // t * nsb + s
+    const uint32_t s = (uint32_t)(ts % nsb), t = (uint32_t)(ts / nsb);
+    const uint32_t r = L & 15, g = L >> 4, n = 16 * t + r;
+    uint8_t* chunk = out + ts * kQ6KChunk;
+    const uint8_t* blk = n < N ? raw + ((uint64_t)n * nsb + s) * 210 : nullptr;
+    // bit position of the high pair of element e in its step's 16-bit pattern
+    constexpr uint32_t kHPos[8] = {4, 20, 8, 24, 12, 28, 0, 16};
+    uint32_t word = 0, hword = 0;
+    if (blk) {
+        uint32_t q[8];
+        for (uint32_t e = 0; e < 8; ++e) {
+            uint32_t hb;
+            int sc;
+            q6k_element(blk, 64 * g + 8 * j + e, q[e], hb, sc);
+        }
+        word = perm_nibbles(q);
+        for (uint32_t st = 0; st < 2 && (j & 1) == 0; ++st)
+            for (uint32_t e = 0; e < 8; ++e) {
+                uint32_t lo, hb;
+                int sc;
+                q6k_element(blk, 64 * g + 8 * (j + st) + e, lo, hb, sc);
+                hword |= hb << (kHPos[e] + 2 * st);
+            }
+    }
+    *(uint32_t*)(chunk + (j >> 2) * 1024 + L * 16 + (j & 3) * 4) = word;
+    if ((j & 1) == 0) *(uint32_t*)(chunk + 2048 + L * 16 + (j >> 1) * 4) = hword;
+    if (g == 0 && j == 0) {
+        uint32_t* dst = (uint32_t*)(chunk + 3072 + r * 16);
+        for (int w = 0; w < 4; ++w) {
+            uint32_t v = 0;
+            if (blk)
+                v = blk[192 + 4 * w] | (blk[193 + 4 * w] << 8) | (blk[194 + 4 * w] << 16) |
+                    ((uint32_t)blk[195 + 4 * w] << 24);
+            dst[w] = v;
+        }
+        *(uint16_t*)(chunk + 3328 + r * 2) = blk ? (uint16_t)(blk[208] | (blk[209] << 8)) : (uint16_t)0;
+    }
+}
+
 // GGUF rows -> fp16 rows (row r to out row out_row0 + r * out_row_step).
 // Q8_0: d * q; Q6_K: d * scale * q with the 6-bit q of ggml's block_q6_K (ql
 // low nibbles, qh 2-bit pairs, int8 scales per 16 elements, fp16 d last);
@@ -188,12 +265,10 @@ __global__ void dequant_rows_f16_kernel(const uint8_t* __restrict__ raw, _Float1
         v = half_bits_to_float(blk[0] | (blk[1] << 8)) * (float)(int8_t)blk[2 + k % 32];
     } else {  // Q6_K
         const uint8_t* blk = r + (uint64_t)(k / 256) * 210;
-        const uint32_t e = k % 256, h = e / 128, p = e % 128, quarter = p / 32, l = p % 32;
-        const uint8_t lo = blk[64 * h + l + (quarter & 1 ? 32 : 0)];
-        const uint32_t nib = quarter < 2 ? (lo & 15u) : (lo >> 4);
-        const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+        uint32_t nib, hb;
+        int sc;
+        q6k_element(blk, k % 256, nib, hb, sc);
         const int q = (int)(nib | (hb << 4)) - 32;
-        const int sc = (int8_t)blk[192 + 8 * h + l / 16 + 2 * quarter];
         v = half_bits_to_float(blk[208] | (blk[209] << 8)) * (float)sc * (float)q;
     }
     out[((uint64_t)out_row0 + row * out_row_step) * K + k] = (_Float16)v;
@@ -432,6 +507,12 @@ struct WBatch<ULSPEC_GGML_Q4_K, CMAX> {
     uint4 w0[CMAX], w1[CMAX], hd[CMAX];
 };
 template <int CMAX>
+struct WBatch<ULSPEC_GGML_Q6_K, CMAX> {
+    static constexpr int kLoadsPerChunk = 5;
+    uint4 w0[CMAX], w1[CMAX], hb[CMAX];
+    uint32_t sc[CMAX], d[CMAX];
+};
+template <int CMAX>
 struct WBatch<ULSPEC_GGML_Q8_0, CMAX> {
     static constexpr int kLoadsPerChunk = 3;
     uint4 w0[CMAX], w1[CMAX];
@@ -467,6 +548,13 @@ __device__ __forceinline__ void load_slot(const GemmArgs& a, __amdgpu_buffer_rsr
         const uint32_t o = ch * kQ40Chunk;
         b.wq[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
         b.sc[i] = buf_load8(wr, ok ? o + 1024 + r * 8 : kOOB);
+    } else if constexpr (TYPE == ULSPEC_GGML_Q6_K) {
+        const uint32_t o = ch * kQ6KChunk;
+        b.w0[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
+        b.w1[i] = buf_load16(wr, ok ? o + 1024 + lane * 16 : kOOB);
+        b.hb[i] = buf_load16(wr, ok ? o + 2048 + lane * 16 : kOOB);
+        b.sc[i] = __builtin_amdgcn_raw_buffer_load_b32(wr, ok ? o + 3072 + r * 16 + (lane >> 4) * 4 : kOOB, 0, 0);
+        b.d[i] = __builtin_amdgcn_raw_buffer_load_b16(wr, ok ? o + 3328 + r * 2 : kOOB, 0, 0);
     } else {
         const uint32_t o = ch * kQ4KChunk;
         b.w0[i] = buf_load16(wr, ok ? o + lane * 16 : kOOB);
@@ -610,6 +698,86 @@ __device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT],
     }
 }
 
+// Q6_K: 8 values -> fp16 (q - 32) * sc, q = low nibble | high pair << 4.  The
+// magic 0x6400 pairs are 1024 + q (pairs a, c) or 1024 + 16 q (b, d), the
+// high pairs ORed in under the magic first; subtracting 1056 / 1536 leaves
+// q - 32 / 16 (q - 32) exactly, and one multiply by sc / sc/16 rounds only
+// where |(q - 32) sc| > 2048 (2^-12 relative, as an fp16 copy of the
+// weight).  hx: the step's high-bit word (shifted right by 2 for odd steps).
+struct Q6Consts {
+    uint32_t m30, m300;  // 0x00300030, 0x03000300
+};
+
+__device__ __forceinline__ Q6Consts q6_consts()
+{
+    Q6Consts k;
+    k.m30 = 0x00300030u;
+    k.m300 = 0x03000300u;
+    asm volatile("" : "+v"(k.m30), "+v"(k.m300));
+    return k;
+}
+
+struct Q6Scale {
+    half2_t s1, s16;  // sc, sc / 16
+};
+
+__device__ __forceinline__ Q6Scale q6_scale(int sc)
+{
+    const float f = (float)sc;
+    return Q6Scale{splat2(f), splat2(f * 0.0625f)};
+}
+
+__device__ __forceinline__ half8_t dequant_q6_k(uint32_t v, uint32_t hx, const Q6Scale& s, const NibbleConsts& k,
+                                                const Q6Consts& k6)
+{
+    const uint32_t v8 = v >> 8;
+    const uint32_t ta = and_or(hx, k6.m30, k.magic), tb = and_or(hx, k6.m300, k.magic);
+    const uint32_t tc = and_or(hx >> 8, k6.m30, k.magic), td = and_or(hx << 8, k6.m300, k.magic);
+    const half2_t c1056 = splat2(-1056.0f), c1536 = splat2(-1536.0f);
+    const half2_t a = as_half2(and_or(v, k.lo, ta)) + c1056, b = as_half2(and_or(v, k.hi, tb)) + c1536;
+    const half2_t c = as_half2(and_or(v8, k.lo, tc)) + c1056, d = as_half2(and_or(v8, k.hi, td)) + c1536;
+    return make_half8(a * s.s1, b * s.s16, c * s.s1, d * s.s16);
+}
+
+// acc += d * (X . B) per chunk; lane group g's steps 2q, 2q + 1 share scale
+// byte q of its scale word (elements 64 g + 16 q ..).
+template <int CMAX, int MT>
+__device__ __forceinline__ void q6_k_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
+                                         int i1, const WBatch<ULSPEC_GGML_Q6_K, CMAX>& b, const NibbleConsts& nk,
+                                         float4_t (&acc)[MT])
+{
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+    const Q6Consts k6 = q6_consts();
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+        if (i < nc) {
+            const uint32_t words[8] = {b.w0[i].x, b.w0[i].y, b.w0[i].z, b.w0[i].w,
+                                       b.w1[i].x, b.w1[i].y, b.w1[i].z, b.w1[i].w};
+            const uint32_t hw[4] = {b.hb[i].x, b.hb[i].y, b.hb[i].z, b.hb[i].w};
+            const float dd = half_bits_to_float(b.d[i] & 0xffffu);
+            float4_t P[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) P[mt] = zero4;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const Q6Scale sc = q6_scale((int)(int8_t)(b.sc[i] >> (8 * q)));
+#pragma unroll
+                for (int st = 0; st < 2; ++st) {
+                    const int j = 2 * q + st;
+                    const half8_t B = dequant_q6_k(words[j], st ? hw[q] >> 2 : hw[q], sc, nk, k6);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + j]);
+                        P[mt] = mfma16x16x32(A, B, P[mt]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_elementwise_fma((float4_t)dd, P[mt], acc[mt]);
+        }
+    }
+}
+
 // F16: four MFMAs of 32 K per chunk, no dequantization.
 template <int CMAX, int MT>
 __device__ __forceinline__ void f16_mma(const uint4* xs, const int (&xrow)[MT], int cs, int c0, int nc, int i0,
@@ -637,6 +805,8 @@ __device__ __forceinline__ void stream_mma(const uint4* xs, const int (&xrow)[MT
         q8_0_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, acc);
     else if constexpr (TYPE == ULSPEC_GGML_Q4_0)
         q4_0_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, nk, acc);
+    else if constexpr (TYPE == ULSPEC_GGML_Q6_K)
+        q6_k_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, nk, acc);
     else
         q4_k_mma<CMAX, MT>(xs, xrow, cs, c0, nc, i0, i1, b, (threadIdx.x & 63) >> 4, nk, acc);
 }
@@ -928,7 +1098,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
     int xrow[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g);
+        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (kSuperBlock<TYPE> ? 8 * g : g);
     const NibbleConsts nk = nibble_consts();
     float4_t acc[MT];
 #pragma unroll
@@ -1107,7 +1277,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int CS = a.xrows * RS;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
-    const int xrow[1] = {xslot_row(a, 0, r) * RS + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g)};
+    const int xrow[1] = {xslot_row(a, 0, r) * RS + (kSuperBlock<TYPE> ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     const EpiPos pos0 = epi_pos0(a);
     const int it = blockIdx.x, t = it * tpi + tw;
@@ -1209,7 +1379,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int CS = a.xrows * RS;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
-    const int xrow[1] = {xslot_row(a, 0, r) * RS + (TYPE == ULSPEC_GGML_Q4_K ? 8 * g : g)};
+    const int xrow[1] = {xslot_row(a, 0, r) * RS + (kSuperBlock<TYPE> ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
@@ -1257,7 +1427,7 @@ template <int TYPE, int MT>
 constexpr int slice_cmax()
 {
     return TYPE == ULSPEC_GGML_Q4_0 ? (MT <= 2 ? 8 : 4)
-           : TYPE == ULSPEC_GGML_Q4_K ? (MT <= 2 ? 4 : MT <= 4 ? 2 : 1)
+           : kSuperBlock<TYPE> ? (MT <= 2 ? 4 : MT <= 4 ? 2 : 1)
            : TYPE == ULSPEC_GGML_Q8_0 ? (MT <= 2 ? 4 : 2)
                                        : (MT <= 2 ? 2 : 1);
 }
@@ -1295,7 +1465,7 @@ constexpr size_t kStaticRing = (size_t)2 * kRingWaves * 4 * 64 * sizeof(float) +
 // LDS bytes of the whole X of `rows` staged rows in the chunk-major layout.
 size_t x_lds_bytes(const Weight& w, int rows)
 {
-    const size_t rs = (w.type == ULSPEC_GGML_Q4_K ? 32 : 16) + 1;
+    const size_t rs = (w.type == ULSPEC_GGML_Q4_K || w.type == ULSPEC_GGML_Q6_K ? 32 : 16) + 1;
     return (size_t)w.n_chunks * rows * rs * 16;
 }
 
@@ -1311,6 +1481,7 @@ template <int... C>
 struct CList {};
 using WideQ40 = CList<1, 2, 3, 4, 6, 8>;
 using WideQ4K = CList<1, 2, 3, 4>;
+using WideQ6K = CList<1, 2, 3>;  // 14 VGPRs of weights per chunk
 using WideF16 = CList<1, 2>;  // 16 VGPRs of weights per chunk
 using WideQ80 = CList<1, 2, 3, 4, 6>;  // 10 VGPRs of weights per chunk
 
@@ -1323,6 +1494,10 @@ struct GemmCfg<ULSPEC_GGML_Q4_0> {
 template <>
 struct GemmCfg<ULSPEC_GGML_Q4_K> {
     using Wide = WideQ4K;
+};
+template <>
+struct GemmCfg<ULSPEC_GGML_Q6_K> {
+    using Wide = WideQ6K;
 };
 template <>
 struct GemmCfg<ULSPEC_GGML_Q8_0> {
@@ -1385,6 +1560,7 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
     type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings);
     type_kernels<ULSPEC_GGML_F16>(wide, small, rings);
     type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings);
+    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings);
     const struct {
         const std::vector<const void*>* fns;
         size_t fixed;
@@ -1457,6 +1633,7 @@ bool stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
     if (w.type == ULSPEC_GGML_Q4_0) return stream_launch_t<ULSPEC_GGML_Q4_0>(ctx, w, a);
     if (w.type == ULSPEC_GGML_Q4_K) return stream_launch_t<ULSPEC_GGML_Q4_K>(ctx, w, a);
+    if (w.type == ULSPEC_GGML_Q6_K) return stream_launch_t<ULSPEC_GGML_Q6_K>(ctx, w, a);
     if (w.type == ULSPEC_GGML_Q8_0) return stream_launch_t<ULSPEC_GGML_Q8_0>(ctx, w, a);
     return stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
 }
@@ -1514,6 +1691,7 @@ void split_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs a, float* part, flo
     const int mt = a.hl ? (a.M + 7) / 8 : (a.M + 15) / 16;
     if (w.type == ULSPEC_GGML_Q4_0) slice_launch_t<ULSPEC_GGML_Q4_0>(a, mt, ctx->stream);
     else if (w.type == ULSPEC_GGML_Q4_K) slice_launch_t<ULSPEC_GGML_Q4_K>(a, mt, ctx->stream);
+    else if (w.type == ULSPEC_GGML_Q6_K) slice_launch_t<ULSPEC_GGML_Q6_K>(a, mt, ctx->stream);
     else if (w.type == ULSPEC_GGML_Q8_0) slice_launch_t<ULSPEC_GGML_Q8_0>(a, mt, ctx->stream);
     else slice_launch_t<ULSPEC_GGML_F16>(a, mt, ctx->stream);
     if (direct) return;
@@ -1590,9 +1768,10 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
                             bool on_device, uint32_t* out_id)
 {
     if (!blocks || !out_id) return fail(ctx, ULSPEC_EINVAL, "weight_upload: null pointer");
-    const bool f16 = type == ULSPEC_GGML_F16 || type == ULSPEC_GGML_Q6_K;  // held as fp16
+    const bool f16 = type == ULSPEC_GGML_F16;
     const bool q80 = type == ULSPEC_GGML_Q8_0;
-    if (type != ULSPEC_GGML_Q4_0 && type != ULSPEC_GGML_Q4_K && !f16 && !q80)
+    const bool sb = type == ULSPEC_GGML_Q4_K || type == ULSPEC_GGML_Q6_K;  // 256-element super-blocks
+    if (type != ULSPEC_GGML_Q4_0 && !sb && !f16 && !q80)
         return fail(ctx, ULSPEC_EUNSUPPORTED, "weight_upload: ggml type %u not supported (Q4_0, Q4_K, Q6_K, Q8_0, F16)",
                     type);
     const int bs = ulspec_ggml_blck_size(type), ts = ulspec_ggml_type_size(type);
@@ -1603,14 +1782,15 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
     const size_t expect = (size_t)N * (K / bs) * ts;
     if (nbytes != expect) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes given, %zu expected", nbytes, expect);
     Weight w;
-    w.type = f16 ? (uint32_t)ULSPEC_GGML_F16 : type;  // Q6_K is held as fp16
+    w.type = type;
     w.src_type = type;
     w.n = N;
     w.k = K;
     w.n_tiles = (N + 15) / 16;
-    w.n_chunks = type == ULSPEC_GGML_Q4_K ? K / 256 : (K + 127) / 128;
+    w.n_chunks = sb ? K / 256 : (K + 127) / 128;
     w.bytes = (size_t)w.n_tiles * w.n_chunks *
-              (f16 ? kF16Chunk : q80 ? kQ80Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk : kQ4KChunk);
+              (f16 ? kF16Chunk : q80 ? kQ80Chunk : type == ULSPEC_GGML_Q4_0 ? kQ40Chunk
+                                              : type == ULSPEC_GGML_Q6_K ? kQ6KChunk : kQ4KChunk);
     if (w.bytes >= kOOB) return fail(ctx, ULSPEC_EINVAL, "weight_upload: %zu bytes exceeds the 2 GiB per-weight limit", w.bytes);
     w.ksplit = choose_ksplit(w.n_tiles, w.n_chunks, ctx->n_cu);
     (void)hipSetDevice(ctx->device);
@@ -1654,8 +1834,9 @@ ulspec_status weight_create(ulspec_ctx* ctx, uint32_t type, const void* blocks, 
                            (const uint8_t*)raw, w.dev, N, K / 32, w.n_chunks, total);
     } else {
         const uint64_t total = (uint64_t)w.n_tiles * w.n_chunks * 512;
-        hipLaunchKernelGGL(repack_q4_k_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream,
-                           (const uint8_t*)raw, w.dev, N, w.n_chunks, total);
+        hipLaunchKernelGGL(type == ULSPEC_GGML_Q6_K ? repack_q6_k_kernel : repack_q4_k_kernel,
+                           dim3((unsigned)((total + 255) / 256)), dim3(256), 0, ctx->stream, (const uint8_t*)raw,
+                           w.dev, N, w.n_chunks, total);
     }
     st = check_launch(ctx, "weight repack launch");
     if (st == ULSPEC_OK) {
