@@ -41,6 +41,10 @@ namespace {
 
 constexpr int kKMax = 256;       // largest supported top_k
 constexpr int kCandMax = 2048;   // candidate buffer of the fast top-k path
+constexpr int kRankMax = 512;    // candidates ranked by counting (more: a bitonic sort)
+constexpr int kMaxK = 16;        // draft tokens per sequence of one acceptance call
+// decide_kernel's dynamic LDS: 2k + 1 lists of up to K entries (u64 weight, i32 token)
+inline size_t decide_lds_bytes(uint32_t k, uint32_t K) { return (size_t)(2 * k + 1) * K * 12; }
 constexpr int kRowThreads = 1024;
 constexpr int kSeqThreads = 1024;
 constexpr int kRound = 8;         // float4 rounds in flight per thread in the vocabulary scans
@@ -276,18 +280,28 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
     }
     __syncthreads();
     const uint32_t nk = cand_count;
-    // re-sort the kept tokens by index (ascending) and store them
-    for (int t = tid; t < kKMax; t += NT)
-        buf[t] = t < (int)nk ? (((uint64_t)(0xffffffffu - (uint32_t)buf[t])) << 32 | (uint32_t)t) : 0;
-    // buf now: (index << 32 | position), positions index keptE; sort ascending by index
-    for (int t = tid; t < kKMax; t += NT)
-        if (t < (int)nk) buf[t] = ~buf[t];  // descending sort of ~x = ascending of x
-    bitonic_desc(buf, kKMax);
+    // the kept tokens in index order (ascending): each one's place is the
+    // count of kept tokens of smaller index (indices are distinct)
     for (int t = tid; t < (int)nk; t += NT) {
-        const uint64_t v = ~buf[t];
-        st->idx[t] = (int32_t)(v >> 32);
-        st->E[t] = keptE[(uint32_t)v];
+        const uint32_t it = 0xffffffffu - (uint32_t)buf[t];
+        int pos = 0;
+        for (int u = 0; u < (int)nk; ++u) pos += 0xffffffffu - (uint32_t)buf[u] < it;
+        st->idx[pos] = (int32_t)it;
+        st->E[pos] = keptE[t];
     }
+}
+
+// buf[0 .. k) = the k largest of the n distinct nonzero order keys c[0 .. n),
+// descending: each key's place is the count of larger keys.
+__device__ void rank_top_desc(const uint64_t* c, int n, uint32_t k, uint64_t* buf)
+{
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint64_t v = c[i];
+        uint32_t gt = 0;
+        for (int j = 0; j < n; ++j) gt += c[j] > v;
+        if (gt < k) buf[gt] = v;
+    }
+    __syncthreads();
 }
 
 // ---- row statistics ----------------------------------------------------------
@@ -721,9 +735,28 @@ __device__ __forceinline__ uint64_t residual_weight(uint64_t P, uint64_t Q, uint
     return r > 0.0 ? (uint64_t)__builtin_ldexp(r, sh) : 0;
 }
 
-// Kept-list helpers of decide_kernel (top-k mode; all threads call them):
-// copy a row's list into LDS with coalesced loads, and look a token's weight
-// up in one pass instead of a binary search of dependent loads.
+// Inverse-CDF draw over a kept list in index order (list_cdf_pick with the
+// workgroup): thread t < n holds weight wt of entry t; T = trunc(u Z); the
+// first entry with T < cumsum, else the last nonzero one, else V - 1.  All
+// threads call it and get the token.
+__device__ int32_t block_list_pick(const int32_t* idx, uint64_t wt, int n, uint64_t Z, float u, uint32_t V,
+                                   uint64_t* scratch, int32_t* pick)
+{
+    const int tid = threadIdx.x;
+    const uint64_t w = tid < n ? wt : 0;
+    const uint64_t T = (uint64_t)((double)u * (double)Z);
+    uint64_t excl = 0;
+    (void)block_exclusive_scan_u64<kSeqThreads>(w, excl, scratch);
+    const uint64_t lastp = block_max_u64<kSeqThreads>(w ? (uint64_t)(tid + 1) : 0, scratch);
+    if (tid == 0) *pick = -1;
+    __syncthreads();
+    if (w && T >= excl && T < excl + w) *pick = idx[tid];
+    __syncthreads();
+    const int32_t r = *pick;
+    return r >= 0 ? r : lastp ? idx[lastp - 1] : (int32_t)V - 1;
+}
+
+// A row's kept list copied into LDS with coalesced loads (all threads call it).
 __device__ __forceinline__ int stage_list(const RowStat& st, int32_t* sidx, uint64_t* sE)
 {
     const int n = st.nk;
@@ -734,84 +767,120 @@ __device__ __forceinline__ int stage_list(const RowStat& st, int32_t* sidx, uint
     return n;
 }
 
-__device__ __forceinline__ uint64_t list_weight(const int32_t* sidx, const uint64_t* sE, int n, int32_t x,
-                                                uint64_t* slot)
-{
-    if (threadIdx.x == 0) *slot = 0;
-    __syncthreads();
-    for (int t = threadIdx.x; t < n; t += blockDim.x)
-        if (sidx[t] == x) *slot = sE[t];  // token ids in a list are distinct
-    __syncthreads();
-    return *slot;
-}
-
 // Top-k / top-p acceptance of one sequence per workgroup (greedy and
-// full-vocabulary acceptance run in the chunk kernels below): the accept walk
-// on the kept lists, then the residual or bonus draw from the lists.
+// full-vocabulary acceptance run in the chunk kernels below).  All 2k + 1
+// kept lists of the sequence (target rows 0..k, draft rows 0..k-1; each at
+// most K = top_k entries) are staged in LDS with one round of loads, the
+// weights P(x_i), Q(x_i) of every draft token looked up in one pass, then the
+// accept walk, and the residual or bonus draw from the staged lists.
+// Dynamic LDS: (2k + 1) K (8 + 4) bytes.
 __global__ __launch_bounds__(kSeqThreads) void decide_kernel(const RowStat* __restrict__ stats,
                                                              const int32_t* __restrict__ draft_tokens,
                                                              const float* __restrict__ uniforms, uint32_t k,
-                                                             uint32_t V, int32_t* __restrict__ out,
+                                                             uint32_t K, uint32_t V, int32_t* __restrict__ out,
                                                              int32_t* __restrict__ nacc)
 {
-    __shared__ int32_t uidx[2 * kKMax];
-    __shared__ uint64_t uR[2 * kKMax];
-    __shared__ int32_t aidx[kKMax], bidx[kKMax];  // the position's target / draft lists
-    __shared__ uint64_t aE[kKMax], bE[kKMax];
-    __shared__ uint64_t wslot[2];
+    extern __shared__ uint64_t dyn[];
+    __shared__ int32_t nks[2 * kMaxK + 1];
+    __shared__ uint64_t Zs[2 * kMaxK + 1];
+    __shared__ int32_t sx[kMaxK];
+    __shared__ uint64_t Pw[kMaxK], Qw[kMaxK];
+    __shared__ uint64_t scratch[kSeqThreads / 64];
+    __shared__ uint32_t s_rej;
+    __shared__ int32_t s_pick;
     const int tid = threadIdx.x;
-    const uint32_t b = blockIdx.x;
-    const RowStat* ts = stats + (size_t)b * (k + 1);          // target rows
-    const RowStat* ds = stats + (size_t)gridDim.x * (k + 1) + (size_t)b * k;  // draft rows
+    const uint32_t b = blockIdx.x, L = 2 * k + 1;
+    const RowStat* ts = stats + (size_t)b * (k + 1);                            // target rows
+    const RowStat* ds = stats + (size_t)gridDim.x * (k + 1) + (size_t)b * k;   // draft rows
+    auto list = [&](uint32_t l) -> const RowStat& { return l <= k ? ts[l] : ds[l - k - 1]; };
+    uint64_t* sE = dyn;                          // [L][K]
+    int32_t* sI = (int32_t*)(dyn + (size_t)L * K);  // [L][K]
     const int32_t* x = draft_tokens + (size_t)b * k;
     const float* u = uniforms + (size_t)b * (k + 1);
     int32_t* o = out + (size_t)b * (k + 1);
 
+    // one round of loads: entries past a list's length are read (in bounds of
+    // its arrays) and never used
+    for (uint32_t e = tid; e < L * K; e += kSeqThreads) {
+        const uint32_t l = e / K, t = e - l * K;
+        sI[e] = list(l).idx[t];
+        sE[e] = list(l).E[t];
+    }
+    if (tid < (int)L) {
+        nks[tid] = list(tid).nk;
+        Zs[tid] = list(tid).Z;
+    }
+    if (tid < (int)k) {
+        sx[tid] = x[tid];
+        Pw[tid] = 0;
+        Qw[tid] = 0;
+    }
     for (uint32_t i = tid; i <= k; i += kSeqThreads) o[i] = -1;
-    for (uint32_t i = 0; i < k; ++i) {
-        const int32_t xi = x[i];
-        const uint64_t Zp = ts[i].Z, Zq = ds[i].Z;
-        __syncthreads();  // the previous position's lists are no longer read
-        const int na = stage_list(ts[i], aidx, aE);
-        const int nb = stage_list(ds[i], bidx, bE);
-        const uint64_t Px = list_weight(aidx, aE, na, xi, &wslot[0]);
-        const uint64_t Qx = list_weight(bidx, bE, nb, xi, &wslot[1]);
-        const double lhs = ((double)u[i] * (double)Qx) * (double)Zp;
-        const double rhs = (double)Px * (double)Zq;
-        if (lhs < rhs) {
-            if (tid == 0) o[i] = xi;
-            continue;
-        }
-        // first rejection: draw from max(0, p - q) with u[k] (from p when that is all zero)
-        const int sh = 62 - bitlen64(Zp) - bitlen64(Zq);
-        if (tid == 0) {  // both lists are in LDS
-            int ia = 0, ib = 0, n = 0;
-            uint64_t SR = 0;
-            while (ia < na || ib < nb) {
-                const int32_t ja = ia < na ? aidx[ia] : 0x7fffffff;
-                const int32_t jb = ib < nb ? bidx[ib] : 0x7fffffff;
-                const int32_t j = ja < jb ? ja : jb;
-                const uint64_t P = ja == j ? aE[ia++] : 0;
-                const uint64_t Q = jb == j ? bE[ib++] : 0;
-                const uint64_t R = residual_weight(P, Q, Zp, Zq, sh);
-                uidx[n] = j;
-                uR[n] = R;
-                SR += R;
-                ++n;
+    __syncthreads();
+    // P(x_i) from target list i, Q(x_i) from draft list i (token ids in a list are distinct)
+    for (uint32_t e = tid; e < L * K; e += kSeqThreads) {
+        const uint32_t l = e / K, t = e - l * K;
+        if (l == k || (int)t >= nks[l]) continue;
+        const uint32_t i = l < k ? l : l - k - 1;
+        if (sI[e] == sx[i]) (l < k ? Pw : Qw)[i] = sE[e];
+    }
+    __syncthreads();
+    if (tid == 0) {  // the accept walk: the first rejected position, k if none
+        uint32_t rej = k;
+        for (uint32_t i = 0; i < k; ++i) {
+            const double lhs = ((double)u[i] * (double)Qw[i]) * (double)Zs[i];
+            const double rhs = (double)Pw[i] * (double)Zs[k + 1 + i];
+            if (!(lhs < rhs)) {
+                rej = i;
+                break;
             }
-            o[i] = SR ? list_cdf_pick(uidx, uR, n, SR, u[k], V) : list_cdf_pick(aidx, aE, na, Zp, u[k], V);
-            nacc[b] = (int32_t)i;
+            o[i] = sx[i];
         }
+        s_rej = rej;
+        nacc[b] = (int32_t)rej;
+    }
+    __syncthreads();
+    const uint32_t i = s_rej;
+    if (i == k) {  // every draft accepted: bonus token from the target row k
+        const int n = nks[k];
+        const int32_t t = block_list_pick(sI + (size_t)k * K, tid < n ? sE[(size_t)k * K + tid] : 0, n, Zs[k], u[k],
+                                          V, scratch, &s_pick);
+        if (tid == 0) o[k] = t;
         return;
     }
-    // every draft accepted: bonus token from the target row k
-    __syncthreads();
-    const int na = stage_list(ts[k], aidx, aE);
-    __syncthreads();
-    if (tid == 0) {
-        o[k] = list_cdf_pick(aidx, aE, na, ts[k].Z, u[k], V);
-        nacc[b] = (int32_t)k;
+    // first rejection at i: draw from max(0, p - q) with u[k] (from p when that
+    // is all zero).  Tokens only in the draft list weigh 0 in the residual, so
+    // the draw runs over the target list's entries (index order) with weights
+    // R = residual(P, Q) -- Q looked up by binary search in the draft list.
+    const uint64_t Zp = Zs[i], Zq = Zs[k + 1 + i];
+    const int sh = 62 - bitlen64(Zp) - bitlen64(Zq);
+    const int32_t* aidx = sI + (size_t)i * K;
+    const uint64_t* aE = sE + (size_t)i * K;
+    const int32_t* bidx = sI + (size_t)(k + 1 + i) * K;
+    const uint64_t* bE = sE + (size_t)(k + 1 + i) * K;
+    const int na = nks[i], nb = nks[k + 1 + i];
+    uint64_t R = 0, P = 0;
+    if (tid < na) {
+        const int32_t j = aidx[tid];
+        P = aE[tid];
+        int lo = 0, hi = nb - 1;
+        uint64_t Q = 0;
+        while (lo <= hi) {
+            const int mid = (lo + hi) >> 1;
+            const int32_t v = bidx[mid];
+            if (v == j) {
+                Q = bE[mid];
+                break;
+            }
+            if (v < j) lo = mid + 1;
+            else hi = mid - 1;
+        }
+        R = residual_weight(P, Q, Zp, Zq, sh);
     }
+    const uint64_t SR = block_sum_u64<kSeqThreads>(R, scratch);
+    const int32_t t = SR ? block_list_pick(aidx, R, na, SR, u[k], V, scratch, &s_pick)
+                         : block_list_pick(aidx, P, na, Zp, u[k], V, scratch, &s_pick);
+    if (tid == 0) o[i] = t;
 }
 
 // ---- tree acceptance ------------------------------------------------------------
@@ -1486,10 +1555,35 @@ inline TopkWs topk_ws(void* ws, uint32_t rows)
     return w;
 }
 
-__global__ __launch_bounds__(kChunkThreads) void topk_scan_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, TopkWs w)
+// Leading per-thread maxima the scan keeps per wave when the candidate
+// threshold comes from them (topk_m > 0): 4 G m distinct tokens per row, so
+// the k-th largest of them is <= the row's k-th largest logit and the tokens
+// at or above it include the top k (about k + k/5 of them at m = ceil(k / 4G)
+// + 1 on N(0, 3^2) rows).  topk_m = 0: the radix-select threshold over all
+// G x 256 per-thread maxima (topk_threshold_kernel), for rows of few chunks.
+constexpr int kTopM = 8;
+constexpr int kScanWaves = kChunkThreads / 64;
+
+__host__ __device__ inline int topk_m(uint32_t k, uint32_t G)
+{
+    const uint32_t waves = kScanWaves * G;
+    const uint32_t m = (k + waves - 1) / waves + 1;
+    if (m <= (uint32_t)kTopM) return (int)m;
+    return waves * kTopM >= k ? kTopM : 0;
+}
+
+// The row's kept per-wave maximum keys [G][kScanWaves][kTopM] (in the
+// per-thread maxima region).
+__device__ __forceinline__ uint32_t* topk_tops(const TopkWs& w, uint32_t r)
+{
+    return w.tm + (size_t)r * kMaxChunks * kScanWaves * kTopM;
+}
+
+__global__ __launch_bounds__(kChunkThreads) void topk_scan_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, int m, TopkWs w)
 {
     __shared__ uint64_t scratch[kChunkThreads / 64];
     const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float* row = rs.row(r, V);
     const uint32_t q1 = min(V4, (g + 1) * cp.CG);
     uint64_t best = 0;  // order key: the thread's largest key, lowest index among equals
@@ -1503,9 +1597,58 @@ __global__ __launch_bounds__(kChunkThreads) void topk_scan_kernel(RowSrc rs, uin
                 best = o > best ? o : best;
             }
     }
-    w.tm[((size_t)r * cp.G + g) * kChunkThreads + threadIdx.x] = (uint32_t)(best >> 32);  // 0: no token
+    if (m == 0) {
+        w.tm[((size_t)r * cp.G + g) * kChunkThreads + threadIdx.x] = (uint32_t)(best >> 32);  // 0: no token
+    } else {
+        // the wave's m largest per-thread maximum keys, strictly decreasing (so
+        // from distinct tokens; a key equal to one taken is skipped; 0 = none)
+        uint32_t* out = topk_tops(w, r) + ((size_t)g * kScanWaves + wave) * kTopM;
+        const uint32_t bk = (uint32_t)(best >> 32);
+        uint32_t prev = 0xffffffffu;
+        for (int j = 0; j < m; ++j) {  // uniform
+            uint32_t v = bk < prev ? bk : 0u;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+            if (lane == j) out[j] = v;
+            prev = v;
+        }
+        if (g == 0 && threadIdx.x == 0) w.cnt[(size_t)r * kCntPad] = 0;
+    }
     best = block_max_u64<kChunkThreads>(best, scratch);
     if (threadIdx.x == 0) w.part[(size_t)r * cp.G + g].top = best;
+}
+
+// Candidate threshold of each row (topk_m > 0), one workgroup per row: the
+// largest kept key v with at least k kept keys >= v (they are keys of
+// distinct tokens, so at least k tokens are >= v; 0 -- every token -- if
+// there is none, and the finish then takes its exact fallback), and the
+// row's max / argmax from the chunk maxima.
+constexpr int kT0Threads = 256;
+__global__ __launch_bounds__(kT0Threads) void topk_t0_kernel(ChunkPlan cp, int m, uint32_t k, TopkWs w)
+{
+    __shared__ uint32_t sv[kMaxChunks * kScanWaves * kTopM];
+    __shared__ uint64_t scratch[kT0Threads / 64];
+    const uint32_t r = blockIdx.x;
+    const int n = (int)cp.G * kScanWaves * m;
+    const uint32_t* tops = topk_tops(w, r);
+    for (int i = threadIdx.x; i < n; i += kT0Threads) sv[i] = tops[(i / m) * kTopM + i % m];
+    const uint64_t top =
+        block_max_u64<kT0Threads>(threadIdx.x < cp.G ? w.part[(size_t)r * cp.G + threadIdx.x].top : 0, scratch);
+    uint32_t thr = 0;
+    for (int i = threadIdx.x; i < n; i += kT0Threads) {
+        const uint32_t v = sv[i];
+        if (!v) continue;
+        uint32_t ge = 0;
+        for (int j = 0; j < n; ++j) ge += sv[j] >= v;
+        if (ge >= k && v > thr) thr = v;
+    }
+    thr = (uint32_t)block_max_u64<kT0Threads>(thr, scratch);
+    if (threadIdx.x == 0) {
+        RowStat* st = w.stats + r;
+        st->lmax = key_float((uint32_t)(top >> 32));
+        st->argmax = (int32_t)(0xffffffffu - (uint32_t)top);
+        w.t0[r] = thr;
+    }
 }
 
 // k-th largest of the row's G x 256 per-thread maxima by an 8-bit radix
@@ -1588,6 +1731,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan c
     }
 }
 
+// Tokens with logit key >= the row's threshold into its candidate list.
 __global__ __launch_bounds__(kChunkThreads) void topk_collect_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, TopkWs w)
 {
     const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
@@ -1635,10 +1779,15 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
     RowStat* st = w.stats + r;
     const uint32_t nc = w.cnt[(size_t)r * kCntPad];
     const float lmax = st->lmax;
-    if (nc <= (uint32_t)kCandMax) {
+    const uint64_t* c = w.cand + (size_t)r * kCandMax;
+    if (nc <= (uint32_t)kRankMax) {  // few candidates (the usual case): places by counting
+        __shared__ uint64_t cs[kRankMax];
+        for (int i = threadIdx.x; i < (int)nc; i += kRowThreads) cs[i] = c[i];
+        __syncthreads();
+        rank_top_desc(cs, (int)nc, k, buf);
+    } else if (nc <= (uint32_t)kCandMax) {
         int n2 = 1;
         while (n2 < (int)nc) n2 <<= 1;
-        const uint64_t* c = w.cand + (size_t)r * kCandMax;
         for (int i = threadIdx.x; i < n2; i += kRowThreads) buf[i] = i < (int)nc ? c[i] : 0;
         bitonic_desc(buf, n2);
     } else {
@@ -1651,8 +1800,10 @@ void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, cons
 {
     const ChunkPlan cp = chunk_plan(V);
     const dim3 grid(cp.G, rows), blk(kChunkThreads);
-    hipLaunchKernelGGL(topk_scan_kernel, grid, blk, 0, s, rs, V, cp, w);
-    hipLaunchKernelGGL(topk_threshold_kernel, dim3(rows), dim3(kRowThreads), 0, s, cp, p.top_k, w);
+    const int m = topk_m(p.top_k, cp.G);
+    hipLaunchKernelGGL(topk_scan_kernel, grid, blk, 0, s, rs, V, cp, m, w);
+    if (m == 0) hipLaunchKernelGGL(topk_threshold_kernel, dim3(rows), dim3(kRowThreads), 0, s, cp, p.top_k, w);
+    else hipLaunchKernelGGL(topk_t0_kernel, dim3(rows), dim3(kT0Threads), 0, s, cp, m, p.top_k, w);
     hipLaunchKernelGGL(topk_collect_kernel, grid, blk, 0, s, rs, V, cp, w);
     hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kRowThreads), 0, s, rs, V, p, w);
 }
@@ -1752,8 +1903,8 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     const TopkWs tw = topk_ws(ws, rows_t + rows_d);
     RowStat* stats = tw.stats;
     launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw);
-    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)stats, draft_tokens,
-                       uniforms, k, V, out_tokens, out_n_accepted);
+    hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), decide_lds_bytes(k, p.top_k), ctx->stream,
+                       (const RowStat*)stats, draft_tokens, uniforms, k, p.top_k, V, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
 }
 
@@ -1882,6 +2033,10 @@ static __device__ __align__(256) uint8_t noalloc_scratch[ULSPEC_ACCEPT_NOALLOC_S
 namespace ulspec {
 ulspec_status accept_init(ulspec_ctx* ctx)
 {
+    // decide_kernel's staged lists reach (2 kMaxK + 1) kKMax (8 + 4) bytes
+    hipError_t ea = hipFuncSetAttribute((const void*)decide_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)decide_lds_bytes(kMaxK, kKMax));
+    if (ea != hipSuccess) return hip_fail(ctx, ea, "hipFuncSetAttribute(decide_kernel)");
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
     if (e != hipSuccess || !p) return hip_fail(ctx, e, "hipGetSymbolAddress(accept scratch)");
