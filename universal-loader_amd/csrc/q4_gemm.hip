@@ -21,7 +21,11 @@
 //     [0,2048)    step j (0..7) of lane l at (j/4)*1024 + l*16 + (j%4)*4; lane
 //                 group g covers qs bytes 32g..32g+31 (sub-blocks 2g, 2g+1);
 //                 steps 0-3 are sub-block 2g, 4-7 sub-block 2g+1
-//     [2048,2304) the 16 header bytes (d, dmin, scales[12]) of row r at r*16
+//     [2048,2304) row r's 16-byte header at r*16: d | dmin << 16, then the
+//                 eight 6-bit scales and mins re-packed per lane group: bits
+//                 24g .. 24g+23 of the next 96 bits are sc[2g], sc[2g+1],
+//                 m[2g], m[2g+1] (6 bits each), the same values as GGUF's
+//                 12-byte packing, placed for a two-word funnel shift
 //   Q6_K chunk (tile t, super-block s) = 3360 B (16 x 210, ggml's block_q6_K
 //   with the 6-bit values split and re-tiled):
 //     [0,2048)    low 4 bits, placed as the Q4_K nibbles (step j of lane l at
@@ -137,6 +141,19 @@ __global__ void repack_q8_0_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
     if (g == 0) *(uint16_t*)(chunk + 2048 + r * 8 + j * 2) = d;
 }
 
+// 6-bit scale / min of sub-block j (0..7) from the 12 packed bytes held in
+// words y (bytes 0-3), z (4-7), w (8-11); branch-free in j.
+__device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w, int j, uint32_t& sc, uint32_t& m)
+{
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t by = (y >> sh) & 255u, bz = (z >> sh) & 255u, bw = (w >> sh) & 255u;
+    const uint32_t sc_lo = by & 63u, m_lo = bz & 63u;
+    const uint32_t sc_hi = (bw & 15u) | ((by >> 6) << 4), m_hi = (bw >> 4) | ((bz >> 6) << 4);
+    const bool lo = j < 4;
+    sc = lo ? sc_lo : sc_hi;
+    m = lo ? m_lo : m_hi;
+}
+
 __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __restrict__ out, uint32_t N,
                                    uint32_t nsb, uint64_t total)
 {
@@ -161,11 +178,24 @@ __global__ void repack_q4_k_kernel(const uint8_t* __restrict__ raw, uint8_t* __r
     *(uint32_t*)(chunk + (j >> 2) * 1024 + L * 16 + (j & 3) * 4) = word;
     if (g == 0 && j == 0) {
         uint32_t* dst = (uint32_t*)(chunk + 2048 + r * 16);
-        for (int w = 0; w < 4; ++w) {
-            uint32_t v = 0;
-            if (blk) v = blk[4 * w] | (blk[4 * w + 1] << 8) | (blk[4 * w + 2] << 16) | ((uint32_t)blk[4 * w + 3] << 24);
-            dst[w] = v;
+        uint32_t hw[4] = {0, 0, 0, 0};
+        if (blk)
+            for (int w = 0; w < 4; ++w)
+                hw[w] = blk[4 * w] | (blk[4 * w + 1] << 8) | (blk[4 * w + 2] << 16) | ((uint32_t)blk[4 * w + 3] << 24);
+        uint64_t lo = 0, hi = 0;  // the 96 re-packed bits
+        for (int gg = 0; gg < 4; ++gg) {
+            uint32_t s0, m0, s1, m1;
+            q4k_scale_min(hw[1], hw[2], hw[3], 2 * gg, s0, m0);
+            q4k_scale_min(hw[1], hw[2], hw[3], 2 * gg + 1, s1, m1);
+            const uint64_t bits = s0 | (s1 << 6) | (m0 << 12) | (m1 << 18);
+            const int at = 24 * gg;
+            if (at < 64) lo |= bits << at;
+            if (at + 24 > 64) hi |= at >= 64 ? bits << (at - 64) : bits >> (64 - at);
         }
+        dst[0] = hw[0];
+        dst[1] = (uint32_t)lo;
+        dst[2] = (uint32_t)(lo >> 32);
+        dst[3] = (uint32_t)hi;
     }
 }
 
@@ -421,18 +451,6 @@ __device__ __forceinline__ half8_t dequant_q4_k(uint32_t v, const SubScale& s, c
     return make_half8(a, b, c, d);
 }
 
-// 6-bit scale / min of sub-block j (0..7) from the 12 packed bytes held in
-// words y (bytes 0-3), z (4-7), w (8-11); branch-free in j.
-__device__ __forceinline__ void q4k_scale_min(uint32_t y, uint32_t z, uint32_t w, int j, uint32_t& sc, uint32_t& m)
-{
-    const uint32_t sh = 8u * (uint32_t)(j & 3);
-    const uint32_t by = (y >> sh) & 255u, bz = (z >> sh) & 255u, bw = (w >> sh) & 255u;
-    const uint32_t sc_lo = by & 63u, m_lo = bz & 63u;
-    const uint32_t sc_hi = (bw & 15u) | ((by >> 6) << 4), m_hi = (bw >> 4) | ((bz >> 6) << 4);
-    const bool lo = j < 4;
-    sc = lo ? sc_lo : sc_hi;
-    m = lo ? m_lo : m_hi;
-}
 
 // ---- X operand and common pieces -------------------------------------------
 // X is fp16 rows [M][K] (hl = 0), or split fp32 activations (hl = 1): the
@@ -659,18 +677,20 @@ __device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT],
             const uint4 h = b.hd[i];
             const float d = half_bits_to_float(h.x & 0xffffu);
             const float dmin = half_bits_to_float(h.x >> 16);
+            // this lane group's 24 bits: (z:y) >> 24g for g < 2, (w:z) >> (24g - 32) beyond
+            const uint64_t pair = g < 2 ? ((uint64_t)h.z << 32 | h.y) : ((uint64_t)h.w << 32 | h.z);
+            const uint32_t bits = (uint32_t)(pair >> (g < 2 ? 24 * g : 24 * g - 32));
             SubScale ss[2];
             half8_t mins[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                uint32_t scv, mn;
-                q4k_scale_min(h.y, h.z, h.w, 2 * g + e, scv, mn);
-                const float fs = (float)scv;
-                ss[e].sc = splat2(fs);
-                ss[e].nsc1024 = splat2(-1024.0f * fs);
-                ss[e].sc16 = splat2(fs * 0.0625f);
-                ss[e].nsc64 = splat2(-64.0f * fs);
-                const _Float16 hm = (_Float16)(float)mn;
+                const uint32_t scv = (bits >> (6 * e)) & 63u, mn = (bits >> (12 + 6 * e)) & 63u;
+                const _Float16 hs = (_Float16)(uint16_t)scv;  // exact, as are the products below
+                ss[e].sc = half2_t{hs, hs};
+                ss[e].nsc1024 = ss[e].sc * splat2(-1024.0f);
+                ss[e].sc16 = ss[e].sc * splat2(0.0625f);
+                ss[e].nsc64 = ss[e].sc * splat2(-64.0f);
+                const _Float16 hm = (_Float16)(uint16_t)mn;
                 mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
             }
             float4_t P1[MT], P2[MT];
