@@ -36,7 +36,7 @@ def _close(y, ref):
 
 @pytest.mark.parametrize("wtype", [1, 8, 14], ids=["f16", "q8_0", "q6_k"])
 @pytest.mark.parametrize("N,K,Ms", [(4096, 4096, (1, 6, 17)), (32000, 4096, (6,)), (100, 1536, (1, 3, 33)),
-                                    (40, 512, (2, 65))])
+                                    (40, 512, (2, 65)), (2048, 11008, (9,))])
 def test_gemm_matches_oracle(ctx, ora, rng, wtype, N, K, Ms):
     print(f"type {wtype} N {N} K {K}", flush=True)
     W = ora.synth_q4(wtype, 13, N + K, N, K)

@@ -42,7 +42,7 @@ CASES = [
     (2, 4096, 11008, (1, 5, 9, 17)),
     (12, 4096, 4096, (1, 6, 17)),
     (12, 11008, 4096, (5, 48)),
-    (12, 4096, 11008, (1, 6)),
+    (12, 4096, 11008, (1, 6, 9, 16)),  # M >= 9: X past LDS, the split-K kernel
     (2, 100, 1376, (1, 3, 16, 33)),   # N % 16 != 0, K = 43 blocks (partial quad)
     (12, 40, 512, (2, 64, 65)),       # M > 64 splits into launches
     (2, 32000, 512, (5,)),            # LM-head shape of the small model
