@@ -324,14 +324,16 @@ extern "C" ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec
     m->n_seq = n_seq;
     // slice partials of the split-K path: the most any of the model's weights
     // needs at R rows (slices are chosen at upload from the tile and chunk
-    // counts; ceil(K / 128) bounds the chunks of every weight type)
+    // counts; a weight's chunks are ceil(K / 128), or ceil(K / 256) for the
+    // super-block types)
     {
         const uint32_t shapes[5][2] = {{(H + 2 * Hkv) * D, c.dim}, {c.dim, H * D}, {2 * F, c.dim}, {c.dim, F},
                                        {c.vocab, c.dim}};
-        for (const auto& nk : shapes) {
-            const uint32_t ks = choose_ksplit((nk[0] + 15) / 16, (nk[1] + 127) / 128, ctx->n_cu);
-            m->part_bytes = std::max(m->part_bytes, (size_t)ks * R * nk[0] * sizeof(float));
-        }
+        for (const auto& nk : shapes)
+            for (uint32_t ck : {128u, 256u}) {
+                const uint32_t ks = choose_ksplit((nk[0] + 15) / 16, (nk[1] + ck - 1) / ck, ctx->n_cu);
+                m->part_bytes = std::max(m->part_bytes, (size_t)ks * R * nk[0] * sizeof(float));
+            }
     }
     m->pss_stride = std::max(embed_partials(c.dim), (c.dim + 15) / 16);
     const size_t kv_bytes = (size_t)n_seq * c.max_ctx * Hkv * D * sizeof(_Float16);

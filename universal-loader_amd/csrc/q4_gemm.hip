@@ -660,6 +660,36 @@ __device__ __forceinline__ void q8_0_mma(const uint4* xs, const int (&xrow)[MT],
     }
 }
 
+// Q4_K chunk header of lane group g: d, dmin, the sub-scales of sub-blocks
+// 2g and 2g + 1 (fp16 products for dequant_q4_k, exact) and their 6-bit mins
+// (bits 0-5 and 6-11 of mn).
+struct Q4KHead {
+    float d, dmin;
+    SubScale ss[2];
+    uint32_t mn;
+};
+
+__device__ __forceinline__ Q4KHead q4k_head(uint4 h, int g)
+{
+    Q4KHead q;
+    q.d = half_bits_to_float(h.x & 0xffffu);
+    q.dmin = half_bits_to_float(h.x >> 16);
+    // this lane group's 24 bits: (z:y) >> 24g for g < 2, (w:z) >> (24g - 32) beyond
+    const uint64_t pair = g < 2 ? ((uint64_t)h.z << 32 | h.y) : ((uint64_t)h.w << 32 | h.z);
+    const uint32_t bits = (uint32_t)(pair >> (g < 2 ? 24 * g : 24 * g - 32));
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t scv = (bits >> (6 * e)) & 63u;
+        const _Float16 hs = (_Float16)(uint16_t)scv;  // exact, as are the products below
+        q.ss[e].sc = half2_t{hs, hs};
+        q.ss[e].nsc1024 = q.ss[e].sc * splat2(-1024.0f);
+        q.ss[e].sc16 = q.ss[e].sc * splat2(0.0625f);
+        q.ss[e].nsc64 = q.ss[e].sc * splat2(-64.0f);
+    }
+    q.mn = (bits >> 12) & 4095u;
+    return q;
+}
+
 // Q4_K: B = q * sc exactly, one MFMA chain per super-block scaled by d, and the
 // min term as a second chain with the 6-bit mins as the B operand, scaled by
 // -dmin.
@@ -674,23 +704,11 @@ __device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT],
         if (i < nc) {
             const uint32_t words[8] = {b.w0[i].x, b.w0[i].y, b.w0[i].z, b.w0[i].w,
                                        b.w1[i].x, b.w1[i].y, b.w1[i].z, b.w1[i].w};
-            const uint4 h = b.hd[i];
-            const float d = half_bits_to_float(h.x & 0xffffu);
-            const float dmin = half_bits_to_float(h.x >> 16);
-            // this lane group's 24 bits: (z:y) >> 24g for g < 2, (w:z) >> (24g - 32) beyond
-            const uint64_t pair = g < 2 ? ((uint64_t)h.z << 32 | h.y) : ((uint64_t)h.w << 32 | h.z);
-            const uint32_t bits = (uint32_t)(pair >> (g < 2 ? 24 * g : 24 * g - 32));
-            SubScale ss[2];
+            const Q4KHead hd = q4k_head(b.hd[i], g);
             half8_t mins[2];
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const uint32_t scv = (bits >> (6 * e)) & 63u, mn = (bits >> (12 + 6 * e)) & 63u;
-                const _Float16 hs = (_Float16)(uint16_t)scv;  // exact, as are the products below
-                ss[e].sc = half2_t{hs, hs};
-                ss[e].nsc1024 = ss[e].sc * splat2(-1024.0f);
-                ss[e].sc16 = ss[e].sc * splat2(0.0625f);
-                ss[e].nsc64 = ss[e].sc * splat2(-64.0f);
-                const _Float16 hm = (_Float16)(uint16_t)mn;
+                const _Float16 hm = (_Float16)(uint16_t)((hd.mn >> (6 * e)) & 63u);
                 mins[e] = half8_t{hm, hm, hm, hm, hm, hm, hm, hm};
             }
             float4_t P1[MT], P2[MT];
@@ -701,7 +719,7 @@ __device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT],
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const half8_t B = dequant_q4_k(words[j], ss[j >> 2], nk);
+                const half8_t B = dequant_q4_k(words[j], hd.ss[j >> 2], nk);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + cs * (c0 + i) + j]);
@@ -711,8 +729,54 @@ __device__ __forceinline__ void q4_k_mma(const uint4* xs, const int (&xrow)[MT],
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                acc[mt] = __builtin_elementwise_fma((float4_t)d, P1[mt], acc[mt]);
-                acc[mt] = __builtin_elementwise_fma((float4_t)(-dmin), P2[mt], acc[mt]);
+                acc[mt] = __builtin_elementwise_fma((float4_t)hd.d, P1[mt], acc[mt]);
+                acc[mt] = __builtin_elementwise_fma((float4_t)(-hd.dmin), P2[mt], acc[mt]);
+            }
+        }
+    }
+}
+
+// Q4_K with the min term from sub-block sums of X (the split-K kernel, which
+// stages X through registers and sums it on the way): xsum holds, per staged
+// row and chunk, the 8 sub-blocks' (hi, lo) fp16 pairs of s / 32 (lo scaled
+// by 2^11, so hi + lo 2^-11 keeps 22 bits of the fp32 sum s); slot
+// srow[mt] + 4 i is lane group g's pairs of sub-blocks 2g, 2g + 1.  One
+// 16x16x16 MFMA per chunk and column tile against B = the row's mins times 32
+// (high slots) and 2^-6 (low slots) -- exact fp16 -- gives sum_sb min * s,
+// in place of a second 16x16x32 chain of 8.
+template <int CMAX, int MT>
+__device__ __forceinline__ void q4_k_mma_xs(const uint4* xs, const uint2* xsum, const int (&xrow)[MT],
+                                            const int (&srow)[MT], int nc, const WBatch<ULSPEC_GGML_Q4_K, CMAX>& b,
+                                            int g, const NibbleConsts& nk, float4_t (&acc)[MT])
+{
+    constexpr int UPC = kUnitsPerChunk<ULSPEC_GGML_Q4_K>;
+    const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) {
+        if (i < nc) {
+            const uint32_t words[8] = {b.w0[i].x, b.w0[i].y, b.w0[i].z, b.w0[i].w,
+                                       b.w1[i].x, b.w1[i].y, b.w1[i].z, b.w1[i].w};
+            const Q4KHead hd = q4k_head(b.hd[i], g);
+            const _Float16 m0 = (_Float16)(uint16_t)(hd.mn & 63u), m1 = (_Float16)(uint16_t)(hd.mn >> 6);
+            const half4_t B2 = {m0 * (_Float16)32.0f, m0 * (_Float16)0.015625f, m1 * (_Float16)32.0f,
+                                m1 * (_Float16)0.015625f};
+            float4_t P1[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) P1[mt] = zero4;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const half8_t B = dequant_q4_k(words[j], hd.ss[j >> 2], nk);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const half8_t A = __builtin_bit_cast(half8_t, xs[xrow[mt] + UPC * i + j]);
+                    P1[mt] = mfma16x16x32(A, B, P1[mt]);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const float4_t P2 = mfma16x16x16(__builtin_bit_cast(half4_t, xsum[srow[mt] + 4 * i]), B2, zero4);
+                acc[mt] = __builtin_elementwise_fma((float4_t)hd.d, P1[mt], acc[mt]);
+                acc[mt] = __builtin_elementwise_fma((float4_t)(-hd.dmin), P2, acc[mt]);
             }
         }
     }
@@ -1053,12 +1117,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
 // ---- split-K kernels (any M) --------------------------------------------------
 // Grid (row groups of kWaves 16-row tiles, K slices).  Wave w of a workgroup
 // owns tile blockIdx.x * kWaves + w over the slice's chunks.  Per batch of
-// CMAX chunks: the batch's X units to registers, every weight load of the
-// batch, X to LDS (XStage rows), barrier, dequantize + MFMA for the MT column
-// tiles.  Each wave accumulates its chunks in K order and stores the slice's
-// partial Y (high plus 2^-11 low part for split X) to out[ks][M][N];
-// gemm_reduce_kernel sums the slices in slice order, so every output row is
-// bitwise independent of M.
+// CMAX chunks: the batch's X from registers to LDS (XStage rows; Q4_K also
+// the sub-block sums of X), barrier, dequantize + MFMA for the MT column
+// tiles.  Double-buffered (slice_db): two LDS buffers, and the next batch's
+// X and weight loads are issued before the multiply, so they fly behind it;
+// otherwise a batch's loads are issued at its start.  Each wave accumulates
+// its chunks in K order and stores the slice's partial Y (high plus 2^-11
+// low part for split X) to out[ks][M][N]; gemm_reduce_kernel sums the slices
+// in slice order, so every output row is bitwise independent of M.
 constexpr int kMaxSlices = 32;
 
 // X slice of one batch in LDS: 16 MT rows of UB units (16 bytes = 8 halves)
@@ -1077,64 +1143,180 @@ template <int MT, int UB>
 __device__ __forceinline__ void x_stage_load(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr,
                                              uint4 (&xv)[XStage<MT, UB>::kXU], int k0, int U)
 {
+    using XS = XStage<MT, UB>;
     const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
     const int k = k0 + 8 * uu;
 #pragma unroll
-    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
-        const int rho = m0 + u * XStage<MT, UB>::kRowsPerPass;
+    for (int u = 0; u < XS::kXU; ++u) {
+        const int rho = m0 + u * XS::kRowsPerPass;
         const bool ok = rho < a.xrows && uu < U && k < a.K;
         xv[u] = buf_load16(xr, ok ? (uint32_t)(x_row(a, rho) * a.K + k) * 2u : kOOB);
     }
 }
 
+// lo_pad: units added to the LDS position of rows >= a.M (the low parts of
+// split X; see slice_lo_pad).
 template <int MT, int UB>
 __device__ __forceinline__ void x_stage_store(const GemmArgs& a, uint4* xs, const uint4 (&xv)[XStage<MT, UB>::kXU],
-                                              int U)
+                                              int U, int lo_pad)
 {
+    using XS = XStage<MT, UB>;
     const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
 #pragma unroll
-    for (int u = 0; u < XStage<MT, UB>::kXU; ++u) {
-        const int rho = m0 + u * XStage<MT, UB>::kRowsPerPass;
-        if (rho < a.xrows && uu < U) xs[rho * XStage<MT, UB>::kUnitsPerRow + uu] = xv[u];
+    for (int u = 0; u < XS::kXU; ++u) {
+        const int rho = m0 + u * XS::kRowsPerPass;
+        if (rho < a.xrows && uu < U) xs[rho * XS::kUnitsPerRow + uu + (rho >= a.M ? lo_pad : 0)] = xv[u];
     }
 }
 
+// Q4_K staging: also each staged row's sub-block sums (32 elements = the 4
+// lanes holding its units; rows and units past the data hold 0): s = the fp32
+// sum, as fp16 hi = s / 32 and lo = (s / 32 - hi) 2^11 at half
+// ((rho CMAX + chunk) 16 + 2 sub-block) of xsum (q4_k_mma_xs).
+template <int MT, int CMAX>
+__device__ __forceinline__ void x_stage_sums(_Float16* xsum, const uint4 (&xv)[XStage<MT, 32 * CMAX>::kXU])
+{
+    constexpr int UB = 32 * CMAX;
+    using XS = XStage<MT, UB>;
+    const int uu = threadIdx.x & (UB - 1), m0 = threadIdx.x / UB;
+#pragma unroll
+    for (int u = 0; u < XS::kXU; ++u) {
+        const int rho = m0 + u * XS::kRowsPerPass;
+        // the unit's 8 halves by dot products with (1, 1) (exact products,
+        // fp32 sums), then the quad's 4 units by DPP lane swaps (xor 1, xor 2)
+        const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+        float v = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, xv[u].x), one2, 0.0f, false);
+        v = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, xv[u].y), one2, v, false);
+        v = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, xv[u].z), one2, v, false);
+        v = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, xv[u].w), one2, v, false);
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, true));
+        v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, true));
+        if ((uu & 3) == 0 && rho < 16 * MT) {
+            v *= 0.03125f;
+            const _Float16 hi = (_Float16)v;
+            const _Float16 lo = (_Float16)((v - (float)hi) * 2048.0f);
+            const half2_t pr = {hi, lo};
+            *(half2_t*)(xsum + (rho * CMAX + (uu >> 5)) * 16 + ((uu & 31) >> 2) * 2) = pr;
+        }
+    }
+}
+
+// The split-K kernel's LDS, in 16-byte units: the X buffer(s) (XStage rows,
+// plus up to 15 units of lo_pad), then for Q4_K the sub-block sum buffer(s)
+// (16 MT rows x CMAX chunks x 32 B).  Double-buffered (DB): two of each,
+// batches alternating.
 template <int TYPE, int MT, int CMAX>
+constexpr int slice_buf_units()
+{
+    return 16 * MT * XStage<MT, kUnitsPerChunk<TYPE> * CMAX>::kUnitsPerRow + 16;
+}
+
+// Split X: the LDS rows of the low parts start lo_pad units later, so that
+// low-part row M + i and high-part row i sit 32 banks apart (of 64 x 4 B)
+// and the 16 A-operand slots of an MFMA (8 high, 8 low rows) read
+// distinct banks: row rho starts at bank 4 RS rho mod 64, RS = 1 mod 16.
+__device__ __forceinline__ int slice_lo_pad(const GemmArgs& a)
+{
+    return a.hl ? (8 - a.M % 16 + 16) % 16 : 0;
+}
+template <int TYPE, int MT, int CMAX>
+constexpr int slice_sum_units()
+{
+    return TYPE == ULSPEC_GGML_Q4_K ? 16 * MT * CMAX * 2 : 0;
+}
+
+template <int TYPE, int MT, int CMAX, bool DB, bool HL>
 __global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
 {
     constexpr int UPC = kUnitsPerChunk<TYPE>;
     constexpr int UB = UPC * CMAX;
+    constexpr bool kSums = TYPE == ULSPEC_GGML_Q4_K;
     using XS = XStage<MT, UB>;
-    __shared__ uint4 xs[16 * MT * XS::kUnitsPerRow];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int XSZ = slice_buf_units<TYPE, MT, CMAX>(), SSZ = slice_sum_units<TYPE, MT, CMAX>();
+    constexpr int NBUF = DB ? 2 : 1;
+    extern __shared__ uint4 xsd[];  // [NBUF][XSZ] X, then [NBUF][SSZ] sums
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
     const int t = blockIdx.x * kWaves + wave;
     const bool live = t < a.n_tiles;
+    const int tl = live ? t : a.n_tiles;  // past the last tile: loads move nothing
     const int ks = blockIdx.y;
     int ca, cb;
     slice_range(a, ks, ca, cb);
+    const int nb = (cb - ca + CMAX - 1) / CMAX;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
-    int xrow[MT];
+    // A-operand slot r of column tile mt reads staged row rho0 + step mt
+    // (HL == a.hl): unclamped, so the tiles' LDS addresses differ by
+    // constants; slots past the last row read rows of other slots, or stale
+    // ones past a.xrows, and their outputs are never stored
+    constexpr int kStep = HL ? 8 : 16;
+    const int lo_pad = slice_lo_pad(a);
+    const int rho0 = HL ? (r & 7) + (r < 8 ? 0 : a.M) : r;
+    const int pad0 = HL && r >= 8 ? lo_pad : 0;
+    int xrow[MT], srow[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-        xrow[mt] = xslot_row(a, mt, r) * XS::kUnitsPerRow + (kSuperBlock<TYPE> ? 8 * g : g);
+    for (int mt = 0; mt < MT; ++mt) {
+        xrow[mt] = (rho0 + kStep * mt) * XS::kUnitsPerRow + pad0 + (kSuperBlock<TYPE> ? 8 * g : g);
+        srow[mt] = (rho0 + kStep * mt) * CMAX * 4 + g;
+    }
     const NibbleConsts nk = nibble_consts();
     float4_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int c0 = ca; c0 < cb; c0 += CMAX) {
-        const int nc = min(CMAX, cb - c0);
-        uint4 xv[XS::kXU];
+    auto nc_of = [&](int bi) { return min(CMAX, cb - (ca + bi * CMAX)); };
+    // batch bi's X from registers into buffer buf
+    auto stage = [&](const uint4 (&xv)[XS::kXU], int bi, int buf) {
+        x_stage_store<MT, UB>(a, xsd + buf * XSZ, xv, UPC * nc_of(bi), lo_pad);
+        if constexpr (kSums) x_stage_sums<MT, CMAX>((_Float16*)(xsd + NBUF * XSZ + buf * SSZ), xv);
+    };
+    auto load = [&](uint4 (&xv)[XS::kXU], WBatch<TYPE, CMAX>& w, int bi) {
+        const int c0 = ca + bi * CMAX, nc = nc_of(bi);
         x_stage_load<MT, UB>(a, xr, xv, c0 * UPC * 8, UPC * nc);
         pin_loads();
-        WBatch<TYPE, CMAX> b;
-        stream_load<TYPE, CMAX>(a, wr, live ? t : a.n_tiles, c0, nc, b);
+        stream_load<TYPE, CMAX>(a, wr, tl, c0, nc, w);
         pin_loads();
-        if (c0 != ca) __syncthreads();  // the previous batch is done reading xs
-        x_stage_store<MT, UB>(a, xs, xv, UPC * nc);
-        __syncthreads();
-        stream_mma<TYPE, CMAX, MT>(xs, xrow, UPC, 0, live ? nc : 0, 0, CMAX, b, nk, acc);
+    };
+    auto mma = [&](const WBatch<TYPE, CMAX>& w, int bi, int buf) {
+        const int nc = live ? nc_of(bi) : 0;
+        if constexpr (kSums)
+            q4_k_mma_xs<CMAX, MT>(xsd + buf * XSZ, (const uint2*)(xsd + NBUF * XSZ + buf * SSZ), xrow, srow, nc, w,
+                                  g, nk, acc);
+        else
+            stream_mma<TYPE, CMAX, MT>(xsd + buf * XSZ, xrow, UPC, 0, nc, 0, CMAX, w, nk, acc);
+    };
+    uint4 xv[XS::kXU];
+    if constexpr (DB) {
+        // batch bi: its X (registers) to buffer bi & 1, barrier (every wave is
+        // past the multiply of batch bi - 2, which read that buffer), batch
+        // bi + 1's loads issued, batch bi multiplied -- two batches per pass,
+        // so the weight registers alternate statically
+        WBatch<TYPE, CMAX> w0, w1;
+        if (nb > 0) load(xv, w0, 0);
+        for (int bi = 0; bi < nb; bi += 2) {
+            stage(xv, bi, 0);
+            __syncthreads();
+            if (bi + 1 < nb) load(xv, w1, bi + 1);
+            mma(w0, bi, 0);
+            if (bi + 1 < nb) {
+                stage(xv, bi + 1, 1);
+                __syncthreads();
+                if (bi + 2 < nb) load(xv, w0, bi + 2);
+                mma(w1, bi + 1, 1);
+            }
+        }
+    } else {
+        // per batch: X and weight loads, barrier (the previous batch is done
+        // reading the buffer), X to LDS, barrier, multiply
+        for (int bi = 0; bi < nb; ++bi) {
+            WBatch<TYPE, CMAX> w;
+            load(xv, w, bi);
+            if (bi) __syncthreads();
+            stage(xv, bi, 0);
+            __syncthreads();
+            mma(w, bi, 0);
+        }
     }
     if (!live) return;  // wave-uniform
     float* out = a.out + (size_t)ks * a.M * a.N;
@@ -1439,24 +1621,53 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     }
 }
 
-// Chunks per batch of the split-K kernel: about 32 weight registers per lane
-// (Q4_0 6 per chunk, Q4_K 12, Q8_0 10, F16 16) up to two column tiles, half
-// that beyond (Q4_K: one super-block past four tiles, whose two partial sums
-// per tile take 8 registers each); a batch covers at most 1024 K (128 X units).
+// Double-buffered split-K kernel (the next batch's weights and X in flight
+// during a multiply) where it fits the 128 registers of 4 waves per SIMD: not
+// for the super-block types past 4 (Q4_K) or 2 (Q6_K) column tiles.
+template <int TYPE, int MT>
+constexpr bool slice_db()
+{
+    return TYPE == ULSPEC_GGML_Q6_K ? MT <= 2 : TYPE == ULSPEC_GGML_Q4_K ? MT <= 4 : true;
+}
+
+// Chunks per batch of the split-K kernel: weight registers per lane (Q4_0 6
+// per chunk, Q4_K 12, Q6_K 14, Q8_0 10, F16 16) times the batches in flight
+// (two when double-buffered) at about 32-48 up to two column tiles, fewer
+// beyond; a batch covers at most 1024 K (128 X units).
 template <int TYPE, int MT>
 constexpr int slice_cmax()
 {
-    return TYPE == ULSPEC_GGML_Q4_0 ? (MT <= 2 ? 8 : 4)
-           : kSuperBlock<TYPE> ? (MT <= 2 ? 4 : MT <= 4 ? 2 : 1)
-           : TYPE == ULSPEC_GGML_Q8_0 ? (MT <= 2 ? 4 : 2)
+    return TYPE == ULSPEC_GGML_Q4_0 ? (MT <= 2 ? 4 : 2)
+           : TYPE == ULSPEC_GGML_Q4_K ? (MT <= 2 ? 2 : 1)
+           : TYPE == ULSPEC_GGML_Q6_K ? (MT <= 4 ? 2 : 1)
+           : TYPE == ULSPEC_GGML_Q8_0 ? (MT <= 2 ? 4 : MT <= 4 ? 2 : 1)
                                        : (MT <= 2 ? 2 : 1);
+}
+
+template <int TYPE, int MT>
+constexpr size_t slice_lds_bytes()
+{
+    constexpr int C = slice_cmax<TYPE, MT>();
+    return (slice_db<TYPE, MT>() ? 2 : 1) *
+           (size_t)(slice_buf_units<TYPE, MT, C>() + slice_sum_units<TYPE, MT, C>()) * sizeof(uint4);
+}
+
+template <int TYPE, int MT, bool HL>
+constexpr const void* slice_fn()
+{
+    return (const void*)gemm_slice_kernel<TYPE, MT, slice_cmax<TYPE, MT>(), slice_db<TYPE, MT>(), HL>;
 }
 
 template <int TYPE, int MT>
 void slice_launch_mt(const GemmArgs& a, hipStream_t st)
 {
+    static_assert(slice_lds_bytes<TYPE, MT>() <= 160 * 1024, "split-K LDS");
     const dim3 grid((a.n_tiles + kWaves - 1) / kWaves, a.ks_count);
-    hipLaunchKernelGGL((gemm_slice_kernel<TYPE, MT, slice_cmax<TYPE, MT>()>), grid, dim3(kWaves * 64), 0, st, a);
+    constexpr size_t lds = slice_lds_bytes<TYPE, MT>();
+    constexpr int C = slice_cmax<TYPE, MT>();
+    constexpr bool DB = slice_db<TYPE, MT>();
+    if (a.hl) hipLaunchKernelGGL((gemm_slice_kernel<TYPE, MT, C, DB, true>), grid, dim3(kWaves * 64), lds, st, a);
+    else hipLaunchKernelGGL((gemm_slice_kernel<TYPE, MT, C, DB, false>), grid, dim3(kWaves * 64), lds, st, a);
 }
 
 template <int TYPE>
@@ -1564,9 +1775,18 @@ void wide_launch(CList<C...>, int cpp, dim3 grid, dim3 block, size_t lds, hipStr
     (one(std::integral_constant<int, C>{}), ...);
 }
 
-template <int TYPE>
-void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& small, std::vector<const void*>& rings)
+template <int TYPE, int... MT>
+void slice_kernels(std::integer_sequence<int, MT...>, std::vector<const void*>& out)
 {
+    (out.push_back(slice_fn<TYPE, MT, true>()), ...);
+    (out.push_back(slice_fn<TYPE, MT, false>()), ...);
+}
+
+template <int TYPE>
+void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& small, std::vector<const void*>& rings,
+                  std::vector<const void*>& slices)
+{
+    slice_kernels<TYPE>(std::integer_sequence<int, 1, 2, 3, 4, 6>{}, slices);
     wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, wide);
     small.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves>);
     rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves>);
@@ -1575,16 +1795,16 @@ void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& smal
 
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
-    std::vector<const void*> wide, small, rings;
-    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings);
-    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings);
-    type_kernels<ULSPEC_GGML_F16>(wide, small, rings);
-    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings);
-    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings);
+    std::vector<const void*> wide, small, rings, slices;
+    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings, slices);
+    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings, slices);
+    type_kernels<ULSPEC_GGML_F16>(wide, small, rings, slices);
+    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings, slices);
+    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings, slices);
     const struct {
         const std::vector<const void*>* fns;
         size_t fixed;
-    } groups[] = {{&wide, kStaticWide}, {&small, kStaticSmall}, {&rings, kStaticRing}};
+    } groups[] = {{&wide, kStaticWide}, {&small, kStaticSmall}, {&rings, kStaticRing}, {&slices, 0}};
     // The launch checks add each group's static LDS to the dynamic size; the
     // opt-in must not let static + dynamic exceed the CU's 160 KB, so both
     // come from the compiled kernel's own static size.
@@ -1658,15 +1878,28 @@ bool stream_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
     return stream_launch_t<ULSPEC_GGML_F16>(ctx, w, a);
 }
 
-// K slices per weight: about one workgroup per CU in total.
+// K slices per weight.  The split-K kernel runs one workgroup per CU at a
+// time, so its time goes as (rounds of n_cu workgroups) x (a workgroup's
+// start-up and partial store, about kSliceFixed chunks' worth, + the chunks
+// of the longest slice); the fewest slices that minimise that (a round that
+// spills a few workgroups over n_cu doubles the time).
+constexpr uint32_t kSliceFixed = 3;
+
 uint32_t choose_ksplit(uint32_t n_tiles, uint32_t n_chunks, int n_cu)
 {
     const uint32_t groups = (n_tiles + kWaves - 1) / kWaves;
-    uint32_t ks = (uint32_t)((n_cu + groups / 2) / groups);
-    if (ks < 1) ks = 1;
-    if (ks > n_chunks) ks = n_chunks;
-    if (ks > (uint32_t)kMaxSlices) ks = kMaxSlices;
-    return ks;
+    const uint32_t cu = n_cu > 0 ? (uint32_t)n_cu : 1u;
+    uint32_t best = 1;
+    uint64_t best_cost = ~0ull;
+    for (uint32_t ks = 1; ks <= n_chunks && ks <= (uint32_t)kMaxSlices; ++ks) {
+        const uint64_t rounds = ((uint64_t)groups * ks + cu - 1) / cu;
+        const uint64_t cost = rounds * (kSliceFixed + (n_chunks + ks - 1) / ks);
+        if (cost < best_cost) {
+            best = ks;
+            best_cost = cost;
+        }
+    }
+    return best;
 }
 
 size_t gemm_workspace_bytes(const Weight& w)
