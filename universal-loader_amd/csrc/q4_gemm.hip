@@ -1332,40 +1332,54 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
         }
 }
 
-// Y[m][n] = the sum of the ks_count slices of part in slice order, times the
-// row scale (if any), then the epilogue of output (m, n) (a.out is Y for the
-// store epilogue).  One thread per element of the padded [M][16 n_tiles]
-// grid, n fastest, so a 16-lane group is one row of one tile (the epilogue's
-// lane pairs and xor tree); the workgroup's rows get their scales first, one
-// wave per row.
+// Y[m][n] = the sum of the ks_count (<= KB) slices of part in slice order,
+// times the row scale (if any), then the epilogue of output (m, n) (a.out is
+// Y for the store epilogue).  Grid (16 n_tiles / 256, M / RPT): thread tid
+// of workgroup (bx, by) takes padded column n = 256 bx + tid of rows RPT by
+// .. RPT by + RPT - 1, all their slice loads issued at once; a 16-lane group
+// is one row of one tile (the epilogue's lane pairs and xor tree); wave w
+// computes the scale of the workgroup's row w.  RPT = 4 for large outputs
+// (fewer workgroups, each with more loads in flight), 1 where that would
+// leave too few workgroups.
+template <int KB, int RPT>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const float* __restrict__ part)
 {
-    __shared__ float rs[256 / 16 + 2];
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    const int NP = 16 * a.n_tiles;
-    const int m = i / NP, n = i - m * NP;
-    const int m_first = (blockIdx.x * 256) / NP;
-    const int n_rows = min((blockIdx.x * 256 + 255) / NP - m_first + 1, 256 / 16 + 2);
+    static_assert(RPT <= 256 / 64, "one wave per row scale");
+    __shared__ float rs[RPT];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int m0 = blockIdx.y * RPT;
     const EpiPos pos0 = epi_pos0(a);
-    const bool ok = m < a.M && n < a.N;
     const size_t MN = (size_t)a.M * a.N;
-    float v[kMaxSlices];
+    float v[RPT][KB];
 #pragma unroll
-    for (int k = 0; k < kMaxSlices; ++k) v[k] = ok && k < a.ks_count ? part[k * MN + (size_t)m * a.N + n] : 0.0f;
-    const float2 pre = epi_load(a, m < a.M ? m : a.M, n, pos0);
+    for (int j = 0; j < RPT; ++j) {
+        const int m = m0 + j;
+        const bool ok = m < a.M && n < a.N;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) v[j][k] = ok && k < a.ks_count ? part[k * MN + (size_t)m * a.N + n] : 0.0f;
+    }
+    float2 pre[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) pre[j] = epi_load(a, m0 + j < a.M ? m0 + j : a.M, n, pos0);
     if (a.f.rs_pss) {
-        for (int j = threadIdx.x >> 6; j < n_rows; j += 4) {  // wave-uniform
-            const float r = rs_reduce(a, rs_load(a, m_first + j));
-            if ((threadIdx.x & 63) == 0) rs[j] = r;
+        if (wave < RPT && m0 + wave < a.M) {  // wave-uniform
+            const float r = rs_reduce(a, rs_load(a, m0 + wave));
+            if (lane == 0) rs[wave] = r;
         }
         __syncthreads();
     }
-    float s = v[0];
 #pragma unroll
-    for (int k = 1; k < kMaxSlices; ++k)
-        if (k < a.ks_count) s += v[k];
-    if (a.f.rs_pss) s *= rs[min(m - m_first, 256 / 16 + 1)];
-    epilogue(a, s, m, n, n >> 4, threadIdx.x & 63, pre, pos0);
+    for (int j = 0; j < RPT; ++j) {
+        const int m = m0 + j;
+        float s = v[j][0];
+#pragma unroll
+        for (int k = 1; k < KB; ++k)
+            if (k < a.ks_count) s += v[j][k];
+        if (a.f.rs_pss && m < a.M) s *= rs[j];
+        epilogue(a, s, m, n, n >> 4, lane, pre[j], pos0);
+    }
 }
 
 // ---- whole-X kernels (small M) ------------------------------------------------
@@ -1931,6 +1945,15 @@ GemmArgs make_args(const Weight& w, const _Float16* x, uint32_t M, bool hl, uint
     return a;
 }
 
+template <int KB>
+void reduce_launch(const GemmArgs& a, const float* part, int cols, bool four_rows, hipStream_t st)
+{
+    if (four_rows)
+        hipLaunchKernelGGL((gemm_reduce_kernel<KB, 4>), dim3(cols, (a.M + 3) / 4), dim3(256), 0, st, a, part);
+    else
+        hipLaunchKernelGGL((gemm_reduce_kernel<KB, 1>), dim3(cols, a.M), dim3(256), 0, st, a, part);
+}
+
 // The split-K kernel over a.M rows into part[ks][M][N], then the slice sum, row
 // scale and a.f's epilogue into y (one slice, no row scale and a plain store:
 // straight into y).
@@ -1949,9 +1972,13 @@ void split_launch(ulspec_ctx* ctx, const Weight& w, GemmArgs a, float* part, flo
     else slice_launch_t<ULSPEC_GGML_F16>(a, mt, ctx->stream);
     if (direct) return;
     a.out = y;
-    const int threads = a.M * 16 * a.n_tiles;
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a,
-                       (const float*)part);
+    const int cols = (16 * a.n_tiles + 255) / 256;
+    const bool wide = cols * ((a.M + 3) / 4) >= 2 * std::max(1, ctx->n_cu);
+    if (a.ks_count <= 2) reduce_launch<2>(a, part, cols, wide, ctx->stream);
+    else if (a.ks_count <= 4) reduce_launch<4>(a, part, cols, wide, ctx->stream);
+    else if (a.ks_count <= 8) reduce_launch<8>(a, part, cols, wide, ctx->stream);
+    else if (a.ks_count <= 16) reduce_launch<16>(a, part, cols, wide, ctx->stream);
+    else reduce_launch<kMaxSlices>(a, part, cols, wide, ctx->stream);
 }
 
 }  // namespace
