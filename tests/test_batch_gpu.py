@@ -13,7 +13,10 @@ Bars:
     the step's logits; the batched logits of each sequence agree with a
     one-sequence GPU model's for the same tokens within LOGIT_TOL of their
     RMS (batched rows take the split-K GEMM path and the cache rows of earlier
-    batched steps, so fp32 order and some fp16 K/V roundings differ).
+    batched steps, so fp32 order and some fp16 K/V roundings differ);
+  - Q4_K, 8 sequences x 6 verify rows (48): every verify row's target logits
+    within LOGIT_TOL_ORACLE of their RMS of the oracle's forward, and the
+    greedy tokens equal to the oracle's loop.
 """
 import numpy as np
 import pytest
@@ -91,6 +94,53 @@ def test_batch_greedy_tokens_bit_exact_with_oracle(pkg, ctx, ora, weights, promp
         assert np.array_equal(got, want), b
         assert (st["n"], st["accepted"], st["proposed"]) == (osp.state()["n"], osp.state()["accepted"],
                                                              osp.state()["proposed"])
+    for m in (sp, gt, gd, ot, od):
+        m.close()
+
+
+# Q4_K (256-element super-blocks: FFN 1536), 8 sequences x (k + 1) = 48 verify
+# rows: the target's GEMMs take the split-K kernel at 6 column tiles of split
+# X (the min term from X sub-block sums, low-part rows bank-offset in LDS)
+TARGET_K = dict(TARGET, n_layers=4, ffn=1536)
+DRAFT_K = dict(TARGET_K, n_layers=2)
+Q4_K = 12
+LOGIT_TOL_ORACLE = 1e-3  # measured 2.5e-4
+
+
+def test_batch_q4_k_48_rows_against_oracle(pkg, ctx, ora, prompts):
+    tw, dw = make_tensors(ora, TARGET_K, Q4_K, seed=303), make_tensors(ora, DRAFT_K, Q4_K, seed=404)
+    B, k = 8, 5
+    gt, gd = _gpu(pkg, ctx, TARGET_K, tw, n_seq=B), _gpu(pkg, ctx, DRAFT_K, dw, n_seq=B)
+    sp = pkg.Speculative(gt, gd, k, pkg.sampling(greedy=True), 7, n_seq=B)
+    sp.prefill(prompts[:B])
+    ot, od = _ora(ora, TARGET_K, tw), _ora(ora, DRAFT_K, dw)
+    seqs = [list(p) for p in prompts[:B]]
+    worst = 0.0
+    for step in range(3):
+        ns = [len(q) for q in seqs]
+        sp.steps(1)
+        r = sp.last_step()
+        for b in range(B):
+            # every verify row's target logits against the oracle's forward
+            n = ns[b]
+            toks = np.concatenate([[seqs[b][n - 1]], r["draft_tokens"][b]]).astype(np.int32)
+            ot.forward(np.array(seqs[b][:n - 1], np.int32), 0)
+            want = ot.forward(toks, n - 1, n_logits=k + 1).astype(np.float64)
+            err = float(np.abs(r["target_logits"][b].astype(np.float64) - want).max() /
+                        np.sqrt((want ** 2).mean()))
+            worst = max(worst, err)
+            seqs[b] += list(r["out_tokens"][b][:r["n_accepted"][b] + 1])
+    print(f"  Q4_K, 48 verify rows: target logits max err / rms vs the oracle {worst:.2e}")
+    assert worst <= LOGIT_TOL_ORACLE
+    # greedy tokens: each sequence equals the oracle's own loop on its prompt
+    steps = sp.state()["steps"]
+    for b in range(B):
+        osp = ora.Speculative(ot, od, k, ora.sampling(greedy=True), 7)
+        osp.prefill(prompts[b])
+        for _ in range(steps):
+            osp.step()
+        assert np.array_equal(sp.tokens(seq=b), osp.tokens()), b
+        assert np.array_equal(sp.tokens(seq=b), np.array(seqs[b], np.int32)), b
     for m in (sp, gt, gd, ot, od):
         m.close()
 
