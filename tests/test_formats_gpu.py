@@ -181,3 +181,59 @@ def test_mixed_type_speculative_loop(pkg, ctx, ora, mixed_file):
     assert list(got) == seq
     for m in (sp, t, d, ref):
         m.close()
+
+
+def test_mixed_type_batch_of_48_verify_rows(pkg, ctx, ora, mixed_file):
+    """Mixed-type target (Q6_K LM head, Q8_0 O projection, fp16 fused and
+    down weights, Q4_K elsewhere), 8 sequences x (k + 1) = 48 verify rows per
+    step: every type's split-K GEMM at 6 column tiles of split X.  Every
+    verify row's target logits within 2e-4 of their RMS (measured 1.8e-5) of a
+    one-sequence
+    GPU model's (whole-X kernels at 6 rows, the same fp16 copies of the mixed
+    fused weights) and within 1e-2 of the oracle's forward (as for one
+    sequence: those fp16 copies round); greedy tokens equal to the oracle's
+    loop."""
+    path, tensors = mixed_file
+    B, k = 8, 5
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, CFG["vocab"], n).astype(np.int32) for n in (9, 14, 20, 11, 25, 7, 16, 30)]
+    draft = make_tensors(ora, CFG, 12, seed=23, norm_std=0.1)
+    t, d = pkg.Model(ctx, **CFG, n_seq=B), pkg.Model(ctx, **CFG, n_seq=B)
+    load(t, tensors)
+    load(d, draft)
+    sp = pkg.Speculative(t, d, k, pkg.sampling(greedy=True), 5, n_seq=B)
+    sp.prefill(prompts)
+    ot, od = ora.Llama(**CFG, nthreads=ora.nthreads_default()), ora.Llama(**CFG, nthreads=ora.nthreads_default())
+    load(ot, tensors)
+    load(od, draft)
+    ref = pkg.Model(ctx, **CFG)
+    load(ref, tensors)
+    seqs = [list(p) for p in prompts]
+    worst, worst_gpu = 0.0, 0.0
+    for _ in range(3):
+        ns = [len(q) for q in seqs]
+        sp.steps(1)
+        r = sp.last_step()
+        for b in range(B):
+            n = ns[b]
+            toks = np.concatenate([[seqs[b][n - 1]], r["draft_tokens"][b]]).astype(np.int32)
+            got = r["target_logits"][b].astype(np.float64)
+            ot.forward(np.array(seqs[b][:n - 1], np.int32), 0)
+            want = ot.forward(toks, n - 1, n_logits=k + 1).astype(np.float64)
+            worst = max(worst, float(np.abs(got - want).max() / np.sqrt((want ** 2).mean())))
+            ref.forward(np.array(seqs[b][:n - 1], np.int32), 0)
+            one = ref.forward(toks, n - 1, n_logits=k + 1).astype(np.float64)
+            worst_gpu = max(worst_gpu, float(np.abs(got - one).max() / np.sqrt((one ** 2).mean())))
+            seqs[b] += list(r["out_tokens"][b][:r["n_accepted"][b] + 1])
+    print(f"  mixed types, 48 verify rows: target logits max err / rms vs one sequence {worst_gpu:.2e}, "
+          f"vs the oracle {worst:.2e}")
+    assert worst_gpu <= 2e-4 and worst <= 1e-2
+    steps = sp.state()["steps"]
+    for b in range(B):
+        osp = ora.Speculative(ot, od, k, ora.sampling(greedy=True), 5)
+        osp.prefill(prompts[b])
+        for _ in range(steps):
+            osp.step()
+        assert np.array_equal(sp.tokens(seq=b), osp.tokens()), b
+    for m in (sp, t, d, ot, od, ref):
+        m.close()
