@@ -1211,6 +1211,12 @@ constexpr int slice_buf_units()
     return 16 * MT * XStage<MT, kUnitsPerChunk<TYPE> * CMAX>::kUnitsPerRow + 16;
 }
 
+template <int TYPE, int MT, int CMAX>
+constexpr int slice_sum_units()
+{
+    return TYPE == ULSPEC_GGML_Q4_K ? 16 * MT * CMAX * 2 : 0;
+}
+
 // Split X: the LDS rows of the low parts start lo_pad units later, so that
 // low-part row M + i and high-part row i sit 32 banks apart (of 64 x 4 B)
 // and the 16 A-operand slots of an MFMA (8 high, 8 low rows) read
@@ -1218,11 +1224,6 @@ constexpr int slice_buf_units()
 __device__ __forceinline__ int slice_lo_pad(const GemmArgs& a)
 {
     return a.hl ? (8 - a.M % 16 + 16) % 16 : 0;
-}
-template <int TYPE, int MT, int CMAX>
-constexpr int slice_sum_units()
-{
-    return TYPE == ULSPEC_GGML_Q4_K ? 16 * MT * CMAX * 2 : 0;
 }
 
 template <int TYPE, int MT, int CMAX, bool DB, bool HL>
