@@ -324,6 +324,11 @@ ulspec_status ulspec_gguf_llama_cfg(const ulspec_gguf* g, uint32_t max_ctx, ulsp
  * type fails with ULSPEC_EUNSUPPORTED naming it.  The file may be closed
  * afterwards. */
 ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx, ulspec_model** out);
+/* The same with K/V caches for n_seq sequences (1 .. 8; a batch model as
+ * ulspec_model_create_batch makes), for InferenceAPI::generate_batch
+ * (src/api/inference_api.h:63) over the batched loop. */
+ulspec_status ulspec_model_load_gguf_batch(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx, uint32_t n_seq,
+                                           ulspec_model** out);
 
 /* ---- speculative decoding loop --------------------------------------------
  * One step (all on the device, captured once into a HIP graph and replayed):

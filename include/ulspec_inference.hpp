@@ -529,6 +529,16 @@ public:
         }
         return generate_tokens(ids, config).text;
     }
+    // InferenceAPI::generate_batch (inference_api.cpp:164-175): generate()
+    // for each prompt, in order, as the reference does (the Python module's
+    // generate_batch steps the prompts together on the batched loop).
+    std::vector<std::string> generate_batch(const std::vector<std::string>& prompts, const GenerationConfig& config)
+    {
+        std::vector<std::string> out;
+        out.reserve(prompts.size());
+        for (const auto& p : prompts) out.push_back(generate(p, config));
+        return out;
+    }
     GenerationResult generate_default(const std::string& prompt)  // inference_api.cpp:80-95
     {
         GenerationConfig c;

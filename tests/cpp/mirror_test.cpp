@@ -104,6 +104,11 @@ static int files_part(Context& ctx, const char* target_path, const char* draft_p
         std::printf("text generation: '%s' vs '%s'\n", spec.c_str(), plain.c_str());
         return 1;
     }
+    const std::vector<std::string> batch = api.generate_batch({"w1 w2 w3 w4", "w5 w6"}, c);
+    if (batch.size() != 2 || batch[0] != plain || batch[1] != api.generate("w5 w6", c)) {
+        std::printf("generate_batch\n");
+        return 1;
+    }
     const float rate = api.get_acceptance_rate();
     if (!(rate >= 0.0f && rate <= 1.0f)) {
         std::printf("acceptance rate %f\n", rate);

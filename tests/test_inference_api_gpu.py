@@ -77,3 +77,28 @@ def test_sampled_generation_is_seeded(pkg, ctx, api_mod, files):
         res.append(api.generate_default([5, 6, 7, 8]).tokens)
         api.unload_model()
     assert res[0] == res[1] and len(res[0]) == 100
+
+
+def test_generate_batch(pkg, ctx, api_mod, files):
+    """generate_batch: the prompts stepped together on the batched loop (groups
+    of up to 8 sequences), greedy outputs equal to one-prompt generation, with
+    and without speculation; text prompts through the tokenizer; the
+    reference's no-model string per prompt."""
+    target, draft = files
+    api = api_mod.InferenceAPI(ctx=ctx, seed=5)
+    assert api.generate_batch(["1 2", "3 4"]) == ["Error: No model loaded"] * 2
+    api.load_model(target)
+    api.load_draft_model(draft)
+    rng = np.random.default_rng(12)
+    prompts = [list(rng.integers(0, 1000, n)) for n in (9, 4, 17, 6, 12, 3, 8, 15, 5, 11)]
+    cfg = api_mod.GenerationConfig(max_tokens=12, do_sample=False)
+    for spec in (True, False):
+        api.enable_speculative_decoding(spec)
+        one = [api.generate_tokens(p, cfg).tokens for p in prompts]
+        batch = api.generate_tokens_batch(prompts, cfg)  # a group of 8, then one of 2
+        assert [r.tokens for r in batch] == one, spec
+        assert all(r.num_tokens == 12 for r in batch) and api.get_throughput() > 0
+    api.register_custom_tokenizer(lambda s: [int(x) for x in s.split()])
+    texts = api.generate_batch([" ".join(str(t) for t in p) for p in prompts[:3]], cfg)
+    assert texts == [api.generate_tokens(p, cfg).text for p in prompts[:3]]
+    api.unload_model()

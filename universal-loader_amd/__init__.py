@@ -151,6 +151,7 @@ ABI = [
     ("ulspec_gguf_get_str", C.c_int, [P, C.c_char_p, C.POINTER(P), C.POINTER(C.c_uint64)]),
     ("ulspec_gguf_llama_cfg", C.c_int, [P, U32, C.POINTER(ModelCfg)]),
     ("ulspec_model_load_gguf", C.c_int, [P, P, U32, C.POINTER(P)]),
+    ("ulspec_model_load_gguf_batch", C.c_int, [P, P, U32, U32, C.POINTER(P)]),
 ]
 
 
@@ -495,15 +496,19 @@ class GGUFFile:
         return cfg
 
 
-def load_gguf_model(ctx, gguf, max_ctx=0):
-    """Model from a GGUFFile (or a path): ulspec_model_load_gguf."""
+def load_gguf_model(ctx, gguf, max_ctx=0, n_seq=1):
+    """Model from a GGUFFile (or a path): ulspec_model_load_gguf; n_seq > 1: a
+    batch model (ulspec_model_load_gguf_batch)."""
     own = not isinstance(gguf, GGUFFile)
     f = GGUFFile(gguf) if own else gguf
     try:
         h = P()
-        ctx._check(lib().ulspec_model_load_gguf(ctx.handle, f.handle, max_ctx, C.byref(h)))
+        if n_seq == 1:
+            ctx._check(lib().ulspec_model_load_gguf(ctx.handle, f.handle, max_ctx, C.byref(h)))
+        else:
+            ctx._check(lib().ulspec_model_load_gguf_batch(ctx.handle, f.handle, max_ctx, n_seq, C.byref(h)))
         m = Model.__new__(Model)
-        m.ctx, m.handle = ctx, h.value
+        m.ctx, m.handle, m.n_seq = ctx, h.value, n_seq
         m.cfg = f.llama_cfg(max_ctx)
         return m
     finally:

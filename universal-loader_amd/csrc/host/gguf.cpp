@@ -444,6 +444,12 @@ extern "C" ulspec_status ulspec_gguf_llama_cfg(const ulspec_gguf* gc, uint32_t m
 extern "C" ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx,
                                                 ulspec_model** out)
 {
+    return ulspec_model_load_gguf_batch(ctx, g, max_ctx, 1, out);
+}
+
+extern "C" ulspec_status ulspec_model_load_gguf_batch(ulspec_ctx* ctx, const ulspec_gguf* g, uint32_t max_ctx,
+                                                      uint32_t n_seq, ulspec_model** out)
+{
     ULSPEC_CHECK_CTX(ctx);
     if (!g || !out) return fail(ctx, ULSPEC_EINVAL, "model_load_gguf: null argument");
     *out = nullptr;
@@ -451,7 +457,7 @@ extern "C" ulspec_status ulspec_model_load_gguf(ulspec_ctx* ctx, const ulspec_gg
     if (ulspec_gguf_llama_cfg(g, max_ctx, &cfg) != ULSPEC_OK)
         return fail(ctx, ULSPEC_EINVAL, "model_load_gguf: %s", g->err.c_str());
     ulspec_model* m = nullptr;
-    ulspec_status st = ulspec_model_create(ctx, &cfg, &m);
+    ulspec_status st = ulspec_model_create_batch(ctx, &cfg, n_seq, &m);
     if (st != ULSPEC_OK) return st;
     for (const auto& t : g->tensors) {
         if (t.name == "rope_freqs.weight") continue;  // angles are computed from rope_base

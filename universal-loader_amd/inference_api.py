@@ -7,6 +7,7 @@ library: same class and method names, argument meaning and result types.
     api.load_draft_model("draft.gguf")       # no counterpart: the reference has no draft model
     api.enable_speculative_decoding(True)    # :214-216 (a no-op there)
     res = api.generate_tokens(prompt_ids, GenerationConfig(max_tokens=64))
+    texts = api.generate_batch(prompts)      # :164-175 (a loop of generate there; the batched loop here)
     api.get_acceptance_rate()                # :222-225 (0.0 there; live here)
     api.get_token_logits(ids)                # :277-280 (empty there; live here)
 
@@ -75,8 +76,9 @@ class InferenceAPI:
         self._lock = threading.RLock()
         self._config = GenerationConfig()
         self._target = self._draft = None
+        self._batch = {}  # n_seq -> (target, draft) batch models for generate_batch
         self._vocab = None
-        self._model_path = ""
+        self._model_path = self._draft_path = ""
         self._model_bytes = 0
         self._spec = False
         self._tokenizer = None
@@ -109,17 +111,38 @@ class InferenceAPI:
                 raise ValueError("draft and target vocabularies differ")
             if self._draft is not None:
                 self._draft.close()
-            self._draft = d
+            self._drop_batch()
+            self._draft, self._draft_path = d, model_path
             return True
 
     def unload_model(self):
         with self._lock:
+            self._drop_batch()
             for m in (self._draft, self._target):
                 if m is not None:
                     m.close()
             self._target = self._draft = None
-            self._model_path, self._vocab, self._model_bytes = "", None, 0
+            self._model_path, self._draft_path, self._vocab, self._model_bytes = "", "", None, 0
             return True
+
+    def _drop_batch(self):
+        for models in self._batch.values():
+            for m in models:
+                if m is not None:
+                    m.close()
+        self._batch = {}
+
+    def _batch_models(self, n_seq, spec):
+        """Target (and draft) models with n_seq sequence slots, loaded from the
+        same files on first use (a second copy of the weights) and kept."""
+        have = self._batch.get(n_seq)
+        if have is None or (spec and have[1] is None):
+            if have is not None:
+                have[0].close()
+            t = load_gguf_model(self._ctx, self._model_path, self._max_ctx, n_seq=n_seq)
+            d = load_gguf_model(self._ctx, self._draft_path, self._max_ctx, n_seq=n_seq) if spec else None
+            self._batch[n_seq] = have = (t, d)
+        return have
 
     @staticmethod
     def _read_vocab(g):
@@ -220,26 +243,86 @@ class InferenceAPI:
             self._throughput = len(toks) / dt if dt > 0 else 0.0
             return GenerationResult(toks, self.token_text(toks), len(toks), dt * 1e3, self._throughput)
 
+    MAX_BATCH = 8  # sequences per batched loop (ulspec_model_create_batch)
+
+    def generate_tokens_batch(self, prompts, config=None):
+        """A GenerationResult per prompt (token ids in), the prompts stepped
+        together in groups of up to MAX_BATCH sequences on the batched device
+        loop: one verify forward of (k + 1) rows per sequence per step
+        (speculative when enabled with a draft model, else target-only
+        decoding).  Greedy results equal generate_tokens() prompt by prompt;
+        sampled ones draw from the batch's uniform stream (sequence b of step
+        s: u(seed, (s B + b)(2k + 1) + j)), not the one-prompt stream.
+        time_ms and tokens_per_second are those of the prompt's group."""
+        with self._lock:
+            if self._target is None:
+                raise UlspecError(EUNSUPPORTED, "no model loaded")
+            config = config or self._config
+            s = self._sampling(config)
+            spec = self._spec and self._draft is not None
+            k = self.SPEC_LENGTH if spec else 0
+            want = int(config.max_tokens)
+            results, n_tok, t_all = [], 0, 0.0
+            for g0 in range(0, len(prompts), self.MAX_BATCH):
+                group = [np.asarray(p, np.int32) for p in prompts[g0:g0 + self.MAX_BATCH]]
+                if len(group) == 1:
+                    results.append(self.generate_tokens(group[0], config))
+                    n_tok += results[-1].num_tokens
+                    t_all += results[-1].time_ms * 1e-3
+                    continue
+                tgt, dft = self._batch_models(len(group), spec)
+                loop = Speculative(tgt, dft if spec else None, k, s, self._seed, n_seq=len(group))
+                try:
+                    t0 = time.perf_counter()
+                    loop.prefill(group)
+                    n0 = [loop.seq_state(b)["n"] for b in range(len(group))]
+                    loop.generate(want)
+                    dt = time.perf_counter() - t0
+                    for b in range(len(group)):
+                        st = loop.seq_state(b)
+                        toks = loop.tokens(n0[b], min(want, st["n"] - n0[b]), seq=b).tolist()
+                        results.append(GenerationResult(toks, self.token_text(toks), len(toks), dt * 1e3,
+                                                        len(toks) / dt if dt > 0 else 0.0))
+                        n_tok += len(toks)
+                        if spec:
+                            self._accepted += st["accepted"]
+                            self._proposed += st["proposed"]
+                    t_all += dt
+                finally:
+                    loop.close()
+            self._throughput = n_tok / t_all if t_all > 0 else 0.0
+            return results
+
+    def generate_batch(self, prompts, config=None):
+        """InferenceAPI::generate_batch (inference_api.cpp:164-175): an output
+        text per prompt (text through the registered tokenizer, or token ids),
+        "Error: No model loaded" for each without a model; the prompts run
+        together on the batched loop (generate_tokens_batch)."""
+        with self._lock:
+            if self._target is None:
+                return ["Error: No model loaded" for _ in prompts]
+            ids = [self._tokenize(p) for p in prompts]
+            return [r.text for r in self.generate_tokens_batch(ids, config)]
+
+    def _tokenize(self, prompt):
+        if isinstance(prompt, str):
+            if self._tokenizer is None:
+                raise UlspecError(EUNSUPPORTED, "text prompts need register_custom_tokenizer()")
+            return self._tokenizer(prompt)
+        return prompt
+
     def generate(self, prompt, config=None):
         """Text (with a registered tokenizer) or token ids in, text out
         (InferenceAPI::generate, :45-63, including its error string)."""
         with self._lock:
             if self._target is None:
                 return "Error: No model loaded"
-            if isinstance(prompt, str):
-                if self._tokenizer is None:
-                    raise UlspecError(EUNSUPPORTED, "text prompts need register_custom_tokenizer()")
-                prompt = self._tokenizer(prompt)
-            return self.generate_tokens(prompt, config).text
+            return self.generate_tokens(self._tokenize(prompt), config).text
 
     def generate_default(self, prompt):
         """generate() with the API's own configuration (:65-77)."""
         with self._lock:
-            if isinstance(prompt, str):
-                if self._tokenizer is None:
-                    raise UlspecError(EUNSUPPORTED, "text prompts need register_custom_tokenizer()")
-                prompt = self._tokenizer(prompt)
-            return self.generate_tokens(prompt, self._config)
+            return self.generate_tokens(self._tokenize(prompt), self._config)
 
     def token_text(self, tokens):
         """Decoded text when the GGUF vocabulary covers the ids, else the ids."""
