@@ -286,6 +286,20 @@ public:
         }
         return step_result();
     }
+    // One step of the loop; the tokens it committed (any step kind).
+    std::vector<uint32_t> step_tokens()
+    {
+        ensure();
+        uint32_t n0 = 0, n1 = 0;
+        uint64_t acc0 = 0, prop0 = 0, acc1 = 0, prop1 = 0;
+        check(ctx(), ulspec_spec_state(sp_, &n0, nullptr, &acc0, &prop0), "ulspec_spec_state");
+        check(ctx(), ulspec_spec_steps(sp_, 1), "ulspec_spec_steps");
+        check(ctx(), ulspec_spec_state(sp_, &n1, nullptr, &acc1, &prop1), "ulspec_spec_state");
+        update_acceptance_stats((uint32_t)(acc1 - acc0), (uint32_t)(prop1 - prop0));
+        std::vector<int32_t> t(n1 - n0);
+        if (n1 > n0) check(ctx(), ulspec_spec_tokens(sp_, n0, n1 - n0, t.data()), "ulspec_spec_tokens");
+        return std::vector<uint32_t>(t.begin(), t.end());
+    }
     // Generate at least n_new tokens; returns the committed sequence after the prompt.
     std::vector<uint32_t> generate(uint32_t n_new)
     {
@@ -359,6 +373,17 @@ struct GenerationResult {
     uint32_t num_tokens = 0;
     float time_ms = 0.0f;
     float tokens_per_second = 0.0f;
+};
+
+// py::GenerationProgress (src/api/inference_api.h:32-40).
+struct GenerationProgress {
+    uint32_t current_step = 0;
+    uint32_t total_steps = 0;
+    float progress_pct = 0.0f;
+    float time_elapsed_ms = 0.0f;
+    float estimated_remaining_ms = 0.0f;
+    float tokens_per_second = 0.0f;
+    std::string last_token;
 };
 
 // The speculative-decoding and sampling entry points of py::InferenceAPI.
@@ -529,6 +554,37 @@ public:
         }
         return generate_tokens(ids, config).text;
     }
+    // InferenceAPI::generate_streaming (inference_api.cpp:96-125): the
+    // callback gets each new token's text as the loop commits it (one step,
+    // then a host fence); returns the whole text.
+    std::string generate_streaming(const std::string& prompt, const GenerationConfig& config,
+                                   std::function<void(const std::string&)> token_callback)
+    {
+        return stream_(prompt, config, [&](const std::string& piece, uint32_t, float) {
+            if (token_callback) token_callback(piece);
+        });
+    }
+    // InferenceAPI::generate_with_progress (inference_api.cpp:127-162): a
+    // GenerationProgress after each committed token; returns the text (the
+    // reference returns an empty string: its result is never filled).
+    std::string generate_with_progress(const std::string& prompt, const GenerationConfig& config,
+                                       std::function<void(const GenerationProgress&)> progress_callback)
+    {
+        const uint32_t total = config.max_tokens;
+        return stream_(prompt, config, [&](const std::string& piece, uint32_t done, float sec) {
+            if (!progress_callback) return;
+            GenerationProgress p;
+            p.current_step = done;
+            p.total_steps = total;
+            p.progress_pct = total ? 100.0f * (float)done / (float)total : 100.0f;
+            p.time_elapsed_ms = sec * 1e3f;
+            p.tokens_per_second = sec > 0.0f ? (float)done / sec : 0.0f;
+            p.estimated_remaining_ms = p.tokens_per_second > 0.0f ? (float)(total - done) / p.tokens_per_second * 1e3f
+                                                                  : 0.0f;
+            p.last_token = piece;
+            progress_callback(p);
+        });
+    }
     // InferenceAPI::generate_batch (inference_api.cpp:164-175): generate()
     // for each prompt, in order, as the reference does (the Python module's
     // generate_batch steps the prompts together on the batched loop).
@@ -583,6 +639,40 @@ private:
         ulspec_sampling s{1.0f, 0, 1.0f, 1};
         if (c.do_sample) s = ulspec_sampling{c.temperature, c.top_k, c.top_p, 0};
         return s;
+    }
+    // The loop one step at a time for the streaming entry points (the lock is
+    // held throughout, as the reference holds api_mutex_); on(text of the
+    // token, tokens so far, seconds) per committed token, up to max_tokens.
+    std::string stream_(const std::string& prompt, const GenerationConfig& config,
+                        const std::function<void(const std::string&, uint32_t, float)>& on)
+    {
+        std::lock_guard<std::mutex> lock(mu_);
+        if (!target_) return "Error: No model loaded";
+        if (!tokenizer_) throw Error(ULSPEC_EUNSUPPORTED, "text prompts need register_custom_tokenizer()");
+        const std::vector<uint32_t> ids = tokenizer_(prompt);
+        const bool spec = spec_ && draft_;
+        SpeculativeDecoder dec(target_->cfg().vocab, spec ? k_ : 0, 0.0f);
+        dec.attach(*target_, spec ? draft_ : nullptr, sampling_(config), seed_);
+        const auto t0 = std::chrono::steady_clock::now();
+        dec.prefill(ids);
+        std::string text;
+        uint32_t done = 0;
+        while (done < config.max_tokens) {
+            for (uint32_t t : dec.step_tokens()) {
+                if (done == config.max_tokens) break;
+                ++done;
+                const std::string piece = token_text({t});
+                text += piece;
+                on(piece, done, std::chrono::duration<float>(std::chrono::steady_clock::now() - t0).count());
+            }
+        }
+        const float sec = std::chrono::duration<float>(std::chrono::steady_clock::now() - t0).count();
+        throughput_ = sec > 0.0f ? (float)done / sec : 0.0f;
+        if (spec) {
+            accepted_ += dec.accepted();
+            proposed_ += dec.proposed();
+        }
+        return text;
     }
     std::vector<uint32_t> run_(const std::vector<uint32_t>& prompt, uint32_t max_tokens, const ulspec_sampling& s)
     {

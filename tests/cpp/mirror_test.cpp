@@ -109,6 +109,22 @@ static int files_part(Context& ctx, const char* target_path, const char* draft_p
         std::printf("generate_batch\n");
         return 1;
     }
+    for (bool sp : {true, false}) {
+        api.enable_speculative_decoding(sp);
+        std::string pieces;
+        uint32_t calls = 0, last_step = 0;
+        const std::string streamed = api.generate_streaming("w1 w2 w3 w4", c, [&](const std::string& t) {
+            pieces += t;
+            ++calls;
+        });
+        const std::string progressed = api.generate_with_progress("w1 w2 w3 w4", c, [&](const GenerationProgress& p) {
+            last_step = p.current_step;
+        });
+        if (streamed != plain || pieces != plain || calls != 16 || progressed != plain || last_step != 16) {
+            std::printf("streaming: '%s' (%u calls), progress %u\n", streamed.c_str(), calls, last_step);
+            return 1;
+        }
+    }
     const float rate = api.get_acceptance_rate();
     if (!(rate >= 0.0f && rate <= 1.0f)) {
         std::printf("acceptance rate %f\n", rate);

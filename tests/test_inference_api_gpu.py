@@ -102,3 +102,25 @@ def test_generate_batch(pkg, ctx, api_mod, files):
     texts = api.generate_batch([" ".join(str(t) for t in p) for p in prompts[:3]], cfg)
     assert texts == [api.generate_tokens(p, cfg).text for p in prompts[:3]]
     api.unload_model()
+
+
+def test_streaming_and_progress(pkg, ctx, api_mod, files):
+    """generate_streaming / generate_with_progress: one callback per committed
+    token, in order, the texts joining to generate()'s output."""
+    target, draft = files
+    api = api_mod.InferenceAPI(ctx=ctx, seed=5)
+    assert api.generate_streaming([1, 2], None, print) == "Error: No model loaded"
+    api.load_model(target)
+    api.load_draft_model(draft)
+    cfg = api_mod.GenerationConfig(max_tokens=14, do_sample=False)
+    prompt = [3, 1, 4, 1, 5, 9]
+    for spec in (True, False):
+        api.enable_speculative_decoding(spec)
+        want = api.generate_tokens(prompt, cfg)
+        pieces, prog = [], []
+        assert api.generate_streaming(prompt, cfg, pieces.append) == want.text
+        assert pieces == [api.token_text([t]) for t in want.tokens]
+        assert api.generate_with_progress(prompt, cfg, prog.append) == want.text
+        assert [p.current_step for p in prog] == list(range(1, 15)) and prog[-1].progress_pct == 100.0
+        assert [p.last_token for p in prog] == pieces and all(p.total_steps == 14 for p in prog)
+    api.unload_model()

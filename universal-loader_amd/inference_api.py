@@ -8,6 +8,7 @@ library: same class and method names, argument meaning and result types.
     api.enable_speculative_decoding(True)    # :214-216 (a no-op there)
     res = api.generate_tokens(prompt_ids, GenerationConfig(max_tokens=64))
     texts = api.generate_batch(prompts)      # :164-175 (a loop of generate there; the batched loop here)
+    api.generate_streaming(p, cfg, print)    # :96-125, token texts as they are committed
     api.get_acceptance_rate()                # :222-225 (0.0 there; live here)
     api.get_token_logits(ids)                # :277-280 (empty there; live here)
 
@@ -48,6 +49,18 @@ class GenerationResult:
     num_tokens: int = 0
     time_ms: float = 0.0
     tokens_per_second: float = 0.0
+
+
+@dataclass
+class GenerationProgress:
+    """py::GenerationProgress (inference_api.h:32-40)."""
+    current_step: int = 0
+    total_steps: int = 0
+    progress_pct: float = 0.0
+    time_elapsed_ms: float = 0.0
+    estimated_remaining_ms: float = 0.0
+    tokens_per_second: float = 0.0
+    last_token: str = ""
 
 
 @dataclass
@@ -242,6 +255,69 @@ class InferenceAPI:
                 self._proposed += st["proposed"]
             self._throughput = len(toks) / dt if dt > 0 else 0.0
             return GenerationResult(toks, self.token_text(toks), len(toks), dt * 1e3, self._throughput)
+
+    def _stream(self, prompt, config, on_token):
+        """The device loop one step at a time (a host fence per step): on_token
+        (token id, text, tokens so far, seconds) for each committed token, up
+        to max_tokens.  Returns the generated text."""
+        config = config or self._config
+        s = self._sampling(config)
+        spec = self._spec and self._draft is not None
+        loop = Speculative(self._target, self._draft if spec else None, self.SPEC_LENGTH if spec else 0, s,
+                           self._seed)
+        want, done, text = int(config.max_tokens), 0, ""
+        try:
+            t0 = time.perf_counter()
+            loop.prefill(np.asarray(self._tokenize(prompt), np.int32))
+            st = loop.state()
+            n = st["n"]
+            while done < want:
+                loop.steps(1)
+                st = loop.state()
+                for t in loop.tokens(n, st["n"] - n).tolist()[:want - done]:
+                    done += 1
+                    piece = self.token_text([t])
+                    text += piece
+                    on_token(t, piece, done, time.perf_counter() - t0)
+                n = st["n"]
+            dt = time.perf_counter() - t0
+        finally:
+            loop.close()
+        if spec:
+            self._accepted += st["accepted"]
+            self._proposed += st["proposed"]
+        self._throughput = done / dt if dt > 0 else 0.0
+        return text
+
+    def generate_streaming(self, prompt, config, token_callback):
+        """InferenceAPI::generate_streaming (inference_api.cpp:96-125): the
+        callback gets each new token's text as it is committed; returns the
+        whole text ("Error: No model loaded" without a model)."""
+        with self._lock:
+            if self._target is None:
+                return "Error: No model loaded"
+            return self._stream(prompt, config,
+                                lambda t, piece, done, sec: token_callback(piece) if token_callback else None)
+
+    def generate_with_progress(self, prompt, config, progress_callback):
+        """InferenceAPI::generate_with_progress (inference_api.cpp:127-162): a
+        GenerationProgress after each committed token.  Returns the generated
+        text (the reference returns an empty string: its result is never
+        filled)."""
+        with self._lock:
+            if self._target is None:
+                return "Error: No model loaded"
+            config = config or self._config
+            total = int(config.max_tokens)
+
+            def on_token(t, piece, done, sec):
+                if progress_callback is None:
+                    return
+                rate = done / sec if sec > 0 else 0.0
+                progress_callback(GenerationProgress(done, total, 100.0 * done / total if total else 100.0,
+                                                     sec * 1e3, (total - done) / rate * 1e3 if rate > 0 else 0.0,
+                                                     rate, piece))
+            return self._stream(prompt, config, on_token)
 
     MAX_BATCH = 8  # sequences per batched loop (ulspec_model_create_batch)
 
