@@ -380,6 +380,8 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
         return fail(ctx, ULSPEC_EINVAL, "verify_attention: %u sequences (1..%d, device prefixes)", c.nseq, kMaxSeqs);
     attn_plan(a.L, a.H * a.nseq, ctx->n_cu, a.splits, a.keys_per_split);
     if (c.dyn_prefix && a.splits == 1) a.splits = 2;  // keep the merge: a split may return early
+    if (a.splits > kAttnMaxSplits)  // the merge stages at most kAttnMaxSplits (m, l) pairs
+        return fail(ctx, ULSPEC_EUNSUPPORTED, "verify_attention: %d splits (at most %d)", a.splits, kAttnMaxSplits);
     void* ws = c.part;
     const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D, a.nseq);
     if (wsb && !ws) {
