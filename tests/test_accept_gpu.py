@@ -159,6 +159,28 @@ def test_accept_edge_cases(ctx, ora, pkg, rng):
         assert nacc[2] == 0
 
 
+def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng):
+    # integer-valued logits, 300 tokens at each of the three largest values:
+    # the candidate threshold of the one-workgroup-per-row top-k lands on a
+    # value that ~900 tokens share (the sorted, not the counted, candidate
+    # list); ties are broken by lowest index, as in the oracle
+    B, k, V = 2, 4, 32000
+    s, so = pkg.sampling(0.8, top_k=40, top_p=0.9), ora.sampling(0.8, top_k=40, top_p=0.9)
+
+    def tied(shape):
+        x = rng.integers(0, 7, size=shape).astype(np.float32)
+        flat = x.reshape(-1, shape[-1])
+        for row in flat:
+            idx = rng.permutation(V)[:900]
+            row[idx[:300]], row[idx[300:600]], row[idx[600:]] = 9.0, 8.0, 7.0
+        return x
+
+    tl, dl = tied((B, k + 1, V)), tied((B, k, V))
+    dt = _draft_tokens(ora, so, dl, 5)
+    u = rng.random((B, k + 1)).astype(np.float32)
+    _check(ctx, ora, pkg, s, tl, dl, dt, u)
+
+
 def test_sample_matches_oracle(ctx, ora, pkg, rng):
     for (T, tk, tp, greedy), V in [((0.8, 40, 0.9, False), 32000), ((1.0, 0, 1.0, False), 32000),
                                    ((1.0, 0, 1.0, True), 128256), ((0.7, 5, 1.0, False), 7),

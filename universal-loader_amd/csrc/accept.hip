@@ -1796,8 +1796,114 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
 
-void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w)
+// A row's whole top-k statistics in one workgroup, for rows that fit in its
+// registers (V <= kRowFusedV) and a k that the 16 waves' kept maxima cover
+// (topk_m > 0): the row is read once (every load in flight), each wave keeps
+// its m largest per-thread maximum keys, the candidate threshold is the
+// largest kept key with at least k kept keys at or above it, the tokens at or
+// above it go from registers into an LDS list, and topk_finish_kernel's finish
+// runs on that list.  The threshold only bounds the candidates (the kept set
+// is the exact top k whatever it is), so the statistics equal those of the
+// scan / threshold / collect / finish launches.
+constexpr int kRowF4 = 8;  // float4 groups per thread
+constexpr uint32_t kRowFusedV = 4u * kRowF4 * kRowThreads;
+
+__global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32_t V, WarpParams p, int m, TopkWs w)
 {
+    constexpr int NWV = kRowThreads / 64;
+    __shared__ uint64_t red[NWV];
+    __shared__ uint64_t buf[kCandMax];
+    __shared__ uint64_t cand[kCandMax];
+    __shared__ uint32_t tops[NWV * kTopM];
+    __shared__ uint32_t cand_count;
+    __shared__ uint64_t keptE[kKMax];
+    const uint32_t r = blockIdx.x, k = p.top_k, V4 = (V + 3) / 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* row = rs.row(r, V);
+    float4 v[kRowF4];
+#pragma unroll
+    for (int i = 0; i < kRowF4; ++i) v[i] = load4(row, V, min((uint32_t)(tid + i * kRowThreads), V4 - 1));
+    uint64_t best = 0;  // order key: the thread's largest key, lowest index among equals
+#pragma unroll
+    for (int i = 0; i < kRowF4; ++i) {
+        const uint32_t q = tid + i * kRowThreads;
+        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q < V4 && 4 * q + c < V) {
+                const uint64_t o = order_key(float_key(e[c]), 4 * q + c);
+                best = o > best ? o : best;
+            }
+    }
+    // the wave's m largest per-thread maximum keys, strictly decreasing (so
+    // from distinct tokens; 0 = none)
+    const uint32_t bk = (uint32_t)(best >> 32);
+    uint32_t prev = 0xffffffffu;
+    for (int j = 0; j < m; ++j) {  // uniform
+        uint32_t t = bk < prev ? bk : 0u;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) t = max(t, (uint32_t)__shfl_xor((int)t, o));
+        if (lane == j) tops[wave * kTopM + j] = t;
+        prev = t;
+    }
+    if (tid == 0) cand_count = 0;
+    const uint64_t top = block_max_u64<kRowThreads>(best, red);  // its barriers publish tops and cand_count
+    const int n = NWV * m;
+    uint32_t thr = 0;
+    if (tid < n) {
+        const uint32_t tv = tops[(tid / m) * kTopM + tid % m];
+        if (tv) {
+            uint32_t ge = 0;
+            for (int j = 0; j < n; ++j) ge += tops[(j / m) * kTopM + j % m] >= tv;
+            if (ge >= k) thr = tv;
+        }
+    }
+    thr = (uint32_t)block_max_u64<kRowThreads>(thr, red);  // 0 (no bound): every token, then the fallback
+#pragma unroll
+    for (int i = 0; i < kRowF4; ++i) {
+        const uint32_t q = tid + i * kRowThreads;
+        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q < V4 && 4 * q + c < V) {
+                const uint32_t key = float_key(e[c]);
+                if (key >= thr) {
+                    const uint32_t slot = atomicAdd(&cand_count, 1u);
+                    if (slot < (uint32_t)kCandMax) cand[slot] = order_key(key, 4 * q + c);
+                }
+            }
+    }
+    __syncthreads();
+    const uint32_t nc = cand_count;
+    if (nc <= (uint32_t)kRankMax) {
+        rank_top_desc(cand, (int)nc, k, buf);
+    } else if (nc <= (uint32_t)kCandMax) {
+        int n2 = 1;
+        while (n2 < (int)nc) n2 <<= 1;
+        for (int i = tid; i < n2; i += kRowThreads) buf[i] = i < (int)nc ? cand[i] : 0;
+        bitonic_desc(buf, n2);
+    } else {
+        topk_tie_fallback(row, V, k, buf, red, cand_count);
+    }
+    RowStat* st = w.stats + r;
+    const float lmax = key_float((uint32_t)(top >> 32));
+    if (tid == 0) {
+        st->lmax = lmax;
+        st->argmax = (int32_t)(0xffffffffu - (uint32_t)top);
+    }
+    finish_topk(buf, k, lmax, p, st, keptE, cand_count);
+}
+
+// rows <= n_cu: the one-workgroup-per-row kernel (one 16-wave workgroup per
+// CU at a time, so more rows than CUs would run it in two rounds).
+void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w,
+                       int n_cu)
+{
+    const int m_row = topk_m(p.top_k, kRowThreads / 64 / kScanWaves);  // the 16 waves of one workgroup
+    if (V <= kRowFusedV && m_row > 0 && rows <= (uint32_t)std::max(1, n_cu)) {
+        hipLaunchKernelGGL(topk_row_kernel, dim3(rows), dim3(kRowThreads), 0, s, rs, V, p, m_row, w);
+        return;
+    }
     const ChunkPlan cp = chunk_plan(V);
     const dim3 grid(cp.G, rows), blk(kChunkThreads);
     const int m = topk_m(p.top_k, cp.G);
@@ -1902,7 +2008,8 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     }
     const TopkWs tw = topk_ws(ws, rows_t + rows_d);
     RowStat* stats = tw.stats;
-    launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw);
+    launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw,
+                      ctx->n_cu);
     hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), decide_lds_bytes(k, p.top_k), ctx->stream,
                        (const RowStat*)stats, draft_tokens, uniforms, k, p.top_k, V, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
@@ -1996,7 +2103,7 @@ ulspec_status sample_mapped_launch(ulspec_ctx* ctx, const ulspec_sampling* s, ui
         return check_launch(ctx, "sample launch");
     }
     const TopkWs tw = topk_ws(ws, R);
-    launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw);
+    launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw, ctx->n_cu);
     hipLaunchKernelGGL(sample_kernel, dim3(D), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, uniforms,
                        V, map, out_tokens);
     return check_launch(ctx, "sample launch");
