@@ -256,27 +256,44 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
         keptE[t] = fixed_e(key_float(key), lmax, p);
     }
     __syncthreads();
-    if (tid == 0) {
+    // Z = the k weights' sum, then the top-p prefix: the first t whose running
+    // sum c_t (as a double) reaches top_p Z keeps t + 1 tokens and Z = c_t
+    // (none: all k, Z unchanged).  Wave 0 scans 64 weights at a time; the u64
+    // sums are exact, so they equal a serial running sum.
+    if (tid < 64) {
+        const int lane = tid;
+        auto scan = [&](uint32_t base, uint64_t carry) {  // running sum at base + lane
+            uint64_t inc = base + lane < k ? keptE[base + lane] : 0;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint64_t y = __shfl_up(inc, o);
+                if (lane >= o) inc += y;
+            }
+            return inc + carry;
+        };
         uint64_t z = 0;
-        for (uint32_t t = 0; t < k; ++t) z += keptE[t];
+        for (uint32_t base = 0; base < k; base += 64) z = __shfl(scan(base, z), 63);
         uint32_t nk = k;
         if (p.top_p < 1.0f) {
             const double thr = (double)p.top_p * (double)z;
-            uint64_t c = 0;
-            uint32_t t = 0;
-            for (; t < k; ++t) {
-                c += keptE[t];
-                if ((double)c >= thr) {
-                    ++t;
+            uint64_t carry = 0;
+            for (uint32_t base = 0; base < k; base += 64) {
+                const uint64_t c = scan(base, carry);
+                const uint64_t hit = __ballot(base + lane < k && (double)c >= thr);
+                if (hit) {
+                    const int first = __ffsll((unsigned long long)hit) - 1;
+                    nk = base + first + 1;
+                    z = __shfl(c, first);
                     break;
                 }
+                carry = __shfl(c, 63);
             }
-            nk = t;
-            z = c;
         }
-        st->Z = z;
-        st->nk = (int32_t)nk;
-        cand_count = nk;
+        if (lane == 0) {
+            st->Z = z;
+            st->nk = (int32_t)nk;
+            cand_count = nk;
+        }
     }
     __syncthreads();
     const uint32_t nk = cand_count;
