@@ -159,12 +159,15 @@ def test_accept_edge_cases(ctx, ora, pkg, rng):
         assert nacc[2] == 0
 
 
-def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng):
+@pytest.mark.parametrize("B,k", [(2, 4), (16, 8)])
+def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, B, k):
     # integer-valued logits, 300 tokens at each of the three largest values:
-    # the candidate threshold of the one-workgroup-per-row top-k lands on a
-    # value that ~900 tokens share (the sorted, not the counted, candidate
-    # list); ties are broken by lowest index, as in the oracle
-    B, k, V = 2, 4, 32000
+    # with 18 rows the one-workgroup-per-row top-k (16 waves) puts its
+    # candidate threshold on a value ~900 tokens share (the sorted, not the
+    # counted, candidate list); with 272 rows the 8-wave workgroups keep fewer
+    # maxima per row and the threshold admits ~9800 tokens (the exact tie
+    # fallback).  Ties are broken by lowest index, as in the oracle.
+    V = 32000
     s, so = pkg.sampling(0.8, top_k=40, top_p=0.9), ora.sampling(0.8, top_k=40, top_p=0.9)
 
     def tied(shape):

@@ -333,7 +333,8 @@ struct RowSel {
 
 // Exact top k of a row whose candidates overflow kCandMax (heavy ties): the
 // k-th largest key by bisection on counts, then the ties at that key taken by
-// lowest index; buf[0..k) = the kept order keys, sorted.  kRowThreads threads.
+// lowest index; buf[0..k) = the kept order keys, sorted.  NT threads.
+template <int NT>
 __device__ void topk_tie_fallback(const float* __restrict__ row, uint32_t V, uint32_t k, uint64_t* buf, uint64_t* red,
                                   uint32_t& cand_count)
 {
@@ -344,15 +345,15 @@ __device__ void topk_tie_fallback(const float* __restrict__ row, uint32_t V, uin
     while (lo < hi) {
         const uint32_t mid = lo + (uint32_t)(((uint64_t)hi - lo + 1) >> 1);
         uint64_t c = 0;
-        for (uint32_t i = tid; i < V; i += kRowThreads) c += float_key(row[i]) >= mid;
-        c = block_sum_u64<kRowThreads>(c, red);
+        for (uint32_t i = tid; i < V; i += NT) c += float_key(row[i]) >= mid;
+        c = block_sum_u64<NT>(c, red);
         if (c >= k) lo = mid;
         else hi = mid - 1;
     }
     const uint32_t kt = lo;
     if (tid == 0) cand_count = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < V; i += kRowThreads) {
+    for (uint32_t i = tid; i < V; i += NT) {
         const uint32_t key = float_key(row[i]);
         if (key > kt) buf[atomicAdd(&cand_count, 1u)] = order_key(key, i);  // < k of them
     }
@@ -360,19 +361,19 @@ __device__ void topk_tie_fallback(const float* __restrict__ row, uint32_t V, uin
     const uint32_t ngt = cand_count;
     const uint32_t need = k - ngt;
     // ties in index order: thread t owns the contiguous chunk [t*C, (t+1)*C)
-    const uint32_t C = (V + kRowThreads - 1) / kRowThreads;
+    const uint32_t C = (V + NT - 1) / NT;
     const uint32_t c0 = tid * C, c1 = min(V, c0 + C);
     uint64_t mine = 0;
     for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == kt;
     uint64_t rank = 0;
-    block_exclusive_scan_u64<kRowThreads>(mine, rank, red);
+    block_exclusive_scan_u64<NT>(mine, rank, red);
     for (uint32_t i = c0; i < c1 && rank < need; ++i)
         if (float_key(row[i]) == kt) {
             buf[ngt + rank] = order_key(kt, i);
             ++rank;
         }
     __syncthreads();
-    for (int i = tid; i < kKMax; i += kRowThreads)
+    for (int i = tid; i < kKMax; i += NT)
         if (i >= (int)k) buf[i] = 0;
     bitonic_desc(buf, kKMax);
 }
@@ -592,7 +593,7 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
             if (i >= (int)nc) buf[i] = 0;  // sorts last
         bitonic_desc(buf, n2);
     } else {
-        topk_tie_fallback(row, V, k, buf, red, cand_count);
+        topk_tie_fallback<kRowThreads>(row, V, k, buf, red, cand_count);
     }
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
@@ -1808,7 +1809,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
         for (int i = threadIdx.x; i < n2; i += kRowThreads) buf[i] = i < (int)nc ? c[i] : 0;
         bitonic_desc(buf, n2);
     } else {
-        topk_tie_fallback(rs.row(r, V), V, k, buf, red, cand_count);
+        topk_tie_fallback<kRowThreads>(rs.row(r, V), V, k, buf, red, cand_count);
     }
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
@@ -1822,12 +1823,17 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
 // runs on that list.  The threshold only bounds the candidates (the kept set
 // is the exact top k whatever it is), so the statistics equal those of the
 // scan / threshold / collect / finish launches.
-constexpr int kRowF4 = 8;  // float4 groups per thread
+// NT = 1024, or 512 (twice the groups per thread) so that two workgroups
+// share a CU (at most 128 registers) when there are more rows than CUs.
+constexpr int kRowF4 = 8;  // float4 groups per thread at kRowThreads
 constexpr uint32_t kRowFusedV = 4u * kRowF4 * kRowThreads;
 
-__global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32_t V, WarpParams p, int m, TopkWs w)
+template <int NT>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void topk_row_kernel(RowSrc rs, uint32_t V,
+                                                                                             WarpParams p, int m,
+                                                                                             TopkWs w)
 {
-    constexpr int NWV = kRowThreads / 64;
+    constexpr int NWV = NT / 64, F4 = kRowF4 * kRowThreads / NT;
     __shared__ uint64_t red[NWV];
     __shared__ uint64_t buf[kCandMax];
     __shared__ uint64_t cand[kCandMax];
@@ -1837,13 +1843,13 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32
     const uint32_t r = blockIdx.x, k = p.top_k, V4 = (V + 3) / 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float* row = rs.row(r, V);
-    float4 v[kRowF4];
+    float4 v[F4];
 #pragma unroll
-    for (int i = 0; i < kRowF4; ++i) v[i] = load4(row, V, min((uint32_t)(tid + i * kRowThreads), V4 - 1));
+    for (int i = 0; i < F4; ++i) v[i] = load4(row, V, min((uint32_t)(tid + i * NT), V4 - 1));
     uint64_t best = 0;  // order key: the thread's largest key, lowest index among equals
 #pragma unroll
-    for (int i = 0; i < kRowF4; ++i) {
-        const uint32_t q = tid + i * kRowThreads;
+    for (int i = 0; i < F4; ++i) {
+        const uint32_t q = tid + i * NT;
         const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -1864,7 +1870,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32
         prev = t;
     }
     if (tid == 0) cand_count = 0;
-    const uint64_t top = block_max_u64<kRowThreads>(best, red);  // its barriers publish tops and cand_count
+    const uint64_t top = block_max_u64<NT>(best, red);  // its barriers publish tops and cand_count
     const int n = NWV * m;
     uint32_t thr = 0;
     if (tid < n) {
@@ -1875,10 +1881,10 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32
             if (ge >= k) thr = tv;
         }
     }
-    thr = (uint32_t)block_max_u64<kRowThreads>(thr, red);  // 0 (no bound): every token, then the fallback
+    thr = (uint32_t)block_max_u64<NT>(thr, red);  // 0 (no bound): every token, then the fallback
 #pragma unroll
-    for (int i = 0; i < kRowF4; ++i) {
-        const uint32_t q = tid + i * kRowThreads;
+    for (int i = 0; i < F4; ++i) {
+        const uint32_t q = tid + i * NT;
         const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -1897,10 +1903,10 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32
     } else if (nc <= (uint32_t)kCandMax) {
         int n2 = 1;
         while (n2 < (int)nc) n2 <<= 1;
-        for (int i = tid; i < n2; i += kRowThreads) buf[i] = i < (int)nc ? cand[i] : 0;
+        for (int i = tid; i < n2; i += NT) buf[i] = i < (int)nc ? cand[i] : 0;
         bitonic_desc(buf, n2);
     } else {
-        topk_tie_fallback(row, V, k, buf, red, cand_count);
+        topk_tie_fallback<NT>(row, V, k, buf, red, cand_count);
     }
     RowStat* st = w.stats + r;
     const float lmax = key_float((uint32_t)(top >> 32));
@@ -1911,14 +1917,19 @@ __global__ __launch_bounds__(kRowThreads) void topk_row_kernel(RowSrc rs, uint32
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
 
-// rows <= n_cu: the one-workgroup-per-row kernel (one 16-wave workgroup per
-// CU at a time, so more rows than CUs would run it in two rounds).
+// The one-workgroup-per-row kernel while the rows fit one round of
+// workgroups: 1024 threads up to one row per CU, 512 (two per CU) up to two.
 void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w,
                        int n_cu)
 {
-    const int m_row = topk_m(p.top_k, kRowThreads / 64 / kScanWaves);  // the 16 waves of one workgroup
-    if (V <= kRowFusedV && m_row > 0 && rows <= (uint32_t)std::max(1, n_cu)) {
-        hipLaunchKernelGGL(topk_row_kernel, dim3(rows), dim3(kRowThreads), 0, s, rs, V, p, m_row, w);
+    const uint32_t cus = (uint32_t)std::max(1, n_cu);
+    const int m16 = topk_m(p.top_k, 16 / kScanWaves), m8 = topk_m(p.top_k, 8 / kScanWaves);  // kept keys per wave
+    if (V <= kRowFusedV && m16 > 0 && rows <= cus) {
+        hipLaunchKernelGGL(topk_row_kernel<1024>, dim3(rows), dim3(1024), 0, s, rs, V, p, m16, w);
+        return;
+    }
+    if (V <= kRowFusedV && m8 > 0 && rows <= 2 * cus) {
+        hipLaunchKernelGGL(topk_row_kernel<512>, dim3(rows), dim3(512), 0, s, rs, V, p, m8, w);
         return;
     }
     const ChunkPlan cp = chunk_plan(V);
