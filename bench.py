@@ -94,10 +94,40 @@ def gemm_roofline(pkg, ctx, ids, M, reps=10):
     return us, alg / len(ids)
 
 
+def instep_gemm_roofline(pkg, model, ids, M, pos, reps=10):
+    """The target's verify GEMMs as a speculative step runs them: every layer's
+    Q|K|V, O, gate|up and down linear plus the LM head, each with its fused
+    prologue and epilogue (split fp16 X operands, RMSNorm row scale, RoPE + K/V
+    append, SiLU, residual), M rows at position pos, launched alone
+    (ulspec_model_linear, direct launches) on the activations the model's last
+    forward left; reps rounds back to back, HIP events on the context stream
+    around them.  Average us per GEMM call (the split-K down projection's
+    reduction launch included) and algorithmic bytes per call."""
+    ctx = model.ctx
+    L = model.cfg.n_layers
+    calls = [(l, w) for l in range(L) for w in range(4)] + [(0, model.LIN_HEAD)]
+
+    def one_round():
+        for l, w in calls:
+            model.linear(l, w, M, pos)
+    one_round()  # warm-up
+    ctx.sync()
+    ctx.timer_mark(2)
+    for _ in range(reps):
+        one_round()
+    ctx.timer_mark(3)
+    ms = ctx.timer_elapsed_ms(2, 3)
+    alg = 0.0
+    for _, (wtype, n, k, _) in ids:
+        alg += n * k * (144 / 256 if wtype == pkg.Q4_K else 18 / 32) + 2 * M * k + 4 * M * n
+    assert len(ids) == len(calls)
+    return ms * 1e3 / (reps * len(calls)), alg / len(ids)
+
+
 def read_traffic():
-    """HBM bytes per launch of the verify GEMM from the committed PMC summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
-    path = os.path.join(REPO, "profiles", "verify_gemm_q4k_7b_m6_pmc.txt")
+    """HBM bytes per call of the in-step verify GEMMs from the committed PMC
+    summary (FETCH_SIZE + WRITE_SIZE, calibrated), or None."""
+    path = os.path.join(REPO, "profiles", "verify_gemm_q4k_7b_m6_instep_pmc.txt")
     try:
         with open(path) as f:
             for line in f:
@@ -111,7 +141,7 @@ def read_traffic():
 def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, n0):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as ora
-    nt = ora.nthreads_default()
+    nproc, allowed, nt = ora.host_cpus()
     s = ora.sampling(greedy=True) if args.greedy else ora.sampling(temperature=args.temperature)
     models = []
     for cfg, host, kv in ((TARGET, target_host, kv_t), (DRAFT, draft_host, kv_d)):
@@ -158,12 +188,12 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
         for a, b in ((r["draft_logits"], dl), (r["target_logits"], tl)):
             b64 = b.astype(np.float64)
             worst = max(worst, float(np.abs(a - b64).max() / np.sqrt((b64 ** 2).mean())))
-    # the same steps on one thread (a bounded sample: at least one step)
+    # the same steps on one thread (a bounded sample: at least two steps)
     for m in models:
         m.set_threads(1)
     busy1, tokens1, steps1 = 0.0, 0, 0
     for n, r in recorded[:steps]:
-        if steps1 and busy1 > args.cpu_seconds / 2:
+        if steps1 >= 2 and busy1 > args.cpu_seconds / 2:
             break
         t0 = time.perf_counter()
         _, _, _, nacc1 = cpu_step(n, r, 1)
@@ -175,10 +205,12 @@ def cpu_leg(pkg, args, target_host, draft_host, kv_t, kv_d, recorded, seq, cap, 
     mode = "greedy" if args.greedy else f"T={args.temperature}"
     return {
         "value": tokens / busy if busy else None, "unit": "tokens/s", "cores": nt, "kind": "port",
+        "nproc": nproc, "cpus_allowed": allowed, "threads": nt,
         "value_1thread": tokens1 / busy1 if busy1 else None, "steps_1thread": steps1, "cpu_model": _cpu_model(),
         "sample": f"{steps} speculative steps (k=5, {mode}) of the 7B-shape Q4_K target/draft pair at context "
                   f"{n0}, from the GPU's post-prefill KV cache; oracle/ C restatement, AVX2 f32 GEMM, {nt} threads "
-                  f"(value), the first {steps1} of them on 1 thread (value_1thread)",
+                  f"(value: the CPUs this process may use, {allowed} of nproc {nproc}, capped at the 16-core host "
+                  f"share of one GPU), the first {steps1} of them on 1 thread (value_1thread)",
         "parity": {"steps": steps, "draft_draws_bit_exact": draws_exact, "accept_bit_exact": accept_exact,
                    "cpu_decisions_equal_gpu": own_agree, "logits_max_err_over_rms": worst},
     }
@@ -514,17 +546,26 @@ def main():
     if args.workload == "roofline":
         target, _ = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=CONTEXT + 64), pkg.Q4_K, seed=1)
         ids = weight_ids(pkg, ctx)
-        us, alg = gemm_roofline(pkg, ctx, ids, K_SPEC + 1)
+        M = K_SPEC + 1
+        prompt = np.random.default_rng(args.seed).integers(0, TARGET["vocab"], 64).astype(np.int32)
+        target.forward(prompt, 0)  # a K/V cache of 64 tokens, then
+        target.forward(prompt[64 - M:], 64 - M, n_logits=1)  # the activations of a 6-row verify forward
+        us, alg = instep_gemm_roofline(pkg, target, ids, M, 64 - M, reps=args.reps // 5 or 1)
         achieved = alg / (us * 1e-6) / 1e9
-        log(f"verify GEMM (target, M=6): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
+        log(f"in-step verify GEMMs (target, M={M}): {len(ids)} calls, {us:.2f} us/call, {alg / 1e6:.2f} MB/call, "
             f"{achieved:.0f} GB/s")
+        us_x, _ = gemm_roofline(pkg, ctx, ids, M, reps=args.reps // 5 or 1)
+        plain = alg / (us_x * 1e-6) / 1e9
+        log(f"the same weights with plain fp16 X (ulspec_verify_gemm): {us_x:.2f} us/launch, {plain:.0f} GB/s")
         target.close()
         ctx.close()
-        print(json.dumps({"metric": "verify-GEMM HBM GB/s, 7B-shape Q4_K target weights, M=6", "value": achieved,
-                          "unit": "GB/s", "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                                                       "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                                                       "traffic": read_traffic(), "avg_us": us,
-                                                       "algorithmic_bytes": alg}}), flush=True)
+        print(json.dumps({"metric": "verify-GEMM HBM GB/s, 7B-shape Q4_K target weights, M=6, in-step fused GEMMs",
+                          "value": achieved, "unit": "GB/s",
+                          "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                       "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic(), "avg_us": us,
+                                       "algorithmic_bytes": alg,
+                                       "plain_x": {"avg_us": us_x, "achieved": plain,
+                                                   "frac": plain / HBM_PEAK_GBS}}}), flush=True)
         return 0
     if args.workload != "step":
         fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
@@ -586,12 +627,24 @@ def main():
         f"accepted {accepted}/{proposed}")
     ids = [(i, info) for i, info in weight_ids(pkg, ctx)[:n_target_w]]
     Mv = (K_SPEC + 1) * B  # the target's verify rows per step
-    us, alg = gemm_roofline(pkg, ctx, ids, Mv)
-    achieved = alg / (us * 1e-6) / 1e9
-    log(f"verify GEMM (target, M={Mv}): {len(ids)} weights, {us:.2f} us/launch, {alg / 1e6:.2f} MB/launch, "
-        f"{achieved:.0f} GB/s")
     seq = sp.tokens(seq=0) if use_cpu else None
+    n_last = sp.seq_state(0)["n"]
     sp.close()
+    plain = None
+    if B == 1:
+        # the step's own target GEMMs (fused prologues / epilogues, split X), on
+        # the activations of the last verify forward, at its positions
+        us, alg = instep_gemm_roofline(pkg, target, ids, Mv, n_last - Mv)
+        us_x, _ = gemm_roofline(pkg, ctx, ids, Mv)
+        plain = {"avg_us": us_x, "achieved": alg / (us_x * 1e-6) / 1e9,
+                 "frac": alg / (us_x * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                 "kernel": "the same 129 weights through ulspec_verify_gemm with plain fp16 X"}
+        log(f"plain-X verify GEMM (target, M={Mv}): {us_x:.2f} us/launch, {plain['achieved']:.0f} GB/s")
+    else:
+        us, alg = gemm_roofline(pkg, ctx, ids, Mv)
+    achieved = alg / (us * 1e-6) / 1e9
+    log(f"verify GEMM (target, M={Mv}): {len(ids)} weights, {us:.2f} us/call, {alg / 1e6:.2f} MB/call, "
+        f"{achieved:.0f} GB/s")
     cpu = None
     if use_cpu:
         cpu = cpu_leg(pkg, args, th, dh, kv_t, kv_d, recorded, seq, cap, CONTEXT)
@@ -609,11 +662,13 @@ def main():
                    "tokens": tokens, "event_ms": ev_ms},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": read_traffic() if B == 1 else None,
-                     "kernel": ("verify dequant-GEMM (gemm_ring_kernel for QKV, gate/up, LM head; gemm_stream_kernel "
-                                "for O, down), the 129 target weights, M=6") if B == 1 else
+                     "kernel": ("the step's verify dequant-GEMMs as it runs them: the 129 target linears at M=6 "
+                                "with fused prologues / epilogues and split fp16 X (gemm_ring_kernel for QKV, "
+                                "gate/up, LM head; gemm_stream_kernel for O; gemm_slice_kernel + gemm_reduce_kernel "
+                                "for down), us per GEMM call") if B == 1 else
                                f"verify dequant-GEMM (split-K gemm_slice_kernel + gemm_reduce_kernel), the 129 target "
                                f"weights, M={Mv}",
-                     "avg_us": us, "algorithmic_bytes": alg},
+                     "avg_us": us, "algorithmic_bytes": alg, "plain_x": plain},
         "cpu_baseline": cpu,
     }
     target.close()

@@ -95,6 +95,16 @@ ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t
  * given size is the streaming-read ceiling the verify kernels are compared
  * with. */
 ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant, uint32_t* sink);
+/* Kernel-route override, no counterpart in the reference (for tests that must
+ * reach each route whatever the device's CU count).  ULSPEC_OPT_TOPK_ROUTE:
+ * how the top-k (kept list, top_k <= 256) statistics run -- 0 chosen from the
+ * rows and CUs (default), 1 one 1024-thread workgroup per row, 2 one
+ * 512-thread workgroup per row, 3 the chunk pipeline (scan, threshold,
+ * collect, finish); a route that cannot take the call (rows past 32768
+ * logits, or k past its kept maxima) falls back to the chunk pipeline.  Every
+ * route gives the same tokens. */
+enum { ULSPEC_OPT_TOPK_ROUTE = 1 };
+ulspec_status ulspec_set_option(ulspec_ctx* ctx, uint32_t option, int64_t value);
 
 /* ---- K1: verify dequant-GEMM ------------------------------------------------
  * Upload one linear weight given as GGUF blocks (host memory, rows of K
@@ -144,8 +154,9 @@ typedef struct {
  * draw from max(0, p_i - q_i) (renormalised) with u[b][k]; if all k pass, draw
  * the bonus token from p_k with u[b][k].  Greedy: accept while argmax p_i ==
  * x_i and emit the argmax.  out_tokens [B][k+1] holds n_accepted + 1 tokens
- * then -1.  All arrays are device memory.  1 <= k <= 16, top_k <= 256,
- * B (2k+1) <= 65535 logit rows per call.
+ * then -1.  All arrays are device memory.  1 <= k <= 16, any top_k (the
+ * kept list path up to 256, a per-row bound over the whole vocabulary
+ * beyond), B (2k+1) <= 65535 logit rows per call.
  * Replaces SpeculativeDecoder::verify_speculation and the sampling of
  * InferenceEngine::sample_token (src/inference/speculative_decoder.cpp:89-110,
  * src/inference/inference_engine.cpp:340-367). */
@@ -259,6 +270,17 @@ ulspec_status ulspec_model_forward_seq(ulspec_model* m, uint32_t seq, const int3
  * a causal forward of its root-to-node path at positions pos, pos+1, .. */
 ulspec_status ulspec_model_forward_tree(ulspec_model* m, const int32_t* tokens, const int32_t* parent, uint32_t M,
                                         uint32_t pos, float* logits);
+/* One linear layer of the model, alone, as a forward runs it: which = 0
+ * Q|K|V (RMSNorm prologue; RoPE, fp16 Q and the K/V append at positions pos
+ * .. pos + M - 1 of sequence slot 0), 1 O (residual epilogue and the next
+ * norm's input), 2 gate|up (RMSNorm prologue, SiLU * up epilogue), 3 down
+ * (residual epilogue), 4 the LM head (final RMSNorm, logits to the model's
+ * own buffer; layer ignored), over the M <= 16 rows the model's activation
+ * buffers hold from its last forward.  The verify GEMM of one linear of
+ * InferenceEngine::forward_layer_gpu (src/inference/inference_engine.cpp:
+ * 602-682) with its neighbours fused; for timing the GEMMs in the
+ * configuration a speculative step runs them.  Asynchronous. */
+ulspec_status ulspec_model_linear(ulspec_model* m, uint32_t layer, uint32_t which, uint32_t M, uint32_t pos);
 /* Commit an accepted tree path: K/V rows pos + path[j] -> pos + j for j = 1
  * .. min(*n_accepted + 1, n_max) - 1 in every layer (row pos, the root,
  * stays).  path and n_accepted are DEVICE memory, as written by
@@ -342,7 +364,8 @@ ulspec_status ulspec_model_load_gguf_batch(ulspec_ctx* ctx, const ulspec_gguf* g
  * (src/inference/speculative_decoder.cpp:25-71).
  * k = 0 (draft may be NULL): plain decoding of the target, the reference's
  * path with speculation off -- a step forwards t_{n-1} and samples t_n from
- * warp(target logits) with u(seed, s).  k <= 16. */
+ * warp(target logits) with u(seed, s).  k <= 15 (k + 1 verify rows of the
+ * 16 one forward takes). */
 typedef struct ulspec_spec ulspec_spec;
 ulspec_status ulspec_spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
                                  uint64_t seed, ulspec_spec** out);

@@ -98,8 +98,23 @@ def _p(a):
     return a.ctypes.data_as(C.c_void_p) if a is not None else None
 
 
+# Worker threads are capped at 16: the host share of one GPU on the MI355X
+# machines this runs on, whatever count the process is allowed to run on.
+MAX_THREADS = 16
+
+
+def host_cpus():
+    """(nproc, the CPUs this process may run on, the threads the oracle uses)."""
+    nproc = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = nproc
+    return nproc, allowed, max(1, min(MAX_THREADS, allowed))
+
+
 def nthreads_default():
-    return max(1, min(16, os.cpu_count() or 1))
+    return host_cpus()[2]
 
 
 # ---- thin numpy wrappers -----------------------------------------------------

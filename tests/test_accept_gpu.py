@@ -159,14 +159,30 @@ def test_accept_edge_cases(ctx, ora, pkg, rng):
         assert nacc[2] == 0
 
 
+TOPK_ROUTES = {1: "one 1024-thread workgroup per row", 2: "one 512-thread workgroup per row",
+               3: "chunk pipeline"}
+
+
+@pytest.fixture
+def topk_route(ctx):
+    """Force a top-k statistics route (ULSPEC_OPT_TOPK_ROUTE); automatic after."""
+    def force(route):
+        ctx.set_option(ctx.OPT_TOPK_ROUTE, route)
+    yield force
+    ctx.set_option(ctx.OPT_TOPK_ROUTE, 0)
+
+
+@pytest.mark.parametrize("route", sorted(TOPK_ROUTES))
 @pytest.mark.parametrize("B,k", [(2, 4), (16, 8)])
-def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, B, k):
+def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, topk_route, route, B, k):
     # integer-valued logits, 300 tokens at each of the three largest values:
-    # with 18 rows the one-workgroup-per-row top-k (16 waves) puts its
-    # candidate threshold on a value ~900 tokens share (the sorted, not the
-    # counted, candidate list); with 272 rows the 8-wave workgroups keep fewer
-    # maxima per row and the threshold admits ~9800 tokens (the exact tie
-    # fallback).  Ties are broken by lowest index, as in the oracle.
+    # the one-workgroup-per-row kernels' candidate threshold lands on a value
+    # ~900 tokens share (16 waves: the sorted, not the counted, candidate
+    # list); with 8 waves they keep fewer maxima per row and the threshold
+    # admits ~9800 tokens (the exact tie fallback); the chunk pipeline's
+    # threshold comes from its per-chunk wave maxima.  Every route is forced
+    # in turn, whatever the device's CU count.  Ties are broken by lowest
+    # index, as in the oracle.
     V = 32000
     s, so = pkg.sampling(0.8, top_k=40, top_p=0.9), ora.sampling(0.8, top_k=40, top_p=0.9)
 
@@ -178,10 +194,69 @@ def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, B, k):
             row[idx[:300]], row[idx[300:600]], row[idx[600:]] = 9.0, 8.0, 7.0
         return x
 
+    topk_route(route)
     tl, dl = tied((B, k + 1, V)), tied((B, k, V))
     dt = _draft_tokens(ora, so, dl, 5)
     u = rng.random((B, k + 1)).astype(np.float32)
     _check(ctx, ora, pkg, s, tl, dl, dt, u)
+
+
+@pytest.mark.parametrize("route", sorted(TOPK_ROUTES))
+def test_accept_topk_routes_random_logits(ctx, ora, pkg, rng, topk_route, route):
+    """N(0, 3^2) logits through each top-k route, forced: B = 32, k = 8 (544
+    rows, more than twice the CUs of an MI355X: the automatic choice at V =
+    32000 would be the chunk pipeline) and B = 16, k = 4."""
+    V = 32000
+    s, so = pkg.sampling(0.8, top_k=40, top_p=0.9), ora.sampling(0.8, top_k=40, top_p=0.9)
+    topk_route(route)
+    for B, k in ((32, 8), (16, 4)):
+        tl = _logits(rng, (B, k + 1, V))
+        dl = (tl[:, :k] * 0.7 + _logits(rng, (B, k, V)) * 0.5).astype(np.float32)
+        dt = _draft_tokens(ora, so, dl, 5)
+        u = rng.random((B, k + 1)).astype(np.float32)
+        _check(ctx, ora, pkg, s, tl, dl, dt, u)
+
+
+@pytest.mark.parametrize("V", [32000, 128256])
+@pytest.mark.parametrize("top_k,top_p", [(257, 1.0), (1000, 0.9), (20000, 0.95), (5000, 1.0)])
+def test_accept_large_top_k(ctx, ora, pkg, rng, V, top_k, top_p):
+    """top_k past the kept-list size (256): the full-vocabulary kernels with a
+    per-row bound (the order key of the k-th token, then the top-p prefix
+    inside the top k), bit-exact with the oracle's sorted warp at the
+    acceptance shapes (B = 16, k = 4)."""
+    B, k = 16, 4
+    s, so = pkg.sampling(0.8, top_k=top_k, top_p=top_p), ora.sampling(0.8, top_k=top_k, top_p=top_p)
+    tl = _logits(rng, (B, k + 1, V), boost=2.0)
+    dl = (tl[:, :k] * 0.7 + _logits(rng, (B, k, V), boost=2.0) * 0.5).astype(np.float32)
+    dt = _draft_tokens(ora, so, dl, 5)
+    dt[3, 0] = V + 7  # out of range: never accepted
+    u = rng.random((B, k + 1)).astype(np.float32)
+    nacc = _check(ctx, ora, pkg, s, tl, dl, dt, u)
+    assert nacc[3] == 0
+    R = 24
+    logits = _logits(rng, (R, V), boost=3.0)
+    uu = ora.uniforms(78, 0, R)
+    bl, bu, bo = ctx.upload(logits), ctx.upload(uu), ctx.alloc(R * 4)
+    ctx.sample(s, R, V, bl, bu, bo)
+    assert np.array_equal(ctx.download(bo, np.int32, (R,)), ora.sample(so, logits, uu))
+    for b in (bl, bu, bo):
+        b.free()
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.5])
+def test_accept_large_top_k_ties_at_the_cut(ctx, ora, pkg, rng, top_p):
+    """Integer-valued logits (every value shared by thousands of tokens): the
+    k-th token falls inside a run of ties, which the bound cuts by lowest
+    index; a row of equal logits; top_k = V - 1."""
+    V, B, k = 32000, 4, 3
+    for top_k in (1000, 4321, V - 1):
+        s, so = pkg.sampling(1.0, top_k=top_k, top_p=top_p), ora.sampling(1.0, top_k=top_k, top_p=top_p)
+        tl = rng.integers(-3, 4, size=(B, k + 1, V)).astype(np.float32)
+        dl = rng.integers(-3, 4, size=(B, k, V)).astype(np.float32)
+        tl[1] = 0.5
+        dt = _draft_tokens(ora, so, dl, 6)
+        u = rng.random((B, k + 1)).astype(np.float32)
+        _check(ctx, ora, pkg, s, tl, dl, dt, u)
 
 
 def test_sample_matches_oracle(ctx, ora, pkg, rng):
@@ -247,9 +322,6 @@ def test_accept_argument_errors(ctx, pkg):
         ctx.accept(pkg.sampling(1.0), 1, 17, 10, b, b, b, b, b, b)
     assert e.value.status == pkg.EINVAL
     with pytest.raises(pkg.UlspecError) as e:
-        ctx.accept(pkg.sampling(1.0, top_k=300), 1, 1, 1000, b, b, b, b, b, b)
-    assert e.value.status == pkg.EUNSUPPORTED
-    with pytest.raises(pkg.UlspecError) as e:
         ctx.accept(pkg.sampling(1.0, top_p=float("nan")), 1, 1, 1000, b, b, b, b, b, b)
     assert e.value.status == pkg.EINVAL
     # rows of one call: B (2k+1) and R at most 65535 (checked before any launch)
@@ -259,4 +331,7 @@ def test_accept_argument_errors(ctx, pkg):
     with pytest.raises(pkg.UlspecError) as e:
         ctx.sample(pkg.sampling(1.0), 70000, 1000, b, b, b)
     assert e.value.status == pkg.EUNSUPPORTED
+    with pytest.raises(pkg.UlspecError) as e:
+        ctx.set_option(ctx.OPT_TOPK_ROUTE, 4)
+    assert e.value.status == pkg.EINVAL
     b.free()

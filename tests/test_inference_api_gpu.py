@@ -92,16 +92,21 @@ def test_generate_batch(pkg, ctx, api_mod, files):
     rng = np.random.default_rng(12)
     prompts = [list(rng.integers(0, 1000, n)) for n in (9, 4, 17, 6, 12, 3, 8, 15, 5, 11)]
     cfg = api_mod.GenerationConfig(max_tokens=12, do_sample=False)
+    pair = None
     for spec in (True, False):
         api.enable_speculative_decoding(spec)
         one = [api.generate_tokens(p, cfg).tokens for p in prompts]
         batch = api.generate_tokens_batch(prompts, cfg)  # a group of 8, then one of 2
         assert [r.tokens for r in batch] == one, spec
         assert all(r.num_tokens == 12 for r in batch) and api.get_throughput() > 0
+        pair = pair or api._batch
     api.register_custom_tokenizer(lambda s: [int(x) for x in s.split()])
     texts = api.generate_batch([" ".join(str(t) for t in p) for p in prompts[:3]], cfg)
     assert texts == [api.generate_tokens(p, cfg).text for p in prompts[:3]]
+    # groups of 8, 2 and 3 sequences all ran on one target / draft pair of 8-slot models
+    assert api._batch is pair and all(m.n_seq == api.MAX_BATCH for m in pair)
     api.unload_model()
+    assert api._batch is None
 
 
 def test_streaming_and_progress(pkg, ctx, api_mod, files):

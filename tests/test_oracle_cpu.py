@@ -291,6 +291,32 @@ def test_warp_top_k_top_p_against_sort(ora, rng):
     assert E[123] == E[456] and Z == int(E.sum())
 
 
+@pytest.mark.parametrize("top_k,top_p", [(300, 1.0), (2999, 1.0), (1500, 0.9), (1000, 0.3)])
+def test_warp_large_top_k_against_sort(ora, rng, top_k, top_p):
+    """top_k past the GPU's kept-list size (256): the kept set is the first
+    top_k of (logit desc, index asc) order, ties at the cut included by
+    lowest index, then the top-p prefix inside it, against a sorted walk."""
+    V = 3000
+    logits = (np.round(rng.standard_normal(V) * 6) / 2).astype(np.float32)  # many ties
+    full, _, _ = ora.warp_row(ora.sampling(0.8), logits)
+    E, Z, nk = ora.warp_row(ora.sampling(0.8, top_k=top_k, top_p=top_p), logits)
+    order = sorted(range(V), key=lambda i: (-float(logits[i]), i))[:top_k]
+    keep = len(order)
+    if top_p < 1.0:
+        thr = float(np.float32(top_p)) * float(sum(int(full[i]) for i in order))
+        c = 0
+        for t, i in enumerate(order):
+            c += int(full[i])
+            if float(c) >= thr:
+                keep = t + 1
+                break
+    kept = order[:keep]
+    assert nk == keep and Z == sum(int(full[i]) for i in kept)
+    assert all(E[i] == full[i] for i in kept) and int(np.count_nonzero(E)) == int(np.count_nonzero(full[kept]))
+    if top_k <= 1500:  # these cuts fall inside a run of equal logits (lower indices of that value kept first)
+        assert logits[order[-1]] == logits[sorted(range(V), key=lambda i: (-float(logits[i]), i))[top_k]]
+
+
 @pytest.mark.parametrize("kind", ["normal", "ties", "flat", "signed_zeros"])
 def test_warp_top_p_without_top_k_is_the_shortest_prefix(ora, rng, kind):
     """Full-vocabulary top-p: the kept tokens are a prefix of (logit desc,

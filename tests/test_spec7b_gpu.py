@@ -12,12 +12,15 @@ Bars:
     of 8 steps are bit-exact with the oracle's own loop;
   - temperature 0.8 over the full vocabulary, teacher-forced on the GPU's
     committed tokens: every draft draw and accept decision is bit-exact with
-    the oracle's rule on the step's logits, and the oracle's own logits for
-    the same tokens are within LOGIT_TOL of their RMS (max |error| / RMS over
-    all rows of the step).  The activations are fp32 on both sides (split
+    the oracle's rule on the step's logits, the oracle's own logits for the
+    same tokens are within LOGIT_TOL of their RMS (max |error| / RMS over all
+    rows of the step), and the oracle's own draws and decisions on its own
+    logits equal the GPU's.  The activations are fp32 on both sides (split
     fp16 pairs into the GPU's MFMAs); only Q and the K/V cache are fp16, so
     the two differ by fp32 summation order and the fp16 roundings that order
     moves.
+  - the growth of that difference with depth: the same weights cut to 1, 2,
+    4, 8, 16 and 32 layers, one 64-token forward on each side.
 """
 import importlib
 
@@ -37,9 +40,18 @@ Q4_K = 12
 
 
 @pytest.fixture(scope="module")
-def models(pkg, ctx, ora):
+def host_target(pkg, ctx):
+    """GGUF bytes of every target tensor (the synthetic weights of seed 1)."""
     synthetic_llama = importlib.import_module("universal_loader_amd.synthetic").synthetic_llama
     gt, th = synthetic_llama(pkg, ctx, dict(TARGET, max_ctx=CAP), Q4_K, seed=1, keep_host=True)
+    yield gt, th
+    gt.close()
+
+
+@pytest.fixture(scope="module")
+def models(pkg, ctx, ora, host_target):
+    synthetic_llama = importlib.import_module("universal_loader_amd.synthetic").synthetic_llama
+    gt, th = host_target
     gd, dh = synthetic_llama(pkg, ctx, dict(DRAFT, max_ctx=CAP), Q4_K, seed=2, keep_host=True)
     oms = []
     for cfg, host in ((TARGET, th), (DRAFT, dh)):
@@ -47,9 +59,9 @@ def models(pkg, ctx, ora):
         for name, (wtype, data, ne0, ne1) in host.items():
             m.set_tensor(name, wtype, data, ne0, ne1)
         oms.append(m)
-    del th, dh
+    del dh
     yield gt, gd, oms[0], oms[1]
-    for m in (gt, gd, *oms):
+    for m in (gd, *oms):
         m.close()
 
 
@@ -108,14 +120,20 @@ def test_7b_sampling_steps_bit_exact(pkg, ora, models, prompt):
         dl = [od.forward(np.array(seq[n - 2:n], np.int32), n - 2, n_logits=1)[0]]
         for j in range(1, k):
             dl.append(od.forward(d[j - 1:j], n - 1 + j, n_logits=1)[0])
+        dl = np.array(dl)
         tl = ot.forward(np.concatenate([[seq[n - 1]], d]).astype(np.int32), n - 1, n_logits=k + 1)
         errs = []
-        for a, b in ((r["draft_logits"], np.array(dl)), (r["target_logits"], tl)):
+        for a, b in ((r["draft_logits"], dl), (r["target_logits"], tl)):
             b64 = b.astype(np.float64)
             errs.append(np.abs(a.astype(np.float64) - b64).max() / np.sqrt((b64 ** 2).mean()))
         worst = max(worst, *errs)
-        print(f"  step {step}: accepted {r['n_accepted']}, logits max err / rms draft {errs[0]:.2e} "
-              f"target {errs[1]:.2e}", flush=True)
+        # the CPU path's own step: its draws on its own draft logits, its decisions on its own logits
+        own_d = [int(ora.sample(s_ora, dl[j][None], u[j:j + 1])[0]) for j in range(k)]
+        out_c, nacc_c = ora.accept(s_ora, tl[None], dl[None], d[None], u[k:][None])
+        print(f"  step {step}: accepted {r['n_accepted']} (oracle's own {int(nacc_c[0])}), logits max err / rms "
+              f"draft {errs[0]:.2e} target {errs[1]:.2e}", flush=True)
+        assert own_d == [int(x) for x in d], step
+        assert int(nacc_c[0]) == r["n_accepted"] and np.array_equal(out_c[0], r["out_tokens"]), step
         seq += list(r["out_tokens"][:r["n_accepted"] + 1])
         accepted += r["n_accepted"]
     assert np.array_equal(sp.tokens(), np.array(seq, np.int32))
@@ -145,3 +163,33 @@ def test_7b_tree_steps_bit_exact(pkg, ora, models, prompt, mode):
                                   mode == "greedy", LOGIT_TOL)
     print(f"  7B tree {mode}: {len(seq) - CONTEXT} tokens in 3 steps, worst logits err {worst:.2e}")
     sp.close()
+
+
+def test_7b_logit_error_by_depth(pkg, ctx, ora, host_target):
+    """The GPU / oracle logit difference as the target grows from 1 to 32
+    layers (the same weights, a fresh 64-token prompt, the last 6 rows): the
+    measured growth behind LOGIT_TOL.  Each depth must stay within it."""
+    _, th = host_target
+    prompt = np.random.default_rng(99).integers(0, TARGET["vocab"], 64).astype(np.int32)
+    rows = []
+    for L in (1, 2, 4, 8, 16, 32):
+        cfg = dict(TARGET, n_layers=L)
+        keep = {name: t for name, t in th.items()
+                if not name.startswith("blk.") or int(name.split(".")[1]) < L}
+        g = pkg.Model(ctx, **cfg, max_ctx=128)
+        o = ora.Llama(**cfg, max_ctx=128, nthreads=ora.nthreads_default())
+        for name, (wtype, data, ne0, ne1) in keep.items():
+            g.set_tensor(name, wtype, data, ne0, ne1)
+            o.set_tensor(name, wtype, data, ne0, ne1)
+        lg = g.forward(prompt, 0, n_logits=K_SPEC + 1).astype(np.float64)
+        lo = o.forward(prompt, 0, n_logits=K_SPEC + 1).astype(np.float64)
+        rms = float(np.sqrt((lo ** 2).mean()))
+        err = float(np.abs(lg - lo).max() / rms)
+        mean = float(np.abs(lg - lo).mean() / rms)
+        same = int((np.argmax(lg, axis=1) == np.argmax(lo, axis=1)).sum())
+        rows.append((L, err, mean, rms, same))
+        print(f"  {L:2d} layers: max err / rms {err:.2e}, mean {mean:.2e} (logit rms {rms:.3f}), "
+              f"argmax equal in {same}/{K_SPEC + 1} rows", flush=True)
+        g.close()
+        o.close()
+    assert all(err <= LOGIT_TOL for _, err, _, _, _ in rows)

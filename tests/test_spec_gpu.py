@@ -292,3 +292,17 @@ def test_model_and_spec_argument_errors(pkg, ctx, weights):
         pkg.Model(ctx, **dict(DRAFT, dim=96 * 8))  # head dim 96
     assert e.value.status == pkg.EUNSUPPORTED
     m.close()
+
+
+def test_spec_k_limit(pkg, ctx, weights):
+    """k draft tokens need k + 1 verify rows of the 16 a forward takes: k = 15
+    is the largest loop, k = 16 fails with EINVAL."""
+    _, dw = weights
+    t, d = _gpu_model(pkg, ctx, DRAFT, dw), _gpu_model(pkg, ctx, DRAFT, dw)
+    sp = pkg.Speculative(t, d, 15, pkg.sampling(greedy=True), 1)
+    sp.close()
+    with pytest.raises(pkg.UlspecError) as e:
+        pkg.Speculative(t, d, 16, pkg.sampling(greedy=True), 1)
+    assert e.value.status == pkg.EINVAL and "k <= 15" in str(e.value)
+    t.close()
+    d.close()

@@ -52,11 +52,12 @@ def _gpu_accept_tree(ctx, s, parent, tl, dl, tokens, u):
     return out, path, nacc
 
 
-@pytest.mark.parametrize("mode", ["topk", "full", "greedy"])
+@pytest.mark.parametrize("mode", ["topk", "full", "greedy", "large_topk"])
 @pytest.mark.parametrize("V", [32000, 128256])
 def test_accept_tree_bit_exact_with_oracle(ctx, ora, pkg, rng, mode, V):
     B, n = 4, 16
-    args = {"topk": (0.8, 40, 0.9, False), "full": (0.8, 0, 1.0, False), "greedy": (1.0, 0, 1.0, True)}[mode]
+    args = {"topk": (0.8, 40, 0.9, False), "full": (0.8, 0, 1.0, False), "greedy": (1.0, 0, 1.0, True),
+            "large_topk": (0.8, 2000, 0.9, False)}[mode]
     s = pkg.sampling(args[0], top_k=args[1], top_p=args[2], greedy=args[3])
     so = ora.sampling(args[0], top_k=args[1], top_p=args[2], greedy=args[3])
     for trial in range(2):

@@ -97,6 +97,7 @@ ABI = [
     ("ulspec_timer_mark", C.c_int, [P, U32]),
     ("ulspec_timer_elapsed_ms", C.c_int, [P, U32, U32, C.POINTER(C.c_float)]),
     ("ulspec_stream_read", C.c_int, [P, P, C.c_size_t, U32, P]),
+    ("ulspec_set_option", C.c_int, [P, U32, C.c_int64]),
     ("ulspec_weight_upload", C.c_int, [P, U32, P, C.c_size_t, U32, U32, C.POINTER(U32)]),
     ("ulspec_weight_info", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32),
                                      C.POINTER(C.c_size_t)]),
@@ -118,6 +119,7 @@ ABI = [
     ("ulspec_model_kv_io", C.c_int, [P, U32, C.c_int, U32, U32, P, P]),
     ("ulspec_model_forward_tree", C.c_int, [P, P, P, U32, U32, P]),
     ("ulspec_model_kv_compact", C.c_int, [P, U32, P, P, U32]),
+    ("ulspec_model_linear", C.c_int, [P, U32, U32, U32, U32]),
     ("ulspec_spec_create", C.c_int, [P, P, U32, C.POINTER(Sampling), C.c_uint64, C.POINTER(P)]),
     ("ulspec_spec_destroy", None, [P]),
     ("ulspec_spec_prefill", C.c_int, [P, P, U32]),
@@ -259,6 +261,11 @@ class Context:
         self._check(lib().ulspec_timer_elapsed_ms(self.handle, a, b, C.byref(ms)))
         return ms.value
 
+    OPT_TOPK_ROUTE = 1
+
+    def set_option(self, option, value):
+        self._check(lib().ulspec_set_option(self.handle, option, value))
+
     def stream_read(self, buf, nbytes, variant, sink):
         """The streaming-read measurement kernel over nbytes of device buffer buf."""
         self._check(lib().ulspec_stream_read(self.handle, _ptr(buf), nbytes, variant, _ptr(sink)))
@@ -366,6 +373,13 @@ class Model:
                                                         parent.ctypes.data_as(P), len(tokens), pos,
                                                         out.ctypes.data_as(P)))
         return out
+
+    LIN_QKV, LIN_O, LIN_GATE_UP, LIN_DOWN, LIN_HEAD = range(5)
+
+    def linear(self, layer, which, M, pos):
+        """One linear of a layer (LIN_*) alone, with its fused prologue and
+        epilogue, over the M rows the activation buffers hold (asynchronous)."""
+        self.ctx._check(lib().ulspec_model_linear(self.handle, layer, which, M, pos))
 
     def kv_compact(self, pos, path, n_accepted, n_max):
         """Keep the accepted path's K/V rows (path, n_accepted: device buffers)."""

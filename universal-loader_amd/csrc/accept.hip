@@ -70,6 +70,23 @@ struct WarpParams {
     int32_t pad;
 };
 
+// top_k modes: a kept list of at most kKMax entries (list_topk), or, for
+// larger k, the full-vocabulary kernels with a per-row bound (bound_topk):
+// the order key of the k-th token, below which every weight is 0.
+__host__ __device__ __forceinline__ bool list_topk(const WarpParams& p, uint32_t V)
+{
+    return p.top_k > 0 && p.top_k < V && p.top_k <= (uint32_t)kKMax;
+}
+__host__ __device__ __forceinline__ bool bound_topk(const WarpParams& p, uint32_t V)
+{
+    return p.top_k > (uint32_t)kKMax && p.top_k < V;
+}
+// Full-vocabulary rows that need a per-row bound (kmin): top-p, or a large top_k.
+__host__ __device__ __forceinline__ bool row_bound(const WarpParams& p, uint32_t V)
+{
+    return !p.greedy && !list_topk(p, V) && (p.top_p < 1.0f || bound_topk(p, V));
+}
+
 // ---- workgroup reductions (all threads call, all get the result) -----------
 template <int NT>
 __device__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
@@ -419,10 +436,102 @@ __device__ __forceinline__ void wave_bin_add(bool act, uint32_t d, uint64_t w, T
     }
 }
 
-// kmin (the order key K*) and the kept sum of a row; all kRowThreads threads
-// call it and get both.
+// (count) of the wave's active tokens into their digit bins (all lanes call it).
+__device__ __forceinline__ void wave_bin_count(bool act, uint32_t d, ToppLds& s)
+{
+    const int lane = threadIdx.x & 63;
+    uint64_t pend = __ballot(act);
+    while (pend) {  // wave-uniform
+        const int leader = __builtin_ctzll(pend);
+        const uint32_t dl = (uint32_t)__shfl((int)d, leader);
+        const uint64_t m = __ballot(act && d == dl);
+        if (lane == leader) atomicAdd(&s.count[dl], (uint32_t)__popcll(m));
+        pend &= ~m;
+    }
+}
+
+// The order key of the row's k-th token by (logit desc, index asc), for
+// 0 < k < V: a radix select on counts over the four 8-bit digits of the logit
+// key gives the k-th largest key kt and the number of tokens above it; the
+// first (k - above) tokens of key kt in index order complete the set, so
+// kmin = order_key(kt, the last of them), or kt << 32 when all of them are
+// in (every order key of kt is above it, every smaller key below).  All
+// kRowThreads threads call it and get kmin.
+__device__ void topk_bound_select(const float* __restrict__ row, uint32_t V, uint32_t k, ToppLds& s, uint64_t* red,
+                                  uint64_t& kmin)
+{
+    constexpr int NT = kRowThreads;
+    constexpr int kBatch = 4;  // float4 groups in flight per thread
+    const int tid = threadIdx.x;
+    const uint32_t V4 = (V + 3) / 4;
+    uint32_t prefix = 0;
+    uint64_t above = 0;
+    for (int lvl = 0; lvl < 4; ++lvl) {
+        const int sh = 24 - 8 * lvl;
+        for (int t = tid; t < 256; t += NT) s.count[t] = 0;
+        __syncthreads();
+        for (uint32_t q0 = 0; q0 < V4; q0 += kBatch * NT) {  // uniform
+            float4 v[kBatch];
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r) v[r] = load4(row, V, min(q0 + (uint32_t)(r * NT + tid), V4 - 1));
+#pragma unroll
+            for (int r = 0; r < kBatch; ++r) {
+                const uint32_t q = q0 + (uint32_t)(r * NT + tid);
+                const float e[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t key = float_key(e[c]);
+                    const bool act = q < V4 && 4 * q + c < V && (lvl == 0 || (key >> (sh + 8)) == prefix);
+                    wave_bin_count(act, (key >> sh) & 255u, s);
+                }
+            }
+        }
+        __syncthreads();
+        // thread t < 256 holds bin 255 - t (descending digit order): the bin
+        // where the count from the top first reaches k (exactly one thread)
+        const uint64_t cv = tid < 256 ? s.count[255 - tid] : 0;
+        uint64_t excl = 0;
+        (void)block_exclusive_scan_u64<NT>(cv, excl, red);
+        if (tid < 256 && above + excl < k && above + excl + cv >= k) {
+            s.digit = 255u - (uint32_t)tid;
+            s.excl_sel = excl;
+            s.count_sel = (uint32_t)cv;
+        }
+        __syncthreads();
+        prefix = (prefix << 8) | s.digit;
+        above += s.excl_sel;
+    }
+    const uint32_t n_t = s.count_sel;
+    const uint64_t need = k - above;  // 1 .. n_t
+    if (need >= n_t) {
+        kmin = (uint64_t)prefix << 32;
+        return;
+    }
+    // the need-th token of key kt in index order: thread t owns [t C, (t+1) C)
+    const uint32_t C = (V + NT - 1) / NT;
+    const uint32_t c0 = min(V, tid * C), c1 = min(V, c0 + C);
+    uint64_t mine = 0;
+    for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == prefix;
+    uint64_t rank = 0;
+    block_exclusive_scan_u64<NT>(mine, rank, red);
+    if (mine && rank < need && need <= rank + mine) {
+        uint64_t r = rank;
+        for (uint32_t i = c0; i < c1; ++i)
+            if (float_key(row[i]) == prefix && ++r == need) {
+                s.tie_idx = i;
+                break;
+            }
+    }
+    __syncthreads();
+    kmin = order_key(prefix, s.tie_idx);
+}
+
+// kmin (the order key K*) and the kept sum of a row, over the tokens whose
+// order key is at least kfloor (0: all; a large top_k's bound otherwise: the
+// top-p prefix is then taken inside the top k, as the oracle's sorted walk
+// does); all kRowThreads threads call it and get both.
 __device__ void topp_select(const float* __restrict__ row, uint32_t V, float lmax, const WarpParams& p, ToppLds& s,
-                            uint64_t* red, uint64_t& kmin, uint64_t& zkept)
+                            uint64_t* red, uint64_t kfloor, uint64_t& kmin, uint64_t& zkept)
 {
     constexpr int NT = kRowThreads;
     constexpr int kBatch = 4;  // float4 groups in flight per thread
@@ -455,7 +564,8 @@ __device__ void topp_select(const float* __restrict__ row, uint32_t V, float lma
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const uint32_t key = float_key(e[c]);
-                    const bool act = q < V4 && 4 * q + c < V && (lvl == 0 || (key >> (sh + 8)) == prefix);
+                    const bool act = q < V4 && 4 * q + c < V && (lvl == 0 || (key >> (sh + 8)) == prefix) &&
+                                     order_key(key, 4 * q + c) >= kfloor;
                     const uint64_t w = act ? fixed_e(e[c], lmax, p) : 0;
                     wave_bin_add(act, (key >> sh) & 255u, w, s);
                 }
@@ -492,27 +602,46 @@ __device__ void topp_select(const float* __restrict__ row, uint32_t V, float lma
         while (j < n_t && (double)(above + (uint64_t)j * e_star) < thr) ++j;
     }
     zkept = above + (uint64_t)j * e_star;
-    if (j == n_t) {
-        kmin = (uint64_t)prefix << 32;
+    if (j == n_t) {  // every active token of that logit (kfloor may cut among its ties)
+        const uint64_t all = (uint64_t)prefix << 32;
+        kmin = all > kfloor ? all : kfloor;
         return;
     }
-    // the j-th token of that logit in index order: thread t owns [t C, (t+1) C)
+    // the j-th token of that logit in index order (of those at or above
+    // kfloor: the lowest indices of that logit): thread t owns [t C, (t+1) C)
     const uint32_t C = (V + NT - 1) / NT;
     const uint32_t c0 = min(V, tid * C), c1 = min(V, c0 + C);
     uint64_t mine = 0;
-    for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == prefix;
+    for (uint32_t i = c0; i < c1; ++i) mine += float_key(row[i]) == prefix && order_key(prefix, i) >= kfloor;
     uint64_t rank = 0;
     block_exclusive_scan_u64<NT>(mine, rank, red);
     if (mine && rank < j && j <= rank + mine) {
         uint64_t r = rank;
         for (uint32_t i = c0; i < c1; ++i)
-            if (float_key(row[i]) == prefix && ++r == j) {
+            if (float_key(row[i]) == prefix && order_key(prefix, i) >= kfloor && ++r == j) {
                 s.tie_idx = i;
                 break;
             }
     }
     __syncthreads();
     kmin = order_key(prefix, s.tie_idx);
+}
+
+// The per-row bound of a full-vocabulary warp (row_bound): the large
+// top_k's bound, then the top-p prefix inside it; z = the kept sum when the
+// top-p select computed it (have_z), else the caller sums the kept weights.
+__device__ void row_bound_select(const float* __restrict__ row, uint32_t V, float lmax, const WarpParams& p,
+                                 ToppLds& s, uint64_t* red, uint64_t& kmin, uint64_t& z, bool& have_z)
+{
+    uint64_t kf = 0;
+    if (bound_topk(p, V)) topk_bound_select(row, V, p.top_k, s, red, kf);
+    have_z = p.top_p < 1.0f;
+    if (have_z) {
+        topp_select(row, V, lmax, p, s, red, kf, kmin, z);
+    } else {
+        kmin = kf;
+        z = 0;
+    }
 }
 
 __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __restrict__ logits, uint32_t V,
@@ -545,11 +674,16 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(const float* __r
     }
     if (p.greedy) return;
 
-    const bool topk = p.top_k > 0 && p.top_k < V;
-    if (!topk && p.top_p < 1.0f) {  // full-vocabulary top-p: the kept prefix and its sum
+    const bool topk = list_topk(p, V);
+    if (row_bound(p, V)) {  // full vocabulary under a bound: top-p, a large top_k, or both
         __shared__ ToppLds tps;
         uint64_t kmin, z;
-        topp_select(row, V, lmax, p, tps, red, kmin, z);
+        bool have_z;
+        row_bound_select(row, V, lmax, p, tps, red, kmin, z, have_z);
+        if (!have_z) {
+            scan_row<kRowThreads>(row, V, [&](uint32_t i, float l) { z += kept_e(l, i, lmax, kmin, p); });
+            z = block_sum_u64<kRowThreads>(z, red);
+        }
         if (tid == 0) {
             st->Z = z;
             st->kmin = kmin;
@@ -946,7 +1080,7 @@ __global__ __launch_bounds__(kSeqThreads) void decide_tree_kernel(const RowStat*
     const float* u = p.greedy ? nullptr : uniforms + (size_t)b * n;
     int32_t* o = out + (size_t)b * n;
     int32_t* pa = path + (size_t)b * n;
-    const bool topk = p.top_k > 0 && p.top_k < V;
+    const bool topk = list_topk(p, V);
 
     for (int i = tid; i < n; i += kSeqThreads) {
         o[i] = -1;
@@ -1330,11 +1464,11 @@ __global__ __launch_bounds__(kChunkThreads) void chunk_pick_kernel(const float* 
     if (threadIdx.x == 0) out[d] = t;
 }
 
-// Top-p bound (kmin) of every row of a chunk launch, one workgroup per row;
-// lmax from the row's chunk maxima.
-__global__ __launch_bounds__(kRowThreads) void topp_rows_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, WarpParams p,
-                                                                const ChunkPart* __restrict__ part,
-                                                                uint64_t* __restrict__ kmin)
+// The bound (kmin: top-p, a large top_k, or both) of every row of a chunk
+// launch, one workgroup per row; lmax from the row's chunk maxima.
+__global__ __launch_bounds__(kRowThreads) void bound_rows_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, WarpParams p,
+                                                                 const ChunkPart* __restrict__ part,
+                                                                 uint64_t* __restrict__ kmin)
 {
     __shared__ uint64_t red[kRowThreads / 64];
     __shared__ ToppLds tps;
@@ -1342,7 +1476,8 @@ __global__ __launch_bounds__(kRowThreads) void topp_rows_kernel(RowSrc rs, uint3
     const ChunkPart* rp = part + (size_t)r * cp.G;
     const uint64_t top = block_max_u64<kRowThreads>(threadIdx.x < cp.G ? rp[threadIdx.x].top : 0, red);
     uint64_t km, z;
-    topp_select(rs.row(r, V), V, key_float((uint32_t)(top >> 32)), p, tps, red, km, z);
+    bool have_z;
+    row_bound_select(rs.row(r, V), V, key_float((uint32_t)(top >> 32)), p, tps, red, km, z, have_z);
     if (threadIdx.x == 0) kmin[r] = km;
 }
 
@@ -1919,16 +2054,18 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
 
 // The one-workgroup-per-row kernel while the rows fit one round of
 // workgroups: 1024 threads up to one row per CU, 512 (two per CU) up to two.
+// route (ULSPEC_OPT_TOPK_ROUTE) forces one of the three where it applies.
 void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w,
-                       int n_cu)
+                       int n_cu, int route)
 {
     const uint32_t cus = (uint32_t)std::max(1, n_cu);
     const int m16 = topk_m(p.top_k, 16 / kScanWaves), m8 = topk_m(p.top_k, 8 / kScanWaves);  // kept keys per wave
-    if (V <= kRowFusedV && m16 > 0 && rows <= cus) {
+    const bool fits16 = V <= kRowFusedV && m16 > 0, fits8 = V <= kRowFusedV && m8 > 0;
+    if (fits16 && (route == 1 || (route == 0 && rows <= cus))) {
         hipLaunchKernelGGL(topk_row_kernel<1024>, dim3(rows), dim3(1024), 0, s, rs, V, p, m16, w);
         return;
     }
-    if (V <= kRowFusedV && m8 > 0 && rows <= 2 * cus) {
+    if (fits8 && (route == 2 || (route == 0 && rows <= 2 * cus))) {
         hipLaunchKernelGGL(topk_row_kernel<512>, dim3(rows), dim3(512), 0, s, rs, V, p, m8, w);
         return;
     }
@@ -1963,8 +2100,6 @@ ulspec_status make_params(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t V,
     if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
         return fail(ctx, ULSPEC_EINVAL, "temperature must be positive and finite (got %g)", (double)s->temperature);
     if (!(s->top_p == s->top_p)) return fail(ctx, ULSPEC_EINVAL, "top_p is NaN");
-    if (s->top_k > (uint32_t)kKMax && s->top_k < V)
-        return fail(ctx, ULSPEC_EUNSUPPORTED, "top_k %u > %d", s->top_k, kKMax);
     p.invT = 1.0f / s->temperature;
     return ULSPEC_OK;
 }
@@ -2007,18 +2142,18 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
         st = workspace(ctx, accept_workspace_bytes(B, k), &ws);
         if (st != ULSPEC_OK) return st;
     }
-    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
+    if (p.greedy || !list_topk(p, V)) {
         const ChunkPlan cp = chunk_plan(V);
         ChunkPart* part = (ChunkPart*)ws;  // [rows_t + rows_d][G]
         ChunkPart* rpart = part + (size_t)(rows_t + rows_d) * cp.G;  // [B][G]
         AcceptPlan* plan = (AcceptPlan*)(rpart + (size_t)B * cp.G);
-        const bool topp = !p.greedy && p.top_p < 1.0f;
-        uint64_t* kmin = topp ? (uint64_t*)(plan + B) : nullptr;  // [rows_t + rows_d]
+        const bool bounded = row_bound(p, V);
+        uint64_t* kmin = bounded ? (uint64_t*)(plan + B) : nullptr;  // [rows_t + rows_d]
         const RowSrc rs{target_logits, rows_t, draft_logits};
         const dim3 grid(cp.G, rows_t + rows_d), blk(kChunkThreads);
         hipLaunchKernelGGL(chunk_max_kernel, grid, blk, 0, ctx->stream, rs, V, cp, part);
-        if (topp)
-            hipLaunchKernelGGL(topp_rows_kernel, dim3(rows_t + rows_d), dim3(kRowThreads), 0, ctx->stream, rs, V, cp,
+        if (bounded)
+            hipLaunchKernelGGL(bound_rows_kernel, dim3(rows_t + rows_d), dim3(kRowThreads), 0, ctx->stream, rs, V, cp,
                                p, (const ChunkPart*)part, kmin);
         if (!p.greedy)
             hipLaunchKernelGGL(chunk_sum_kernel, grid, blk, 0, ctx->stream, rs, V, cp, p, (const uint64_t*)kmin, part);
@@ -2037,7 +2172,7 @@ ulspec_status accept_launch(ulspec_ctx* ctx, const ulspec_sampling* s, uint32_t 
     const TopkWs tw = topk_ws(ws, rows_t + rows_d);
     RowStat* stats = tw.stats;
     launch_topk_stats(ctx->stream, RowSrc{target_logits, rows_t, draft_logits}, rows_t + rows_d, V, p, tw,
-                      ctx->n_cu);
+                      ctx->n_cu, ctx->topk_route);
     hipLaunchKernelGGL(decide_kernel, dim3(B), dim3(kSeqThreads), decide_lds_bytes(k, p.top_k), ctx->stream,
                        (const RowStat*)stats, draft_tokens, uniforms, k, p.top_k, V, out_tokens, out_n_accepted);
     return check_launch(ctx, "accept launch");
@@ -2113,15 +2248,15 @@ ulspec_status sample_mapped_launch(ulspec_ctx* ctx, const ulspec_sampling* s, ui
         st = workspace(ctx, sample_workspace_bytes(R), &ws);
         if (st != ULSPEC_OK) return st;
     }
-    if (p.greedy || p.top_k == 0 || p.top_k >= V) {
+    if (p.greedy || !list_topk(p, V)) {
         const ChunkPlan cp = chunk_plan(V);
         ChunkPart* part = (ChunkPart*)ws;
-        const bool topp = !p.greedy && p.top_p < 1.0f;
-        uint64_t* kmin = topp ? (uint64_t*)(part + (size_t)R * cp.G) : nullptr;  // [R]
+        const bool bounded = row_bound(p, V);
+        uint64_t* kmin = bounded ? (uint64_t*)(part + (size_t)R * cp.G) : nullptr;  // [R]
         const RowSrc rs{logits, R, nullptr};
         hipLaunchKernelGGL(chunk_max_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, part);
-        if (topp)
-            hipLaunchKernelGGL(topp_rows_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, rs, V, cp, p,
+        if (bounded)
+            hipLaunchKernelGGL(bound_rows_kernel, dim3(R), dim3(kRowThreads), 0, ctx->stream, rs, V, cp, p,
                                (const ChunkPart*)part, kmin);
         if (!p.greedy)
             hipLaunchKernelGGL(chunk_sum_kernel, dim3(cp.G, R), dim3(kChunkThreads), 0, ctx->stream, rs, V, cp, p,
@@ -2131,7 +2266,7 @@ ulspec_status sample_mapped_launch(ulspec_ctx* ctx, const ulspec_sampling* s, ui
         return check_launch(ctx, "sample launch");
     }
     const TopkWs tw = topk_ws(ws, R);
-    launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw, ctx->n_cu);
+    launch_topk_stats(ctx->stream, RowSrc{logits, R, nullptr}, R, V, p, tw, ctx->n_cu, ctx->topk_route);
     hipLaunchKernelGGL(sample_kernel, dim3(D), dim3(kSeqThreads), 0, ctx->stream, (const RowStat*)tw.stats, uniforms,
                        V, map, out_tokens);
     return check_launch(ctx, "sample launch");

@@ -155,6 +155,82 @@ bool ulspec_model::complete() const
     return true;
 }
 
+GemmFuse ulspec_model::fuse_base() const
+{
+    GemmFuse f;  // split-K partials when a GEMM takes that path
+    f.part = part;
+    f.part_bytes = part_bytes;
+    return f;
+}
+
+// X of a GEMM after an RMSNorm is split(h * w), written with h by its
+// producer; the GEMM scales its rows by 1 / rms(h) from the partial sums.
+void ulspec_model::normed(GemmFuse& f, const float* pss_rows, int P) const
+{
+    f.rs_pss = pss_rows;
+    f.rs_P = P;
+    f.rs_eps = cfg.rms_eps;
+}
+
+// Linear `which` of layer l over the rows of one forward with its fused
+// prologue and epilogue (P: RMSNorm partials per row of h):
+//   kLinQkv     X = RMSNorm(h) (from xn); RoPE, fp16 Q -> q16, K / V -> cache
+//   kLinO       X = attention output (att); h += Y, next norm's X -> xn
+//   kLinGateUp  X = RMSNorm(h); SiLU(gate) * up -> act
+//   kLinDown    X = act; h += Y, the next layer's (or the final) norm's X -> xn
+ulspec_status ulspec_model::linear(uint32_t l, int which, const Rows& rw, int P)
+{
+    const ulspec_model_cfg& c = cfg;
+    const Layer& L = layers[l];
+    const std::vector<Weight>& W = ctx->weights;
+    GemmFuse f = fuse_base();
+    switch (which) {
+    case kLinQkv:
+        normed(f, pss, P);
+        f.epi = kEpiRope;
+        f.pos_dev = rw.pos_dev;
+        f.pos_add = rw.pos_add;
+        f.nseq = (int)rw.nseq;
+        f.seq_rows = (int)rw.r;
+        f.seq0 = (int)rw.seq0;
+        f.seq_slots = c.max_ctx;
+        f.rope_rows = c.max_ctx;
+        f.tree = rw.tree;
+        f.row_depth = rw.depth_bits;
+        f.rope = rope;
+        f.q16 = q16;
+        f.kc = L.kc;
+        f.vc = L.vc;
+        f.qdim = (int)(c.n_heads * head_dim);
+        f.kvdim = (int)(c.n_kv_heads * head_dim);
+        f.hd = (int)head_dim;
+        return gemm_fused(ctx, W[L.wqkv], f, (const uint16_t*)xn, rw.M, rw.M, nullptr);
+    case kLinO:
+        f.epi = kEpiResid;
+        f.h = h;
+        f.pss_out = pss;
+        f.xn_w = L.ffn_norm;
+        f.xn = xn;
+        f.xn_lo = (int)rw.M;
+        return gemm_fused(ctx, W[L.wo], f, (const uint16_t*)att, rw.M, rw.M, nullptr);
+    case kLinGateUp:
+        normed(f, pss, P);
+        f.epi = kEpiSilu;
+        f.act = act;
+        return gemm_fused(ctx, W[L.wgu], f, (const uint16_t*)xn, rw.M, rw.M, nullptr);
+    case kLinDown:
+        f.epi = kEpiResid;
+        f.h = h;
+        f.pss_out = pss;
+        f.xn_w = l + 1 < c.n_layers ? layers[l + 1].attn_norm : out_norm;
+        f.xn = xn;
+        f.xn_lo = (int)rw.M;
+        return gemm_fused(ctx, W[L.wdown], f, (const uint16_t*)act, rw.M, rw.M, nullptr);
+    default:
+        return fail(ctx, ULSPEC_EINVAL, "linear: %d is not a layer linear", which);
+    }
+}
+
 ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const int32_t* pos_dev, int32_t pos_add,
                                     float* logits_dev, uint32_t n_logits, const int32_t* parent, uint32_t nseq,
                                     uint32_t seq0)
@@ -179,45 +255,13 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         }
     }
     const std::vector<Weight>& W = ctx->weights;
-    // every GEMM: split-K partials when it takes that path
-    auto fuse = [&]() {
-        GemmFuse f;
-        f.part = part;
-        f.part_bytes = part_bytes;
-        return f;
-    };
-    // X of a GEMM after an RMSNorm is split(h * w), written with h by its
-    // producer; the GEMM scales its rows by 1 / rms(h) from the partial sums
-    auto normed = [&](GemmFuse& f, const float* pss_rows, int P) {
-        f.rs_pss = pss_rows;
-        f.rs_P = P;
-        f.rs_eps = c.rms_eps;
-    };
+    const Rows rows{M, r, nseq, seq0, pos_dev, pos_add, parent != nullptr, depth_bits};
     launch_embed(ctx->stream, embed, embed_type, c.dim, tok_dev, M, c.vocab, h, pss, layers[0].attn_norm, xn);
     int P = (int)embed_partials(c.dim);
     ulspec_status s = ULSPEC_OK;
     for (uint32_t l = 0; l < c.n_layers && s == ULSPEC_OK; ++l) {
         const Layer& L = layers[l];
-        GemmFuse q = fuse();
-        normed(q, pss, P);
-        q.epi = kEpiRope;
-        q.pos_dev = pos_dev;
-        q.pos_add = pos_add;
-        q.nseq = (int)nseq;
-        q.seq_rows = (int)r;
-        q.seq0 = (int)seq0;
-        q.seq_slots = c.max_ctx;
-        q.rope_rows = c.max_ctx;
-        q.tree = parent != nullptr;
-        q.row_depth = depth_bits;
-        q.rope = rope;
-        q.q16 = q16;
-        q.kc = L.kc;
-        q.vc = L.vc;
-        q.qdim = (int)(H * D);
-        q.kvdim = (int)(Hkv * D);
-        q.hd = (int)D;
-        s = gemm_fused(ctx, W[L.wqkv], q, (const uint16_t*)xn, M, M, nullptr);
+        s = linear(l, kLinQkv, rows, P);
         if (s != ULSPEC_OK) break;
         AttnCall a;
         a.q = (const uint16_t*)q16;
@@ -239,30 +283,12 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         a.part = attn_part;
         s = attn_launch(ctx, a);
         if (s != ULSPEC_OK) break;
-        GemmFuse o = fuse();
-        o.epi = kEpiResid;
-        o.h = h;
-        o.pss_out = pss;
-        o.xn_w = L.ffn_norm;
-        o.xn = xn;
-        o.xn_lo = (int)M;
-        s = gemm_fused(ctx, W[L.wo], o, (const uint16_t*)att, M, M, nullptr);
+        s = linear(l, kLinO, rows, P);
         if (s != ULSPEC_OK) break;
         P = (int)W[L.wo].n_tiles;
-        GemmFuse u = fuse();
-        normed(u, pss, P);
-        u.epi = kEpiSilu;
-        u.act = act;
-        s = gemm_fused(ctx, W[L.wgu], u, (const uint16_t*)xn, M, M, nullptr);
+        s = linear(l, kLinGateUp, rows, P);
         if (s != ULSPEC_OK) break;
-        GemmFuse d = fuse();
-        d.epi = kEpiResid;
-        d.h = h;
-        d.pss_out = pss;
-        d.xn_w = l + 1 < c.n_layers ? layers[l + 1].attn_norm : out_norm;
-        d.xn = xn;
-        d.xn_lo = (int)M;
-        s = gemm_fused(ctx, W[L.wdown], d, (const uint16_t*)act, M, M, nullptr);
+        s = linear(l, kLinDown, rows, P);
         P = (int)W[L.wdown].n_tiles;
     }
     if (s != ULSPEC_OK) return s;
@@ -270,14 +296,14 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         // the last n_logits rows (every row of every sequence when n_logits = r):
         // their high parts from row M - nseq n_logits, low parts M rows below
         const uint32_t nl = nseq * n_logits;
-        GemmFuse z = fuse();
+        GemmFuse z = fuse_base();
         normed(z, pss + (size_t)(M - nl) * P, P);
         s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)(xn + (size_t)(M - nl) * c.dim), nl, M, logits_dev);
     } else if (n_logits) {
         // the last n_logits rows of each sequence, gathered first
         const uint32_t nl = nseq * n_logits;
         launch_gather_rows(ctx->stream, xn, pss, M, c.dim, (uint32_t)P, r, n_logits, nseq, xg, pg);
-        GemmFuse z = fuse();
+        GemmFuse z = fuse_base();
         normed(z, pg, P);
         s = gemm_fused(ctx, W[w_out], z, (const uint16_t*)xg, nl, nl, logits_dev);
     }
@@ -629,6 +655,38 @@ extern "C" ulspec_status ulspec_model_forward_tree(ulspec_model* m, const int32_
     if (e != hipSuccess) return hip_fail(ctx, e, "model_forward_tree logits");
     e = hipStreamSynchronize(ctx->stream);
     return e == hipSuccess ? ULSPEC_OK : hip_fail(ctx, e, "model_forward_tree sync");
+}
+
+extern "C" ulspec_status ulspec_model_linear(ulspec_model* m, uint32_t layer, uint32_t which, uint32_t M,
+                                             uint32_t pos)
+{
+    if (!m) return ULSPEC_EINVAL;
+    ulspec_ctx* ctx = m->ctx;
+    const ulspec_model_cfg& c = m->cfg;
+    if (which > (uint32_t)ulspec_model::kLinHead || (which != (uint32_t)ulspec_model::kLinHead && layer >= c.n_layers))
+        return fail(ctx, ULSPEC_EINVAL, "model_linear: linear %u of layer %u (0..4, layer < %u)", which, layer,
+                    c.n_layers);
+    if (M == 0 || M > m->rows_max || (uint64_t)pos + M > c.max_ctx)
+        return fail(ctx, ULSPEC_EINVAL, "model_linear: %u rows at %u (1 .. %u rows within max_ctx %u)", M, pos,
+                    m->rows_max, c.max_ctx);
+    if (!m->complete()) return fail(ctx, ULSPEC_EINVAL, "model_linear: model tensors missing");
+    (void)hipSetDevice(ctx->device);
+    const std::vector<Weight>& W = ctx->weights;
+    const ulspec_model::Layer& L = m->layers[which == (uint32_t)ulspec_model::kLinHead ? c.n_layers - 1 : layer];
+    // RMSNorm partials per row of h where each linear reads them: after the
+    // previous layer's down projection (the embedding's for layer 0), or after O
+    const int P_in = layer == 0 ? (int)embed_partials(c.dim) : (int)W[m->layers[layer - 1].wdown].n_tiles;
+    launch_set_i32(ctx->stream, m->pos, (int32_t)pos);
+    const ulspec_model::Rows rows{M, M, 1, 0, m->pos, 0, false, 0};
+    ulspec_status st;
+    if (which == (uint32_t)ulspec_model::kLinHead) {
+        GemmFuse z = m->fuse_base();
+        m->normed(z, m->pss, (int)W[L.wdown].n_tiles);
+        st = gemm_fused(ctx, W[m->w_out], z, (const uint16_t*)m->xn, M, M, m->logits);
+    } else {
+        st = m->linear(layer, (int)which, rows, which == (uint32_t)ulspec_model::kLinGateUp ? (int)W[L.wo].n_tiles : P_in);
+    }
+    return st != ULSPEC_OK ? st : check_launch(ctx, "model_linear launch");
 }
 
 extern "C" ulspec_status ulspec_model_kv_compact(ulspec_model* m, uint32_t pos, const int32_t* path,

@@ -69,7 +69,24 @@ struct ulspec_model {
     _Float16** kv_tab = nullptr;  // device [2][n_layers]: every layer's K cache, then every V cache
     std::vector<void*> allocs;
 
+    // The rows of one forward (see forward): M = nseq groups of r rows,
+    // group b on sequence slot seq0 + b from position pos_dev[b] + pos_add;
+    // a tree's rows take RoPE position pos + depth (4 bits per row).
+    struct Rows {
+        uint32_t M, r, nseq, seq0;
+        const int32_t* pos_dev;
+        int32_t pos_add;
+        bool tree;
+        uint64_t depth_bits;
+    };
+    enum { kLinQkv = 0, kLinO = 1, kLinGateUp = 2, kLinDown = 3, kLinHead = 4 };
+
     bool complete() const;
+    ulspec::GemmFuse fuse_base() const;
+    void normed(ulspec::GemmFuse& f, const float* pss_rows, int P) const;
+    // One linear of layer l with its fused prologue / epilogue, on the
+    // model's activation buffers (P: RMSNorm partials per row of h).
+    ulspec_status linear(uint32_t l, int which, const Rows& rows, int P);
     // Forward M tokens read from device memory: nseq groups of r = M / nseq
     // <= rows_max rows, group b on sequence slot seq0 + b at positions
     // pos_dev[b] + pos_add ... (pos_dev: nseq device ints); logits of the

@@ -373,8 +373,10 @@ ulspec_status ulspec_spec::prefill(const int32_t* prompts, const uint32_t* lens)
     return sync_state();
 }
 
+// tree: the caller sizes and allocates the acceptance and draw workspaces
+// (those of a tree step), so the chain step's are not allocated here.
 static ulspec_status spec_create(ulspec_model* target, ulspec_model* draft, uint32_t k, const ulspec_sampling* s,
-                                 uint64_t seed, uint32_t B, ulspec_spec** out)
+                                 uint64_t seed, uint32_t B, ulspec_spec** out, bool tree = false)
 {
     if (!target || (!draft && k > 0)) return ULSPEC_EINVAL;
     ulspec_ctx* ctx = target->ctx;
@@ -384,10 +386,10 @@ static ulspec_status spec_create(ulspec_model* target, ulspec_model* draft, uint
     if (B == 0 || B > (uint32_t)kMaxSeqs || target->n_seq < B || (draft && draft->n_seq < B))
         return fail(ctx, ULSPEC_EINVAL, "spec_create: %u sequences (1 .. %d, and at most the models' slots)", B,
                     kMaxSeqs);
-    if (k > 16 || k + 1 > target->rows_max || (k + 1) * B > target->rows_cap ||
+    if (k + 1 > target->rows_max || (k + 1) * B > target->rows_cap ||
         (draft && (draft->rows_max < 2 || 2 * B > draft->rows_cap)))
-        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u for %u sequences (k <= 16, (k + 1) B <= %u target rows)", k,
-                    B, target->rows_cap);
+        return fail(ctx, ULSPEC_EINVAL, "spec_create: k=%u for %u sequences (k <= %u, (k + 1) B <= %u target rows)", k,
+                    B, target->rows_max - 1, target->rows_cap);
     if (draft && target->cfg.vocab != draft->cfg.vocab)
         return fail(ctx, ULSPEC_EINVAL, "spec_create: vocabularies differ");
     if (!target->complete() || (draft && !draft->complete()))
@@ -398,7 +400,6 @@ static ulspec_status spec_create(ulspec_model* target, ulspec_model* draft, uint
     if (!s->greedy) {
         if (!(s->temperature > 0.0f) || !(s->temperature < __builtin_inff()))
             return fail(ctx, ULSPEC_EINVAL, "spec_create: temperature must be positive and finite");
-        if (s->top_k > 256 && s->top_k < V) return fail(ctx, ULSPEC_EUNSUPPORTED, "spec_create: top_k > 256");
         if (!(s->top_p == s->top_p)) return fail(ctx, ULSPEC_EINVAL, "spec_create: top_p is NaN");
     }
     (void)hipSetDevice(ctx->device);
@@ -434,8 +435,8 @@ static ulspec_status spec_create(ulspec_model* target, ulspec_model* draft, uint
         {(void**)&sp->dl_s, (size_t)k * B * V * 4},
         {(void**)&sp->dlogits, B > 1 ? (size_t)k * B * V * 4 : 0},
         {(void**)&sp->tlogits, (size_t)(k + 1) * B * V * 4},
-        {(void**)&sp->ws_accept, k ? accept_workspace_bytes(B, k) : 0},
-        {(void**)&sp->ws_sample, sample_workspace_bytes(B)},
+        {(void**)&sp->ws_accept, k && !tree ? accept_workspace_bytes(B, k) : 0},
+        {(void**)&sp->ws_sample, tree ? 0 : sample_workspace_bytes(B)},
     };
     ulspec_status st = ULSPEC_OK;
     for (const Want& w : wants) {
@@ -500,7 +501,7 @@ extern "C" ulspec_status ulspec_spec_create_tree(ulspec_model* target, ulspec_mo
         if (first[p] < 0) first[p] = (int32_t)i;
         ++count[p];
     }
-    ulspec_status st = spec_create(target, draft, n - 1, s, seed, 1, out);
+    ulspec_status st = spec_create(target, draft, n - 1, s, seed, 1, out, true);
     if (st != ULSPEC_OK) return st;
     ulspec_spec* sp = *out;
     sp->tree = true;

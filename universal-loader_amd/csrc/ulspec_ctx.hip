@@ -269,6 +269,17 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
 
 }  // namespace
 
+extern "C" ulspec_status ulspec_set_option(ulspec_ctx* ctx, uint32_t option, int64_t value)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (option == ULSPEC_OPT_TOPK_ROUTE) {
+        if (value < 0 || value > 3) return fail(ctx, ULSPEC_EINVAL, "set_option: top-k route %lld (0 .. 3)", (long long)value);
+        ctx->topk_route = (int)value;
+        return ULSPEC_OK;
+    }
+    return fail(ctx, ULSPEC_EINVAL, "set_option: unknown option %u", option);
+}
+
 extern "C" ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant,
                                             uint32_t* sink)
 {

@@ -41,6 +41,8 @@ struct ulspec_ctx {
     size_t staging_bytes = 0;
     // Device address of the no-allocation scratch on this context's device.
     void* noalloc_scratch = nullptr;
+    // ULSPEC_OPT_TOPK_ROUTE (0: automatic)
+    int topk_route = 0;
     // Captured graphs and timing events.
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;

@@ -89,7 +89,7 @@ class InferenceAPI:
         self._lock = threading.RLock()
         self._config = GenerationConfig()
         self._target = self._draft = None
-        self._batch = {}  # n_seq -> (target, draft) batch models for generate_batch
+        self._batch = None  # (target, draft) with MAX_BATCH sequence slots, for generate_batch
         self._vocab = None
         self._model_path = self._draft_path = ""
         self._model_bytes = 0
@@ -139,23 +139,24 @@ class InferenceAPI:
             return True
 
     def _drop_batch(self):
-        for models in self._batch.values():
-            for m in models:
-                if m is not None:
-                    m.close()
-        self._batch = {}
+        for m in self._batch or ():
+            if m is not None:
+                m.close()
+        self._batch = None
 
-    def _batch_models(self, n_seq, spec):
-        """Target (and draft) models with n_seq sequence slots, loaded from the
-        same files on first use (a second copy of the weights) and kept."""
-        have = self._batch.get(n_seq)
-        if have is None or (spec and have[1] is None):
-            if have is not None:
-                have[0].close()
-            t = load_gguf_model(self._ctx, self._model_path, self._max_ctx, n_seq=n_seq)
-            d = load_gguf_model(self._ctx, self._draft_path, self._max_ctx, n_seq=n_seq) if spec else None
-            self._batch[n_seq] = have = (t, d)
-        return have
+    def _batch_models(self, spec):
+        """One target (and draft) model pair with MAX_BATCH sequence slots,
+        loaded from the same files on first use (a second copy of the weights)
+        and kept; every group of 2 .. MAX_BATCH prompts runs on it (a loop of
+        B sequences uses slots 0 .. B - 1).  The draft is added when a later
+        call first needs it."""
+        if self._batch is None:
+            t = load_gguf_model(self._ctx, self._model_path, self._max_ctx, n_seq=self.MAX_BATCH)
+            self._batch = (t, None)
+        if spec and self._batch[1] is None:
+            d = load_gguf_model(self._ctx, self._draft_path, self._max_ctx, n_seq=self.MAX_BATCH)
+            self._batch = (self._batch[0], d)
+        return self._batch
 
     @staticmethod
     def _read_vocab(g):
@@ -346,7 +347,7 @@ class InferenceAPI:
                     n_tok += results[-1].num_tokens
                     t_all += results[-1].time_ms * 1e-3
                     continue
-                tgt, dft = self._batch_models(len(group), spec)
+                tgt, dft = self._batch_models(spec)
                 loop = Speculative(tgt, dft if spec else None, k, s, self._seed, n_seq=len(group))
                 try:
                     t0 = time.perf_counter()
