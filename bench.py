@@ -472,7 +472,7 @@ def workload_read(pkg, ctx, args):
     for nbytes in (25362432, 28311552, 50724864):
         bufs = [ctx.alloc(nbytes) for _ in range(24)]  # contents do not matter (the XOR only feeds the sink test)
         best = None
-        for variant in range(3):
+        for variant in range(4):
             it = iter(range(1 << 30))
             us = _time_direct(ctx, lambda: ctx.stream_read(bufs[next(it) % 24], nbytes, variant, sink),
                               24 * args.reps)
@@ -496,6 +496,45 @@ def workload_read(pkg, ctx, args):
                      "traffic": None, "avg_us": us, "algorithmic_bytes": 25362432},
         "cpu_baseline": None,
     }
+
+
+def workload_launch(pkg, ctx, args):
+    """The per-launch floor of a graph-replayed step: 100 back-to-back launches
+    of a tiny kernel (the uniforms kernel: one 256-thread workgroup, and 1024
+    of them) captured into one HIP graph and replayed, HIP events around the
+    replays; against the grid-wide barrier a persistent kernel would use in
+    place of a kernel boundary (ulspec_sync_probe: one workgroup per CU, all
+    co-resident, 2000 rounds), with agent-scope release / acquire (mode 0) and
+    with write-through data and flags (mode 1)."""
+    rows = []
+    buf = ctx.alloc(256 * 1024 * 4)
+    for n in (64, 256 * 1024):
+        ctx.capture_begin()
+        for _ in range(100):
+            ctx.uniforms(1, 0, n, buf)
+        gid = ctx.capture_end()
+        ctx.graph_replay(gid, 2)
+        ctx.sync()
+        ctx.timer_mark(0)
+        ctx.graph_replay(gid, 20)
+        ctx.timer_mark(1)
+        ctx.sync()
+        us = ctx.timer_elapsed_ms(0, 1) * 1e3 / 2000
+        ctx.graph_destroy(gid)
+        rows.append({"what": f"graph-replayed launch, {(n + 255) // 256} workgroups of 256", "us": us})
+        log(f"graph-replayed launch of {(n + 255) // 256} workgroups: {us:.3f} us")
+    buf.free()
+    n_cu = ctx.n_cu
+    for mode in (0, 1):
+        for wg, thr in ((n_cu, 1024), (n_cu, 256), (n_cu // 2, 1024)):
+            us, err = ctx.sync_probe(mode, wg, thr, 2000)
+            rows.append({"what": f"grid barrier mode {mode}, {wg} x {thr}", "us": us, "stale_reads": err})
+            log(f"grid barrier mode {mode}: {wg} workgroups x {thr}: {us:.2f} us per round, {err} stale reads")
+    floor = rows[0]["us"]
+    return {"metric": "graph-replayed launch floor (us)", "value": floor, "unit": "us", "higher_is_better": False,
+            "ms_per_step": floor / 1e3, "dtype": "n/a",
+            "config": {"workload": "launch floor against grid-wide barriers", "table": rows},
+            "roofline": None, "cpu_baseline": None}
 
 
 def workload_copy(pkg, ctx, args):
@@ -527,11 +566,13 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=12, help="GPU steps recorded for the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read", "q6k"),
+    ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read", "q6k",
+                                           "launch"),
                     default="step",
                     help="step: the speculative step (default); roofline: only the step's verify-GEMM roofline "
                          "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration; "
-                         "read: the streaming-read ceiling; q6k: the native Q6_K GEMM against fp16 at 32000x4096")
+                         "read: the streaming-read ceiling; q6k: the native Q6_K GEMM against fp16 at 32000x4096; "
+                         "launch: the graph-replayed launch floor against grid-wide barriers")
     ap.add_argument("--reps", type=int, default=50, help="launches per timing (kernel workloads)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch each step's kernels directly instead of replaying the captured graph")
@@ -569,7 +610,8 @@ def main():
         return 0
     if args.workload != "step":
         fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
-              "copy": workload_copy, "read": workload_read, "q6k": workload_q6k}[args.workload]
+              "copy": workload_copy, "read": workload_read, "q6k": workload_q6k,
+              "launch": workload_launch}[args.workload]
         out = fn(pkg, ctx, args)
         base = {"n_gpus": 1, "steps": args.reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic, seeded"}

@@ -89,12 +89,14 @@ ulspec_status ulspec_timer_mark(ulspec_ctx* ctx, uint32_t slot /* < 16 */);
 ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t slot_b, float* ms);
 /* Measurement kernel with no counterpart in the reference: reads every 16-byte
  * unit of the device buffer `buf` (bytes a multiple of 16) once, 256 threads
- * per workgroup and 4 << variant (variant 0..2) loads per thread, all issued
+ * per workgroup and 4 << variant (variant 0..3) loads per thread, all issued
  * before the first use.  *sink (device) is written only when the XOR of all
  * words is 0x5eed5eed, so the loads cannot be elided.  Its duration for a
  * given size is the streaming-read ceiling the verify kernels are compared
  * with. */
 ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant, uint32_t* sink);
+/* The context's HIP device and its compute-unit count. */
+ulspec_status ulspec_device_info(ulspec_ctx* ctx, int* device, int* n_cu);
 /* Kernel-route override, no counterpart in the reference (for tests that must
  * reach each route whatever the device's CU count).  ULSPEC_OPT_TOPK_ROUTE:
  * how the top-k (kept list, top_k <= 256) statistics run -- 0 chosen from the
@@ -104,6 +106,17 @@ ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes,
  * logits, or k past its kept maxima) falls back to the chunk pipeline.  Every
  * route gives the same tokens. */
 enum { ULSPEC_OPT_TOPK_ROUTE = 1 };
+/* Measurement kernel with no counterpart in the reference: the cost of one
+ * grid-wide barrier between co-resident workgroups (a persistent kernel's
+ * alternative to a kernel boundary).  `workgroups` x `threads` (256, 512 or
+ * 1024) run `rounds` rounds of: write 256 floats, barrier (a flag per
+ * workgroup, all polled), read another workgroup's floats.  mode 0: agent-scope
+ * release / acquire around the flags (L2 write-back and invalidate); mode 1:
+ * data and flags through agent-scope relaxed accesses, no write-back.  Gives
+ * the microseconds per round and the number of stale reads.  Allocates, and
+ * synchronises the context stream; EDEVICE if a wait passed its bound. */
+ulspec_status ulspec_sync_probe(ulspec_ctx* ctx, uint32_t mode, uint32_t workgroups, uint32_t threads,
+                                uint32_t rounds, float* us_per_round, uint32_t* errors);
 ulspec_status ulspec_set_option(ulspec_ctx* ctx, uint32_t option, int64_t value);
 
 /* ---- K1: verify dequant-GEMM ------------------------------------------------

@@ -98,6 +98,8 @@ ABI = [
     ("ulspec_timer_elapsed_ms", C.c_int, [P, U32, U32, C.POINTER(C.c_float)]),
     ("ulspec_stream_read", C.c_int, [P, P, C.c_size_t, U32, P]),
     ("ulspec_set_option", C.c_int, [P, U32, C.c_int64]),
+    ("ulspec_device_info", C.c_int, [P, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    ("ulspec_sync_probe", C.c_int, [P, U32, U32, U32, U32, C.POINTER(C.c_float), C.POINTER(U32)]),
     ("ulspec_weight_upload", C.c_int, [P, U32, P, C.c_size_t, U32, U32, C.POINTER(U32)]),
     ("ulspec_weight_info", C.c_int, [P, U32, C.POINTER(U32), C.POINTER(U32), C.POINTER(U32),
                                      C.POINTER(C.c_size_t)]),
@@ -262,6 +264,19 @@ class Context:
         return ms.value
 
     OPT_TOPK_ROUTE = 1
+
+    @property
+    def n_cu(self):
+        dev, n = C.c_int(), C.c_int()
+        self._check(lib().ulspec_device_info(self.handle, C.byref(dev), C.byref(n)))
+        return n.value
+
+    def sync_probe(self, mode, workgroups, threads, rounds):
+        """(us per grid-barrier round, stale reads) of ulspec_sync_probe."""
+        us, err = C.c_float(), U32()
+        self._check(lib().ulspec_sync_probe(self.handle, mode, workgroups, threads, rounds, C.byref(us),
+                                            C.byref(err)))
+        return us.value, err.value
 
     def set_option(self, option, value):
         self._check(lib().ulspec_set_option(self.handle, option, value))

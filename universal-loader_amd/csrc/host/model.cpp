@@ -380,6 +380,7 @@ extern "C" ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec
         {(void**)&m->part, m->part_bytes},
         {(void**)&m->tok, (size_t)R * 4},
         {(void**)&m->pos, 4 * kMaxSeqs},
+        {(void**)&m->lin_pos, 4},
         {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},
         {(void**)&m->rope, (size_t)c.max_ctx * (D / 2) * sizeof(float2)},
         {(void**)&m->kv_tab, (size_t)2 * c.n_layers * sizeof(_Float16*)},
@@ -676,8 +677,11 @@ extern "C" ulspec_status ulspec_model_linear(ulspec_model* m, uint32_t layer, ui
     // RMSNorm partials per row of h where each linear reads them: after the
     // previous layer's down projection (the embedding's for layer 0), or after O
     const int P_in = layer == 0 ? (int)embed_partials(c.dim) : (int)W[m->layers[layer - 1].wdown].n_tiles;
-    launch_set_i32(ctx->stream, m->pos, (int32_t)pos);
-    const ulspec_model::Rows rows{M, M, 1, 0, m->pos, 0, false, 0};
+    if (m->lin_pos_set != (int64_t)pos) {  // written once per position: consecutive calls launch only the GEMM
+        launch_set_i32(ctx->stream, m->lin_pos, (int32_t)pos);
+        m->lin_pos_set = pos;
+    }
+    const ulspec_model::Rows rows{M, M, 1, 0, m->lin_pos, 0, false, 0};
     ulspec_status st;
     if (which == (uint32_t)ulspec_model::kLinHead) {
         GemmFuse z = m->fuse_base();

@@ -63,6 +63,8 @@ struct ulspec_model {
     size_t part_bytes = 0;
     int32_t* tok = nullptr;    // [kRows]
     int32_t* pos = nullptr;    // [1]
+    int32_t* lin_pos = nullptr;  // [1] the position of ulspec_model_linear calls
+    int64_t lin_pos_set = -1;    // the value last written there (-1: none)
     float* attn_part = nullptr;
     _Float16* xg = nullptr;    // split [2 rows_cap][dim]: the LM head's rows gathered from xn
     float* pg = nullptr;       // [rows_cap][pss_stride]: their row-scale partials

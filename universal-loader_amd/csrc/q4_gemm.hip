@@ -994,36 +994,74 @@ __device__ __forceinline__ size_t kv_row(const GemmFuse& f, EpiPos ps, int m)
 // where a thread has no output), none otherwise:
 //   resid: (h[m][n], xn_w[n])   rope: (cos, sin) of the pair at the row's
 //                               RoPE position (rope_pos)
-__device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, EpiPos pos0)
+// Split in two: epi_addr (the buffer descriptors and the offsets, most of the
+// address arithmetic) and epi_issue (the loads), so that a wave without an
+// output slot skips the arithmetic while every wave still issues the same
+// number of loads (the vmcnt waits count them).
+struct EpiAddr {
+    __amdgpu_buffer_rsrc_t r0, r1;
+    uint32_t o0, o1;
+};
+
+// Descriptors of the epilogue's operands, offsets out of range (no output).
+__device__ __forceinline__ EpiAddr epi_none(const GemmArgs& a)
+{
+    const GemmFuse& f = a.f;
+    EpiAddr e;
+    if (f.epi == kEpiResid) {
+        e.r0 = make_rsrc(f.h, (uint32_t)a.M * (uint32_t)a.N * 4u);
+        e.r1 = make_rsrc(f.xn_w, f.xn ? (uint32_t)a.N * 4u : 0u);
+    } else if (f.epi == kEpiRope) {
+        e.r0 = make_rsrc(f.rope, (uint32_t)min((uint64_t)f.rope_rows * (uint64_t)(f.hd / 2) * 8u, (uint64_t)0xffffffffu));
+        e.r1 = e.r0;
+    } else {
+        e.r0 = e.r1 = make_rsrc(a.out, 0u);
+    }
+    e.o0 = e.o1 = kOOB;
+    return e;
+}
+
+// The offsets of output (m, n)'s operands into e (out of range where the
+// thread has no output).
+__device__ __forceinline__ void epi_offsets(const GemmArgs& a, int m, int n, EpiPos pos0, EpiAddr& e)
 {
     const GemmFuse& f = a.f;
     const bool ok = m < a.M && n < a.N;
-    __amdgpu_buffer_rsrc_t r0, r1;
-    uint32_t o0 = kOOB, o1 = kOOB;
+    if (!ok) return;
     if (f.epi == kEpiResid) {
-        r0 = make_rsrc(f.h, (uint32_t)a.M * (uint32_t)a.N * 4u);
-        r1 = make_rsrc(f.xn_w, f.xn ? (uint32_t)a.N * 4u : 0u);
-        if (ok) {
-            o0 = (uint32_t)(m * a.N + n) * 4u;
-            o1 = (uint32_t)n * 4u;
-        }
-    } else if (f.epi == kEpiRope) {
-        r0 = make_rsrc(f.rope, (uint32_t)min((uint64_t)f.rope_rows * (uint64_t)(f.hd / 2) * 8u, (uint64_t)0xffffffffu));
-        r1 = r0;
-        if (ok && n < f.qdim + f.kvdim) {
-            const int nn = n < f.qdim ? n : n - f.qdim;
-            o0 = (uint32_t)(rope_pos(f, pos0, m) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
-            o1 = o0 + 4u;
-        }
-    } else {
-        r0 = r1 = make_rsrc(a.out, 0u);
+        e.o0 = (uint32_t)(m * a.N + n) * 4u;
+        e.o1 = (uint32_t)n * 4u;
+    } else if (f.epi == kEpiRope && n < f.qdim + f.kvdim) {
+        const int nn = n < f.qdim ? n : n - f.qdim;
+        e.o0 = (uint32_t)(rope_pos(f, pos0, m) * (f.hd / 2) + (nn % f.hd) / 2) * 8u;
+        e.o1 = e.o0 + 4u;
     }
+}
+
+__device__ __forceinline__ float2 epi_issue(const GemmArgs& a, const EpiAddr& e)
+{
     float2 v = {0.f, 0.f};
-    if (f.epi == kEpiResid || f.epi == kEpiRope) {
-        v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r0, o0, 0, 0));
-        v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r1, o1, 0, 0));
+    if (a.f.epi == kEpiResid || a.f.epi == kEpiRope) {
+        v.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(e.r0, e.o0, 0, 0));
+        v.y = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(e.r1, e.o1, 0, 0));
     }
     return v;
+}
+
+__device__ __forceinline__ float2 epi_load(const GemmArgs& a, int m, int n, EpiPos pos0)
+{
+    EpiAddr e = epi_none(a);
+    epi_offsets(a, m, n, pos0, e);
+    return epi_issue(a, e);
+}
+
+// epi_load for the threads of tile slot j (wave-uniform): slots past the
+// iteration's tiles skip the address arithmetic and issue out-of-range loads.
+__device__ __forceinline__ float2 epi_load_slot(const GemmArgs& a, int j, int tpi, int m, int n, EpiPos pos0)
+{
+    EpiAddr e = epi_none(a);
+    if (__builtin_amdgcn_readfirstlane(j) < tpi) epi_offsets(a, m, n, pos0, e);
+    return epi_issue(a, e);
 }
 
 // Vector loads epi_load issues (wave-uniform).
@@ -1387,43 +1425,83 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a, const floa
 // The whole X sits in LDS for the workgroup's lifetime.  Per iteration the NW
 // waves cover tpi = NW / P tiles x P parts of K (P a power of two, at most NW
 // and at most the chunks per row); wave p owns chunks [ca, cb) of its tiles
-// and the X of those chunks, which only it reads.  LDS layout, chunk-major:
-// unit c * CS + rho * RS + j holds X[x_row(rho)][8 (UPC c + j) .. + 7], RS =
-// UPC + 1 units per staged row and chunk (the pad unit spreads the rows over
-// the banks), CS = xrows * RS per chunk.  Each wave copies the X of its own
-// chunks (one contiguous LDS run) with direct buffer->LDS loads before its
-// weight loads and waits for those copies only (loads complete in issue
-// order): no barrier before the first multiply.  Parts are summed in part
-// order in LDS, then the row scale and the epilogue run.
+// and the X of those chunks, which only it reads.  Each wave copies the X of
+// its own chunks with direct buffer->LDS loads (the LDS side of one is 64
+// consecutive units) before its weight loads and waits for those copies only
+// (loads complete in issue order): no barrier before the first multiply.
+// Parts are summed in part order in LDS, then the row scale and the epilogue
+// run.  Two LDS layouts (XLayout), chosen per kernel by the length of a part:
+//   chunk-major (parts of one chunk or short rows): unit c * CS + rho * RS + j
+//     holds X[x_row(rho)][8 (UPC c + j) .. + 7], RS = UPC + 1 units per staged
+//     row and chunk (the pad unit spreads the rows over the banks), CS =
+//     xrows * RS per chunk -- a wave's X is one contiguous run, copied in full
+//     64-unit loads whose sources each lane finds by dividing by CS and RS;
+//   row-major (parts of at least 64 units per row): unit rho * RSTR + u holds
+//     X[x_row(rho)][8 u .. 8 u + 7], RSTR = n_chunks UPC + 1 (odd: the 16 rows
+//     of an A operand start in distinct bank groups) -- a wave's X is one run
+//     per staged row on both sides, no division.
+// Units past K read as 0.  The chunk-major size bounds both (the launch's LDS).
 constexpr int kWideWaves = 16;
 
 template <int TYPE>
 constexpr int kRowStride = kUnitsPerChunk<TYPE> + 1;
 
-// This wave's X: chunks [ca, cb), all staged rows, into their LDS blocks --
-// one contiguous run of (cb - ca) * CS units, ceil((cb - ca) * CS / 64)
-// loads of 64 units (the pad units and units past K read as 0).
-template <int TYPE>
+struct XLayout {
+    int row;    // units from one staged row to the next
+    int chunk;  // units from one chunk of a row to the next
+};
+
+template <int TYPE, bool RM>
+__device__ __forceinline__ XLayout x_layout(const GemmArgs& a)
+{
+    constexpr int UPC = kUnitsPerChunk<TYPE>;
+    if constexpr (RM) return XLayout{a.n_chunks * UPC + 1, UPC};
+    else return XLayout{kRowStride<TYPE>, a.xrows * kRowStride<TYPE>};
+}
+
+// Row-major for parts of CMAX chunks that fill a 64-unit load per row.
+template <int TYPE, int CMAX>
+constexpr bool kXRowMajor = CMAX * kUnitsPerChunk<TYPE> >= 64;
+
+// This wave's X: chunks [ca, cb) of every staged row into their LDS places.
+template <int TYPE, bool RM>
 __device__ __forceinline__ void x_copy_region(const GemmArgs& a, __amdgpu_buffer_rsrc_t xr, uint8_t* xs_bytes, int ca,
-                                              int cb, int CS)
+                                              int cb, XLayout L)
 {
     constexpr int UPC = kUnitsPerChunk<TYPE>, RS = kRowStride<TYPE>;
     const int lane = threadIdx.x & 63;
     const int KU = a.K / 8;
-    const int u0 = ca * CS, u1 = cb * CS;
-    const float inv_cs = 1.0f / (float)CS;
-    for (int q = u0; q < u1; q += 64) {
-        const int u = q + lane;
-        int c = (int)((float)u * inv_cs);  // u / CS, corrected below (u < 2^22)
-        if (c * CS > u) --c;
-        if ((c + 1) * CS <= u) ++c;
-        const int rem = u - c * CS;
-        const int rho = rem / RS, j = rem - rho * RS;
-        const int ku = c * UPC + j;
-        const uint32_t off = j < UPC && ku < KU && rho < a.xrows ? (uint32_t)(x_row(a, rho) * KU + ku) * 16u : kOOB;
-        if (u < u1)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                xr, (__attribute__((address_space(3))) void*)(xs_bytes + (size_t)q * 16), 16, off, 0, 0, 0);
+    if constexpr (RM) {  // one run of (cb - ca) UPC units per staged row
+        const int k0 = ca * UPC, k1 = cb * UPC;
+        for (int rho = 0; rho < a.xrows; ++rho) {
+            const uint32_t grow = (uint32_t)x_row(a, rho) * (uint32_t)KU;
+            for (int q = k0; q < k1; q += 64) {
+                const int ku = q + lane;
+                const uint32_t off = ku < KU ? (grow + (uint32_t)ku) * 16u : kOOB;
+                if (ku < k1)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        xr, (__attribute__((address_space(3))) void*)(xs_bytes + (size_t)(rho * L.row + q) * 16), 16,
+                        off, 0, 0, 0);
+            }
+        }
+    } else {  // one contiguous run of (cb - ca) CS units (the pad units load nothing)
+        const int CS = L.chunk;
+        const int u0 = ca * CS, u1 = cb * CS;
+        const float inv_cs = 1.0f / (float)CS;
+        for (int q = u0; q < u1; q += 64) {
+            const int u = q + lane;
+            int c = (int)((float)u * inv_cs);  // u / CS, corrected below (u < 2^22)
+            if (c * CS > u) --c;
+            if ((c + 1) * CS <= u) ++c;
+            const int rem = u - c * CS;
+            const int rho = rem / RS, j = rem - rho * RS;
+            const int ku = c * UPC + j;
+            const uint32_t off =
+                j < UPC && ku < KU && rho < a.xrows ? (uint32_t)(x_row(a, rho) * KU + ku) * 16u : kOOB;
+            if (u < u1)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xr, (__attribute__((address_space(3))) void*)(xs_bytes + (size_t)q * 16), 16, off, 0, 0, 0);
+        }
     }
 }
 
@@ -1482,7 +1560,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     extern __shared__ uint4 xs[];
     __shared__ float red[NW * 4 * 64];
     __shared__ float rs[16];
-    constexpr int RS = kRowStride<TYPE>, NWL = WBatch<TYPE, CMAX>::kLoadsPerChunk;
+    constexpr int NWL = WBatch<TYPE, CMAX>::kLoadsPerChunk;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -1491,10 +1569,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int ca = p * a.ks_q + min(p, a.ks_r);
     const int cb = ca + a.ks_q + (p < a.ks_r ? 1 : 0);
     const int nc0 = max(0, min(CMAX, cb - ca));
-    const int CS = a.xrows * RS;
+    constexpr bool RM = kXRowMajor<TYPE, CMAX>;
+    const XLayout L = x_layout<TYPE, RM>(a);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
-    const int xrow[1] = {xslot_row(a, 0, r) * RS + (kSuperBlock<TYPE> ? 8 * g : g)};
+    const int xrow[1] = {xslot_row(a, 0, r) * L.row + (kSuperBlock<TYPE> ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     const EpiPos pos0 = epi_pos0(a);
     const int it = blockIdx.x, t = it * tpi + tw;
@@ -1503,24 +1582,24 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     // first batch of weights, the epilogue operands
     float4 ps[2];
     if (a.f.rs_pss) rs_issue<NW>(a, ps);
-    x_copy_region<TYPE>(a, xr, (uint8_t*)xs, ca, cb, CS);
+    x_copy_region<TYPE, RM>(a, xr, (uint8_t*)xs, ca, cb, L);
     pin_loads();
     WBatch<TYPE, CMAX> A;
     stream_load<TYPE, CMAX>(a, wr, t, ca, nc0, A);
     // the epilogue operands of this thread's output (tile slot j = tid / 256)
     const int j_epi = threadIdx.x >> 8;
-    const float2 pre = epi_load(a, j_epi < tpi ? epi_row(a, lane, (threadIdx.x >> 6) & 3) : a.M,
-                                16 * (it * tpi + j_epi) + (lane & 15), pos0);
+    const float2 pre = epi_load_slot(a, j_epi, tpi, epi_row(a, lane, (threadIdx.x >> 6) & 3),
+                                     16 * (it * tpi + j_epi) + (lane & 15), pos0);
     pin_loads();
     if (a.f.rs_pss) rs_finish<NW>(a, ps, rs);
     vm_wait_dyn(CMAX * NWL + epi_nloads(a));  // this wave's X copies, issued before its weights
     float4_t acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-    stream_mma<TYPE, CMAX, 1>(xs, xrow, CS, ca, t < a.n_tiles ? nc0 : 0, 0, CMAX, A, nk, acc);
+    stream_mma<TYPE, CMAX, 1>(xs, xrow, L.chunk, ca, t < a.n_tiles ? nc0 : 0, 0, CMAX, A, nk, acc);
     for (int c0 = ca + CMAX; c0 < cb; c0 += CMAX) {  // the rest of a long part (not prefetched)
         const int nc = min(CMAX, cb - c0);
         stream_load<TYPE, CMAX>(a, wr, t, c0, nc, A);
         pin_loads();
-        stream_mma<TYPE, CMAX, 1>(xs, xrow, CS, c0, t < a.n_tiles ? nc : 0, 0, CMAX, A, nk, acc);
+        stream_mma<TYPE, CMAX, 1>(xs, xrow, L.chunk, c0, t < a.n_tiles ? nc : 0, 0, CMAX, A, nk, acc);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[0][i];
@@ -1573,8 +1652,7 @@ __device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc
 __device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, EpiPos pos0)
 {
     const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = threadIdx.x >> 8;
-    const int m = j < tpi ? epi_row(a, l, row) : a.M;
-    return epi_load(a, m, 16 * (it * tpi + j) + (l & 15), pos0);
+    return epi_load_slot(a, j, tpi, epi_row(a, l, row), 16 * (it * tpi + j) + (l & 15), pos0);
 }
 
 template <int TYPE, int C, int D, int NW>
@@ -1583,7 +1661,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     extern __shared__ uint4 xs[];
     __shared__ float red[2][NW * 4 * 64];
     __shared__ float rs[16];
-    constexpr int RS = kRowStride<TYPE>, NWL = WBatch<TYPE, C>::kLoadsPerChunk;
+    constexpr int NWL = WBatch<TYPE, C>::kLoadsPerChunk;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
@@ -1593,10 +1671,11 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int nc = a.ks_q + (p < a.ks_r ? 1 : 0);  // <= C (checked by the host)
     const int n_iter = (a.n_tiles + tpi - 1) / tpi;
     const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int CS = a.xrows * RS;
+    constexpr bool RM = kXRowMajor<TYPE, C>;
+    const XLayout L = x_layout<TYPE, RM>(a);
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, x_bytes(a));
-    const int xrow[1] = {xslot_row(a, 0, r) * RS + (kSuperBlock<TYPE> ? 8 * g : g)};
+    const int xrow[1] = {xslot_row(a, 0, r) * L.row + (kSuperBlock<TYPE> ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
     auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
@@ -1607,7 +1686,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     // (each followed by its epilogue operands)
     float4 ps[2];
     if (a.f.rs_pss) rs_issue<NW>(a, ps);
-    x_copy_region<TYPE>(a, xr, (uint8_t*)xs, ca, ca + nc, CS);
+    x_copy_region<TYPE, RM>(a, xr, (uint8_t*)xs, ca, ca + nc, L);
     pin_loads();
     WBatch<TYPE, C> ring[D];
     float2 pre[D];
@@ -1626,7 +1705,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
             if (li >= n_loc) break;
             const int t = tile_of(li);
             float4_t acc[1] = {{0.f, 0.f, 0.f, 0.f}};
-            stream_mma<TYPE, C, 1>(xs, xrow, CS, ca, t < a.n_tiles ? nc : 0, 0, C, ring[k], nk, acc);
+            stream_mma<TYPE, C, 1>(xs, xrow, L.chunk, ca, t < a.n_tiles ? nc : 0, 0, C, ring[k], nk, acc);
             const float2 pk = pre[k];
             stream_load<TYPE, C>(a, wr, tile_of(li + D), ca, nc, ring[k]);
             pre[k] = ring_epi_load(a, git(li + D), tpi, pos0);
@@ -1708,7 +1787,8 @@ constexpr size_t kStaticWide = (size_t)kWideWaves * 4 * 64 * sizeof(float) + 16 
 constexpr size_t kStaticSmall = (size_t)8 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
 constexpr size_t kStaticRing = (size_t)2 * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
 
-// LDS bytes of the whole X of `rows` staged rows in the chunk-major layout.
+// LDS bytes of the whole X of `rows` staged rows (the chunk-major layout, which
+// bounds the row-major one).
 size_t x_lds_bytes(const Weight& w, int rows)
 {
     const size_t rs = (w.type == ULSPEC_GGML_Q4_K || w.type == ULSPEC_GGML_Q6_K ? 32 : 16) + 1;

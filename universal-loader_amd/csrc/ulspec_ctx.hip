@@ -1,6 +1,7 @@
 // ulspec_ctx.hip -- context, memory and error entry points of the C ABI.
 #include "ulspec_internal.h"
 
+#include <algorithm>
 #include <cstring>
 
 using namespace ulspec;
@@ -267,7 +268,137 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
     if (acc == 0x5eed5eedu) *sink = acc;
 }
 
+// Grid-wide barrier probe: `rounds` rounds of (each workgroup writes 256
+// floats, barrier, reads another workgroup's) on co-resident workgroups.  The
+// barrier: thread 0 of each workgroup stores the round number into its own
+// flag; wave 0 polls all flags (64 lanes, agent-scope loads) until every one
+// has reached it.  mode 0: plain data stores and loads, the flag stored with
+// agent-scope release and the poll followed by an agent-scope acquire (the
+// L2 write-back and invalidate of the memory model); mode 1: data through
+// agent-scope relaxed stores and loads, the flag stored after s_waitcnt (no
+// L2 write-back or invalidate).  Every wait is bounded: past `spin_limit`
+// polls a workgroup raises ctl[0] and every workgroup skips all later rounds,
+// so every wave exits.
+template <int MODE>
+__device__ __forceinline__ bool probe_barrier(uint32_t* flags, uint32_t* ctl, uint32_t G, uint32_t round,
+                                              uint32_t spin_limit)
+{
+    __shared__ int ok_s;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int ok = 1;
+        if (lane == 0) {
+            if (MODE == 0) {
+                __hip_atomic_store(flags + blockIdx.x, round, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                __builtin_amdgcn_s_waitcnt(0);
+                __hip_atomic_store(flags + blockIdx.x, round, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        for (uint32_t n = 0;; ++n) {
+            bool mine = true;
+            for (uint32_t g = lane; g < G; g += 64)
+                mine &= __hip_atomic_load(flags + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= round;
+            if (__ballot(!mine) == 0) break;
+            if (__hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) || n > spin_limit) {
+                if (lane == 0) __hip_atomic_store(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (MODE == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        if (lane == 0) ok_s = ok;
+    }
+    __syncthreads();
+    return ok_s != 0;
+}
+
+template <int MODE>
+__global__ void sync_probe_kernel(uint32_t* flags, uint32_t* ctl, float* data, uint32_t rounds, uint32_t spin_limit)
+{
+    const uint32_t G = gridDim.x;
+    uint32_t bad = 0;
+    for (uint32_t it = 0; it < rounds; ++it) {
+        // rounds alternate two halves of data: a workgroup writing round it's
+        // half has passed barrier it - 1, so nobody still reads it
+        float* half = data + (size_t)(it & 1) * G * 256;
+        for (uint32_t i = threadIdx.x; i < 256; i += blockDim.x) {
+            const float v = (float)(it * 7 + blockIdx.x + i);
+            if (MODE == 0) half[(size_t)blockIdx.x * 256 + i] = v;
+            else __hip_atomic_store(half + (size_t)blockIdx.x * 256 + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (MODE == 1) __builtin_amdgcn_s_waitcnt(0);
+        if (!probe_barrier<MODE>(flags, ctl, G, it + 1, spin_limit)) break;
+        if (threadIdx.x < 256) {
+            const uint32_t o = (blockIdx.x + 1 + it) % G, i = threadIdx.x;
+            const float* src = half + (size_t)o * 256 + i;
+            const float v = MODE == 0 ? *src : __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (v != (float)(it * 7 + o + i)) ++bad;
+        }
+    }
+    if (bad) atomicAdd(ctl + 1, bad);
+}
+
 }  // namespace
+
+extern "C" ulspec_status ulspec_sync_probe(ulspec_ctx* ctx, uint32_t mode, uint32_t workgroups, uint32_t threads,
+                                           uint32_t rounds, float* us_per_round, uint32_t* errors)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (mode > 1 || workgroups == 0 || (threads != 256 && threads != 512 && threads != 1024) || rounds == 0 ||
+        rounds > 100000 || !us_per_round || !errors)
+        return fail(ctx, ULSPEC_EINVAL, "sync_probe: mode 0..1, threads 256/512/1024, 1..100000 rounds, outputs");
+    (void)hipSetDevice(ctx->device);
+    const void* fn = mode == 0 ? (const void*)sync_probe_kernel<0> : (const void*)sync_probe_kernel<1>;
+    int per_cu = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, (int)threads, 0);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sync_probe occupancy");
+    if ((uint64_t)per_cu * (uint64_t)std::max(1, ctx->n_cu) < workgroups)
+        return fail(ctx, ULSPEC_EINVAL, "sync_probe: %u workgroups of %u threads are not co-resident", workgroups,
+                    threads);
+    uint32_t *flags = nullptr, *ctl = nullptr;
+    float* data = nullptr;
+    e = hipMalloc(&flags, (size_t)workgroups * 4);
+    if (e == hipSuccess) e = hipMalloc(&ctl, 256);
+    if (e == hipSuccess) e = hipMalloc(&data, (size_t)2 * workgroups * 256 * 4);
+    if (e == hipSuccess) e = hipMemsetAsync(flags, 0, (size_t)workgroups * 4, ctx->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(ctl, 0, 256, ctx->stream);
+    const uint32_t spin_limit = 400000;  // polls of ~1 us: far past any barrier, under a second
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventRecord(e0, ctx->stream);
+    if (e == hipSuccess) {
+        void* args[] = {&flags, &ctl, &data, &rounds, (void*)&spin_limit};
+        e = hipLaunchCooperativeKernel(fn, dim3(workgroups), dim3(threads), args, 0, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    float ms = 0.f;
+    uint32_t hc[2] = {0, 0};
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+    if (e == hipSuccess) e = hipMemcpy(hc, ctl, 8, hipMemcpyDeviceToHost);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipFree(flags);
+    (void)hipFree(ctl);
+    (void)hipFree(data);
+    if (e != hipSuccess) return hip_fail(ctx, e, "sync_probe");
+    if (hc[0]) return fail(ctx, ULSPEC_EDEVICE, "sync_probe: a barrier wait passed its spin limit");
+    *us_per_round = ms * 1e3f / (float)rounds;
+    *errors = hc[1];
+    return ULSPEC_OK;
+}
+
+extern "C" ulspec_status ulspec_device_info(ulspec_ctx* ctx, int* device, int* n_cu)
+{
+    ULSPEC_CHECK_CTX(ctx);
+    if (device) *device = ctx->device;
+    if (n_cu) *n_cu = ctx->n_cu;
+    return ULSPEC_OK;
+}
 
 extern "C" ulspec_status ulspec_set_option(ulspec_ctx* ctx, uint32_t option, int64_t value)
 {
@@ -284,8 +415,8 @@ extern "C" ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, si
                                             uint32_t* sink)
 {
     ULSPEC_CHECK_CTX(ctx);
-    if (!buf || !sink || bytes == 0 || bytes % 16 || variant > 2)
-        return fail(ctx, ULSPEC_EINVAL, "stream_read: buffer, sink, bytes %% 16 == 0 and variant 0..2 required");
+    if (!buf || !sink || bytes == 0 || bytes % 16 || variant > 3)
+        return fail(ctx, ULSPEC_EINVAL, "stream_read: buffer, sink, bytes %% 16 == 0 and variant 0..3 required");
     (void)hipSetDevice(ctx->device);
     const size_t n16 = bytes / 16;
     const int U = 4 << variant;
@@ -294,7 +425,8 @@ extern "C" ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, si
     const uint4* p = (const uint4*)buf;
     if (U == 4) hipLaunchKernelGGL(stream_read_kernel<4>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
     else if (U == 8) hipLaunchKernelGGL(stream_read_kernel<8>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
-    else hipLaunchKernelGGL(stream_read_kernel<16>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    else if (U == 16) hipLaunchKernelGGL(stream_read_kernel<16>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    else hipLaunchKernelGGL(stream_read_kernel<32>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
     return check_launch(ctx, "stream_read launch");
 }
 
