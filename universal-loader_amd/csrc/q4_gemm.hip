@@ -1617,59 +1617,50 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 
 // ---- ring kernel (more tiles than CUs) ----------------------------------------
 // One 16-wave workgroup per CU walks its iterations (tpi = 16 / P tiles x P
-// parts each, as above) with a ring of D register batches: the first D
-// iterations' weights are issued (after the wave's X copies) before the first
-// multiply, and each iteration refills the batch it has
-// just multiplied with the weights of the iteration D ahead, so D iterations
-// of weight loads stay in flight behind the arithmetic.  Part sums go through
-// two alternating LDS buffers, so one barrier per iteration suffices.
+// parts each, as above) in groups of G: a ring of G register batches holds
+// the weights of one group, the first group's issued (after the wave's X
+// copies) before the first multiply, and each multiply refills its batch with
+// the weights of the same slot of the next group, so a group of weight loads
+// stays in flight behind the arithmetic.  Each iteration of a group writes its
+// part sums to its own LDS buffer; after the group's G multiplies one barrier,
+// and 256-thread slots sum and run the epilogue of all G tpi tiles together
+// (a wave reaches its next multiply without waiting on each tile's
+// reduction; a second barrier keeps the next group's part sums off the
+// buffers until they have been read).
 constexpr int kRingWaves = 16;
-constexpr int kRingDepth = 2;
 
-// Sum the P part sums of the tpi (<= NW / 4) tiles of global iteration `it`,
-// scale and run their epilogue (threads 256 j .. 256 j + 255 take tile slot
-// j); pre is this thread's epi_load of the same output.
-template <int NW>
-__device__ __forceinline__ void tile_sums(const GemmArgs& a, const float4_t& acc, float* red, const float* rs, int it,
-                                          int P, int tpi, float2 pre, EpiPos pos0)
+// The epilogue slots of a group: thread t takes slot t / 256 + 4 q of pass q;
+// slot j is tile j % TPI of the group's iteration j / TPI.
+template <int G, int TPI>
+constexpr int kRingPasses = (G * TPI + 3) / 4;
+
+// epi_load of this thread's output in pass q of the group starting at local
+// iteration base (nothing when its slot is past the group's tiles).
+template <int G, int TPI>
+__device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int base, int n_loc, int q, EpiPos pos0)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[(wave * 4 + i) * 64 + lane] = acc[i];
-    lds_barrier();
-    const int row = (threadIdx.x >> 6) & 3, l = lane, j = threadIdx.x >> 8;
-    if (j < tpi) {
-        float s = red_sum(a, red, j, P, row, l);
-        const int tt = it * tpi + j;
-        const int m = epi_row(a, l, row);
-        if (a.f.rs_pss && m < a.M) s *= rs[m];
-        epilogue(a, s, m, 16 * tt + (l & 15), tt, l, pre, pos0);
-    }
+    const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = (threadIdx.x >> 8) + 4 * q;
+    const int g = j / TPI, jj = j - g * TPI, li = base + g;
+    const int live = __builtin_amdgcn_readfirstlane(j < G * TPI && li < n_loc ? 1 : 0);
+    const int it = (int)blockIdx.x + li * (int)gridDim.x;
+    return epi_load_slot(a, live ? jj : TPI, TPI, epi_row(a, l, row), 16 * (it * TPI + jj) + (l & 15), pos0);
 }
 
-// epi_load of this thread's output in global iteration `it` (nothing when its
-// tile slot is unused).
-__device__ __forceinline__ float2 ring_epi_load(const GemmArgs& a, int it, int tpi, EpiPos pos0)
-{
-    const int l = threadIdx.x & 63, row = (threadIdx.x >> 6) & 3, j = threadIdx.x >> 8;
-    return epi_load_slot(a, j, tpi, epi_row(a, l, row), 16 * (it * tpi + j) + (l & 15), pos0);
-}
-
-template <int TYPE, int C, int D, int NW>
-__global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
+template <int TYPE, int C, int G, int TPI>
+__global__ __launch_bounds__(kRingWaves * 64) void gemm_ring_kernel(GemmArgs a)
 {
     extern __shared__ uint4 xs[];
-    __shared__ float red[2][NW * 4 * 64];
+    constexpr int NW = kRingWaves, P = NW / TPI, NP = kRingPasses<G, TPI>;
+    __shared__ float red[G][NW * 4 * 64];
     __shared__ float rs[16];
     constexpr int NWL = WBatch<TYPE, C>::kLoadsPerChunk;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int P = a.ks_count, tpi = NW / P;
-    const int tw = wave / P, p = wave - (wave / P) * P;
+    const int tw = wave / P, p = wave % P;
     const int ca = p * a.ks_q + min(p, a.ks_r);
     const int nc = a.ks_q + (p < a.ks_r ? 1 : 0);  // <= C (checked by the host)
-    const int n_iter = (a.n_tiles + tpi - 1) / tpi;
+    const int n_iter = (a.n_tiles + TPI - 1) / TPI;
     const int n_loc = (n_iter - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     constexpr bool RM = kXRowMajor<TYPE, C>;
     const XLayout L = x_layout<TYPE, RM>(a);
@@ -1678,39 +1669,58 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring_kernel(GemmArgs a)
     const int xrow[1] = {xslot_row(a, 0, r) * L.row + (kSuperBlock<TYPE> ? 8 * g : g)};
     const NibbleConsts nk = nibble_consts();
     // tile of local iteration li for this wave (>= n_tiles: nothing to load or multiply)
-    auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * tpi + tw : a.n_tiles; };
+    auto tile_of = [&](int li) { return li < n_loc ? ((int)blockIdx.x + li * (int)gridDim.x) * TPI + tw : a.n_tiles; };
     const EpiPos pos0 = epi_pos0(a);
-    auto git = [&](int li) { return (int)blockIdx.x + li * (int)gridDim.x; };  // global iteration
 
-    // issue order: row-scale partials, this wave's X, D batches of weights
-    // (each followed by its epilogue operands)
+    // issue order: row-scale partials, this wave's X, the first group's
+    // weights, then its epilogue operands
     float4 ps[2];
     if (a.f.rs_pss) rs_issue<NW>(a, ps);
     x_copy_region<TYPE, RM>(a, xr, (uint8_t*)xs, ca, ca + nc, L);
     pin_loads();
-    WBatch<TYPE, C> ring[D];
-    float2 pre[D];
+    WBatch<TYPE, C> ring[G];
 #pragma unroll
-    for (int k = 0; k < D; ++k) {
-        stream_load<TYPE, C>(a, wr, tile_of(k), ca, nc, ring[k]);
-        pre[k] = ring_epi_load(a, git(k), tpi, pos0);
-    }
+    for (int k = 0; k < G; ++k) stream_load<TYPE, C>(a, wr, tile_of(k), ca, nc, ring[k]);
+    float2 pre[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) pre[q] = ring_epi_load<G, TPI>(a, 0, n_loc, q, pos0);
     pin_loads();
     if (a.f.rs_pss) rs_finish<NW>(a, ps, rs);
-    vm_wait_dyn(D * (C * NWL + epi_nloads(a)));  // this wave's X copies
-    for (int base = 0; base < n_loc; base += D) {
+    vm_wait_dyn(G * C * NWL + NP * epi_nloads(a));  // this wave's X copies
+    const int row = (threadIdx.x >> 6) & 3;
+    for (int base = 0; base < n_loc; base += G) {
 #pragma unroll
-        for (int k = 0; k < D; ++k) {
-            const int li = base + k;
-            if (li >= n_loc) break;
-            const int t = tile_of(li);
+        for (int k = 0; k < G; ++k) {
+            const int t = tile_of(base + k);
             float4_t acc[1] = {{0.f, 0.f, 0.f, 0.f}};
             stream_mma<TYPE, C, 1>(xs, xrow, L.chunk, ca, t < a.n_tiles ? nc : 0, 0, C, ring[k], nk, acc);
-            const float2 pk = pre[k];
-            stream_load<TYPE, C>(a, wr, tile_of(li + D), ca, nc, ring[k]);
-            pre[k] = ring_epi_load(a, git(li + D), tpi, pos0);
+            stream_load<TYPE, C>(a, wr, tile_of(base + G + k), ca, nc, ring[k]);
             pin_loads();
-            tile_sums<NW>(a, acc[0], red[li & 1], rs, git(li), P, tpi, pk, pos0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[k][(wave * 4 + i) * 64 + lane] = acc[0][i];
+        }
+        lds_barrier();
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+            const int j = (threadIdx.x >> 8) + 4 * q;
+            if (j < G * TPI) {
+                const int gk = j / TPI, jj = j - gk * TPI, li = base + gk;
+                if (li < n_loc) {
+                    float s = red_sum(a, red[gk], jj, P, row, lane);
+                    const int tt = ((int)blockIdx.x + li * (int)gridDim.x) * TPI + jj;
+                    const int m = epi_row(a, lane, row);
+                    if (a.f.rs_pss && m < a.M) s *= rs[m];
+                    epilogue(a, s, m, 16 * tt + (lane & 15), tt, lane, pre[q], pos0);
+                }
+            }
+        }
+        if (base + G < n_loc) {
+            // the next group's epilogue operands (behind its weights), then
+            // the barrier before its part sums reuse red
+#pragma unroll
+            for (int q = 0; q < NP; ++q) pre[q] = ring_epi_load<G, TPI>(a, base + G, n_loc, q, pos0);
+            pin_loads();
+            lds_barrier();
         }
     }
 }
@@ -1785,7 +1795,10 @@ namespace ulspec {
 constexpr size_t kWideLdsMax = 160 * 1024;
 constexpr size_t kStaticWide = (size_t)kWideWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
 constexpr size_t kStaticSmall = (size_t)8 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
-constexpr size_t kStaticRing = (size_t)2 * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+constexpr size_t ring_static(int G)
+{
+    return (size_t)G * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+}
 
 // LDS bytes of the whole X of `rows` staged rows (the chunk-major layout, which
 // bounds the row-major one).
@@ -1870,6 +1883,24 @@ void wide_launch(CList<C...>, int cpp, dim3 grid, dim3 block, size_t lds, hipStr
     (one(std::integral_constant<int, C>{}), ...);
 }
 
+template <int TYPE, int C, int G>
+void ring_kernels(std::vector<const void*>& out)
+{
+    out.push_back((const void*)gemm_ring_kernel<TYPE, C, G, 1>);
+    out.push_back((const void*)gemm_ring_kernel<TYPE, C, G, 2>);
+    out.push_back((const void*)gemm_ring_kernel<TYPE, C, G, 4>);
+}
+
+// The ring kernel for C chunks per part, groups of G, TPI = 16 / P tiles per
+// iteration.
+template <int TYPE, int C, int G>
+void ring_launch(int tpi, dim3 grid, dim3 block, size_t lds, hipStream_t st, const GemmArgs& a)
+{
+    if (tpi == 1) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, C, G, 1>), grid, block, lds, st, a);
+    else if (tpi == 2) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, C, G, 2>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, C, G, 4>), grid, block, lds, st, a);
+}
+
 template <int TYPE, int... MT>
 void slice_kernels(std::integer_sequence<int, MT...>, std::vector<const void*>& out)
 {
@@ -1879,27 +1910,29 @@ void slice_kernels(std::integer_sequence<int, MT...>, std::vector<const void*>& 
 
 template <int TYPE>
 void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& small, std::vector<const void*>& rings,
-                  std::vector<const void*>& slices)
+                  std::vector<const void*>& rings3, std::vector<const void*>& slices)
 {
     slice_kernels<TYPE>(std::integer_sequence<int, 1, 2, 3, 4, 6>{}, slices);
     wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, wide);
     small.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves>);
-    rings.push_back((const void*)gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves>);
+    ring_kernels<TYPE, 1, 2>(rings);
+    ring_kernels<TYPE, 2, 2>(rings);
+    rings3.push_back((const void*)gemm_ring_kernel<TYPE, 1, 3, 1>);
 }
 
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
-    std::vector<const void*> wide, small, rings, slices;
-    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings, slices);
-    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings, slices);
-    type_kernels<ULSPEC_GGML_F16>(wide, small, rings, slices);
-    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings, slices);
-    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings, slices);
+    std::vector<const void*> wide, small, rings, rings3, slices;
+    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings, rings3, slices);
+    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings, rings3, slices);
+    type_kernels<ULSPEC_GGML_F16>(wide, small, rings, rings3, slices);
+    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings, rings3, slices);
+    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings, rings3, slices);
     const struct {
         const std::vector<const void*>* fns;
         size_t fixed;
-    } groups[] = {{&wide, kStaticWide}, {&small, kStaticSmall}, {&rings, kStaticRing}, {&slices, 0}};
+    } groups[] = {{&wide, kStaticWide},    {&small, kStaticSmall}, {&rings, ring_static(2)},
+                  {&rings3, ring_static(3)}, {&slices, 0}};
     // The launch checks add each group's static LDS to the dynamic size; the
     // opt-in must not let static + dynamic exceed the CU's 160 KB, so both
     // come from the compiled kernel's own static size.
@@ -1949,12 +1982,17 @@ bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
         int P = kRingWaves;
         while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
         const int cpp = (int)((w.n_chunks + P - 1) / P);
-        if (P < 4 || cpp > 2 || lds + kStaticRing > kWideLdsMax) return false;
+        if (P < 4 || cpp > 2 || lds + ring_static(2) > kWideLdsMax) return false;
         split(P);
         const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
         const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
-        if (cpp <= 1) hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, kRingDepth, kRingWaves>), grid, block, lds, st, a);
-        else hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 2, kRingDepth, kRingWaves>), grid, block, lds, st, a);
+        // groups of 3 iterations for one-chunk parts of one tile per
+        // iteration where their part sums fit beside X (the other shapes run
+        // out of registers at 3), else groups of 2
+        if (cpp <= 1 && tpi == 1 && lds + ring_static(3) <= kWideLdsMax)
+            hipLaunchKernelGGL((gemm_ring_kernel<TYPE, 1, 3, 1>), grid, block, lds, st, a);
+        else if (cpp <= 1) ring_launch<TYPE, 1, 2>(tpi, grid, block, lds, st, a);
+        else ring_launch<TYPE, 2, 2>(tpi, grid, block, lds, st, a);
         return true;
     }
     if (lds + kStaticWide > kWideLdsMax) return false;
