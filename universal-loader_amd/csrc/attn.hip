@@ -384,6 +384,9 @@ ulspec_status attn_launch(ulspec_ctx* ctx, const AttnCall& c)
         return fail(ctx, ULSPEC_EUNSUPPORTED, "verify_attention: %d splits (at most %d)", a.splits, kAttnMaxSplits);
     void* ws = c.part;
     const size_t wsb = attn_workspace_bytes(a.splits, a.H, a.nq, (int)c.D, a.nseq);
+    if (wsb && ws && wsb > c.part_bytes)
+        return fail(ctx, ULSPEC_EINVAL, "verify_attention: %d splits need %zu B of partials, the workspace holds %zu B",
+                    a.splits, wsb, c.part_bytes);
     if (wsb && !ws) {
         ulspec_status st = workspace(ctx, wsb, &ws);
         if (st != ULSPEC_OK) return st;

@@ -281,6 +281,7 @@ ulspec_status ulspec_model::forward(const int32_t* tok_dev, uint32_t M, const in
         a.dyn_prefix = pos_dev;
         a.prefix_add = pos_add;
         a.part = attn_part;
+        a.part_bytes = attn_part_bytes;
         s = attn_launch(ctx, a);
         if (s != ULSPEC_OK) break;
         s = linear(l, kLinO, rows, P);
@@ -366,6 +367,7 @@ extern "C" ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec
     int splits = 0, kps = 0;
     attn_plan((int)c.max_ctx, (int)H, ctx->n_cu, splits, kps);
     if (splits < 2) splits = 2;
+    m->attn_part_bytes = attn_workspace_bytes(splits, (int)H, (int)R, (int)D);
     struct Want {
         void** p;
         size_t bytes;
@@ -381,7 +383,7 @@ extern "C" ulspec_status ulspec_model_create_batch(ulspec_ctx* ctx, const ulspec
         {(void**)&m->tok, (size_t)R * 4},
         {(void**)&m->pos, 4 * kMaxSeqs},
         {(void**)&m->lin_pos, 4},
-        {(void**)&m->attn_part, attn_workspace_bytes(splits, (int)H, (int)R, (int)D)},
+        {(void**)&m->attn_part, m->attn_part_bytes},
         {(void**)&m->rope, (size_t)c.max_ctx * (D / 2) * sizeof(float2)},
         {(void**)&m->kv_tab, (size_t)2 * c.n_layers * sizeof(_Float16*)},
         {(void**)&m->xg, (size_t)2 * R * c.dim * 2},

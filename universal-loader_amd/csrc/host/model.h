@@ -66,6 +66,7 @@ struct ulspec_model {
     int32_t* lin_pos = nullptr;  // [1] the position of ulspec_model_linear calls
     int64_t lin_pos_set = -1;    // the value last written there (-1: none)
     float* attn_part = nullptr;
+    size_t attn_part_bytes = 0;
     _Float16* xg = nullptr;    // split [2 rows_cap][dim]: the LM head's rows gathered from xn
     float* pg = nullptr;       // [rows_cap][pss_stride]: their row-scale partials
     _Float16** kv_tab = nullptr;  // device [2][n_layers]: every layer's K cache, then every V cache

@@ -155,6 +155,7 @@ struct AttnCall {
     const int32_t* dyn_prefix = nullptr;  // device int per sequence: prefix = dyn_prefix[b] + prefix_add
     int prefix_add = 0;
     void* part = nullptr;    // split partials; NULL = the context workspace
+    size_t part_bytes = 0;   // bytes at part (the launch fails if its plan needs more)
     // nseq sequences: q and out hold nseq groups of nq rows, sequence b's
     // cache starts kv_seq elements after sequence b-1's (needs dyn_prefix)
     uint32_t nseq = 1;
