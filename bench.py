@@ -462,11 +462,21 @@ def workload_q6k(pkg, ctx, args):
     }
 
 
+# Weight bytes of the 7B-shape step's linears (Q4_K: 144 B per 256 weights)
+STEP_WEIGHTS = (("draft O", 2359296), ("draft down", 6488064), ("draft QKV", 7077888), ("target O", 9437184),
+                ("draft gate/up", 12976128), ("target down", 25362432), ("target QKV", 28311552),
+                ("target gate/up", 50724864))
+
+
 def workload_read(pkg, ctx, args):
     """Streaming-read ceiling: the plain 16-byte-load read kernel over the
     byte counts of the verify GEMMs (the Q4_0 4096x11008 weight, the 7B Q4_K
     QKV and gate/up weights), 24 rotated copies of each (> 512 MB, past the
-    MALL), every load variant; the fastest variant per size is the ceiling."""
+    MALL), every load variant, direct launches; the fastest variant per size
+    is the ceiling.  Then the same reads at the weight sizes of every linear
+    of the 7B-shape step, 48 launches over 24 copies captured in a HIP graph
+    and replayed (the setting the step runs in): the per-launch floor of a
+    GEMM that reads those bytes."""
     sink = ctx.alloc(16)
     rows, head = [], None
     for nbytes in (25362432, 28311552, 50724864):
@@ -485,13 +495,37 @@ def workload_read(pkg, ctx, args):
             head = best
         for b in bufs:
             b.free()
+    graph_rows = []
+    for name, nbytes in STEP_WEIGHTS:
+        bufs = [ctx.alloc(nbytes) for _ in range(24)]
+        per = []
+        for variant in range(4):
+            ctx.capture_begin()
+            for i in range(48):
+                ctx.stream_read(bufs[i % 24], nbytes, variant, sink)
+            gid = ctx.capture_end()
+            ctx.graph_replay(gid, 2)
+            ctx.sync()
+            ctx.timer_mark(0)
+            ctx.graph_replay(gid, args.reps)
+            ctx.timer_mark(1)
+            ctx.sync()
+            per.append(ctx.timer_elapsed_ms(0, 1) * 1e3 / (48 * args.reps))
+            ctx.graph_destroy(gid)
+        us = min(per)
+        log(f"graph-replayed read, {name} weight ({nbytes / 1e6:.2f} MB): " +
+            " / ".join(f"{u:.2f}" for u in per) + f" us (4 / 8 / 16 / 32 loads per thread), best "
+            f"{nbytes / us / 1e3:.0f} GB/s")
+        graph_rows.append({"linear": name, "bytes": nbytes, "us_by_loads_per_thread": per, "best_us": us})
+        for b in bufs:
+            b.free()
     sink.free()
     us, gbs, variant = head
     return {
         "metric": "streaming-read ceiling GB/s (25.4 MB, the Q4_0 4096x11008 weight)", "value": gbs, "unit": "GB/s",
         "ms_per_step": us / 1e3, "dtype": "u8",
         "config": {"workload": "plain 16-byte-load read of 25 / 28 / 51 MB buffers, 24 rotated copies", "table": rows,
-                   "best_loads_per_thread": 4 << variant},
+                   "best_loads_per_thread": 4 << variant, "graph_replayed_step_weights": graph_rows},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "avg_us": us, "algorithmic_bytes": 25362432},
         "cpu_baseline": None,
