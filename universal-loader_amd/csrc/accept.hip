@@ -2001,7 +2001,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
         uint32_t t = bk < prev ? bk : 0u;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) t = max(t, (uint32_t)__shfl_xor((int)t, o));
-        if (lane == j) tops[wave * kTopM + j] = t;
+        if (lane == j) tops[wave * m + j] = t;  // packed: the n = NWV m kept keys in a row
         prev = t;
     }
     if (tid == 0) cand_count = 0;
@@ -2009,27 +2009,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
     const int n = NWV * m;
     uint32_t thr = 0;
     if (tid < n) {
-        const uint32_t tv = tops[(tid / m) * kTopM + tid % m];
+        const uint32_t tv = tops[tid];
         if (tv) {
             uint32_t ge = 0;
-            for (int j = 0; j < n; ++j) ge += tops[(j / m) * kTopM + j % m] >= tv;
+            for (int j = 0; j < n; ++j) ge += tops[j] >= tv;
             if (ge >= k) thr = tv;
         }
     }
     thr = (uint32_t)block_max_u64<NT>(thr, red);  // 0 (no bound): every token, then the fallback
+    if (bk >= thr) {  // a thread whose largest key is below the bound holds no candidate
 #pragma unroll
-    for (int i = 0; i < F4; ++i) {
-        const uint32_t q = tid + i * NT;
-        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        for (int i = 0; i < F4; ++i) {
+            const uint32_t q = tid + i * NT;
+            const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (q < V4 && 4 * q + c < V) {
-                const uint32_t key = float_key(e[c]);
-                if (key >= thr) {
-                    const uint32_t slot = atomicAdd(&cand_count, 1u);
-                    if (slot < (uint32_t)kCandMax) cand[slot] = order_key(key, 4 * q + c);
+            for (int c = 0; c < 4; ++c)
+                if (q < V4 && 4 * q + c < V) {
+                    const uint32_t key = float_key(e[c]);
+                    if (key >= thr) {
+                        const uint32_t slot = atomicAdd(&cand_count, 1u);
+                        if (slot < (uint32_t)kCandMax) cand[slot] = order_key(key, 4 * q + c);
+                    }
                 }
-            }
+        }
     }
     __syncthreads();
     const uint32_t nc = cand_count;
