@@ -1952,7 +1952,8 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
 }
 
 // Launch a whole-X kernel if one fits; false when the split-K path must run.
-// At most 8 chunks per row and 1-4 tiles per CU: the 8-wave one-tile kernel.
+// At most 8 chunks per row and 1-4 tiles per CU: the 8-wave one-tile kernel
+// (below 8 staged rows, or while the ring would leave CUs idle).
 // More tiles than CUs and at most two chunks per part: the ring kernel, one
 // 16-wave workgroup per CU, P parts per tile (the largest power of two <=
 // min(16, chunks per row), P >= 4), 16 / P tiles per iteration.  At most one
@@ -1971,18 +1972,25 @@ bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
         a.ks_q = (int)(w.n_chunks / P);
         a.ks_r = (int)(w.n_chunks % P);
     };
-    if (pipe && w.n_chunks <= (uint32_t)kSmallWaves && (int)w.n_tiles <= kSmallTilesPerCu * n_cu &&
-        lds + kStaticSmall <= kWideLdsMax) {
+    // the ring: P parts per tile, 16 / P tiles per iteration
+    int P = kRingWaves;
+    while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
+    const int cpp = (int)((w.n_chunks + P - 1) / P);
+    const int ring_iters = ((int)w.n_tiles + kRingWaves / P - 1) / (kRingWaves / P);
+    const bool ring_ok = pipe && P >= 4 && cpp <= 2 && lds + ring_static(2) <= kWideLdsMax;
+    const bool small_ok = pipe && w.n_chunks <= (uint32_t)kSmallWaves &&
+                          (int)w.n_tiles <= kSmallTilesPerCu * n_cu && lds + kStaticSmall <= kWideLdsMax;
+    // the one-tile kernel stages the whole X per tile: from 8 staged rows on,
+    // the ring (X once per CU) where its iterations cover every CU
+    const bool small_x = a.xrows < 8 || ring_iters < n_cu;
+    if (small_ok && (small_x || !ring_ok)) {
         split(kSmallWaves);  // one chunk (or none) per wave
         hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves>), dim3(w.n_tiles), dim3(kSmallWaves * 64), lds,
                            st, a);
         return true;
     }
     if (pipe) {
-        int P = kRingWaves;
-        while (P > 1 && (uint32_t)P > w.n_chunks) P >>= 1;
-        const int cpp = (int)((w.n_chunks + P - 1) / P);
-        if (P < 4 || cpp > 2 || lds + ring_static(2) > kWideLdsMax) return false;
+        if (!ring_ok) return false;
         split(P);
         const int tpi = kRingWaves / P, n_iter = ((int)w.n_tiles + tpi - 1) / tpi;
         const dim3 grid(std::min(n_iter, n_cu)), block(kRingWaves * 64);
@@ -1997,8 +2005,8 @@ bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
     }
     if (lds + kStaticWide > kWideLdsMax) return false;
     split(kWideWaves);
-    const int cpp = a.ks_q + (a.ks_r ? 1 : 0);
-    wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, cpp, dim3(w.n_tiles), dim3(kWideWaves * 64), lds, st, a);
+    wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, a.ks_q + (a.ks_r ? 1 : 0), dim3(w.n_tiles),
+                      dim3(kWideWaves * 64), lds, st, a);
     return true;
 }
 
