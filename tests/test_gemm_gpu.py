@@ -48,6 +48,9 @@ CASES = [
     (2, 32000, 512, (5,)),            # LM-head shape of the small model
     (12, 11264, 2048, (1, 2, 6)),     # 704 tiles of <= 8 chunks: one-tile kernel, 2.75 tiles per CU
     (2, 16384, 1024, (1, 5)),         # 1024 tiles of 8 chunks: one-tile kernel, 4 tiles per CU
+    (12, 11264, 2048, (8,)),          # 8 staged rows: the ring instead, 2 tiles per iteration
+    (2, 8192, 1536, (1, 5)),          # 12 chunks: ring parts of 2 chunks, 2 tiles per iteration
+    (12, 16384, 1536, (8,)),          # 6 chunks at 8 rows: ring parts of 2 chunks, 4 tiles per iteration
 ]
 
 
