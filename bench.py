@@ -473,22 +473,27 @@ def workload_read(pkg, ctx, args):
     byte counts of the verify GEMMs (the Q4_0 4096x11008 weight, the 7B Q4_K
     QKV and gate/up weights), 24 rotated copies of each (> 512 MB, past the
     MALL), every load variant, direct launches; the fastest variant per size
-    is the ceiling.  Then the same reads at the weight sizes of every linear
-    of the 7B-shape step, 48 launches over 24 copies captured in a HIP graph
-    and replayed (the setting the step runs in): the per-launch floor of a
-    GEMM that reads those bytes."""
+    is the ceiling.  Variants 4..7 repeat 0..3 with non-temporal loads (the
+    cache policy the verify GEMMs read their weights with).  Then the same
+    reads at the weight sizes of every linear of the 7B-shape step, 48
+    launches over 24 copies captured in a HIP graph and replayed (the setting
+    the step runs in): the per-launch floor of a GEMM that reads those
+    bytes."""
     sink = ctx.alloc(16)
     rows, head = [], None
     for nbytes in (25362432, 28311552, 50724864):
         bufs = [ctx.alloc(nbytes) for _ in range(24)]  # contents do not matter (the XOR only feeds the sink test)
         best = None
-        for variant in range(4):
+        for variant in range(8):
             it = iter(range(1 << 30))
             us = _time_direct(ctx, lambda: ctx.stream_read(bufs[next(it) % 24], nbytes, variant, sink),
                               24 * args.reps)
             gbs = nbytes / us / 1e3
-            log(f"read {nbytes / 1e6:.1f} MB, {4 << variant} loads per thread: {us:.2f} us, {gbs:.0f} GB/s")
-            rows.append({"bytes": nbytes, "loads_per_thread": 4 << variant, "us": us, "GB/s": gbs})
+            nt = variant >= 4
+            log(f"read {nbytes / 1e6:.1f} MB, {4 << (variant & 3)} loads per thread{' non-temporal' if nt else ''}: "
+                f"{us:.2f} us, {gbs:.0f} GB/s")
+            rows.append({"bytes": nbytes, "loads_per_thread": 4 << (variant & 3), "non_temporal": nt, "us": us,
+                         "GB/s": gbs})
             if best is None or us < best[0]:
                 best = (us, gbs, variant)
         if nbytes == 25362432:
@@ -499,7 +504,7 @@ def workload_read(pkg, ctx, args):
     for name, nbytes in STEP_WEIGHTS:
         bufs = [ctx.alloc(nbytes) for _ in range(24)]
         per = []
-        for variant in range(4):
+        for variant in range(8):
             ctx.capture_begin()
             for i in range(48):
                 ctx.stream_read(bufs[i % 24], nbytes, variant, sink)
@@ -514,9 +519,10 @@ def workload_read(pkg, ctx, args):
             ctx.graph_destroy(gid)
         us = min(per)
         log(f"graph-replayed read, {name} weight ({nbytes / 1e6:.2f} MB): " +
-            " / ".join(f"{u:.2f}" for u in per) + f" us (4 / 8 / 16 / 32 loads per thread), best "
+            " / ".join(f"{u:.2f}" for u in per) + f" us (4 / 8 / 16 / 32 loads per thread, plain then "
+            f"non-temporal), best "
             f"{nbytes / us / 1e3:.0f} GB/s")
-        graph_rows.append({"linear": name, "bytes": nbytes, "us_by_loads_per_thread": per, "best_us": us})
+        graph_rows.append({"linear": name, "bytes": nbytes, "us_by_variant": per, "best_us": us})
         for b in bufs:
             b.free()
     sink.free()
@@ -525,7 +531,8 @@ def workload_read(pkg, ctx, args):
         "metric": "streaming-read ceiling GB/s (25.4 MB, the Q4_0 4096x11008 weight)", "value": gbs, "unit": "GB/s",
         "ms_per_step": us / 1e3, "dtype": "u8",
         "config": {"workload": "plain 16-byte-load read of 25 / 28 / 51 MB buffers, 24 rotated copies", "table": rows,
-                   "best_loads_per_thread": 4 << variant, "graph_replayed_step_weights": graph_rows},
+                   "best_loads_per_thread": 4 << (variant & 3), "best_non_temporal": variant >= 4,
+                   "graph_replayed_step_weights": graph_rows},
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
                      "traffic": None, "avg_us": us, "algorithmic_bytes": 25362432},
         "cpu_baseline": None,
@@ -588,6 +595,58 @@ def workload_copy(pkg, ctx, args):
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None}, "cpu_baseline": None}
 
 
+def workload_cache(pkg, ctx, args):
+    """Last-level cache residency under non-temporal reads (why the verify
+    GEMMs load weights non-temporally): a 160 MB buffer D is read with plain
+    loads until cache-resident, then 2 GB of other data T is read with plain
+    or non-temporal loads, then D again.  D's re-read time against its
+    resident and cold times shows whether T's reads allocated in the cache;
+    T's time gives each policy's streaming rate.  Medians over --reps."""
+    sink = ctx.alloc(16)
+    DB, TB = 160 << 20, 2048 << 20
+    d, t = ctx.alloc(DB), ctx.alloc(TB)
+
+    def timed(buf, nbytes, variant):
+        ctx.timer_mark(0)
+        ctx.stream_read(buf, nbytes, variant, sink)
+        ctx.timer_mark(1)
+        ctx.sync()
+        return ctx.timer_elapsed_ms(0, 1) * 1e3
+
+    reps = max(3, min(args.reps, 20))
+    for _ in range(2):
+        timed(t, TB, 0)
+        timed(d, DB, 0)
+    rows = []
+    for variant, label in ((0, "plain"), (4, "non-temporal")):
+        hot, tt, after = [], [], []
+        for _ in range(reps):
+            timed(t, TB, 0)
+            timed(d, DB, 0)
+            hot.append(timed(d, DB, 0))
+            tt.append(timed(t, TB, variant))
+            after.append(timed(d, DB, 0))
+        row = {"T_policy": label, "T_us": float(np.median(tt)), "T_GB/s": TB / float(np.median(tt)) / 1e3,
+               "D_resident_us": float(np.median(hot)), "D_after_T_us": float(np.median(after))}
+        log(f"T (2048 MB) read {label}: {row['T_us']:.1f} us ({row['T_GB/s']:.0f} GB/s); D (160 MB) resident "
+            f"{row['D_resident_us']:.1f} us, D after T {row['D_after_T_us']:.1f} us")
+        rows.append(row)
+    cold = []
+    for _ in range(reps):
+        timed(t, TB, 0)
+        cold.append(timed(d, DB, 0))
+    log(f"D (160 MB) after a plain 2048 MB read of T: {float(np.median(cold)):.1f} us (cold)")
+    for b in (d, t, sink):
+        b.free()
+    nt = rows[1]
+    return {"metric": "2 GB streaming read rate with non-temporal loads (GB/s)", "value": nt["T_GB/s"], "unit": "GB/s",
+            "ms_per_step": nt["T_us"] / 1e3, "dtype": "u8",
+            "config": {"workload": "160 MB resident buffer, 2048 MB streamed past it with each load policy",
+                       "table": rows, "D_cold_us": float(np.median(cold))},
+            "roofline": {"bound": "hbm", "achieved": nt["T_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": nt["T_GB/s"] / HBM_PEAK_GBS, "traffic": None}, "cpu_baseline": None}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -601,12 +660,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU work budget of the baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workload", choices=("step", "roofline", "gemm", "attention", "accept", "copy", "read", "q6k",
-                                           "launch"),
+                                           "launch", "cache"),
                     default="step",
                     help="step: the speculative step (default); roofline: only the step's verify-GEMM roofline "
                          "measurement; gemm / attention / accept: one kernel alone; copy: counter calibration; "
                          "read: the streaming-read ceiling; q6k: the native Q6_K GEMM against fp16 at 32000x4096; "
-                         "launch: the graph-replayed launch floor against grid-wide barriers")
+                         "launch: the graph-replayed launch floor against grid-wide barriers; cache: last-level "
+                         "cache residency under plain and non-temporal streaming reads")
     ap.add_argument("--reps", type=int, default=50, help="launches per timing (kernel workloads)")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch each step's kernels directly instead of replaying the captured graph")
@@ -645,7 +705,7 @@ def main():
     if args.workload != "step":
         fn = {"gemm": workload_gemm, "attention": workload_attention, "accept": workload_accept,
               "copy": workload_copy, "read": workload_read, "q6k": workload_q6k,
-              "launch": workload_launch}[args.workload]
+              "launch": workload_launch, "cache": workload_cache}[args.workload]
         out = fn(pkg, ctx, args)
         base = {"n_gpus": 1, "steps": args.reps, "warmup": 1, "higher_is_better": True, "scaling": "weak",
                 "vs_baseline": None, "data": "synthetic, seeded"}

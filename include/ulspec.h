@@ -89,9 +89,10 @@ ulspec_status ulspec_timer_mark(ulspec_ctx* ctx, uint32_t slot /* < 16 */);
 ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t slot_a, uint32_t slot_b, float* ms);
 /* Measurement kernel with no counterpart in the reference: reads every 16-byte
  * unit of the device buffer `buf` (bytes a multiple of 16) once, 256 threads
- * per workgroup and 4 << variant (variant 0..3) loads per thread, all issued
- * before the first use.  *sink (device) is written only when the XOR of all
- * words is 0x5eed5eed, so the loads cannot be elided.  Its duration for a
+ * per workgroup and 4 << (variant & 3) loads per thread, all issued before the
+ * first use; variants 4..7 load with the non-temporal cache policy (no
+ * last-level cache allocation, as the verify GEMMs load their weights).  *sink (device) is written only by a thread whose loaded
+ * words XOR to 0x5eed5eed, so the loads cannot be elided.  Its duration for a
  * given size is the streaming-read ceiling the verify kernels are compared
  * with. */
 ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, size_t bytes, uint32_t variant, uint32_t* sink);

@@ -250,8 +250,10 @@ extern "C" ulspec_status ulspec_timer_elapsed_ms(ulspec_ctx* ctx, uint32_t a, ui
 namespace {
 
 // Streaming read: thread t of workgroup b reads units (b * 256 * U + t + 256 u),
-// u < U, every load issued before the XOR that consumes them.
-template <int U>
+// u < U, every load issued before the XOR that consumes them; NT: with the
+// non-temporal cache policy (no last-level cache allocation), as the verify
+// GEMMs read their weights.
+template <int U, bool NT>
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ p, size_t n16,
                                                           uint32_t* __restrict__ sink)
 {
@@ -260,7 +262,13 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const size_t k = i + (size_t)u * 256;
-        v[u] = k < n16 ? p[k] : uint4{0u, 0u, 0u, 0u};
+        if constexpr (NT) {
+            typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+            v[u] = k < n16 ? __builtin_bit_cast(uint4, __builtin_nontemporal_load((const u32x4*)(p + k)))
+                           : uint4{0u, 0u, 0u, 0u};
+        } else {
+            v[u] = k < n16 ? p[k] : uint4{0u, 0u, 0u, 0u};
+        }
     }
     uint32_t acc = 0;
 #pragma unroll
@@ -415,18 +423,20 @@ extern "C" ulspec_status ulspec_stream_read(ulspec_ctx* ctx, const void* buf, si
                                             uint32_t* sink)
 {
     ULSPEC_CHECK_CTX(ctx);
-    if (!buf || !sink || bytes == 0 || bytes % 16 || variant > 3)
-        return fail(ctx, ULSPEC_EINVAL, "stream_read: buffer, sink, bytes %% 16 == 0 and variant 0..3 required");
+    if (!buf || !sink || bytes == 0 || bytes % 16 || variant > 7)
+        return fail(ctx, ULSPEC_EINVAL, "stream_read: buffer, sink, bytes %% 16 == 0 and variant 0..7 required");
     (void)hipSetDevice(ctx->device);
     const size_t n16 = bytes / 16;
-    const int U = 4 << variant;
+    const int U = 4 << (variant & 3);
     const size_t grid = (n16 + 256 * (size_t)U - 1) / (256 * (size_t)U);
     if (grid > 0x7fffffffu) return fail(ctx, ULSPEC_EINVAL, "stream_read: %zu bytes is too large", bytes);
     const uint4* p = (const uint4*)buf;
-    if (U == 4) hipLaunchKernelGGL(stream_read_kernel<4>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
-    else if (U == 8) hipLaunchKernelGGL(stream_read_kernel<8>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
-    else if (U == 16) hipLaunchKernelGGL(stream_read_kernel<16>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
-    else hipLaunchKernelGGL(stream_read_kernel<32>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
+    using Kern = void (*)(const uint4*, size_t, uint32_t*);
+    static const Kern kern[8] = {stream_read_kernel<4, false>,  stream_read_kernel<8, false>,
+                                 stream_read_kernel<16, false>, stream_read_kernel<32, false>,
+                                 stream_read_kernel<4, true>,   stream_read_kernel<8, true>,
+                                 stream_read_kernel<16, true>,  stream_read_kernel<32, true>};
+    hipLaunchKernelGGL(kern[variant], dim3((unsigned)grid), dim3(256), 0, ctx->stream, p, n16, sink);
     return check_launch(ctx, "stream_read launch");
 }
 
