@@ -51,6 +51,8 @@ CASES = [
     (12, 11264, 2048, (8,)),          # 8 staged rows: the ring instead, 2 tiles per iteration
     (2, 8192, 1536, (1, 5)),          # 12 chunks: ring parts of 2 chunks, 2 tiles per iteration
     (12, 16384, 1536, (8,)),          # 6 chunks at 8 rows: ring parts of 2 chunks, 4 tiles per iteration
+    (12, 22016, 4096, (1, 6)),        # the 7B gate/up: 5-6 ring iterations per CU in groups of 3, the
+                                      # first iteration's weights issued ahead of X
 ]
 
 
