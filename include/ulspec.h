@@ -102,10 +102,12 @@ ulspec_status ulspec_device_info(ulspec_ctx* ctx, int* device, int* n_cu);
  * reach each route whatever the device's CU count).  ULSPEC_OPT_TOPK_ROUTE:
  * how the top-k (kept list, top_k <= 256) statistics run -- 0 chosen from the
  * rows and CUs (default), 1 one 1024-thread workgroup per row, 2 one
- * 512-thread workgroup per row, 3 the chunk pipeline (scan, threshold,
- * collect, finish); a route that cannot take the call (rows past 32768
- * logits, or k past its kept maxima) falls back to the chunk pipeline.  Every
- * route gives the same tokens. */
+ * 512-thread workgroup per row, 3 the scanned chunk pipeline (scan,
+ * threshold, collect, finish), 4 the sampled chunk pipeline (a threshold from
+ * a sample of each row, collect, finish: the default past the one-workgroup
+ * routes, for top_k <= 128); a route that cannot take the call (rows past
+ * 32768 logits, or k past its kept maxima) falls back to a chunk pipeline.
+ * Every route gives the same tokens. */
 enum { ULSPEC_OPT_TOPK_ROUTE = 1 };
 /* Measurement kernel with no counterpart in the reference: the cost of one
  * grid-wide barrier between co-resident workgroups (a persistent kernel's

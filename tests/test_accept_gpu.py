@@ -160,7 +160,7 @@ def test_accept_edge_cases(ctx, ora, pkg, rng):
 
 
 TOPK_ROUTES = {1: "one 1024-thread workgroup per row", 2: "one 512-thread workgroup per row",
-               3: "chunk pipeline"}
+               3: "scanned chunk pipeline", 4: "sampled chunk pipeline"}
 
 
 @pytest.fixture
@@ -179,8 +179,10 @@ def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, topk_route, route
     # the one-workgroup-per-row kernels' candidate threshold lands on a value
     # ~900 tokens share (16 waves: the sorted, not the counted, candidate
     # list); with 8 waves they keep fewer maxima per row and the threshold
-    # admits ~9800 tokens (the exact tie fallback); the chunk pipeline's
-    # threshold comes from its per-chunk wave maxima.  Every route is forced
+    # admits ~9800 tokens (the exact tie fallback); the scanned chunk
+    # pipeline's threshold comes from its per-chunk wave maxima, the sampled
+    # one's from an eighth of each row (~300 or ~600 tied candidates: the
+    # sorted list).  Every route is forced
     # in turn, whatever the device's CU count.  Ties are broken by lowest
     # index, as in the oracle.
     V = 32000
@@ -202,13 +204,25 @@ def test_accept_topk_ties_at_the_threshold(ctx, ora, pkg, rng, topk_route, route
 
 
 @pytest.mark.parametrize("route", sorted(TOPK_ROUTES))
-def test_accept_topk_routes_random_logits(ctx, ora, pkg, rng, topk_route, route):
+@pytest.mark.parametrize("V", [32000, 128256])
+def test_accept_topk_routes_random_logits(ctx, ora, pkg, rng, topk_route, route, V):
     """N(0, 3^2) logits through each top-k route, forced: B = 32, k = 8 (544
     rows, more than twice the CUs of an MI355X: the automatic choice at V =
-    32000 would be the chunk pipeline) and B = 16, k = 4."""
-    V = 32000
+    32000 would be a chunk pipeline) and B = 16, k = 4; at V = 128256 (rows
+    past the one-workgroup kernels' registers: routes 1 and 2 fall back to
+    the sampled pipeline) B = 16, k = 8, and top_k 100 (a quarter of each row
+    sampled) with k = 4."""
     s, so = pkg.sampling(0.8, top_k=40, top_p=0.9), ora.sampling(0.8, top_k=40, top_p=0.9)
     topk_route(route)
+    if V == 128256:
+        for B, k, tk in ((16, 8, 40), (16, 4, 100)):
+            s, so = pkg.sampling(0.8, top_k=tk, top_p=0.9), ora.sampling(0.8, top_k=tk, top_p=0.9)
+            tl = _logits(rng, (B, k + 1, V))
+            dl = (tl[:, :k] * 0.7 + _logits(rng, (B, k, V)) * 0.5).astype(np.float32)
+            dt = _draft_tokens(ora, so, dl, 5)
+            u = rng.random((B, k + 1)).astype(np.float32)
+            _check(ctx, ora, pkg, s, tl, dl, dt, u)
+        return
     for B, k in ((32, 8), (16, 4)):
         tl = _logits(rng, (B, k + 1, V))
         dl = (tl[:, :k] * 0.7 + _logits(rng, (B, k, V)) * 0.5).astype(np.float32)
@@ -332,6 +346,6 @@ def test_accept_argument_errors(ctx, pkg):
         ctx.sample(pkg.sampling(1.0), 70000, 1000, b, b, b)
     assert e.value.status == pkg.EUNSUPPORTED
     with pytest.raises(pkg.UlspecError) as e:
-        ctx.set_option(ctx.OPT_TOPK_ROUTE, 4)
+        ctx.set_option(ctx.OPT_TOPK_ROUTE, 5)
     assert e.value.status == pkg.EINVAL
     b.free()

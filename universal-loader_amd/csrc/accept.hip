@@ -326,13 +326,22 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
 }
 
 // buf[0 .. k) = the k largest of the n distinct nonzero order keys c[0 .. n),
-// descending: each key's place is the count of larger keys.
+// descending: each key's place is the count of larger keys.  The count reads
+// 8 keys per step, all in flight (one LDS round trip per step, not per key).
 __device__ void rank_top_desc(const uint64_t* c, int n, uint32_t k, uint64_t* buf)
 {
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const uint64_t v = c[i];
         uint32_t gt = 0;
-        for (int j = 0; j < n; ++j) gt += c[j] > v;
+        int j = 0;
+        for (; j + 8 <= n; j += 8) {
+            uint64_t x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) x[u] = c[j + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) gt += x[u] > v;
+        }
+        for (; j < n; ++j) gt += c[j] > v;
         if (gt < k) buf[gt] = v;
     }
     __syncthreads();
@@ -1804,28 +1813,17 @@ __global__ __launch_bounds__(kT0Threads) void topk_t0_kernel(ChunkPlan cp, int m
     }
 }
 
-// k-th largest of the row's G x 256 per-thread maxima by an 8-bit radix
-// select (four histogram rounds); the row's max / argmax from the chunk maxima.
-__global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan cp, uint32_t k, TopkWs w)
+// The k-th largest of the n values v[e] of thread t at index t + kRowThreads e
+// (< n) in a kRowThreads workgroup: an 8-bit radix select, four histogram
+// rounds (every thread calls it; the result in every thread).
+template <int E>
+__device__ uint32_t radix_kth_largest(const uint32_t (&v)[E], uint32_t n, uint32_t k)
 {
-    constexpr int E = kMaxChunks * kChunkThreads / kRowThreads;  // values per thread
     constexpr int NWV = kRowThreads / 64 * 4;
     __shared__ uint32_t whist[NWV][256];  // per (wave, lane & 3) histograms: most values share their top bytes
     __shared__ uint32_t hist[256];
     __shared__ uint32_t sel_bucket, sel_k;
-    __shared__ uint64_t scratch[kRowThreads / 64];
-    const uint32_t r = blockIdx.x, n = cp.G * kChunkThreads;
     const int tid = threadIdx.x;
-    const uint32_t* tm = w.tm + (size_t)r * cp.G * kChunkThreads;
-    uint32_t v[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {  // unconditional loads (clamped index), then masked: all in flight together
-        const uint32_t i = tid + kRowThreads * e;
-        v[e] = tm[min(i, n - 1)];
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e)
-        if (tid + kRowThreads * e >= n) v[e] = 0u;
     uint32_t prefix = 0, mask = 0, kk = k;
     const int wv = (tid >> 6) * 4 + (tid & 3);
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -1874,6 +1872,28 @@ __global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan c
         kk = sel_k;
         __syncthreads();
     }
+    return prefix;
+}
+
+// k-th largest of the row's G x 256 per-thread maxima; the row's max / argmax
+// from the chunk maxima.
+__global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan cp, uint32_t k, TopkWs w)
+{
+    constexpr int E = kMaxChunks * kChunkThreads / kRowThreads;  // values per thread
+    __shared__ uint64_t scratch[kRowThreads / 64];
+    const uint32_t r = blockIdx.x, n = cp.G * kChunkThreads;
+    const int tid = threadIdx.x;
+    const uint32_t* tm = w.tm + (size_t)r * cp.G * kChunkThreads;
+    uint32_t v[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {  // unconditional loads (clamped index), then masked: all in flight together
+        const uint32_t i = tid + kRowThreads * e;
+        v[e] = tm[min(i, n - 1)];
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+        if (tid + kRowThreads * e >= n) v[e] = 0u;
+    const uint32_t prefix = radix_kth_largest<E>(v, n, k);
     const uint64_t top = block_max_u64<kRowThreads>(tid < (int)cp.G ? w.part[(size_t)r * cp.G + tid].top : 0, scratch);
     if (tid == 0) {
         RowStat* st = w.stats + r;
@@ -1884,24 +1904,115 @@ __global__ __launch_bounds__(kRowThreads) void topk_threshold_kernel(ChunkPlan c
     }
 }
 
-// Tokens with logit key >= the row's threshold into its candidate list.
+// Candidate threshold from a sample of the row (the sampled pipeline: sample,
+// collect, finish), one workgroup per row: every F-th run of 64 float4
+// groups (1 KB; a wave's load is one run, E per thread, all in flight) --
+// 1 / F of the row, where the scan reads all of it.  Each wave keeps its m
+// largest per-thread maximum keys (strictly decreasing, so of distinct
+// tokens), and the threshold is the largest kept key with at least k kept
+// keys at or above it: at least k tokens of the row reach it, so the tokens
+// at or above it include the row's top k -- about F k of them on rows
+// without heavy ties (past kCandMax the finish takes its exact path).  The
+// row's max comes from the candidates in the finish.
+__device__ __forceinline__ uint32_t sample_group(uint32_t j, uint32_t F) { return (j >> 6) * 64u * F + (j & 63u); }
+
+template <int E>
+__global__ __launch_bounds__(kRowThreads) void topk_sample_kernel(RowSrc rs, uint32_t V, uint32_t F, int m,
+                                                                  uint32_t k, TopkWs w)
+{
+    constexpr int NT = kRowThreads, NWV = NT / 64;
+    __shared__ uint32_t tops[NWV * kTopM];
+    __shared__ uint64_t red[NWV];
+    const uint32_t r = blockIdx.x, V4 = (V + 3) / 4;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* row = rs.row(r, V);
+    float4 x[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) x[e] = load4(row, V, min(sample_group(tid + NT * e, F), V4 - 1));
+    uint32_t bk = 0;  // the thread's largest sampled key (0: none)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint32_t q = sample_group(tid + NT * e, F);
+        const float f[4] = {x[e].x, x[e].y, x[e].z, x[e].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (q < V4 && 4 * q + c < V) bk = max(bk, float_key(f[c]));
+    }
+    uint32_t prev = 0xffffffffu;
+    for (int j = 0; j < m; ++j) {  // uniform
+        uint32_t t = bk < prev ? bk : 0u;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) t = max(t, (uint32_t)__shfl_xor((int)t, o));
+        if (lane == j) tops[wave * m + j] = t;
+        prev = t;
+    }
+    __syncthreads();
+    const int n = NWV * m;
+    uint32_t thr = 0;
+    if (tid < n) {
+        const uint32_t tv = tops[tid];
+        if (tv) {
+            uint32_t ge = 0;
+            for (int j = 0; j < n; ++j) ge += tops[j] >= tv;
+            if (ge >= k) thr = tv;
+        }
+    }
+    thr = (uint32_t)block_max_u64<NT>(thr, red);  // 0 (no bound): every token, then the exact path
+    if (tid == 0) {
+        w.t0[r] = thr;
+        w.cnt[(size_t)r * kCntPad] = 0;
+    }
+}
+
+// Sample fraction 1 / F of the sampled pipeline for top-k k (about F k
+// candidates: F = 8 up to k = 64, 4 up to 128) and the sample kernel's
+// float4 groups per thread (a power of two <= 8: 32 keys per thread, within
+// the registers of a 1024-thread workgroup); 0 where it does not apply.
+inline uint32_t topk_sample_F(uint32_t k) { return k <= 64 ? 8u : (k <= 128 ? 4u : 0u); }
+inline int topk_sample_E(uint32_t V, uint32_t F)
+{
+    const uint32_t runs = ((V + 3) / 4 + 63) / 64, ng = (runs + F - 1) / F * 64;  // sampled float4 groups
+    const uint32_t per = (ng + kRowThreads - 1) / kRowThreads;
+    int e = 1;
+    while ((uint32_t)e < per) e <<= 1;
+    return e <= 8 ? e : 0;
+}
+
+// Tokens with logit key >= the row's threshold into its candidate list: per
+// pass, kCollectU float4 groups per thread (all loads in flight); each
+// wave's candidates go to a list of the workgroup in LDS (one LDS slot
+// reservation per wave and pass), and the workgroup reserves its range of
+// the row's list with one device atomic at its end -- a wave never waits on
+// a device atomic between its loads (with ~F k candidates per row nearly
+// every wave holds one).  Past kCandMax candidates only the count matters
+// (the finish then takes its exact path).
+constexpr int kCollectU = 4;
 __global__ __launch_bounds__(kChunkThreads) void topk_collect_kernel(RowSrc rs, uint32_t V, ChunkPlan cp, TopkWs w)
 {
+    __shared__ uint64_t lc[kCandMax];
+    __shared__ uint32_t ln, lbase;
     const uint32_t r = blockIdx.y, g = blockIdx.x, V4 = (V + 3) / 4;
     const float* row = rs.row(r, V);
     const uint32_t thr = w.t0[r], q1 = min(V4, (g + 1) * cp.CG);
     const int lane = threadIdx.x & 63;
-    for (uint32_t qb = g * cp.CG; qb < q1; qb += kChunkThreads) {  // uniform
-        const uint32_t q = qb + threadIdx.x;
-        const float4 v = load4(row, V, min(q, V4 - 1));
-        const float e[4] = {v.x, v.y, v.z, v.w};
-        uint32_t key[4], n = 0;
+    if (threadIdx.x == 0) ln = 0;
+    __syncthreads();
+    for (uint32_t qb = g * cp.CG; qb < q1; qb += kChunkThreads * kCollectU) {  // uniform
+        float4 v[kCollectU];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            key[c] = float_key(e[c]);
-            n += q < q1 && 4 * q + c < V && key[c] >= thr;
+        for (int u = 0; u < kCollectU; ++u) v[u] = load4(row, V, min(qb + threadIdx.x + u * kChunkThreads, V4 - 1));
+        uint32_t key[kCollectU][4], n = 0;
+#pragma unroll
+        for (int u = 0; u < kCollectU; ++u) {
+            const uint32_t q = qb + threadIdx.x + u * kChunkThreads;
+            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                key[u][c] = float_key(e[c]);
+                n += q < q1 && 4 * q + c < V && key[u][c] >= thr;
+            }
         }
-        // one slot reservation per wave: exclusive prefix of the lanes' counts
+        // one LDS slot reservation per wave: exclusive prefix of the lanes' counts
         uint32_t incl = n;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -1909,17 +2020,30 @@ __global__ __launch_bounds__(kChunkThreads) void topk_collect_kernel(RowSrc rs, 
             if (lane >= o) incl += t;
         }
         const uint32_t total = __shfl(incl, 63);
+        if (!total) continue;  // uniform in the wave
         uint32_t base = 0;
-        if (lane == 0 && total) base = atomicAdd(&w.cnt[(size_t)r * kCntPad], total);
+        if (lane == 0) base = atomicAdd(&ln, total);
         base = __shfl(base, 0);
         uint32_t slot = base + incl - n;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (q < q1 && 4 * q + c < V && key[c] >= thr) {
-                if (slot < (uint32_t)kCandMax) w.cand[(size_t)r * kCandMax + slot] = order_key(key[c], 4 * q + c);
-                ++slot;
-            }
+        for (int u = 0; u < kCollectU; ++u) {
+            const uint32_t q = qb + threadIdx.x + u * kChunkThreads;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (q < q1 && 4 * q + c < V && key[u][c] >= thr) {
+                    if (slot < (uint32_t)kCandMax) lc[slot] = order_key(key[u][c], 4 * q + c);
+                    ++slot;
+                }
+        }
     }
+    __syncthreads();
+    const uint32_t n = ln;
+    if (!n) return;  // uniform
+    if (threadIdx.x == 0) lbase = atomicAdd(&w.cnt[(size_t)r * kCntPad], n);
+    __syncthreads();
+    const uint32_t base = lbase, nl = min(n, (uint32_t)kCandMax);
+    for (uint32_t i = threadIdx.x; i < nl && base + i < (uint32_t)kCandMax; i += kChunkThreads)
+        w.cand[(size_t)r * kCandMax + base + i] = lc[i];
 }
 
 __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uint32_t V, WarpParams p, TopkWs w)
@@ -1931,7 +2055,6 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
     const uint32_t r = blockIdx.x, k = p.top_k;
     RowStat* st = w.stats + r;
     const uint32_t nc = w.cnt[(size_t)r * kCntPad];
-    const float lmax = st->lmax;
     const uint64_t* c = w.cand + (size_t)r * kCandMax;
     if (nc <= (uint32_t)kRankMax) {  // few candidates (the usual case): places by counting
         __shared__ uint64_t cs[kRankMax];
@@ -1945,6 +2068,15 @@ __global__ __launch_bounds__(kRowThreads) void topk_finish_kernel(RowSrc rs, uin
         bitonic_desc(buf, n2);
     } else {
         topk_tie_fallback<kRowThreads>(rs.row(r, V), V, k, buf, red, cand_count);
+    }
+    __syncthreads();
+    // buf holds the top k in descending (logit, then lowest index) order: its
+    // first entry is the row's maximum and argmax (the same as the chunk
+    // maxima give, which the sampled pipeline does not compute)
+    const float lmax = key_float((uint32_t)(buf[0] >> 32));
+    if (threadIdx.x == 0) {
+        st->lmax = lmax;
+        st->argmax = (int32_t)(0xffffffffu - (uint32_t)buf[0]);
     }
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
@@ -2055,8 +2187,9 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
 }
 
 // The one-workgroup-per-row kernel while the rows fit one round of
-// workgroups: 1024 threads up to one row per CU, 512 (two per CU) up to two.
-// route (ULSPEC_OPT_TOPK_ROUTE) forces one of the three where it applies.
+// workgroups: 1024 threads up to one row per CU, 512 (two per CU) up to two;
+// past that the sampled chunk pipeline (top_k <= 128), else the scanned one.
+// route (ULSPEC_OPT_TOPK_ROUTE) forces one of the four where it applies.
 void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w,
                        int n_cu, int route)
 {
@@ -2073,6 +2206,28 @@ void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, cons
     }
     const ChunkPlan cp = chunk_plan(V);
     const dim3 grid(cp.G, rows), blk(kChunkThreads);
+    const uint32_t F = topk_sample_F(p.top_k);
+    const int E = F ? topk_sample_E(V, F) : 0;
+    if (E && route != 3) {  // the sampled pipeline: 1 / F of the row, then one pass (route 3: the scan)
+        const dim3 g1(rows), b1(kRowThreads);
+        // kept keys per wave of 16: two more than an even share of k (fewer
+        // waves' leading maxima cut off, so a threshold closer to the
+        // sample's k-th largest and fewer candidates), at most kTopM
+        const int ms = (int)std::min<uint32_t>(kTopM, (p.top_k + 15) / 16 + 2);
+        switch (E) {
+        case 1: hipLaunchKernelGGL(topk_sample_kernel<1>, g1, b1, 0, s, rs, V, F, ms, p.top_k, w); break;
+        case 2: hipLaunchKernelGGL(topk_sample_kernel<2>, g1, b1, 0, s, rs, V, F, ms, p.top_k, w); break;
+        case 4: hipLaunchKernelGGL(topk_sample_kernel<4>, g1, b1, 0, s, rs, V, F, ms, p.top_k, w); break;
+        default: hipLaunchKernelGGL(topk_sample_kernel<8>, g1, b1, 0, s, rs, V, F, ms, p.top_k, w); break;
+        }
+        // the collect in chunks of one pass (kCollectU float4 groups per thread)
+        const uint32_t V4 = (V + 3) / 4, CGc = std::min<uint32_t>(kChunkThreads * kCollectU,
+                                                                  (V4 + kChunkThreads - 1) / kChunkThreads * kChunkThreads);
+        const ChunkPlan cpc{(V4 + CGc - 1) / CGc, CGc};
+        hipLaunchKernelGGL(topk_collect_kernel, dim3(cpc.G, rows), blk, 0, s, rs, V, cpc, w);
+        hipLaunchKernelGGL(topk_finish_kernel, dim3(rows), dim3(kRowThreads), 0, s, rs, V, p, w);
+        return;
+    }
     const int m = topk_m(p.top_k, cp.G);
     hipLaunchKernelGGL(topk_scan_kernel, grid, blk, 0, s, rs, V, cp, m, w);
     if (m == 0) hipLaunchKernelGGL(topk_threshold_kernel, dim3(rows), dim3(kRowThreads), 0, s, cp, p.top_k, w);

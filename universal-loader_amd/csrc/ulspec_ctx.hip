@@ -412,7 +412,7 @@ extern "C" ulspec_status ulspec_set_option(ulspec_ctx* ctx, uint32_t option, int
 {
     ULSPEC_CHECK_CTX(ctx);
     if (option == ULSPEC_OPT_TOPK_ROUTE) {
-        if (value < 0 || value > 3) return fail(ctx, ULSPEC_EINVAL, "set_option: top-k route %lld (0 .. 3)", (long long)value);
+        if (value < 0 || value > 4) return fail(ctx, ULSPEC_EINVAL, "set_option: top-k route %lld (0 .. 4)", (long long)value);
         ctx->topk_route = (int)value;
         return ULSPEC_OK;
     }
