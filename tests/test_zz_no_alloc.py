@@ -51,6 +51,8 @@ def _run(ctx, fn, s, tl, dl, dt, u):
 
 MODES = {
     "topk40_topp09": ((0.8, 40, 0.9, False), 32000),
+    # rows past the one-workgroup kernels' registers: the sampled chunk pipeline
+    "topk40_topp09_v128256": ((0.8, 40, 0.9, False), 128256),
     "full_vocab": ((0.8, 0, 1.0, False), 32000),
     "greedy": ((1.0, 0, 1.0, True), 128256),
 }
