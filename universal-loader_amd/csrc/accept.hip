@@ -2186,10 +2186,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
     finish_topk(buf, k, lmax, p, st, keptE, cand_count);
 }
 
-// The one-workgroup-per-row kernel while the rows fit one round of
-// workgroups: 1024 threads up to one row per CU, 512 (two per CU) up to two;
-// past that the sampled chunk pipeline (top_k <= 128), else the scanned one.
-// route (ULSPEC_OPT_TOPK_ROUTE) forces one of the four where it applies.
+// The one-workgroup-per-row kernel while the rows fit one round of 1024-
+// thread workgroups (one row per CU); past that the sampled chunk pipeline
+// (top_k <= 128), else the 512-thread one-workgroup kernel up to two rows per
+// CU, else the scanned chunk pipeline.  route (ULSPEC_OPT_TOPK_ROUTE) forces
+// one of the four where it applies.
 void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, const WarpParams& p, const TopkWs& w,
                        int n_cu, int route)
 {
@@ -2200,14 +2201,16 @@ void launch_topk_stats(hipStream_t s, RowSrc rs, uint32_t rows, uint32_t V, cons
         hipLaunchKernelGGL(topk_row_kernel<1024>, dim3(rows), dim3(1024), 0, s, rs, V, p, m16, w);
         return;
     }
-    if (fits8 && (route == 2 || (route == 0 && rows <= 2 * cus))) {
+    const uint32_t F = topk_sample_F(p.top_k);
+    const int E = F ? topk_sample_E(V, F) : 0;
+    // up to two rows per CU the sampled pipeline beats the 512-thread
+    // one-workgroup kernel too (k=8, V=32000, 272 rows: 40.1 against 41.4 us)
+    if (fits8 && (route == 2 || (route == 0 && rows <= 2 * cus && !E))) {
         hipLaunchKernelGGL(topk_row_kernel<512>, dim3(rows), dim3(512), 0, s, rs, V, p, m8, w);
         return;
     }
     const ChunkPlan cp = chunk_plan(V);
     const dim3 grid(cp.G, rows), blk(kChunkThreads);
-    const uint32_t F = topk_sample_F(p.top_k);
-    const int E = F ? topk_sample_E(V, F) : 0;
     if (E && route != 3) {  // the sampled pipeline: 1 / F of the row, then one pass (route 3: the scan)
         const dim3 g1(rows), b1(kRowThreads);
         // kept keys per wave of 16: two more than an even share of k (fewer
