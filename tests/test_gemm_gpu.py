@@ -46,13 +46,14 @@ CASES = [
     (2, 100, 1376, (1, 3, 16, 33)),   # N % 16 != 0, K = 43 blocks (partial quad)
     (12, 40, 512, (2, 64, 65)),       # M > 64 splits into launches
     (2, 32000, 512, (5,)),            # LM-head shape of the small model
-    (12, 11264, 2048, (1, 2, 6)),     # 704 tiles of <= 8 chunks: one-tile kernel, 2.75 tiles per CU
+    (12, 11264, 2048, (1, 2, 6)),     # 704 tiles of <= 8 chunks: one-tile kernel (4 waves of 2 chunks), 2.75 tiles per CU
     (2, 16384, 1024, (1, 5)),         # 1024 tiles of 8 chunks: one-tile kernel, 4 tiles per CU
     (12, 11264, 2048, (8,)),          # 8 staged rows: the ring instead, 2 tiles per iteration
     (2, 8192, 1536, (1, 5)),          # 12 chunks: ring parts of 2 chunks, 2 tiles per iteration
     (12, 16384, 1536, (8,)),          # 6 chunks at 8 rows: ring parts of 2 chunks, 4 tiles per iteration
     (12, 22016, 4096, (1, 6)),        # the 7B gate/up: 5-6 ring iterations per CU in groups of 3, the
                                       # first iteration's weights issued ahead of X
+    (12, 2048, 2048, (1, 2, 6)),      # 128 tiles of 8 chunks, fewer than CUs: the one-tile kernel too
 ]
 
 

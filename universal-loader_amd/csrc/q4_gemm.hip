@@ -1570,6 +1570,7 @@ __device__ __forceinline__ void rs_issue(const GemmArgs& a, float4 (&ps)[2])
 template <int TYPE, int CMAX, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 {
+    static_assert(NW >= 4 && NW % 4 == 0, "the reduction and epilogue take 256-thread tile slots");
     extern __shared__ uint4 xs[];
     __shared__ float red[NW * 4 * 64];
     __shared__ float rs[16];
@@ -1817,7 +1818,7 @@ namespace ulspec {
 // keeps besides X (part sums and row scales).
 constexpr size_t kWideLdsMax = 160 * 1024;
 constexpr size_t kStaticWide = (size_t)kWideWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
-constexpr size_t kStaticSmall = (size_t)8 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+constexpr size_t kStaticSmall = (size_t)4 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
 constexpr size_t ring_static(int G)
 {
     return (size_t)G * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
@@ -1876,13 +1877,17 @@ void wide_kernels(CList<C...>, std::vector<const void*>& out)
     (out.push_back((const void*)gemm_stream_kernel<TYPE, C, kWideWaves>), ...);
 }
 
-// One tile per 8-wave workgroup, one chunk per wave: weights of at most 8
-// chunks per row (Q4_K K <= 2048) with up to 4 tiles per CU.  The workgroups
-// of one launch are all resident at once, so every CU works, where the ring
-// kernel's 16-wave workgroups would leave CUs idle (384 tiles of 8 chunks:
-// 192 of them).  With more tiles per CU the ring kernel, which copies X once
-// per CU instead of once per tile, is faster.
-constexpr int kSmallWaves = 8;
+// One tile per 4-wave workgroup, two chunks per wave: weights of at most 8
+// chunks per row (Q4_K K <= 2048) with up to 4 tiles per CU, and with fewer
+// tiles than CUs too.  The workgroups of one launch are all resident at
+// once, so every CU works, where the ring kernel's 16-wave workgroups would
+// leave CUs idle (384 tiles of 8 chunks: 192 of them).  With more tiles per
+// CU the ring kernel, which copies X once per CU instead of once per tile, is
+// faster.  (8 waves of one chunk each, and the 16-wave kernel, half of whose
+// waves idle, below one tile per CU: the draft's O projection at M = 1 5.28
+// -> 4.63 us, gate/up 7.47 -> 6.92 us, the 7B step 1.7 % faster.)
+constexpr int kSmallWaves = 4;
+constexpr int kSmallChunks = 2;  // per wave
 constexpr int kSmallTilesPerCu = 4;
 
 // Launch the one-tile kernel with the smallest batch >= cpp (the largest when none is).
@@ -1937,7 +1942,7 @@ void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& smal
 {
     slice_kernels<TYPE>(std::integer_sequence<int, 1, 2, 3, 4, 6>{}, slices);
     wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, wide);
-    small.push_back((const void*)gemm_stream_kernel<TYPE, 1, kSmallWaves>);
+    small.push_back((const void*)gemm_stream_kernel<TYPE, kSmallChunks, kSmallWaves>);
     ring_kernels<TYPE, 1, 2>(rings);
     ring_kernels<TYPE, 2, 2>(rings);
     rings3.push_back((const void*)gemm_ring_kernel<TYPE, 1, 3, 1>);
@@ -1975,13 +1980,13 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
 }
 
 // Launch a whole-X kernel if one fits; false when the split-K path must run.
-// At most 8 chunks per row and 1-4 tiles per CU: the 8-wave one-tile kernel
-// (below 8 staged rows, or while the ring would leave CUs idle).
+// At most 8 chunks per row and up to 4 tiles per CU: the 4-wave one-tile
+// kernel (below 8 staged rows, or while the ring would leave CUs idle).
 // More tiles than CUs and at most two chunks per part: the ring kernel, one
 // 16-wave workgroup per CU, P parts per tile (the largest power of two <=
-// min(16, chunks per row), P >= 4), 16 / P tiles per iteration.  At most one
-// tile per CU: one 16-wave workgroup per tile with 16 parts (waves with an
-// empty part idle).
+// min(16, chunks per row), P >= 4), 16 / P tiles per iteration.  Otherwise,
+// at most one tile per CU: one 16-wave workgroup per tile with 16 parts
+// (waves with an empty part idle).
 template <int TYPE>
 bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
@@ -2001,15 +2006,15 @@ bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
     const int cpp = (int)((w.n_chunks + P - 1) / P);
     const int ring_iters = ((int)w.n_tiles + kRingWaves / P - 1) / (kRingWaves / P);
     const bool ring_ok = pipe && P >= 4 && cpp <= 2 && lds + ring_static(2) <= kWideLdsMax;
-    const bool small_ok = pipe && w.n_chunks <= (uint32_t)kSmallWaves &&
+    const bool small_ok = w.n_chunks <= (uint32_t)(kSmallWaves * kSmallChunks) &&
                           (int)w.n_tiles <= kSmallTilesPerCu * n_cu && lds + kStaticSmall <= kWideLdsMax;
     // the one-tile kernel stages the whole X per tile: from 8 staged rows on,
     // the ring (X once per CU) where its iterations cover every CU
     const bool small_x = a.xrows < 8 || ring_iters < n_cu;
     if (small_ok && (small_x || !ring_ok)) {
-        split(kSmallWaves);  // one chunk (or none) per wave
-        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 1, kSmallWaves>), dim3(w.n_tiles), dim3(kSmallWaves * 64), lds,
-                           st, a);
+        split(kSmallWaves);  // at most kSmallChunks chunks per wave
+        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, kSmallChunks, kSmallWaves>), dim3(w.n_tiles),
+                           dim3(kSmallWaves * 64), lds, st, a);
         return true;
     }
     if (pipe) {
