@@ -1541,14 +1541,18 @@ __device__ __forceinline__ float red_sum(const GemmArgs& a, const float* red, in
     return s;
 }
 
-// Row scales of rows wave and wave + NW into rs (LDS), from loads issued by
-// the same wave before its X and weights.
+// Row scales of rows wave, wave + NW, ... (every row of a whole-X kernel, at
+// most 16) into rs (LDS), from loads issued by the same wave before its X and
+// weights.
 template <int NW>
-__device__ __forceinline__ void rs_finish(const GemmArgs& a, const float4 (&ps)[2], float* rs)
+constexpr int kRsIters = (16 + NW - 1) / NW;
+
+template <int NW>
+__device__ __forceinline__ void rs_finish(const GemmArgs& a, const float4 (&ps)[kRsIters<NW>], float* rs)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < (NW < 16 ? 2 : 1); ++i) {
+    for (int i = 0; i < kRsIters<NW>; ++i) {
         const int m = wave + NW * i;
         if (m < a.M) {  // wave-uniform
             const float r = rs_reduce(a, ps[i]);
@@ -1558,11 +1562,11 @@ __device__ __forceinline__ void rs_finish(const GemmArgs& a, const float4 (&ps)[
 }
 
 template <int NW>
-__device__ __forceinline__ void rs_issue(const GemmArgs& a, float4 (&ps)[2])
+__device__ __forceinline__ void rs_issue(const GemmArgs& a, float4 (&ps)[kRsIters<NW>])
 {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-    for (int i = 0; i < (NW < 16 ? 2 : 1); ++i)
+    for (int i = 0; i < kRsIters<NW>; ++i)
         if (wave + NW * i < a.M) ps[i] = rs_load(a, wave + NW * i);
 }
 
@@ -1594,7 +1598,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
 
     // issue order: row-scale partials, this wave's X (its whole part), the
     // first batch of weights, the epilogue operands
-    float4 ps[2];
+    float4 ps[kRsIters<NW>];
     if (a.f.rs_pss) rs_issue<NW>(a, ps);
     x_copy_region<TYPE, RM>(a, xr, (uint8_t*)xs, ca, cb, L);
     pin_loads();
@@ -1692,7 +1696,7 @@ __global__ __launch_bounds__(kRingWaves * 64) void gemm_ring_kernel(GemmArgs a)
     // multiply waits for both; the 7B gate/up at M = 6, 5-6 iterations per
     // workgroup: 17.8 -> 17.1 us, where the QKV's single group of 3 was
     // 0.2 us slower that way)
-    float4 ps[2];
+    float4 ps[kRsIters<NW>];
     if (a.f.rs_pss) rs_issue<NW>(a, ps);
     WBatch<TYPE, C> ring[G];
     const bool wfirst = n_loc > G;  // uniform over the workgroup
@@ -1817,8 +1821,9 @@ namespace ulspec {
 // LDS available to one workgroup on gfx950, and what each whole-X kernel
 // keeps besides X (part sums and row scales).
 constexpr size_t kWideLdsMax = 160 * 1024;
-constexpr size_t kStaticWide = (size_t)kWideWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
-constexpr size_t kStaticSmall = (size_t)4 * 4 * 64 * sizeof(float) + 16 * sizeof(float);
+constexpr size_t stream_static(int nw) { return (size_t)nw * 4 * 64 * sizeof(float) + 16 * sizeof(float); }
+constexpr size_t kStaticWide = stream_static(kWideWaves);
+constexpr size_t kStaticSmall = stream_static(4);
 constexpr size_t ring_static(int G)
 {
     return (size_t)G * kRingWaves * 4 * 64 * sizeof(float) + 16 * sizeof(float);
@@ -1938,11 +1943,14 @@ void slice_kernels(std::integer_sequence<int, MT...>, std::vector<const void*>& 
 
 template <int TYPE>
 void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& small, std::vector<const void*>& rings,
-                  std::vector<const void*>& rings3, std::vector<const void*>& slices)
+                  std::vector<const void*>& rings3, std::vector<const void*>& slices, std::vector<const void*>& mid8,
+                  std::vector<const void*>& mid12)
 {
     slice_kernels<TYPE>(std::integer_sequence<int, 1, 2, 3, 4, 6>{}, slices);
     wide_kernels<TYPE>(typename GemmCfg<TYPE>::Wide{}, wide);
     small.push_back((const void*)gemm_stream_kernel<TYPE, kSmallChunks, kSmallWaves>);
+    mid8.push_back((const void*)gemm_stream_kernel<TYPE, 2, 8>);
+    mid12.push_back((const void*)gemm_stream_kernel<TYPE, 2, 12>);
     ring_kernels<TYPE, 1, 2>(rings);
     ring_kernels<TYPE, 2, 2>(rings);
     rings3.push_back((const void*)gemm_ring_kernel<TYPE, 1, 3, 1>);
@@ -1950,17 +1958,18 @@ void type_kernels(std::vector<const void*>& wide, std::vector<const void*>& smal
 
 ulspec_status gemm_init(ulspec_ctx* ctx)
 {
-    std::vector<const void*> wide, small, rings, rings3, slices;
-    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings, rings3, slices);
-    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings, rings3, slices);
-    type_kernels<ULSPEC_GGML_F16>(wide, small, rings, rings3, slices);
-    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings, rings3, slices);
-    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings, rings3, slices);
+    std::vector<const void*> wide, small, rings, rings3, slices, mid8, mid12;
+    type_kernels<ULSPEC_GGML_Q4_0>(wide, small, rings, rings3, slices, mid8, mid12);
+    type_kernels<ULSPEC_GGML_Q4_K>(wide, small, rings, rings3, slices, mid8, mid12);
+    type_kernels<ULSPEC_GGML_F16>(wide, small, rings, rings3, slices, mid8, mid12);
+    type_kernels<ULSPEC_GGML_Q8_0>(wide, small, rings, rings3, slices, mid8, mid12);
+    type_kernels<ULSPEC_GGML_Q6_K>(wide, small, rings, rings3, slices, mid8, mid12);
     const struct {
         const std::vector<const void*>* fns;
         size_t fixed;
-    } groups[] = {{&wide, kStaticWide},    {&small, kStaticSmall}, {&rings, ring_static(2)},
-                  {&rings3, ring_static(3)}, {&slices, 0}};
+    } groups[] = {{&wide, kStaticWide},       {&small, kStaticSmall},    {&rings, ring_static(2)},
+                  {&rings3, ring_static(3)},    {&slices, 0},              {&mid8, stream_static(8)},
+                  {&mid12, stream_static(12)}};
     // The launch checks add each group's static LDS to the dynamic size; the
     // opt-in must not let static + dynamic exceed the CU's 160 KB, so both
     // come from the compiled kernel's own static size.
@@ -1985,8 +1994,9 @@ ulspec_status gemm_init(ulspec_ctx* ctx)
 // More tiles than CUs and at most two chunks per part: the ring kernel, one
 // 16-wave workgroup per CU, P parts per tile (the largest power of two <=
 // min(16, chunks per row), P >= 4), 16 / P tiles per iteration.  Otherwise,
-// at most one tile per CU: one 16-wave workgroup per tile with 16 parts
-// (waves with an empty part idle).
+// at most one tile per CU: one workgroup per tile, 8 or 12 waves of at most
+// two chunks up to 24 chunks per row, else 16 waves (a wave with an empty
+// part idles).
 template <int TYPE>
 bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
 {
@@ -2032,6 +2042,19 @@ bool stream_launch_t(ulspec_ctx* ctx, const Weight& w, GemmArgs& a)
         return true;
     }
     if (lds + kStaticWide > kWideLdsMax) return false;
+    // one tile per workgroup: up to 24 chunks 8 or 12 waves of at most two
+    // (fewer idle waves than 16: the 7B O projection 7.58 -> 7.24 us, the
+    // draft's down 6.74 -> 6.41 us at M = 2), past that 16 waves
+    if (w.n_chunks <= 16) {
+        split(8);
+        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 2, 8>), dim3(w.n_tiles), dim3(8 * 64), lds, st, a);
+        return true;
+    }
+    if (w.n_chunks <= 24) {
+        split(12);
+        hipLaunchKernelGGL((gemm_stream_kernel<TYPE, 2, 12>), dim3(w.n_tiles), dim3(12 * 64), lds, st, a);
+        return true;
+    }
     split(kWideWaves);
     wide_launch<TYPE>(typename GemmCfg<TYPE>::Wide{}, a.ks_q + (a.ks_r ? 1 : 0), dim3(w.n_tiles),
                       dim3(kWideWaves * 64), lds, st, a);
