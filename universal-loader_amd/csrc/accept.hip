@@ -31,6 +31,8 @@
 //   workgroup per row for the candidate sort and the kept list (sorted by
 //   index), then decide (one workgroup per sequence, lists staged in LDS).
 // Tree acceptance keeps one workgroup per row (row_stats) and per tree.
+#include <type_traits>
+
 #include "detmath.h"
 #include "hip_common.h"
 #include "ulspec_internal.h"
@@ -87,15 +89,75 @@ __host__ __device__ __forceinline__ bool row_bound(const WarpParams& p, uint32_t
     return !p.greedy && !list_topk(p, V) && (p.top_p < 1.0f || bound_topk(p, V));
 }
 
+// ---- wave scans over DPP lane moves ---------------------------------------------
+// Inclusive prefix (max or sum) over the 64 lanes of a fully active wave:
+// shifts by 1, 2, 4 and 8 lanes within each row of 16, then lane 15 of rows 0
+// and 2 into rows 1 and 3, then lane 31 into rows 2 and 3 (lanes with no
+// source take 0, the identity of both).  A DPP move costs a few cycles where
+// an LDS permute (__shfl_*) costs a round trip of ~100; on integers the
+// result is the same whatever the order.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_move(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_move(uint64_t v)
+{
+    return (uint64_t)dpp_move<CTRL, ROW_MASK>((uint32_t)v) | (uint64_t)dpp_move<CTRL, ROW_MASK>((uint32_t)(v >> 32))
+                                                                 << 32;
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_scan_incl(T v, Op op)
+{
+    v = op(v, dpp_move<0x111, 0xf>(v));  // row_shr:1
+    v = op(v, dpp_move<0x112, 0xf>(v));  // row_shr:2
+    v = op(v, dpp_move<0x114, 0xf>(v));  // row_shr:4
+    v = op(v, dpp_move<0x118, 0xf>(v));  // row_shr:8
+    v = op(v, dpp_move<0x142, 0xa>(v));  // row_bcast:15 into rows 1, 3
+    v = op(v, dpp_move<0x143, 0xc>(v));  // row_bcast:31 into rows 2, 3
+    return v;
+}
+__device__ __forceinline__ uint32_t lane63_u32(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+__device__ __forceinline__ uint64_t lane63_u64(uint64_t v)
+{
+    return (uint64_t)lane63_u32((uint32_t)v) | (uint64_t)lane63_u32((uint32_t)(v >> 32)) << 32;
+}
+struct OpMax {
+    template <typename T>
+    __device__ T operator()(T a, T b) const { return a > b ? a : b; }
+};
+struct OpAdd {
+    template <typename T>
+    __device__ T operator()(T a, T b) const { return a + b; }
+};
+// Largest / sum over a fully active wave, in every lane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) { return lane63_u32(wave_scan_incl(v, OpMax{})); }
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return lane63_u64(wave_scan_incl(v, OpMax{})); }
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) { return lane63_u64(wave_scan_incl(v, OpAdd{})); }
+
+// Number of the n keys of tops (LDS, 16-byte aligned) that are >= tv: 32
+// keys per step, their LDS reads all in flight.
+__device__ __forceinline__ uint32_t count_ge(const uint32_t* tops, int n, uint32_t tv)
+{
+    uint32_t ge = 0;
+    int j = 0;
+    for (; j + 32 <= n; j += 32) {
+        uint4 x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = ((const uint4*)tops)[j / 4 + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) ge += (x[u].x >= tv) + (x[u].y >= tv) + (x[u].z >= tv) + (x[u].w >= tv);
+    }
+    for (; j < n; ++j) ge += tops[j] >= tv;
+    return ge;
+}
+
 // ---- workgroup reductions (all threads call, all get the result) -----------
 template <int NT>
 __device__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
+    v = wave_max_u64(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) scratch[wave] = v;
@@ -109,8 +171,7 @@ __device__ uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
 template <int NT>
 __device__ uint64_t block_sum_u64(uint64_t v, uint64_t* scratch)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    v = wave_sum_u64(v);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     __syncthreads();
     if (lane == 0) scratch[wave] = v;
@@ -126,12 +187,7 @@ template <int NT>
 __device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t& excl, uint64_t* scratch)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint64_t incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t w = __shfl_up(incl, o);
-        if (lane >= o) incl += w;
-    }
+    const uint64_t incl = wave_scan_incl(v, OpAdd{});
     __syncthreads();
     if (lane == 63) scratch[wave] = incl;
     __syncthreads();
@@ -143,13 +199,6 @@ __device__ uint64_t block_exclusive_scan_u64(uint64_t v, uint64_t& excl, uint64_
     }
     excl = before + incl - v;
     return total;
-}
-
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t x)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-    return x;
 }
 
 // Bitonic sort of n (power of two) u64 keys in LDS, descending.  Strides of
@@ -290,22 +339,20 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
     if (tid < 64) {
         const int lane = tid;
         auto scan = [&](uint32_t base, uint64_t carry) {  // running sum at base + lane
-            uint64_t inc = base + lane < k ? keptE[base + lane] : 0;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint64_t y = __shfl_up(inc, o);
-                if (lane >= o) inc += y;
-            }
-            return inc + carry;
+            return wave_scan_incl((uint64_t)(base + lane < k ? keptE[base + lane] : 0), OpAdd{}) + carry;
         };
-        uint64_t z = 0;
-        for (uint32_t base = 0; base < k; base += 64) z = __shfl(scan(base, z), 63);
+        uint64_t z = 0, c0 = 0;
+        for (uint32_t base = 0; base < k; base += 64) {
+            const uint64_t c = scan(base, z);
+            if (base == 0) c0 = c;
+            z = lane63_u64(c);
+        }
         uint32_t nk = k;
         if (p.top_p < 1.0f) {
             const double thr = (double)p.top_p * (double)z;
             uint64_t carry = 0;
             for (uint32_t base = 0; base < k; base += 64) {
-                const uint64_t c = scan(base, carry);
+                const uint64_t c = base == 0 ? c0 : scan(base, carry);
                 const uint64_t hit = __ballot(base + lane < k && (double)c >= thr);
                 if (hit) {
                     const int first = __ffsll((unsigned long long)hit) - 1;
@@ -313,7 +360,7 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
                     z = __shfl(c, first);
                     break;
                 }
-                carry = __shfl(c, 63);
+                carry = lane63_u64(c);
             }
         }
         if (lane == 0) {
@@ -1523,16 +1570,6 @@ struct AcceptPlan {
     float lpm, lqm;
 };
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v)
-{
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint64_t w = __shfl_xor(v, o);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
 // Row total and top from the row's chunk parts (one wave, G <= 64).
 __device__ __forceinline__ void row_totals(const ChunkPart* rp, ChunkPlan cp, bool sums, uint64_t& top, uint64_t& Z)
 {
@@ -1788,9 +1825,7 @@ __global__ __launch_bounds__(kChunkThreads) void topk_scan_kernel(RowSrc rs, uin
         const uint32_t bk = (uint32_t)(best >> 32);
         uint32_t prev = 0xffffffffu;
         for (int j = 0; j < m; ++j) {  // uniform
-            uint32_t v = bk < prev ? bk : 0u;
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
+            const uint32_t v = wave_max_u32(bk < prev ? bk : 0u);
             if (lane == j) out[j] = v;
             prev = v;
         }
@@ -1941,7 +1976,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_sample_kernel(RowSrc rs, uin
                                                                   uint32_t k, TopkWs w)
 {
     constexpr int NT = kRowThreads, NWV = NT / 64;
-    __shared__ uint32_t tops[NWV * kTopM];
+    __shared__ __align__(16) uint32_t tops[NWV * kTopM];
     __shared__ uint64_t red[NWV];
     const uint32_t r = blockIdx.x, V4 = (V + 3) / 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1960,9 +1995,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_sample_kernel(RowSrc rs, uin
     }
     uint32_t prev = 0xffffffffu;
     for (int j = 0; j < m; ++j) {  // uniform
-        uint32_t t = bk < prev ? bk : 0u;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) t = max(t, (uint32_t)__shfl_xor((int)t, o));
+        const uint32_t t = wave_max_u32(bk < prev ? bk : 0u);
         if (lane == j) tops[wave * m + j] = t;
         prev = t;
     }
@@ -1971,11 +2004,7 @@ __global__ __launch_bounds__(kRowThreads) void topk_sample_kernel(RowSrc rs, uin
     uint32_t thr = 0;
     if (tid < n) {
         const uint32_t tv = tops[tid];
-        if (tv) {
-            uint32_t ge = 0;
-            for (int j = 0; j < n; ++j) ge += tops[j] >= tv;
-            if (ge >= k) thr = tv;
-        }
+        if (tv && count_ge(tops, n, tv) >= k) thr = tv;
     }
     thr = (uint32_t)block_max_u64<NT>(thr, red);  // 0 (no bound): every token, then the exact path
     if (tid == 0) {
@@ -2033,17 +2062,12 @@ __global__ __launch_bounds__(kChunkThreads) void topk_collect_kernel(RowSrc rs, 
             }
         }
         // one LDS slot reservation per wave: exclusive prefix of the lanes' counts
-        uint32_t incl = n;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t t = __shfl_up(incl, o);
-            if (lane >= o) incl += t;
-        }
-        const uint32_t total = __shfl(incl, 63);
+        const uint32_t incl = wave_scan_incl(n, OpAdd{});
+        const uint32_t total = lane63_u32(incl);
         if (!total) continue;  // uniform in the wave
         uint32_t base = 0;
         if (lane == 0) base = atomicAdd(&ln, total);
-        base = __shfl(base, 0);
+        base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
         uint32_t slot = base + incl - n;
 #pragma unroll
         for (int u = 0; u < kCollectU; ++u) {
@@ -2127,8 +2151,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
     constexpr int NWV = NT / 64, F4 = kRowF4 * kRowThreads / NT;
     __shared__ uint64_t red[NWV];
     __shared__ uint64_t buf[kCandMax];
-    __shared__ uint64_t cand[kCandMax];
-    __shared__ uint32_t tops[NWV * kTopM];
+    __shared__ uint64_t cand[kCandMax + 64];  // + a spare entry per lane (below)
+    __shared__ __align__(16) uint32_t tops[NWV * kTopM];
     __shared__ uint32_t cand_count;
     __shared__ uint64_t keptE[kKMax];
     const uint32_t r = blockIdx.x, k = p.top_k, V4 = (V + 3) / 4;
@@ -2154,9 +2178,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
     const uint32_t bk = (uint32_t)(best >> 32);
     uint32_t prev = 0xffffffffu;
     for (int j = 0; j < m; ++j) {  // uniform
-        uint32_t t = bk < prev ? bk : 0u;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) t = max(t, (uint32_t)__shfl_xor((int)t, o));
+        const uint32_t t = wave_max_u32(bk < prev ? bk : 0u);
         if (lane == j) tops[wave * m + j] = t;  // packed: the n = NWV m kept keys in a row
         prev = t;
     }
@@ -2166,27 +2188,42 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void to
     uint32_t thr = 0;
     if (tid < n) {
         const uint32_t tv = tops[tid];
-        if (tv) {
-            uint32_t ge = 0;
-            for (int j = 0; j < n; ++j) ge += tops[j] >= tv;
-            if (ge >= k) thr = tv;
-        }
+        if (tv && count_ge(tops, n, tv) >= k) thr = tv;
     }
     thr = (uint32_t)block_max_u64<NT>(thr, red);  // 0 (no bound): every token, then the fallback
-    if (bk >= thr) {  // a thread whose largest key is below the bound holds no candidate
+    // this thread's candidates (bit 4 i + c: element 4 (tid + i NT) + c),
+    // written at slots reserved with one LDS atomic per wave (a wave prefix
+    // sum of the counts), not one dependent atomic per candidate.  Both
+    // loops are branch-free: every lane of a wave holding a candidate stores
+    // every element, the others into the lane's spare entry past kCandMax
+    // (unrolled with a branch per element, the loops took ~4 us).
+    using Mask = std::conditional_t<(4 * F4 > 32), uint64_t, uint32_t>;
+    Mask cm = 0;
+#pragma unroll
+    for (int i = 0; i < F4; ++i) {
+        const uint32_t q = tid + i * NT;
+        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            cm |= (Mask)((q < V4) & (4 * q + c < V) & (float_key(e[c]) >= thr)) << (4 * i + c);
+    }
+    const uint32_t cnt = (uint32_t)__builtin_popcountll((unsigned long long)cm);
+    const uint32_t incl = wave_scan_incl(cnt, OpAdd{});
+    const uint32_t wtot = lane63_u32(incl);
+    if (wtot) {  // uniform
+        uint32_t base = 0;
+        if (lane == 63) base = atomicAdd(&cand_count, wtot);
+        uint32_t slot = lane63_u32(base) + incl - cnt;
 #pragma unroll
         for (int i = 0; i < F4; ++i) {
             const uint32_t q = tid + i * NT;
             const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (q < V4 && 4 * q + c < V) {
-                    const uint32_t key = float_key(e[c]);
-                    if (key >= thr) {
-                        const uint32_t slot = atomicAdd(&cand_count, 1u);
-                        if (slot < (uint32_t)kCandMax) cand[slot] = order_key(key, 4 * q + c);
-                    }
-                }
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t ok = (uint32_t)(cm >> (4 * i + c)) & 1u;
+                cand[ok && slot < (uint32_t)kCandMax ? slot : kCandMax + lane] = order_key(float_key(e[c]), 4 * q + c);
+                slot += ok;
+            }
         }
     }
     __syncthreads();
