@@ -160,8 +160,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
                 tmax = fmaxf(tmax, s2[i][r]);
             }
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        tmax = fmaxf(tmax, xor_lane<16>(tmax));
+        tmax = fmaxf(tmax, xor_lane<32>(tmax));
         const float mnew = fmaxf(m, tmax);
         const float muse = mnew == -INFINITY ? 0.0f : mnew;
         const float alpha = exp2_fast(m - muse);
@@ -173,8 +173,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
                 p[i][r] = exp2_fast(s2[i][r] - muse);
                 psum += p[i][r];
             }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
+        psum += xor_lane<16>(psum);
+        psum += xor_lane<32>(psum);
         l = l * alpha + psum;
         m = mnew;
         if (jr != j0) {  // the first round starts from O = 0: nothing to rescale

@@ -33,6 +33,44 @@ __device__ __forceinline__ half2_t splat2(float v)
     return h;
 }
 
+// v from lane (lane ^ M) of the wave, M = 1, 2, 4, 8, 16 or 32: DPP moves
+// (quad permutes, row shifts and rotates) and the gfx950 row and half swaps
+// (v_permlane16_swap, v_permlane32_swap) instead of an LDS permute
+// (ds_bpermute: a round trip through the LDS crossbar, ~100 cycles, where
+// these take a few).  The values moved are the same, so a reduction written
+// with them gives the same bits.  Every lane of the wave must be active.
+template <int M>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v)
+{
+    const int x = (int)v;
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_update_dpp(x, x, 0xb1, 0xf, 0xf, false);  // quad_perm [1, 0, 3, 2]
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_update_dpp(x, x, 0x4e, 0xf, 0xf, false);  // quad_perm [2, 3, 0, 1]
+    } else if constexpr (M == 4) {
+        r = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0x5, false);  // row_shl:4 into lanes 0-3, 8-11 of each row
+        r = __builtin_amdgcn_update_dpp(r, x, 0x114, 0xf, 0xa, false);  // row_shr:4 into lanes 4-7, 12-15
+    } else if constexpr (M == 8) {
+        r = __builtin_amdgcn_update_dpp(x, x, 0x128, 0xf, 0xf, false);  // row_ror:8
+    } else if constexpr (M == 16) {
+        // rows (0, 1, 2, 3) -> p[0] = rows (0, 0, 2, 2), p[1] = rows (1, 1, 3, 3)
+        const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        r = (int)((threadIdx.x & 16) ? p[0] : p[1]);
+    } else {
+        static_assert(M == 32, "xor_lane: M is 1, 2, 4, 8, 16 or 32");
+        // halves (lo, hi) -> p[0] = (lo, lo), p[1] = (hi, hi)
+        const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        r = (int)((threadIdx.x & 32) ? p[0] : p[1]);
+    }
+    return (uint32_t)r;
+}
+template <int M>
+__device__ __forceinline__ float xor_lane(float v)
+{
+    return __builtin_bit_cast(float, xor_lane_u32<M>(__builtin_bit_cast(uint32_t, v)));
+}
+
 // Split operand of an fp32 activation for the fp16 MFMAs: hi = fp16(x), lo =
 // fp16((x - hi) * 2^11) (x - hi is exact in fp32), so x = hi + lo * 2^-11 to
 // about 22 bits.  Products of either part with an fp16 weight are exact in

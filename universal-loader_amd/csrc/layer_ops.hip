@@ -80,8 +80,12 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint8_t* __restrict__ 
         }
     }
     float sq = v * v;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+    sq += xor_lane<32>(sq);
+    sq += xor_lane<16>(sq);
+    sq += xor_lane<8>(sq);
+    sq += xor_lane<4>(sq);
+    sq += xor_lane<2>(sq);
+    sq += xor_lane<1>(sq);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = sq;
     __syncthreads();
     if (threadIdx.x == 0) pss[(size_t)m * gridDim.x + blockIdx.x] = ((part[0] + part[1]) + part[2]) + part[3];

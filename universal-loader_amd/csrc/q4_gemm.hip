@@ -928,8 +928,12 @@ __device__ __forceinline__ float rs_reduce(const GemmArgs& a, float4 v)
 {
     const int p0 = 4 * (threadIdx.x & 63), P = a.f.rs_P;
     float ss = ((p0 < P ? v.x : 0.0f) + (p0 + 1 < P ? v.y : 0.0f)) + ((p0 + 2 < P ? v.z : 0.0f) + (p0 + 3 < P ? v.w : 0.0f));
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss += xor_lane<32>(ss);
+    ss += xor_lane<16>(ss);
+    ss += xor_lane<8>(ss);
+    ss += xor_lane<4>(ss);
+    ss += xor_lane<2>(ss);
+    ss += xor_lane<1>(ss);
     return 1.0f / __builtin_sqrtf(ss / (float)a.K + a.f.rs_eps);
 }
 
@@ -1106,7 +1110,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
     const GemmFuse& f = a.f;
     switch (f.epi) {
     case kEpiRope: {
-        const float other = __shfl_xor(s, 1);
+        const float other = xor_lane<1>(s);
         if (!ok) break;
         const bool odd = n & 1;
         const size_t pos = kv_row(f, pos0, m);
@@ -1130,7 +1134,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
         break;
     }
     case kEpiSilu: {
-        const float u = __shfl_xor(s, 1);
+        const float u = xor_lane<1>(s);
         if (ok && !(n & 1)) {
             const float sg = s * (1.0f / (1.0f + det_expf(-s)));
             _Float16 hi, lo;
@@ -1153,10 +1157,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float s, int m, int 
             }
         }
         float sq = v * v;
-        sq += __shfl_xor(sq, 1);
-        sq += __shfl_xor(sq, 2);
-        sq += __shfl_xor(sq, 4);
-        sq += __shfl_xor(sq, 8);
+        sq += xor_lane<1>(sq);
+        sq += xor_lane<2>(sq);
+        sq += xor_lane<4>(sq);
+        sq += xor_lane<8>(sq);
         if (m < a.M && t < a.n_tiles && (l & 15) == 0) f.pss_out[(size_t)m * a.n_tiles + t] = sq;
         break;
     }
@@ -1378,7 +1382,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemm_slice_kernel(GemmArgs a)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float v = acc[mt][i];
-            if (a.hl) v = v + __shfl_xor(v, 32) * kLoUnscale;  // lanes 0-31: + their low-part slot
+            if (a.hl) v = v + xor_lane<32>(v) * kLoUnscale;  // lanes 0-31: + their low-part slot
             const int m = acc_row(a, mt, lane, i);
             if (m >= 0 && m < a.M && n < a.N) out[(size_t)m * a.N + n] = v;
         }
