@@ -357,7 +357,8 @@ __device__ void finish_topk(uint64_t* buf, uint32_t k, float lmax, const WarpPar
                 if (hit) {
                     const int first = __ffsll((unsigned long long)hit) - 1;
                     nk = base + first + 1;
-                    z = __shfl(c, first);
+                    z = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)c, first) |
+                        (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(c >> 32), first) << 32;
                     break;
                 }
                 carry = lane63_u64(c);
@@ -500,7 +501,7 @@ __device__ __forceinline__ void wave_bin_add(bool act, uint32_t d, uint64_t w, T
     uint64_t pend = __ballot(act);
     while (pend) {  // wave-uniform
         const int leader = __builtin_ctzll(pend);
-        const uint32_t dl = (uint32_t)__shfl((int)d, leader);
+        const uint32_t dl = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
         const bool mine = act && d == dl;
         const uint64_t m = __ballot(mine);
         const uint64_t x = wave_sum_u64(mine ? w : 0);
@@ -519,7 +520,7 @@ __device__ __forceinline__ void wave_bin_count(bool act, uint32_t d, ToppLds& s)
     uint64_t pend = __ballot(act);
     while (pend) {  // wave-uniform
         const int leader = __builtin_ctzll(pend);
-        const uint32_t dl = (uint32_t)__shfl((int)d, leader);
+        const uint32_t dl = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
         const uint64_t m = __ballot(act && d == dl);
         if (lane == leader) atomicAdd(&s.count[dl], (uint32_t)__popcll(m));
         pend &= ~m;
