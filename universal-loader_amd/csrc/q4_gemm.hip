@@ -1531,18 +1531,26 @@ __device__ __forceinline__ int epi_row(const GemmArgs& a, int l, int row)
 }
 
 // Sum of the P part sums of tile slot j in LDS, in part order; with split X
-// the high-part sum (lane l) plus 2^-11 times the low-part sum (lane l + 32).
-__device__ __forceinline__ float red_sum(const GemmArgs& a, const float* red, int j, int P, int row, int l)
+// the high-part sum (lane l) plus 2^-11 times the low-part sum (lane l ^ 32).
+// All 2P reads are issued before the first add (one LDS round trip; a loop
+// over a run-time P waited on each read).
+template <int P>
+__device__ __forceinline__ float red_sum(const GemmArgs& a, const float* red, int j, int row, int l)
 {
-    float s = red[((j * P) * 4 + row) * 64 + l];
-    for (int p = 1; p < P; ++p) s += red[((j * P + p) * 4 + row) * 64 + l];
-    if (a.hl) {
-        const int lo_lane = l ^ 32;
-        float t = red[((j * P) * 4 + row) * 64 + lo_lane];
-        for (int p = 1; p < P; ++p) t += red[((j * P + p) * 4 + row) * 64 + lo_lane];
-        s = s + t * kLoUnscale;
+    const float* b = red + (j * P * 4 + row) * 64;
+    float hv[P], lv[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        hv[p] = b[p * 256 + l];
+        lv[p] = b[p * 256 + (l ^ 32)];
     }
-    return s;
+    float s = hv[0], t = lv[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p) {
+        s += hv[p];
+        t += lv[p];
+    }
+    return a.hl ? s + t * kLoUnscale : s;
 }
 
 // Row scales of rows wave, wave + NW, ... (every row of a whole-X kernel, at
@@ -1586,8 +1594,10 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
-    const int P = a.ks_count, tpi = NW / P;
-    const int tw = wave / P, p = wave - (wave / P) * P;
+    // every launch splits K into NW parts (ks_count == NW): one tile per
+    // workgroup, part p = wave
+    constexpr int P = NW, tpi = 1;
+    const int tw = 0, p = wave;
     const int ca = p * a.ks_q + min(p, a.ks_r);
     const int cb = ca + a.ks_q + (p < a.ks_r ? 1 : 0);
     const int nc0 = max(0, min(CMAX, cb - ca));
@@ -1629,7 +1639,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     // 256 threads per tile slot, NW / 4 slots per pass
     const int row = (threadIdx.x >> 6) & 3, l = lane;
     for (int j = j_epi; j < tpi; j += NW / 4) {
-        float s = red_sum(a, red, j, P, row, l);
+        float s = red_sum<P>(a, red, j, row, l);
         const int tt = it * tpi + j;
         const int m = epi_row(a, l, row), n = 16 * tt + (l & 15);
         if (a.f.rs_pss && m < a.M) s *= rs[m];
@@ -1738,7 +1748,7 @@ __global__ __launch_bounds__(kRingWaves * 64) void gemm_ring_kernel(GemmArgs a)
             if (j < G * TPI) {
                 const int gk = j / TPI, jj = j - gk * TPI, li = base + gk;
                 if (li < n_loc) {
-                    float s = red_sum(a, red[gk], jj, P, row, lane);
+                    float s = red_sum<P>(a, red[gk], jj, row, lane);
                     const int tt = ((int)blockIdx.x + li * (int)gridDim.x) * TPI + jj;
                     const int m = epi_row(a, lane, row);
                     if (a.f.rs_pss && m < a.M) s *= rs[m];
