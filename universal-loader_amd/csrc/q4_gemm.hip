@@ -1639,10 +1639,12 @@ __global__ __launch_bounds__(NW * 64) void gemm_stream_kernel(GemmArgs a)
     // 256 threads per tile slot, NW / 4 slots per pass
     const int row = (threadIdx.x >> 6) & 3, l = lane;
     for (int j = j_epi; j < tpi; j += NW / 4) {
+        const int m = epi_row(a, l, row);
+        const float rsm = rs[min(m, 15)];  // read beside the part sums (m <= 16)
         float s = red_sum<P>(a, red, j, row, l);
         const int tt = it * tpi + j;
-        const int m = epi_row(a, l, row), n = 16 * tt + (l & 15);
-        if (a.f.rs_pss && m < a.M) s *= rs[m];
+        const int n = 16 * tt + (l & 15);
+        if (a.f.rs_pss && m < a.M) s *= rsm;
         epilogue(a, s, m, n, tt, l, j == j_epi ? pre : epi_load(a, m, n, pos0), pos0);
     }
 }
@@ -1748,10 +1750,11 @@ __global__ __launch_bounds__(kRingWaves * 64) void gemm_ring_kernel(GemmArgs a)
             if (j < G * TPI) {
                 const int gk = j / TPI, jj = j - gk * TPI, li = base + gk;
                 if (li < n_loc) {
+                    const int m = epi_row(a, lane, row);
+                    const float rsm = rs[min(m, 15)];  // read beside the part sums (m <= 16)
                     float s = red_sum<P>(a, red[gk], jj, row, lane);
                     const int tt = ((int)blockIdx.x + li * (int)gridDim.x) * TPI + jj;
-                    const int m = epi_row(a, lane, row);
-                    if (a.f.rs_pss && m < a.M) s *= rs[m];
+                    if (a.f.rs_pss && m < a.M) s *= rsm;
                     epilogue(a, s, m, 16 * tt + (lane & 15), tt, lane, pre[q], pos0);
                 }
             }
