@@ -249,23 +249,25 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attn_kernel(AttnArgs a)
 
 // out[qi][h][d] = sum_s O_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the
 // splits that hold keys, in split order (deterministic).  Grid (H, nq), D
-// threads; (m, l) of every split staged in LDS, O loads 16 splits at a time.
-// The first loads do not wait for the device-side prefix length: they read
-// splits 0..min(16, splits)-1 of the workspace (which holds all `splits`
-// partials, so every read is in bounds; a split past the last one holding
-// keys reads stale values that are never used) and the count of live splits
-// masks them afterwards.
-template <int D>
+// threads; (m, l) of every split staged in LDS.  SU >= splits (16, 32 or
+// 64): every O load and every LDS read is issued before the first use, none
+// waits for the device-side prefix length.  They read splits
+// 0..min(u, splits - 1) of the workspace (which holds all `splits` partials,
+// so every read is in bounds; a split past the last one holding keys reads
+// stale values) and the count of live splits masks them afterwards with
+// selects, so the sums keep split order.
+template <int D, int SU>
 __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
 {
     __shared__ float sm[kAttnMaxSplits], sl[kAttnMaxSplits];
+    static_assert(SU <= kAttnMaxSplits, "SU splits staged in LDS");
     const int h = blockIdx.x, qi = blockIdx.y, b = blockIdx.z, d = threadIdx.x;
     const int S = a.splits;
     const size_t stride = (size_t)a.nq * (D + 2);
     const float* q0 = a.part + ((size_t)b * a.H + h) * S * stride + qi * (D + 2);
-    float first[16];
+    float ov[SU];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) first[u] = q0[min(u, S - 1) * stride + d];
+    for (int u = 0; u < SU; ++u) ov[u] = q0[min(u, S - 1) * stride + d];
     const int ds = min(d, S - 1);
     const float mv = q0[ds * stride + D], lv = q0[ds * stride + D + 1];
     int n_prefix, L;
@@ -276,21 +278,23 @@ __global__ __launch_bounds__(D) void attn_merge_kernel(AttnArgs a)
         sl[d] = lv;
     }
     __syncthreads();
+    float mu[SU], lu[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+        mu[u] = sm[u];
+        lu[u] = sl[u];
+    }
     float M = -INFINITY;
-    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, sm[sp]);
+#pragma unroll
+    for (int u = 0; u < SU; ++u) M = u < ns ? fmaxf(M, mu[u]) : M;
     const float Mu = M == -INFINITY ? 0.0f : M;
     float o = 0.0f, Ls = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 16) {
-        float ov[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) ov[u] = s0 == 0 ? first[u] : q0[min(s0 + u, S - 1) * stride + d];
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-            if (s0 + u < ns) {
-                const float f = exp2_fast(sm[s0 + u] - Mu);
-                o += ov[u] * f;
-                Ls += sl[s0 + u] * f;
-            }
+    for (int u = 0; u < SU; ++u) {
+        const float f = exp2_fast(mu[u] - Mu);
+        const bool live = u < ns;
+        o = live ? o + ov[u] * f : o;
+        Ls = live ? Ls + lu[u] * f : Ls;
     }
     store_out<D>(a, (((size_t)b * a.nq + qi) * a.H + h) * D + d, o / Ls);
 }
@@ -304,7 +308,12 @@ void launch_attn(const AttnArgs& a, int T, hipStream_t st)
     case 2: hipLaunchKernelGGL((attn_kernel<D, 2>), grid, block, 0, st, a); break;
     default: hipLaunchKernelGGL((attn_kernel<D, 4>), grid, block, 0, st, a); break;
     }
-    if (a.splits > 1) hipLaunchKernelGGL(attn_merge_kernel<D>, dim3(a.H, a.nq, a.nseq), dim3(D), 0, st, a);
+    if (a.splits > 1) {
+        const dim3 mg(a.H, a.nq, a.nseq);
+        if (a.splits <= 16) hipLaunchKernelGGL((attn_merge_kernel<D, 16>), mg, dim3(D), 0, st, a);
+        else if (a.splits <= 32) hipLaunchKernelGGL((attn_merge_kernel<D, 32>), mg, dim3(D), 0, st, a);
+        else hipLaunchKernelGGL((attn_merge_kernel<D, kAttnMaxSplits>), mg, dim3(D), 0, st, a);
+    }
 }
 
 }  // namespace
