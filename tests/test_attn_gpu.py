@@ -75,6 +75,7 @@ def test_attention_config_shape(ctx, ora, rng, mode):
 @pytest.mark.parametrize("P,nq,H,Hkv,D", [
     (0, 1, 4, 4, 64), (0, 16, 2, 1, 128), (7, 3, 8, 2, 64), (63, 5, 8, 8, 128),
     (64, 6, 8, 8, 128), (250, 16, 6, 3, 64), (1000, 9, 4, 1, 128), (2047, 1, 16, 16, 64),
+    (4096, 5, 8, 8, 64),  # 33 splits: the merge's 64-split instantiation
 ])
 def test_attention_shapes(ctx, ora, rng, P, nq, H, Hkv, D):
     for parent in (None, random_tree(rng, nq)):
